@@ -1,0 +1,129 @@
+/*
+ * kvx — C ABI of the MI355X decode-time KV data plane (libkvx.so).
+ *
+ * Every entry point takes plain integers: device addresses of caller-owned
+ * buffers (tensor.data_ptr()), sizes, and a hipStream_t passed as uint64_t
+ * (0 = the null stream).  Launches are asynchronous and never synchronise the
+ * host.  A nonzero return is an error; kvx_last_error() gives the message
+ * (thread-local), with the same text the reference's pybind layer raises.
+ *
+ * Each declaration names the reference entry point it replaces
+ * (jsun8686/kv_offload_proto, kvops/kvops_ext/kvops_ext.cpp).
+ *
+ * Status protocol (a fix of the reference's inconsistent layout): the status
+ * ring is made of 64-byte slots; for a launch with status address `st`, the
+ * word at st + myNode*64 + b*8 (b < block_dim <= 8) receives
+ *     err (bits 0..31) | doneSeq=1 (bits 32..39) | queued (bits 40..63)
+ * once every row of that launch has landed.  kvx_poll_status() masks the
+ * doneSeq byte, so EmsPool-style waits that poll st + s*64 + b*8 work as-is.
+ */
+#ifndef KVX_KVX_H
+#define KVX_KVX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* kvops_ext.cpp:139-185 kv_init.  Selects the device and allocates the 8-byte
+ * tail-slot word.  The kernels are linked into libkvx.so, so code_object_path
+ * and rt_lib are accepted for signature compatibility and not opened.
+ * Errors: "kvops already inited", "hipSetDevice failed ...". */
+int kvx_init(int device_id, const char *code_object_path, const char *rt_lib);
+
+/* kvops_ext.cpp:187-196 kv_alloc_status.  count*64 zeroed bytes of coherent
+ * pinned host memory whose host and device addresses are equal; *out_addr
+ * receives that address. */
+int kvx_alloc_status(int count, uint64_t *out_addr);
+
+/* kvops_ext.cpp:198-218 kv_poll_status.  Reads the word at status_addr from
+ * the host until its doneSeq byte is 1 and returns the err field; returns
+ * -0x2000 after timeout_us microseconds (timeout_us < 0 waits forever) and
+ * -0x1000 if status_addr is not inside a status allocation. */
+int64_t kvx_poll_status(uint64_t status_addr, int64_t timeout_us);
+
+/* kvops_ext.cpp:221-254 kv_import_seg: copy this segment's miss rows into the
+ * hot buffer.  Error: "import blockDim must be <= 8 (status slot layout)". */
+int kvx_import_seg(uint64_t channel, uint64_t seg_base, uint32_t layer_offset_rows,
+                   uint32_t per_layer_seg_rows, uint32_t row_bytes, uint64_t topk_indices,
+                   uint64_t req_pool_indices, uint64_t req_host_base, uint64_t topk_device_slots,
+                   uint64_t is_miss, uint64_t num_real, uint64_t hot_row_base, uint32_t top_k,
+                   uint32_t max_num_reqs, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node,
+                   uint64_t status, uint64_t stream, uint32_t block_dim);
+
+/* kv_import_seg with the per-request hot-row stride the reference leaves in
+ * KvcGatherArgs.reserved (kvc_args.h:37): hot row = slot + bid*stride. */
+int kvx_import_seg_strided(uint64_t channel, uint64_t seg_base, uint32_t layer_offset_rows,
+                           uint32_t per_layer_seg_rows, uint32_t row_bytes, uint64_t topk_indices,
+                           uint64_t req_pool_indices, uint64_t req_host_base,
+                           uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real,
+                           uint64_t hot_row_base, uint32_t top_k, uint32_t max_num_reqs,
+                           uint32_t stripe_rows, uint32_t node_num, uint32_t my_node, uint64_t status,
+                           uint64_t stream, uint32_t block_dim, uint32_t hot_req_stride_rows);
+
+/* All N segments in one launch sequence (xds_ems_pool.py:204-217 batch_read
+ * issues N kv_import_seg calls; this is the fused form).  seg_bases points to
+ * node_num host integers; status words are written for every node. */
+int kvx_import_all(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,
+                   uint32_t row_bytes, uint64_t topk_indices, uint64_t req_pool_indices,
+                   uint64_t req_host_base, uint64_t topk_device_slots, uint64_t is_miss,
+                   uint64_t num_real, uint64_t hot_row_base, uint32_t top_k, uint32_t max_num_reqs,
+                   uint32_t stripe_rows, uint32_t node_num, uint64_t status, uint64_t stream,
+                   uint32_t block_dim, uint32_t hot_req_stride_rows);
+
+/* kvops_ext.cpp:256-278 kv_export_seg_alllayer: copy rows [row_lo,
+ * row_lo+row_cnt) of every layer owned by my_node from HBM to the segment.
+ * block_dim only sets how many status words are written (<= 8). */
+int kvx_export_seg_alllayer(uint64_t channel, uint64_t seg_base, uint32_t per_layer_seg_rows,
+                            uint32_t row_bytes, uint32_t row_lo, uint32_t row_cnt, uint32_t layer_num,
+                            uint64_t src_layer0_base, uint64_t src_layer_stride, uint32_t stripe_rows,
+                            uint32_t node_num, uint32_t my_node, uint64_t status, uint64_t stream,
+                            uint32_t block_dim);
+
+/* kvops_ext.cpp:281-336 kv_sieve_update.  Same validation messages; the hash
+ * table size is derived identically; block_dim is accepted and only feeds the
+ * informational reqsPerCore field (the grid is one workgroup per batch row). */
+int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t seq_lens,
+                     uint64_t prefill_lens, uint64_t device_buffer_tokens,
+                     uint64_t device_buffer_visited, uint64_t device_buffer_ht, uint64_t sieve_hand,
+                     uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real, uint32_t top_k,
+                     uint32_t device_buffer_size, uint32_t padded_buffer_size,
+                     uint32_t visited_stride_b, uint32_t max_num_reqs, uint32_t pool_size,
+                     uint64_t stream, uint32_t block_dim);
+
+/* kvops_ext.cpp:339-358 kv_sieve_ht_init.  The grid always covers
+ * layer_num*num_reqs (layer, request) pairs; block_dim is accepted and unused. */
+int kvx_sieve_ht_init(uint64_t device_buffer_tokens, uint64_t device_buffer_ht, uint64_t prefill_lens,
+                      uint32_t req_start, uint32_t num_reqs, uint32_t layer_num, uint32_t pool_size,
+                      uint32_t device_buffer_size, uint32_t padded_buffer_size, uint32_t ht_size,
+                      uint64_t stream, uint32_t block_dim);
+
+/* kvops_ext.cpp:360-371 kv_close.  Frees the tail-slot word, the status
+ * allocations and the library scratch; idempotent. */
+int kvx_close(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *kvx_last_error(void);
+
+/* Host segment memory (replaces the EMS daemon's mmap'd segments,
+ * ems/emsd/pool_mgr.cc:23-41): pinned host memory mapped into the device
+ * address space with equal host/device addresses.  flags: 0 = non-coherent
+ * (coarse-grained), 1 = coherent (fine-grained). */
+int kvx_host_alloc(uint64_t bytes, uint32_t flags, uint64_t *out_addr);
+int kvx_host_free(uint64_t addr);
+
+/* Value of the device tail-slot word (0 = no kernel hit a bound); reading it
+ * synchronises the device.  kvx_clear_overflow() zeroes it. */
+int kvx_read_overflow(uint64_t *out_value);
+int kvx_clear_overflow(void);
+
+/* Which SIEVE kernel variant the last kvx_sieve_update launched
+ * (0 = LDS-staged, 1 = HBM-resident).  For tests and benchmarks. */
+int kvx_last_sieve_variant(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVX_KVX_H */

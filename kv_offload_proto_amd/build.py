@@ -1,0 +1,76 @@
+"""Build the native parts of kv_offload_proto_amd in-tree.
+
+* ``kvops_ext/libkvx.so`` -- the gfx950 kernels and the C ABI (include/kvx/kvx.h),
+  compiled by hipcc for ``--offload-arch=gfx950``.
+* ``kvops_ext/_kvops*.so`` -- the pybind11 module with the reference's
+  ``kvops_ext._kvops`` surface, linked against libkvx.so (rpath $ORIGIN).
+
+Run ``python -m kv_offload_proto_amd.build`` (or call :func:`build`).
+"""
+import os
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "kvops_ext")
+INCLUDE = os.path.join(ROOT, "include")
+
+HIP_SOURCES = ["sieve.hip", "rows.hip", "kvx_host.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    # hand-packed FP32 forms are not used anywhere; keep the compiler from
+    # forming them either
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def lib_path():
+    return os.path.join(OUT, "libkvx.so")
+
+
+def ext_path():
+    return os.path.join(OUT, "_kvops" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build(verbose=False):
+    """Compile libkvx.so (gfx950) and the _kvops module.  Always recompiles."""
+    os.makedirs(OUT, exist_ok=True)
+    lib = lib_path()
+    tmp = lib + ".tmp"
+    cmd = [HIPCC] + HIP_FLAGS + ["-shared", "-I", INCLUDE, "-I", CSRC, "-o", tmp]
+    cmd += [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    _run(cmd, verbose)
+    os.replace(tmp, lib)
+
+    import pybind11
+
+    ext = ext_path()
+    tmp = ext + ".tmp"
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+        "-I", pybind11.get_include(), "-I", sysconfig.get_paths()["include"], "-I", INCLUDE,
+        "-o", tmp, os.path.join(CSRC, "kvops_pybind.cpp"),
+        "-L", OUT, "-lkvx", "-Wl,-rpath,$ORIGIN",
+    ]
+    _run(cmd, verbose)
+    os.replace(tmp, ext)
+    return lib, ext
+
+
+if __name__ == "__main__":
+    build(verbose="-q" not in sys.argv)

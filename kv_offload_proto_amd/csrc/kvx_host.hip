@@ -1,0 +1,583 @@
+// C-ABI of libkvx.so: validation, derived geometry, status slots, host
+// segments and kernel launches.  Mirrors kvops/kvops_ext/kvops_ext.cpp of the
+// reference (same entry points, argument meaning and error texts); the
+// Ascend fatbin loading chain is replaced by kernels linked into this library.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "kvx/kvx.h"
+#include "kvx_internal.h"
+
+namespace {
+
+thread_local std::string t_lastError;
+
+struct Alloc {
+    uint64_t addr;
+    uint64_t bytes;
+};
+
+struct State {
+    bool inited = false;
+    int device = 0;
+    uint64_t *overflow = nullptr;   // the 8-byte tail-slot word
+    size_t ldsLimit = 0;            // dynamic LDS per workgroup usable by SIEVE
+    std::vector<Alloc> status;      // kvx_alloc_status allocations
+    kvx::RowScratch scratch{};
+    uint32_t epoch = 0;
+    int lastSieveVariant = -1;
+};
+
+State g;
+std::mutex g_hostMu;
+std::map<uint64_t, uint64_t> g_hostAllocs;  // kvx_host_alloc: addr -> bytes
+std::mutex g_statusMu;
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void hipCheck(hipError_t e, const char *what)
+{
+    if (e != hipSuccess) throw Error(std::string(what) + " failed: " + hipGetErrorString(e));
+}
+
+void EnsureInited()
+{
+    if (!g.inited) throw Error("kvops not inited");
+}
+
+template <typename F>
+int Guarded(F &&f)
+{
+    try {
+        f();
+        t_lastError.clear();
+        return 0;
+    } catch (const std::exception &e) {
+        t_lastError = e.what();
+        return -1;
+    }
+}
+
+hipStream_t AsStream(uint64_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+void CheckAligned16(uint64_t addr, const char *what)
+{
+    if ((addr & 15u) != 0) throw Error(std::string(what) + " must be 16-byte aligned");
+}
+
+// Host-visible pointer for a status word inside one of our allocations, or null.
+volatile uint64_t *StatusWord(uint64_t addr)
+{
+    std::lock_guard<std::mutex> lk(g_statusMu);
+    for (const Alloc &a : g.status) {
+        if (addr >= a.addr && addr + 8 <= a.addr + a.bytes && (addr & 7u) == 0) {
+            return reinterpret_cast<volatile uint64_t *>(addr);
+        }
+    }
+    return nullptr;
+}
+
+// Clear `words` status words of node slot `node` from the host, before the
+// launch is queued (kvops_ext.cpp:252,276 clear synchronously too).
+void ClearStatusWords(uint64_t status, uint32_t node, uint32_t words)
+{
+    if (status == 0) return;
+    for (uint32_t b = 0; b < words; ++b) {
+        volatile uint64_t *w = StatusWord(status + node * 64ull + b * 8ull);
+        if (w != nullptr) *w = 0;
+    }
+}
+
+void EnsureWinScratch(uint64_t entries)
+{
+    if (g.scratch.winEntries >= entries) return;
+    uint64_t cap = std::max<uint64_t>(entries, 65536);
+    if (g.scratch.win != nullptr) {
+        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        hipCheck(hipFree(g.scratch.win), "hipFree");
+        g.scratch.win = nullptr;
+        g.scratch.winEntries = 0;
+    }
+    void *p = nullptr;
+    hipCheck(hipMalloc(&p, cap * sizeof(unsigned long long)), "hipMalloc(gather scratch)");
+    hipCheck(hipMemset(p, 0, cap * sizeof(unsigned long long)), "hipMemset(gather scratch)");
+    g.scratch.win = static_cast<unsigned long long *>(p);
+    g.scratch.winEntries = cap;
+    g.epoch = 0;
+}
+
+uint32_t NextEpoch(hipStream_t stream)
+{
+    if (++g.epoch == 0) {  // tags of 2^32 calls ago could alias: clear and restart
+        hipCheck(hipMemsetAsync(g.scratch.win, 0, g.scratch.winEntries * sizeof(unsigned long long), stream),
+                 "hipMemsetAsync(gather scratch)");
+        g.epoch = 1;
+    }
+    return g.epoch;
+}
+
+struct GatherCall {
+    uint64_t segBases[64];
+    uint32_t nSeg;
+    bool fused;
+    uint64_t channel, segBase;
+    uint32_t layerOffsetRows, perLayerSegRows, rowBytes;
+    uint64_t topk, pool, hostBase, slots, isMiss, numReal, hotRowBase;
+    uint32_t topK, maxNumReqs, stripeRows, nodeNum, myNode;
+    uint64_t status, stream;
+    uint32_t blockDim, stride;
+};
+
+void DoGather(const GatherCall &c)
+{
+    EnsureInited();
+    if (c.blockDim > 8) throw Error("import blockDim must be <= 8 (status slot layout)");  // kvops_ext.cpp:228-230
+    if (c.rowBytes == 0 || c.rowBytes % 16 != 0) throw Error("import_seg: row_bytes must be a positive multiple of 16");
+    if (c.nodeNum == 0 || c.nodeNum > 64) throw Error("import_seg: node_num must be in [1, 64]");
+    if (!c.fused && c.myNode >= c.nodeNum) throw Error("import_seg: my_node must be < node_num");
+    CheckAligned16(c.hotRowBase, "import_seg: hot_row_base");
+    if (c.fused) {
+        for (uint32_t s = 0; s < c.nSeg; ++s) CheckAligned16(c.segBases[s], "import_all: seg_bases");
+    } else {
+        CheckAligned16(c.segBase, "import_seg: seg_base");
+    }
+    const uint32_t bd = c.blockDim == 0 ? 1u : c.blockDim;
+    const uint64_t positions = static_cast<uint64_t>(c.maxNumReqs) * c.topK;
+    if (positions == 0) return;
+
+    kvx::GatherPlan plan{};
+    KvcGatherArgs &a = plan.a;
+    a.channel = c.channel;
+    a.segBase = c.segBase;
+    a.topkIndices = c.topk;
+    a.reqPoolIndices = c.pool;
+    a.reqHostBase = c.hostBase;
+    a.topKDeviceSlots = c.slots;
+    a.isMiss = c.isMiss;
+    a.numReal = c.numReal;
+    a.hotRowBase = c.hotRowBase;
+    a.status = c.status;
+    a.layerOffsetRows = c.layerOffsetRows;
+    a.perLayerSegRows = c.perLayerSegRows;
+    a.rowBytes = c.rowBytes;
+    a.stripeRows = c.stripeRows;
+    a.nodeNum = c.nodeNum;
+    a.myNode = c.fused ? 0u : c.myNode;
+    a.topK = c.topK;
+    a.maxNumReqs = c.maxNumReqs;
+    a.positionsPerCore = static_cast<uint32_t>((positions + bd - 1) / bd);  // kvops_ext.cpp:250-251
+    a.hotReqStrideRows = c.stride;
+    plan.segBases = c.segBases;
+    plan.fused = c.fused ? 1u : 0u;
+    plan.spanRows = c.stride == 0 ? 0u : std::min<uint32_t>(c.stride, 65536u);
+    plan.statusWords = bd;
+
+    const uint64_t need = static_cast<uint64_t>(c.maxNumReqs - 1) * plan.spanRows + 65536ull;
+    EnsureWinScratch(need);
+    hipStream_t st = AsStream(c.stream);
+    plan.epoch = NextEpoch(st);
+    if (c.fused) {
+        for (uint32_t s = 0; s < c.nodeNum; ++s) ClearStatusWords(c.status, s, bd);
+    } else {
+        ClearStatusWords(c.status, c.myNode, bd);
+    }
+    hipCheck(kvx::launch_gather(plan, g.scratch, reinterpret_cast<uint64_t>(g.overflow), st), "kvc_gather_rows launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *kvx_last_error(void) { return t_lastError.c_str(); }
+
+int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
+{
+    (void)code_object_path;
+    (void)rt_lib;
+    return Guarded([&] {
+        if (g.inited) throw Error("kvops already inited");  // kvops_ext.cpp:141-143
+        if (hipSetDevice(device_id) != hipSuccess) throw Error("hipSetDevice failed");
+        g.device = device_id;
+        void *p = nullptr;
+        if (hipMalloc(&p, 8) != hipSuccess || p == nullptr) throw Error("alloc overflow buf failed");
+        hipCheck(hipMemset(p, 0, 8), "hipMemset(overflow)");
+        g.overflow = static_cast<uint64_t *>(p);
+        int lds = 0;
+        hipCheck(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_id),
+                 "hipDeviceGetAttribute(LDS)");
+        g.ldsLimit = static_cast<size_t>(lds) - 64;  // room for the kernel's static LDS
+        hipCheck(kvx::sieve_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS)");
+        void *c = nullptr;
+        constexpr size_t kTable = 64 * 8 * sizeof(uint32_t);
+        hipCheck(hipMalloc(&c, 2 * kTable + 64), "hipMalloc(counters)");
+        hipCheck(hipMemset(c, 0, 2 * kTable + 64), "hipMemset(counters)");
+        g.scratch.counters = static_cast<uint32_t *>(c);
+        g.scratch.errs = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + kTable);
+        g.scratch.tickets = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + 2 * kTable);
+        g.inited = true;
+    });
+}
+
+int kvx_alloc_status(int count, uint64_t *out_addr)
+{
+    return Guarded([&] {
+        EnsureInited();
+        if (count <= 0) throw Error("alloc status failed");
+        void *p = nullptr;
+        const size_t bytes = static_cast<size_t>(count) * 64;
+        if (hipHostMalloc(&p, bytes, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess || p == nullptr) {
+            throw Error("alloc status failed");
+        }
+        void *d = nullptr;
+        if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess || d != p) {
+            (void)hipHostFree(p);
+            throw Error("alloc status failed: device address differs from host address");
+        }
+        std::memset(p, 0, bytes);
+        {
+            std::lock_guard<std::mutex> lk(g_statusMu);
+            g.status.push_back({reinterpret_cast<uint64_t>(p), bytes});
+        }
+        *out_addr = reinterpret_cast<uint64_t>(p);
+    });
+}
+
+int64_t kvx_poll_status(uint64_t status_addr, int64_t timeout_us)
+{
+    if (!g.inited) {
+        t_lastError = "kvops not inited";
+        return -0x1000;
+    }
+    volatile uint64_t *w = StatusWord(status_addr);
+    if (w == nullptr) return -0x1000;
+    const auto t0 = std::chrono::steady_clock::now();
+    uint32_t spins = 0;
+    while (true) {
+        const uint64_t v = __atomic_load_n(const_cast<uint64_t *>(w), __ATOMIC_ACQUIRE);
+        if (((v >> 32) & 0xFFu) == 1u) return static_cast<int64_t>(v & 0xFFFFFFFFull);  // F2: doneSeq byte
+        if (timeout_us >= 0) {
+            const auto us = std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0);
+            if (us.count() >= timeout_us) return -0x2000;
+        }
+        if (++spins < 4096) {
+            __builtin_ia32_pause();
+        } else {
+            std::this_thread::sleep_for(std::chrono::microseconds(20));
+        }
+    }
+}
+
+int kvx_import_seg(uint64_t channel, uint64_t seg_base, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,
+                   uint32_t row_bytes, uint64_t topk_indices, uint64_t req_pool_indices, uint64_t req_host_base,
+                   uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real, uint64_t hot_row_base,
+                   uint32_t top_k, uint32_t max_num_reqs, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node,
+                   uint64_t status, uint64_t stream, uint32_t block_dim)
+{
+    return kvx_import_seg_strided(channel, seg_base, layer_offset_rows, per_layer_seg_rows, row_bytes, topk_indices,
+                                  req_pool_indices, req_host_base, topk_device_slots, is_miss, num_real, hot_row_base,
+                                  top_k, max_num_reqs, stripe_rows, node_num, my_node, status, stream, block_dim, 0);
+}
+
+int kvx_import_seg_strided(uint64_t channel, uint64_t seg_base, uint32_t layer_offset_rows,
+                           uint32_t per_layer_seg_rows, uint32_t row_bytes, uint64_t topk_indices,
+                           uint64_t req_pool_indices, uint64_t req_host_base, uint64_t topk_device_slots,
+                           uint64_t is_miss, uint64_t num_real, uint64_t hot_row_base, uint32_t top_k,
+                           uint32_t max_num_reqs, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node,
+                           uint64_t status, uint64_t stream, uint32_t block_dim, uint32_t hot_req_stride_rows)
+{
+    return Guarded([&] {
+        GatherCall c{};
+        c.fused = false;
+        c.channel = channel;
+        c.segBase = seg_base;
+        c.layerOffsetRows = layer_offset_rows;
+        c.perLayerSegRows = per_layer_seg_rows;
+        c.rowBytes = row_bytes;
+        c.topk = topk_indices;
+        c.pool = req_pool_indices;
+        c.hostBase = req_host_base;
+        c.slots = topk_device_slots;
+        c.isMiss = is_miss;
+        c.numReal = num_real;
+        c.hotRowBase = hot_row_base;
+        c.topK = top_k;
+        c.maxNumReqs = max_num_reqs;
+        c.stripeRows = stripe_rows;
+        c.nodeNum = node_num;
+        c.myNode = my_node;
+        c.status = status;
+        c.stream = stream;
+        c.blockDim = block_dim;
+        c.stride = hot_req_stride_rows;
+        DoGather(c);
+    });
+}
+
+int kvx_import_all(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,
+                   uint32_t row_bytes, uint64_t topk_indices, uint64_t req_pool_indices, uint64_t req_host_base,
+                   uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real, uint64_t hot_row_base,
+                   uint32_t top_k, uint32_t max_num_reqs, uint32_t stripe_rows, uint32_t node_num, uint64_t status,
+                   uint64_t stream, uint32_t block_dim, uint32_t hot_req_stride_rows)
+{
+    return Guarded([&] {
+        if (seg_bases == nullptr) throw Error("import_all: seg_bases is null");
+        if (node_num == 0 || node_num > 64) throw Error("import_seg: node_num must be in [1, 64]");
+        GatherCall c{};
+        c.fused = true;
+        c.nSeg = node_num;
+        for (uint32_t s = 0; s < node_num; ++s) c.segBases[s] = seg_bases[s];
+        c.channel = 0;
+        c.segBase = seg_bases[0];
+        c.layerOffsetRows = layer_offset_rows;
+        c.perLayerSegRows = per_layer_seg_rows;
+        c.rowBytes = row_bytes;
+        c.topk = topk_indices;
+        c.pool = req_pool_indices;
+        c.hostBase = req_host_base;
+        c.slots = topk_device_slots;
+        c.isMiss = is_miss;
+        c.numReal = num_real;
+        c.hotRowBase = hot_row_base;
+        c.topK = top_k;
+        c.maxNumReqs = max_num_reqs;
+        c.stripeRows = stripe_rows;
+        c.nodeNum = node_num;
+        c.myNode = 0;
+        c.status = status;
+        c.stream = stream;
+        c.blockDim = block_dim;
+        c.stride = hot_req_stride_rows;
+        DoGather(c);
+    });
+}
+
+int kvx_export_seg_alllayer(uint64_t channel, uint64_t seg_base, uint32_t per_layer_seg_rows, uint32_t row_bytes,
+                            uint32_t row_lo, uint32_t row_cnt, uint32_t layer_num, uint64_t src_layer0_base,
+                            uint64_t src_layer_stride, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node,
+                            uint64_t status, uint64_t stream, uint32_t block_dim)
+{
+    return Guarded([&] {
+        EnsureInited();
+        if (block_dim > 8) throw Error("export blockDim must be <= 8 (status slot layout)");
+        if (row_bytes == 0 || row_bytes % 16 != 0) throw Error("export_seg_alllayer: row_bytes must be a positive multiple of 16");
+        if (node_num == 0 || node_num > 64) throw Error("export_seg_alllayer: node_num must be in [1, 64]");
+        if (my_node >= node_num) throw Error("export_seg_alllayer: my_node must be < node_num");
+        CheckAligned16(seg_base, "export_seg_alllayer: seg_base");
+        CheckAligned16(src_layer0_base, "export_seg_alllayer: src_layer0_base");
+        if (src_layer_stride % 16 != 0) throw Error("export_seg_alllayer: src_layer_stride must be a multiple of 16");
+        if (static_cast<uint64_t>(row_lo) + row_cnt > 0xFFFFFFFFull) throw Error("export_seg_alllayer: row range exceeds 32 bits");
+        KvcScatterAllArgs a{};
+        a.channel = channel;
+        a.segBase = seg_base;
+        a.srcLayer0Base = src_layer0_base;
+        a.srcLayerStride = src_layer_stride;
+        a.status = status;
+        a.perLayerSegRows = per_layer_seg_rows;
+        a.rowBytes = row_bytes;
+        a.rowLo = row_lo;
+        a.rowCnt = row_cnt;
+        a.layerNum = layer_num;
+        a.stripeRows = stripe_rows;
+        a.nodeNum = node_num;
+        a.myNode = my_node;
+        a.blockDim = block_dim == 0 ? 1u : block_dim;
+        const kvx::ExportGeometry geo = kvx::export_geometry(a);
+        if (geo.nStripes != 0 && geo.maxSegRow >= per_layer_seg_rows) {
+            throw Error("export_seg_alllayer: rows [row_lo, row_lo+row_cnt) exceed per_layer_seg_rows of the segment");
+        }
+        ClearStatusWords(status, my_node, a.blockDim);
+        hipCheck(kvx::launch_export(a, g.scratch, reinterpret_cast<uint64_t>(g.overflow), AsStream(stream)),
+                 "kvc_scatter_rows_alllayer launch");
+    });
+}
+
+int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t seq_lens, uint64_t prefill_lens,
+                     uint64_t device_buffer_tokens, uint64_t device_buffer_visited, uint64_t device_buffer_ht,
+                     uint64_t sieve_hand, uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real,
+                     uint32_t top_k, uint32_t device_buffer_size, uint32_t padded_buffer_size,
+                     uint32_t visited_stride_b, uint32_t max_num_reqs, uint32_t pool_size, uint64_t stream,
+                     uint32_t block_dim)
+{
+    return Guarded([&] {
+        EnsureInited();
+        // kvops_ext.cpp:288-296, same messages
+        if (padded_buffer_size % 16 != 0) {
+            throw Error("sieve_update: padded_buffer_size must be a multiple of 16 (64-byte rows)");
+        }
+        if (padded_buffer_size > 65534) {
+            throw Error("sieve_update: padded_buffer_size must be <= 65534 (uint16 hash slots)");
+        }
+        if (visited_stride_b % 64 != 0 || visited_stride_b < (padded_buffer_size + 7) / 8) {
+            throw Error("sieve_update: visited bitmap stride must be 64B aligned and cover padded");
+        }
+        // The reference's sweep never terminates for an empty buffer; reject it.
+        if (device_buffer_size < 1 || device_buffer_size > padded_buffer_size) {
+            throw Error("sieve_update: device_buffer_size must be in [1, padded_buffer_size]");
+        }
+        CheckAligned16(device_buffer_tokens, "sieve_update: device_buffer_tokens");
+        CheckAligned16(device_buffer_visited, "sieve_update: device_buffer_visited");
+        CheckAligned16(device_buffer_ht, "sieve_update: device_buffer_ht");
+        int64_t htSize = 1024;  // kvops_ext.cpp:297-300
+        while (htSize < 2 * (static_cast<int64_t>(padded_buffer_size) + top_k)) htSize <<= 1;
+        // kvops_ext.cpp:307-312 (kept for the args block; the grid is one workgroup per row)
+        const uint32_t bd = block_dim == 0 ? 1u : block_dim;
+        int64_t a0 = top_k, b0 = 64;
+        while (b0 != 0) {
+            const int64_t t = a0 % b0;
+            a0 = b0;
+            b0 = t;
+        }
+        const int64_t rpcAlign = 64 / (a0 == 0 ? 64 : a0);
+        int64_t rpc = (static_cast<int64_t>(max_num_reqs) + bd - 1) / bd;
+        rpc = (rpc + rpcAlign - 1) / rpcAlign * rpcAlign;
+        if (rpc < 1) rpc = 1;
+
+        HispSieveUpdateArgs a{};
+        a.topkIndices = topk_indices;
+        a.reqPoolIndices = req_pool_indices;
+        a.seqLens = seq_lens;
+        a.prefillLens = prefill_lens;
+        a.deviceBufferTokens = device_buffer_tokens;
+        a.deviceBufferVisited = device_buffer_visited;
+        a.deviceBufferHt = device_buffer_ht;
+        a.sieveHand = sieve_hand;
+        a.topKDeviceSlots = topk_device_slots;
+        a.isMiss = is_miss;
+        a.numReal = num_real;
+        a.status = 0;
+        a.topK = top_k;
+        a.deviceBufferSize = device_buffer_size;
+        a.paddedBufferSize = padded_buffer_size;
+        a.visitedStrideB = visited_stride_b;
+        a.maxNumReqs = max_num_reqs;
+        a.reqsPerCore = static_cast<uint32_t>(rpc);
+        a.htSize = static_cast<uint32_t>(htSize);
+        a.poolSize = pool_size;
+        const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
+                           visited_stride_b;
+        const int variant = lds <= g.ldsLimit ? 0 : 1;
+        a.reserved = static_cast<uint32_t>(variant);
+        g.lastSieveVariant = variant;
+        if (max_num_reqs == 0) return;
+        hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), variant, variant == 0 ? lds : 0,
+                                          AsStream(stream)),
+                 "hisp_sieve_update launch");
+    });
+}
+
+int kvx_sieve_ht_init(uint64_t device_buffer_tokens, uint64_t device_buffer_ht, uint64_t prefill_lens,
+                      uint32_t req_start, uint32_t num_reqs, uint32_t layer_num, uint32_t pool_size,
+                      uint32_t device_buffer_size, uint32_t padded_buffer_size, uint32_t ht_size, uint64_t stream,
+                      uint32_t block_dim)
+{
+    (void)block_dim;
+    return Guarded([&] {
+        EnsureInited();
+        if (ht_size < 8 || (ht_size & (ht_size - 1)) != 0) throw Error("sieve_ht_init: ht_size must be a power of two >= 8");
+        if (device_buffer_size > padded_buffer_size) {
+            throw Error("sieve_ht_init: device_buffer_size must be <= padded_buffer_size");
+        }
+        CheckAligned16(device_buffer_ht, "sieve_ht_init: device_buffer_ht");
+        HispSieveHtInitArgs a{};
+        a.deviceBufferTokens = device_buffer_tokens;
+        a.deviceBufferHt = device_buffer_ht;
+        a.prefillLens = prefill_lens;
+        a.status = 0;
+        a.reqStart = req_start;
+        a.numReqs = num_reqs;
+        a.layerNum = layer_num;
+        a.poolSize = pool_size;
+        a.deviceBufferSize = device_buffer_size;
+        a.paddedBufferSize = padded_buffer_size;
+        a.htSize = ht_size;
+        if (static_cast<uint64_t>(num_reqs) * layer_num == 0) return;
+        const size_t lds = static_cast<size_t>(ht_size) * 2;
+        hipCheck(kvx::launch_sieve_ht_init(a, reinterpret_cast<uint64_t>(g.overflow), lds <= g.ldsLimit ? lds : 0,
+                                           AsStream(stream)),
+                 "hisp_sieve_ht_init launch");
+    });
+}
+
+int kvx_close(void)
+{
+    return Guarded([&] {
+        if (g.overflow != nullptr) (void)hipFree(g.overflow);
+        g.overflow = nullptr;
+        if (g.scratch.win != nullptr) (void)hipFree(g.scratch.win);
+        if (g.scratch.counters != nullptr) (void)hipFree(g.scratch.counters);
+        g.scratch = kvx::RowScratch{};
+        {
+            std::lock_guard<std::mutex> lk(g_statusMu);
+            for (const Alloc &a : g.status) (void)hipHostFree(reinterpret_cast<void *>(a.addr));
+            g.status.clear();
+        }
+        g.epoch = 0;
+        g.inited = false;
+    });
+}
+
+int kvx_host_alloc(uint64_t bytes, uint32_t flags, uint64_t *out_addr)
+{
+    return Guarded([&] {
+        if (bytes == 0) throw Error("host_alloc: bytes must be > 0");
+        const unsigned f = hipHostMallocMapped | (flags == 1 ? hipHostMallocCoherent : hipHostMallocNonCoherent);
+        void *p = nullptr;
+        hipError_t e = hipHostMalloc(&p, bytes, f);
+        if (e != hipSuccess || p == nullptr) {
+            throw Error("host_alloc: hipHostMalloc of " + std::to_string(bytes) + " bytes failed: " + hipGetErrorString(e));
+        }
+        void *d = nullptr;
+        if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess || d != p) {
+            (void)hipHostFree(p);
+            throw Error("host_alloc: device address differs from host address");
+        }
+        std::lock_guard<std::mutex> lk(g_hostMu);
+        g_hostAllocs[reinterpret_cast<uint64_t>(p)] = bytes;
+        *out_addr = reinterpret_cast<uint64_t>(p);
+    });
+}
+
+int kvx_host_free(uint64_t addr)
+{
+    return Guarded([&] {
+        std::lock_guard<std::mutex> lk(g_hostMu);
+        auto it = g_hostAllocs.find(addr);
+        if (it == g_hostAllocs.end()) throw Error("host_free: unknown address");
+        hipCheck(hipHostFree(reinterpret_cast<void *>(addr)), "hipHostFree");
+        g_hostAllocs.erase(it);
+    });
+}
+
+int kvx_read_overflow(uint64_t *out_value)
+{
+    return Guarded([&] {
+        EnsureInited();
+        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        hipCheck(hipMemcpy(out_value, g.overflow, 8, hipMemcpyDeviceToHost), "hipMemcpy(overflow)");
+    });
+}
+
+int kvx_clear_overflow(void)
+{
+    return Guarded([&] {
+        EnsureInited();
+        hipCheck(hipMemset(g.overflow, 0, 8), "hipMemset(overflow)");
+    });
+}
+
+int kvx_last_sieve_variant(void) { return g.lastSieveVariant; }
+
+}  // extern "C"

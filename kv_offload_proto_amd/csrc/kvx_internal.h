@@ -1,0 +1,111 @@
+// Internal declarations shared by the gfx950 kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kvx/kv_layout.h"
+#include "kvx/kvc_args.h"
+
+namespace kvx {
+
+// ---------------------------------------------------------------------------
+// Hash and bitmap helpers (the state format of hisp_kernel_common.h:19-130).
+// ---------------------------------------------------------------------------
+
+// Knuth multiplicative hash, top 16 bits (hisp_kernel_common.h:23-26).
+__host__ __device__ __forceinline__ uint32_t ht_hash(int32_t token)
+{
+    return (static_cast<uint32_t>(token) * 2654435761u) >> 16;
+}
+
+// Codes stored in the tail-slot word when a kernel stops a loop that the
+// reference would spin on forever.
+constexpr uint64_t kOverflowProbe = 0x50524F4245ull;   // probe run longer than the table
+constexpr uint64_t kOverflowSweep = 0x5357454550ull;   // hand sweep longer than the buffer
+
+// Status error code of a miss row whose segment row lies outside the
+// segment's layer region: the reference's per-row band 0x2xx + (pos & 0xFF)
+// with op return code 1 in bits 16.. (kvc_gather_rows.cpp:78-81).
+__host__ __device__ __forceinline__ uint32_t row_error_code(uint64_t pos)
+{
+    return 0x200u + static_cast<uint32_t>(pos & 0xFFu) + (1u << 16);
+}
+
+// Stride of sieve_hand rows in int32 (64 bytes; hisp_kernel_common.h:20-21).
+constexpr int32_t kHandStride = 16;
+
+// ---------------------------------------------------------------------------
+// Scratch owned by the library (one per device), used by the row movers.
+// ---------------------------------------------------------------------------
+struct RowScratch {
+    unsigned long long *win;   // winner tags, (epoch << 32) | position
+    uint64_t winEntries;       // capacity of win[]
+    uint32_t *counters;        // [64 nodes][8 status words] queued counts
+    uint32_t *errs;            // [64 nodes][8 status words] first error code
+    uint32_t *tickets;         // [4] last-block tickets (gather, export)
+};
+
+// Launchers (implemented next to their kernels).
+hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int variant,
+                               size_t ldsBytes, hipStream_t stream);
+hipError_t launch_sieve_ht_init(const HispSieveHtInitArgs &a, uint64_t overflowSlot, size_t ldsBytes,
+                                hipStream_t stream);
+hipError_t sieve_set_lds_limit(size_t bytes);
+
+struct GatherPlan {
+    KvcGatherArgs a;               // args of the first (or only) segment
+    const uint64_t *segBases;      // device-visible bases of all segments (fused) or null
+    uint32_t fused;                // 1: copy for every node; 0: only a.myNode
+    uint32_t epoch;                // winner tag epoch of this call
+    uint32_t spanRows;             // bid stride used for the winner index
+    uint32_t statusWords;          // words per node slot (block_dim)
+};
+hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t overflowSlot,
+                         hipStream_t stream);
+hipError_t launch_export(const KvcScatterAllArgs &a, const RowScratch &scr, uint64_t overflowSlot,
+                         hipStream_t stream);
+
+// Export geometry of one segment: the stripes q of [rowLo, rowLo+rowCnt)
+// owned by myNode are q0, q0+N, ... (nStripes of them); each contributes its
+// highest in-range row.  ownedRows counts every in-range row of those stripes
+// (the reference's queued count per layer).  S == 0 is the identity layout on
+// node 0 (kv_layout.h:31-39), i.e. S = N = 1.
+struct ExportGeometry {
+    uint64_t q0 = 0, nStripes = 0, ownedRows = 0, maxSegRow = 0;
+    uint32_t S = 1, N = 1;
+};
+
+inline ExportGeometry export_geometry(const KvcScatterAllArgs &a)
+{
+    ExportGeometry g;
+    const uint64_t rowLo = a.rowLo, rowHi = static_cast<uint64_t>(a.rowLo) + a.rowCnt;
+    uint64_t S = a.stripeRows, N = a.nodeNum;
+    uint64_t my = a.myNode;
+    bool none = (a.rowCnt == 0 || N == 0);
+    if (S == 0) {
+        S = 1;
+        N = 1;
+        if (a.myNode != 0) none = true;
+        my = 0;
+    }
+    g.S = static_cast<uint32_t>(S);
+    g.N = static_cast<uint32_t>(N);
+    if (none) return g;
+    const uint64_t qlo = rowLo / S, qhi = (rowHi - 1) / S;
+    const uint64_t q0 = qlo + ((my + N - (qlo % N)) % N);
+    if (q0 > qhi) return g;
+    const uint64_t n = (qhi - q0) / N + 1;
+    uint64_t owned = n * S;
+    if (q0 == qlo) owned -= rowLo - qlo * S;
+    const uint64_t qlast = q0 + (n - 1) * N;
+    if (qlast == qhi) owned -= (qhi * S + S) - rowHi;
+    g.q0 = q0;
+    g.nStripes = n;
+    g.ownedRows = owned;
+    g.maxSegRow = qlast / N;
+    return g;
+}
+
+}  // namespace kvx

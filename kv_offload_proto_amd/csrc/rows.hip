@@ -1,0 +1,355 @@
+// Row movers for gfx950: decode miss import (host segments -> HBM hot buffer)
+// and prefill export (HBM -> host segments).
+//
+// Semantics follow kvops/kernel/kvc_gather_rows.cpp:12-96 and
+// kvc_scatter_rows_alllayer.cpp:11-67 of the reference, with the row
+// ownership of kv_layout.h.  The reference moves each row with one HCOMM
+// ReadNbi/WriteNbi; here the host segments are pinned host memory mapped
+// into the device address space, and each wave moves up to 64 rows at a time
+// as 16-byte chunks, 8 chunks in flight per lane, so hundreds of kilobytes of
+// host-link reads are outstanding across the grid.
+//
+// Completion: the last workgroup to finish (atomicInc ticket) stores the
+// status words with a system-scope release, after every workgroup fenced its
+// own row stores.  The reference's per-block Commit/Drain + MTE3 flush has the
+// same meaning: all rows of the launch have landed.
+#include "kvx_internal.h"
+
+namespace kvx {
+namespace {
+
+constexpr int kWaves = 4;          // waves per workgroup
+constexpr int kUnroll = 8;         // 16-byte chunks in flight per lane
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct GatherExtra {
+    uint64_t segBases[64];
+    unsigned long long *win;
+    uint64_t winEntries;
+    uint32_t *counters;
+    uint32_t *errs;
+    uint32_t *tickets;
+    uint32_t fused;
+    uint32_t epoch;
+    uint32_t spanRows;
+    uint32_t statusWords;
+};
+
+struct GatherParams {
+    KvxLaunch<KvcGatherArgs> l;  // the reference launch block comes first
+    GatherExtra x;
+};
+
+struct ExportExtra {
+    uint32_t *tickets;
+    uint64_t q0;          // first stripe owned by myNode
+    uint64_t nStripes;    // stripes owned by myNode inside [rowLo, rowLo+rowCnt)
+    uint64_t ownedRows;   // rows owned by myNode inside the range (reference queued / layer)
+    uint32_t S;           // stripe rows used for item math (S == 0 mapped to 1)
+    uint32_t N;           // node count used for item math (S == 0 mapped to 1)
+};
+
+struct ExportParams {
+    KvxLaunch<KvcScatterAllArgs> l;
+    ExportExtra x;
+};
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ void wave_sync_lds()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void store_status(uint64_t addr, uint64_t word)
+{
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(addr), word, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Copy `n` rows whose byte addresses sit in src[0..n), dst[0..n) (LDS, per
+// wave) with the whole wave: chunk c covers bytes [16*(c%cpr), +16) of row
+// c/cpr.  kUnroll loads are issued before their stores.
+__device__ __forceinline__ void wave_copy_rows(const uint64_t *src, const uint64_t *dst, uint32_t n, uint32_t cpr)
+{
+    const uint32_t total = n * cpr;
+    const uint32_t lane = static_cast<uint32_t>(lane_id());
+    for (uint32_t base = 0; base < total; base += 64u * kUnroll) {
+        u32x4 v[kUnroll];
+        uint64_t d[kUnroll];
+#pragma unroll
+        for (int j = 0; j < kUnroll; ++j) {
+            const uint32_t c = base + static_cast<uint32_t>(j) * 64u + lane;
+            d[j] = 0;
+            if (c < total) {
+                const uint32_t r = c / cpr;
+                const uint32_t o = (c - r * cpr) * 16u;
+                v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src[r] + o));
+                d[j] = dst[r] + o;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kUnroll; ++j) {
+            if (d[j] != 0) __builtin_nontemporal_store(v[j], reinterpret_cast<u32x4 *>(d[j]));
+        }
+    }
+}
+
+__device__ __forceinline__ int32_t clamp_num_real(uint64_t numRealAddr, uint32_t maxNumReqs)
+{
+    int32_t n = *reinterpret_cast<const int32_t *>(numRealAddr);
+    if (n > static_cast<int32_t>(maxNumReqs)) n = static_cast<int32_t>(maxNumReqs);  // kvc_gather_rows.cpp:17-21
+    return n < 0 ? 0 : n;
+}
+
+__device__ __forceinline__ uint64_t win_index(int64_t bid, int32_t slot, uint32_t spanRows)
+{
+    return static_cast<uint64_t>(bid) * spanRows + static_cast<uint64_t>(slot);
+}
+
+// Pass 1: per destination row, the last valid miss position (tagged with the
+// call's epoch so the scratch never needs clearing).  Block 0 also zeroes the
+// queued counters and the status words of the nodes this call reports.
+__global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
+{
+    const KvcGatherArgs &a = P.l.a;
+    const GatherExtra &x = P.x;
+    const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
+    const int64_t total = static_cast<int64_t>(numReal) * a.topK;
+    if (blockIdx.x == 0) {
+        const uint32_t n0 = x.fused ? 0u : a.myNode;
+        const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
+        for (uint32_t i = threadIdx.x; i < (n1 - n0) * 8u; i += blockDim.x) {
+            x.counters[n0 * 8u + i] = 0u;
+            x.errs[n0 * 8u + i] = 0u;
+        }
+        if (a.status != 0) {
+            for (uint32_t i = threadIdx.x; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
+                const uint32_t node = n0 + i / x.statusWords, b = i % x.statusWords;
+                store_status(a.status + node * 64ull + b * 8ull, 0ull);
+            }
+        }
+    }
+    const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
+    const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
+    const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
+    const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
+    const unsigned long long tagHi = static_cast<unsigned long long>(x.epoch) << 32;
+    for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < total;
+         p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        if (miss[p] == 0) continue;
+        const int32_t t = topk[p], s = slots[p];
+        if (t < 0 || s < 0 || s >= 65536) continue;
+        const int64_t bid = p / a.topK;
+        if (pool[bid] < 0) continue;
+        const uint64_t d = win_index(bid, s, x.spanRows);
+        if (d < x.winEntries) atomicMax(&x.win[d], tagHi | static_cast<unsigned long long>(p));
+    }
+}
+
+// Pass 2: copy the winners owned by the node(s) of this call, count the
+// reference's queued rows per (node, status word), last workgroup reports.
+__global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
+{
+    __shared__ uint64_t sSrc[kWaves][64];
+    __shared__ uint64_t sDst[kWaves][64];
+    __shared__ int sLast;
+    const KvcGatherArgs &a = P.l.a;
+    const GatherExtra &x = P.x;
+    const int wave = threadIdx.x / 64;
+    const uint32_t lane = static_cast<uint32_t>(lane_id());
+    const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
+    const int64_t total = static_cast<int64_t>(numReal) * a.topK;
+    const uint32_t cpr = a.rowBytes / 16u;
+    const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
+    const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
+    const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
+    const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
+    const int64_t *hostBase = reinterpret_cast<const int64_t *>(a.reqHostBase);
+    const unsigned long long tagHi = static_cast<unsigned long long>(x.epoch) << 32;
+    const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
+
+    for (int64_t chunk = static_cast<int64_t>(blockIdx.x) * kWaves + wave; chunk * 64 < total;
+         chunk += static_cast<int64_t>(gridDim.x) * kWaves) {
+        const int64_t p = chunk * 64 + lane;
+        bool owned = false, copy = false;
+        uint32_t key = 0;
+        uint64_t src = 0, dst = 0;
+        if (p < total && miss[p] != 0) {
+            const int32_t t = topk[p], s = slots[p];
+            const int64_t bid = p / a.topK;
+            if (t >= 0 && s >= 0 && pool[bid] >= 0) {
+                const uint32_t row = static_cast<uint32_t>(hostBase[bid] + t);  // kvc_gather_rows.cpp:69-73
+                const uint32_t node = kvx_node_of(row, a.stripeRows, a.nodeNum);
+                owned = x.fused ? (node < a.nodeNum) : (node == a.myNode);
+                if (owned) {
+                    key = node * 8u + static_cast<uint32_t>(static_cast<uint64_t>(p) / ppc);
+                    bool winner = true;
+                    if (s < 65536) {
+                        const uint64_t d = win_index(bid, s, x.spanRows);
+                        if (d < x.winEntries) winner = (x.win[d] == (tagHi | static_cast<unsigned long long>(p)));
+                    }
+                    const uint64_t segBase = x.fused ? x.segBases[node] : a.segBase;
+                    const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
+                    if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
+                        atomicCAS(&x.errs[key], 0u, row_error_code(static_cast<uint64_t>(p)));
+                        winner = false;
+                    }
+                    copy = winner;
+                    src = segBase + (static_cast<uint64_t>(a.layerOffsetRows) + segRow) * a.rowBytes;
+                    dst = a.hotRowBase +
+                          (static_cast<uint64_t>(s) + static_cast<uint64_t>(bid) * a.hotReqStrideRows) * a.rowBytes;
+                }
+            }
+        }
+        // queued counts, one atomic per distinct (node, status word) in the wave
+        uint64_t rem = __ballot(owned);
+        while (rem != 0) {
+            const int leader = __ffsll(static_cast<long long>(rem)) - 1;
+            const uint32_t k = __shfl(key, leader);
+            const uint64_t same = __ballot(owned && key == k);
+            if (lane == static_cast<uint32_t>(leader)) atomicAdd(&x.counters[k], static_cast<uint32_t>(__popcll(same)));
+            rem &= ~same;
+        }
+        const uint64_t cmask = __ballot(copy);
+        if (cmask == 0) continue;
+        const uint32_t rank = static_cast<uint32_t>(__popcll(cmask & ((1ull << lane) - 1ull)));
+        if (copy) {
+            sSrc[wave][rank] = src;
+            sDst[wave][rank] = dst;
+        }
+        wave_sync_lds();
+        wave_copy_rows(sSrc[wave], sDst[wave], static_cast<uint32_t>(__popcll(cmask)), cpr);
+        wave_sync_lds();
+    }
+
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int ticket = atomicInc(&x.tickets[0], gridDim.x - 1u);
+        sLast = (ticket == gridDim.x - 1u) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sLast || a.status == 0) return;
+    __threadfence();
+    const uint32_t n0 = x.fused ? 0u : a.myNode;
+    const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
+    for (uint32_t i = threadIdx.x; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
+        const uint32_t node = n0 + i / x.statusWords, b = i % x.statusWords;
+        uint64_t word = 1ull << 32;  // kvc_gather_rows.cpp:29-33, :93
+        if (static_cast<int64_t>(b * ppc) < total) {
+            const uint32_t q = __hip_atomic_load(&x.counters[node * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t err = __hip_atomic_load(&x.errs[node * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            word |= (static_cast<uint64_t>(q) << 40) | err;
+        }
+        store_status(a.status + node * 64ull + b * 8ull, word);
+    }
+}
+
+// Prefill export: item (layer l, owned stripe i) copies the stripe's winning
+// row (its highest row inside the range) to segment row q/N of layer l.
+__global__ __launch_bounds__(256) void kvx_export_alllayer(ExportParams P)
+{
+    __shared__ uint64_t sSrc[kWaves][64];
+    __shared__ uint64_t sDst[kWaves][64];
+    __shared__ int sLast;
+    const KvcScatterAllArgs &a = P.l.a;
+    const ExportExtra &x = P.x;
+    const int wave = threadIdx.x / 64;
+    const uint32_t lane = static_cast<uint32_t>(lane_id());
+    const uint64_t items = x.nStripes * a.layerNum;
+    const uint64_t rowHi = static_cast<uint64_t>(a.rowLo) + a.rowCnt;
+    const uint32_t cpr = a.rowBytes / 16u;
+
+    for (uint64_t base = (static_cast<uint64_t>(blockIdx.x) * kWaves + wave) * 64ull; base < items;
+         base += static_cast<uint64_t>(gridDim.x) * kWaves * 64ull) {
+        const uint64_t it = base + lane;
+        if (it < items) {
+            const uint64_t l = it / x.nStripes, i = it - l * x.nStripes;
+            const uint64_t q = x.q0 + i * x.N;
+            uint64_t w = q * x.S + x.S - 1ull;
+            if (w > rowHi - 1ull) w = rowHi - 1ull;
+            const uint64_t segRow = q / x.N;
+            sSrc[wave][lane] = a.srcLayer0Base + l * a.srcLayerStride + w * a.rowBytes;
+            sDst[wave][lane] = a.segBase + (l * a.perLayerSegRows + segRow) * a.rowBytes;
+        }
+        wave_sync_lds();
+        const uint64_t left = items - base;
+        wave_copy_rows(sSrc[wave], sDst[wave], static_cast<uint32_t>(left < 64ull ? left : 64ull), cpr);
+        wave_sync_lds();
+    }
+
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int ticket = atomicInc(&x.tickets[1], gridDim.x - 1u);
+        sLast = (ticket == gridDim.x - 1u) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sLast || a.status == 0) return;
+    __threadfence_system();
+    const uint32_t words = a.blockDim == 0 ? 1u : a.blockDim;
+    for (uint32_t b = threadIdx.x; b < words; b += blockDim.x) {
+        uint64_t word = 1ull << 32;  // kvc_scatter_rows_alllayer.cpp:59-61
+        if (b == 0) word |= (x.ownedRows * a.layerNum) << 40;
+        store_status(a.status + a.myNode * 64ull + b * 8ull, word);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t overflowSlot, hipStream_t stream)
+{
+    GatherParams P{};
+    P.l.a = plan.a;
+    P.l.overflowSlot = overflowSlot;
+    if (plan.fused) {
+        for (uint32_t s = 0; s < plan.a.nodeNum && s < 64u; ++s) P.x.segBases[s] = plan.segBases[s];
+    }
+    P.x.win = scr.win;
+    P.x.winEntries = scr.winEntries;
+    P.x.counters = scr.counters;
+    P.x.errs = scr.errs;
+    P.x.tickets = scr.tickets;
+    P.x.fused = plan.fused;
+    P.x.epoch = plan.epoch;
+    P.x.spanRows = plan.spanRows;
+    P.x.statusWords = plan.statusWords;
+    const uint64_t positions = static_cast<uint64_t>(plan.a.maxNumReqs) * plan.a.topK;
+    uint64_t prepBlocks = (positions + 255ull) / 256ull;
+    if (prepBlocks < 1) prepBlocks = 1;
+    if (prepBlocks > 2048) prepBlocks = 2048;
+    hipLaunchKernelGGL(kvx_gather_prep, dim3(static_cast<uint32_t>(prepBlocks)), dim3(256), 0, stream, P);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    uint64_t copyBlocks = (positions + 64ull * kWaves - 1ull) / (64ull * kWaves);
+    if (copyBlocks < 1) copyBlocks = 1;
+    if (copyBlocks > 4096) copyBlocks = 4096;
+    hipLaunchKernelGGL(kvx_gather_copy, dim3(static_cast<uint32_t>(copyBlocks)), dim3(256), 0, stream, P);
+    return hipGetLastError();
+}
+
+hipError_t launch_export(const KvcScatterAllArgs &a, const RowScratch &scr, uint64_t overflowSlot,
+                         hipStream_t stream)
+{
+    ExportParams P{};
+    P.l.a = a;
+    P.l.overflowSlot = overflowSlot;
+    P.x.tickets = scr.tickets;
+    const ExportGeometry geo = export_geometry(a);
+    P.x.q0 = geo.q0;
+    P.x.nStripes = geo.nStripes;
+    P.x.ownedRows = geo.ownedRows;
+    P.x.S = geo.S;
+    P.x.N = geo.N;
+    const uint64_t items = P.x.nStripes * a.layerNum;
+    uint64_t blocks = (items + 64ull * kWaves - 1ull) / (64ull * kWaves);
+    if (blocks < 1) blocks = 1;
+    if (blocks > 2048) blocks = 2048;
+    hipLaunchKernelGGL(kvx_export_alllayer, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, P);
+    return hipGetLastError();
+}
+
+}  // namespace kvx

@@ -1,0 +1,125 @@
+"""GPU parity of the row movers against the C oracle: prefill export into the
+host segments, miss import into the hot buffer (per segment and fused), and
+the status words of both."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import DevSieve, to_dev
+from kv_offload_proto_amd.xds import HostSegPool, streams
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DONE = 1 << 32
+
+
+def _src(layers, rows, row_bytes, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return torch.randint(0, 256, (layers, rows, row_bytes), dtype=torch.uint8, device="cuda", generator=g)
+
+
+@pytest.mark.parametrize("layers,layer_rows,N,S,row_lo,row_cnt,block_dim", [
+    (2, 2048, 2, 1, 0, 2048, 1),
+    (3, 1000, 3, 1, 17, 900, 2),
+    (2, 4096, 4, 64, 0, 4096, 1),     # striped: rows of a stripe alias one segment row
+    (2, 1500, 4, 64, 10, 1337, 3),    # partial first and last stripes
+    (1, 777, 1, 5, 0, 777, 8),
+])
+def test_export_parity(kvops, layers, layer_rows, N, S, row_lo, row_cnt, block_dim):
+    row_bytes = 1152
+    pool = HostSegPool(0, layers, layer_rows, row_bytes, stripe_rows=S, node_num=N)
+    pool.create_pool()
+    try:
+        segs = pool.segment_views()
+        for v in segs:
+            v[...] = 0xAB
+        src = _src(layers, layer_rows, row_bytes, 1234 + layer_rows)
+        st = pool.batch_write_alllayers(row_lo, row_cnt, src, layer_rows * row_bytes, block_dim=block_dim)
+        pool.wait(st, block_dim=block_dim)
+        torch.cuda.synchronize()
+        src_np = src.cpu().numpy()
+        plsr = pool.per_layer_seg_rows
+        for s in range(N):
+            exp = np.full(layers * plsr * row_bytes, 0xAB, dtype=np.uint8)
+            q = orc.export_alllayer(exp, src_np.reshape(-1), layer_rows * row_bytes, plsr, row_bytes, row_lo, row_cnt,
+                                    layers, S, N, s)
+            np.testing.assert_array_equal(segs[s].reshape(-1), exp, err_msg="segment {}".format(s))
+            words = _read_words(st + s * 64, block_dim)
+            assert words[0] == (q << 40) | DONE
+            assert all(w == DONE for w in words[1:])
+    finally:
+        pool.destroy(close_ext=False)
+
+
+def _read_words(addr, n):
+    buf = (ctypes.c_uint64 * n).from_address(addr)
+    return [int(x) for x in buf]
+
+
+@pytest.mark.parametrize("stride_mode", ["reference", "per_request"])
+@pytest.mark.parametrize("fused", [False, True])
+def test_gather_parity_after_sieve(kvops, stride_mode, fused):
+    """config-1 shapes: SIEVE on the GPU, then import; the hot buffer must equal
+    the oracle's byte for byte after every step (last-position-wins rule when
+    destinations collide, which stride 0 makes common)."""
+    req, prefill, top_k, dbs, L, N = 8, 256, 64, 64, 2, 2
+    row_bytes = 1152
+    layer_rows = req * prefill
+    pool = HostSegPool(0, L, layer_rows, row_bytes, stripe_rows=1, node_num=N)
+    pool.create_pool()
+    try:
+        src = _src(L, layer_rows, row_bytes, 99)
+        stt = pool.batch_write_alllayers(0, layer_rows, src, layer_rows * row_bytes)
+        pool.wait(stt)
+        st = orc.SieveState(L, req, dbs, top_k)
+        for r in range(req):
+            st.admit(r, prefill)
+        dev = DevSieve(st)
+        padded = st.padded
+        stride = 0 if stride_mode == "reference" else padded
+        hot_rows = padded if stride == 0 else req * padded
+        hot = torch.zeros((L, hot_rows, row_bytes), dtype=torch.uint8, device="cuda")
+        hot_np = np.zeros((L, hot_rows, row_bytes), dtype=np.uint8)
+        host_base = np.arange(req, dtype=np.int64) * prefill
+        host_base_d = to_dev(host_base)
+        segs = [v.reshape(-1) for v in pool.segment_views()]
+        rng = np.random.default_rng(42)
+        req_pool = np.arange(req)
+        seq = np.full(req, prefill)
+        plsr = pool.per_layer_seg_rows
+        for step in range(8):
+            layer = step % L
+            batch = streams.state_batch(rng, st.tokens[layer, :, :dbs], prefill, top_k, 0.5)
+            e_slots, e_miss = st.update(layer, batch, req_pool, seq, req)
+            g_slots, g_miss, keep = dev.update(kvops, layer, batch, req_pool, seq, req, req, top_k)
+            np.testing.assert_array_equal(g_slots, e_slots)
+            np.testing.assert_array_equal(g_miss, e_miss)
+            topk_d, pool_d, seq_d, nr, slots_d, miss_d = keep
+            if fused:
+                status = pool.batch_read_fused(layer, topk_d, pool_d, host_base_d, slots_d, miss_d, nr, hot[layer],
+                                               req, top_k, block_dim=2, hot_req_stride_rows=stride)
+            else:
+                status = pool.batch_read(layer, topk_d, pool_d, host_base_d, slots_d, miss_d, nr, hot[layer], req,
+                                         top_k, block_dim=2, hot_req_stride_rows=stride)
+            pool.wait(status, block_dim=2)
+            torch.cuda.synchronize()
+            for s in range(N):
+                _, words = orc.gather_rows(segs, hot_np[layer].reshape(-1), layer * plsr, row_bytes, batch, req_pool,
+                                           host_base, e_slots, e_miss, req, top_k, req, 1, N, s,
+                                           hot_req_stride_rows=stride, block_dim=2)
+                assert _read_words(status + s * 64, 2) == [int(w) for w in words], (step, s)
+            np.testing.assert_array_equal(hot.cpu().numpy(), hot_np, err_msg="step {}".format(step))
+    finally:
+        pool.destroy(close_ext=False)
+
+
+def test_status_poll_and_timeout(kvops):
+    st = kvops.alloc_status(4)
+    # nothing launched: the slot stays pending and the poll times out
+    assert kvops.poll_status(st, 2000) == -0x2000
+    # not a status address
+    assert kvops.poll_status(12345, 10) == -0x1000

@@ -1,0 +1,133 @@
+"""GPU parity of the SIEVE kernels against the C oracle: slots, is_miss and
+the full state (tokens, visited, hand, hash table) after every launch."""
+import numpy as np
+import pytest
+
+from gpu_helpers import DevSieve, to_dev
+from kv_offload_proto_amd.xds import streams
+from kv_offload_proto_amd.xds.configs import CONFIGS
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _admit_all(st, cfg):
+    for r in range(cfg.req_num):
+        st.admit(r, cfg.prefill)
+
+
+def test_ht_init_parity(kvops):
+    import torch
+
+    rng = np.random.default_rng(11)
+    layers, pool, dbs, top_k = 3, 5, 300, 64
+    st = orc.SieveState(layers, pool, dbs, top_k)
+    st.tokens[:] = -1
+    for l in range(layers):
+        for r in range(pool):
+            n = int(rng.integers(0, dbs + 1))
+            st.tokens[l, r, :n] = rng.choice(50000, size=n, replace=False)
+    dev = DevSieve(st)
+    dev.ht.fill_(77)
+    orc.sieve_ht_init(st.tokens, st.ht, 0, pool, layers, pool, dbs, st.padded, st.ht_size)
+    kvops.sieve_ht_init(dev.tokens.data_ptr(), dev.ht.data_ptr(), dev.prefill.data_ptr(), 0, pool, layers, pool,
+                        dbs, st.padded, st.ht_size, 0, layers)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dev.ht.cpu().numpy().view(np.uint16), st.ht)
+    assert kvops.read_overflow() == 0
+
+
+@pytest.mark.parametrize("cfg_id", [0, 1])
+def test_sieve_ref_stream_parity(kvops, cfg_id):
+    """The reference driver's stream (xds_decode.py:211-225): one layer per step."""
+    cfg = CONFIGS[cfg_id]
+    st = orc.SieveState(cfg.layers, cfg.req_num, cfg.dbs, cfg.top_k)
+    _admit_all(st, cfg)
+    dev = DevSieve(st)
+    rng = np.random.default_rng(cfg.seed)
+    req_pool = np.arange(cfg.req_num)
+    seq = np.full(cfg.req_num, cfg.prefill)
+    for step in range(cfg.steps):
+        batch = streams.ref_batch(rng, cfg.req_num, cfg.top_k, cfg.prefill, cfg.dbs, cfg.miss_ratio)
+        layer = step % cfg.layers
+        e_slots, e_miss = st.update(layer, batch, req_pool, seq, cfg.req_num)
+        g_slots, g_miss, _ = dev.update(kvops, layer, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
+        np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+        np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+        dev.assert_state_equal(layer)
+    assert kvops.read_overflow() == 0
+
+
+def test_sieve_state_stream_parity_all_layers(kvops):
+    """config 1 shapes, state-driven stream (~50% non-resident), every layer every step."""
+    cfg = CONFIGS[1]
+    st = orc.SieveState(cfg.layers, cfg.req_num, cfg.dbs, cfg.top_k)
+    _admit_all(st, cfg)
+    dev = DevSieve(st)
+    rng = np.random.default_rng(cfg.seed)
+    req_pool = np.arange(cfg.req_num)
+    seq = np.full(cfg.req_num, cfg.prefill)
+    for step in range(cfg.steps):
+        for layer in range(cfg.layers):
+            batch = streams.state_batch(rng, st.tokens[layer, :cfg.req_num, :cfg.dbs], cfg.prefill, cfg.top_k,
+                                        cfg.miss_ratio)
+            e_slots, e_miss = st.update(layer, batch, req_pool, seq, cfg.req_num)
+            g_slots, g_miss, _ = dev.update(kvops, layer, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
+            np.testing.assert_array_equal(g_miss, e_miss)
+            np.testing.assert_array_equal(g_slots, e_slots)
+    dev.assert_state_equal()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_sieve_defensive_cases_parity(kvops, seed):
+    """Padding rows, out-of-range pool rows, num_real > max, dirty hands,
+    invalid and decode-extension positions, duplicates, tiny buffers (wrap)."""
+    rng = np.random.default_rng(500 + seed)
+    dbs = int(rng.integers(1, 70))
+    top_k = int(rng.integers(1, 90))
+    pool, max_reqs = 6, 7
+    st = orc.SieveState(1, pool, dbs, top_k)
+    prefills = [int(rng.integers(1, 4 * dbs + 8)) for _ in range(pool)]
+    for r in range(pool):
+        st.admit(r, prefills[r])
+    st.hand[0, 1, 0] = dbs + 3
+    dev = DevSieve(st)
+    for step in range(5):
+        rows = list(rng.permutation(pool))[: int(rng.integers(1, pool + 1))]
+        req_pool = rows + [-1] * (max_reqs - len(rows))
+        req_pool[int(rng.integers(max_reqs))] = int(rng.choice([-4, pool, pool + 9]))
+        seen = set()
+        for i, p in enumerate(req_pool):
+            if 0 <= p < pool:
+                if p in seen:
+                    req_pool[i] = -1
+                seen.add(p)
+        num_real = int(rng.integers(0, max_reqs + 3))
+        seq = [int((prefills[p] if 0 <= p < pool else 5) + rng.integers(-3, 6)) for p in req_pool]
+        topk = np.stack([rng.integers(-3, max(s + 4, 2), size=top_k) for s in seq]).astype(np.int32)
+        e_slots, e_miss = st.update(0, topk, req_pool, seq, num_real, max_num_reqs=max_reqs)
+        g_slots, g_miss, _ = dev.update(kvops, 0, topk, req_pool, seq, num_real, max_reqs, top_k)
+        np.testing.assert_array_equal(g_miss, e_miss, err_msg="seed {} step {}".format(seed, step))
+        np.testing.assert_array_equal(g_slots, e_slots, err_msg="seed {} step {}".format(seed, step))
+        dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
+
+
+def test_sieve_validation_messages(kvops):
+    base = dict(topk_indices=0, req_pool_indices=0, seq_lens=0, prefill_lens=0, device_buffer_tokens=0,
+                device_buffer_visited=0, device_buffer_ht=0, sieve_hand=0, topk_device_slots=0, is_miss=0,
+                num_real=0, top_k=8, device_buffer_size=16, padded_buffer_size=16, visited_stride_b=64,
+                max_num_reqs=0, pool_size=1)
+    cases = [
+        (dict(padded_buffer_size=24), "padded_buffer_size must be a multiple of 16"),
+        (dict(padded_buffer_size=65536, device_buffer_size=65536), "padded_buffer_size must be <= 65534"),
+        (dict(visited_stride_b=32), "visited bitmap stride must be 64B aligned"),
+        (dict(padded_buffer_size=1024, device_buffer_size=1024, visited_stride_b=64),
+         "visited bitmap stride must be 64B aligned and cover padded"),
+    ]
+    for over, msg in cases:
+        kw = dict(base)
+        kw.update(over)
+        with pytest.raises(RuntimeError, match=msg):
+            kvops.sieve_update(**kw)
+    kvops.sieve_update(**base)  # max_num_reqs == 0: nothing to launch
