@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode-time KV data plane on one MI355X.
+
+A step is one decode step of the workload: for every layer, the SIEVE update
+of that layer's hot-buffer state followed by the import of its miss rows from
+the N host-pinned segments into the layer's hot buffer (for the reference
+stream, one layer per step).  Inputs (topK batches) are generated beforehand
+by running SIEVE over the same state and are resident in HBM; the state is
+restored before the timed replay, which therefore repeats the same work.
+
+Prints one JSON line.  ``value`` is miss rows imported per second through the
+whole path (SIEVE + import) over the timed steps.  SIEVE us/layer, import
+GB/s against the measured host-link peak, the prefill export rate, the
+roofline of the dominant kernel and the CPU oracle's rate are reported beside.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "SIEVE µs/layer; miss-row gather GB/s (% of host-link peak); rows/sec"
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--config", type=int, default=2, help="workload id (0-4), default 2 = DSA-decode scale")
+    p.add_argument("--per-segment", action="store_true", help="N per-segment imports instead of the fused import")
+    p.add_argument("--coherent", action="store_true", help="fine-grained (coherent) pinned segments")
+    p.add_argument("--cpu-sample-s", type=float, default=12.0, help="seconds of CPU oracle work for the baseline")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--verify", action="store_true", help="check the last step's imported rows on the GPU")
+    p.add_argument("--link-mib", type=int, default=256)
+    return p.parse_args()
+
+
+def pct(xs, q):
+    import numpy as np
+
+    return float(np.percentile(np.asarray(xs), q)) if len(xs) else None
+
+
+def measure_link_peak(runner, mib, log):
+    """Best of hipMemcpyAsync H2D from pinned memory and a zero-copy streaming
+    read from a host segment (16 B loads), both of `mib` MiB."""
+    import torch
+    from kv_offload_proto_amd.kvops_ext import _kvops
+
+    n = mib << 20
+    dst = torch.empty(n, dtype=torch.uint8, device=runner.dev)
+    pinned = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    pinned.fill_(1)
+    stream = torch.cuda.current_stream()
+    res = {}
+    best = 0.0
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        dst.copy_(pinned, non_blocking=True)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = max(best, n / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    res["memcpy_h2d_GBps"] = best
+    seg = runner.seg_bases[0]
+    seg_bytes = runner.pool.pool.segments[0].size_bytes
+    m = min(n, seg_bytes // 16 * 16)
+    best = 0.0
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        _kvops.stream_copy(dst.data_ptr(), seg, m, stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = max(best, m / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    res["zero_copy_read_GBps"] = best
+    res["peak_GBps"] = max(res["memcpy_h2d_GBps"], res["zero_copy_read_GBps"])
+    log("[bench] host link: memcpy H2D {:.1f} GB/s, zero-copy read {:.1f} GB/s".format(
+        res["memcpy_h2d_GBps"], res["zero_copy_read_GBps"]))
+    del dst, pinned
+    return res
+
+
+def sieve_bytes(cfg, padded, vis_stride, ht_size, dirty_reqs):
+    """Algorithmic HBM bytes of one SIEVE launch: per request topk/slots/miss
+    (9 B per position), 24 B of per-request scalars, the visited row in and
+    out, and the tokens + table rows in, and out again when the request had a
+    miss (the staging traffic of hisp_sieve_update.cpp:103-105,165-172)."""
+    per_req = 9 * cfg.top_k + 24 + 2 * vis_stride + (padded * 4 + ht_size * 2)
+    return cfg.req_num * per_req + dirty_reqs * (padded * 4 + ht_size * 2)
+
+
+def cpu_baseline(runner, plan, budget_s, log):
+    """The C oracle (oracle/liboracle.so) replaying the same batches from the
+    same initial state on one host core, SIEVE + import, for about budget_s."""
+    import numpy as np
+    import torch
+    from oracle import oracle as orc
+
+    cfg = runner.cfg
+    st = orc.SieveState(cfg.layers, cfg.req_num, cfg.dbs, cfg.top_k)
+    c = runner.coord
+    st.tokens[:] = c.device_buffer_tokens.cpu().numpy()
+    st.vis[:] = c.device_buffer_visited.cpu().numpy()
+    st.ht[:] = c.device_buffer_ht.cpu().numpy().view(np.uint16)
+    st.hand[:] = c.sieve_hand.cpu().numpy()
+    st.prefill_lens[:] = c.prefill_lens.cpu().numpy()
+    segs = [sg.view() for sg in runner.pool.pool.segments]
+    hot = np.zeros(cfg.req_num * runner.padded * cfg.row_bytes, dtype=np.uint8)
+    req_pool = np.arange(cfg.req_num, dtype=np.int64)
+    seq = np.full(cfg.req_num, cfg.prefill, dtype=np.int32)
+    host_base = np.array([cfg.host_base(r) for r in range(cfg.req_num)], dtype=np.int64)
+    plsr = runner.pool.per_layer_seg_rows
+    t_sieve = t_gather = 0.0
+    rows = done = 0
+    sieve_mismatch = 0
+    for step, layer, _, batch, gpu_misses in plan:
+        t0 = time.perf_counter()
+        slots, miss = st.update(layer, batch, req_pool, seq, cfg.req_num)
+        t1 = time.perf_counter()
+        for s in range(cfg.node_num):
+            orc.gather_rows(segs, hot, layer * plsr, cfg.row_bytes, batch, req_pool, host_base, slots, miss,
+                            cfg.req_num, cfg.top_k, cfg.req_num, cfg.stripe_rows, cfg.node_num, s,
+                            hot_req_stride_rows=runner.padded)
+        t2 = time.perf_counter()
+        t_sieve += t1 - t0
+        t_gather += t2 - t1
+        n = int(miss.sum())
+        sieve_mismatch += int(n != gpu_misses)
+        rows += n
+        done += 1
+        if t_sieve + t_gather >= budget_s:
+            break
+    total = t_sieve + t_gather
+    log("[bench] cpu oracle: {} layer-steps in {:.1f} s, {:.0f} rows/s, sieve {:.0f} us/layer".format(
+        done, total, rows / total, t_sieve / done * 1e6))
+    return {
+        "value": rows / total,
+        "unit": "rows/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": "first {} layer-steps of the benchmark stream ({} miss rows), oracle SIEVE + import, 1 thread".format(
+            done, rows),
+        "sieve_us_per_layer": t_sieve / done * 1e6,
+        "gather_GBps": rows * cfg.row_bytes / t_gather / 1e9 if t_gather > 0 else None,
+        "miss_count_mismatches": sieve_mismatch,
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this data plane runs on a single MI355X here "
+              "(--gpus {} is not supported; run with --gpus 1)".format(args.gpus), file=sys.stderr)
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import numpy as np
+    import torch
+
+    import kv_offload_proto_amd  # noqa: F401  (loads the native module)
+    from kv_offload_proto_amd.xds.configs import CONFIGS
+    from kv_offload_proto_amd.xds.workload import DecodeRunner
+
+    def log(msg):
+        print(msg, file=sys.stderr, flush=True)
+
+    if not torch.cuda.is_available():
+        log("[bench] no GPU visible")
+        return 1
+    cfg = CONFIGS[args.config]
+    t_start = time.perf_counter()
+    runner = DecodeRunner(cfg, coherent=args.coherent, log=log)
+    log("[bench] {}: setup {:.1f} s (HBM pool + {} pinned segments of {:.2f} GiB)".format(
+        cfg.name, runner.setup_s, cfg.node_num, runner.pool.pool.segments[0].size_bytes / 2**30))
+    export_us = runner.export_prefill()
+    export_gbps = runner.export_bytes / (export_us * 1e-6) / 1e9
+    log("[bench] prefill export: {} rows x {} layers = {} B in {:.1f} us ({:.1f} GB/s)".format(
+        cfg.host_reqs * cfg.prefill, cfg.layers, runner.export_bytes, export_us, export_gbps))
+    runner.admit_all()
+    link = measure_link_peak(runner, args.link_mib, log)
+
+    n_steps = args.warmup + args.steps
+    t0 = time.perf_counter()
+    plan, snap = runner.generate(n_steps)
+    log("[bench] generated {} layer-steps in {:.1f} s".format(len(plan), time.perf_counter() - t0))
+    per_step = len(plan) // n_steps if cfg.stream != "ref" else 1
+    warm, timed = plan[: args.warmup * per_step], plan[args.warmup * per_step:]
+
+    fused = not args.per_segment
+    stream = torch.cuda.current_stream()
+    for _, layer, topk_d, _, _ in warm:
+        runner.sieve(layer, topk_d)
+        runner.gather(layer, topk_d, fused=fused)
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in timed]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for (a, b, c), (_, layer, topk_d, _, _) in zip(ev, timed):
+        a.record(stream)
+        runner.sieve(layer, topk_d)
+        b.record(stream)
+        runner.gather(layer, topk_d, fused=fused)
+        c.record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    sieve_us = [a.elapsed_time(b) * 1e3 for a, b, _ in ev]
+    gather_us = [b.elapsed_time(c) * 1e3 for _, b, c in ev]
+    rows = sum(m for *_, m in timed)
+    ok, checked = (None, 0)
+    if args.verify and timed:
+        ok, checked = runner.verify_last_gather(timed[-1][1], timed[-1][2])
+        log("[bench] verify last step: {} ({} rows)".format(ok, checked))
+
+    # roofline of the dominant kernel
+    c = runner.coord
+    positions = cfg.req_num * cfg.top_k
+    gather_bytes = [m * cfg.row_bytes * 2 + positions * 9 for *_, m in timed]
+    gather_gbps_alg = sum(gather_bytes) / (sum(gather_us) * 1e-6) / 1e9
+    link_gbps = rows * cfg.row_bytes / (sum(gather_us) * 1e-6) / 1e9
+    sb = sieve_bytes(cfg, c.padded_buffer_size, c.visited_stride_b, c.ht_size, cfg.req_num)
+    sieve_gbps_alg = sb * len(timed) / (sum(sieve_us) * 1e-6) / 1e9
+    gather_roof = {"kernel": "kvx_gather_prep+kvx_gather_copy", "bound": "hbm", "achieved": gather_gbps_alg,
+                   "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gather_gbps_alg / HBM_PEAK_GBPS, "traffic": None,
+                   "bytes_per_launch": sum(gather_bytes) / len(timed),
+                   "avg_launch_us": sum(gather_us) / len(timed),
+                   "link": {"achieved": link_gbps, "peak": link["peak_GBps"], "unit": "GB/s",
+                            "frac": link_gbps / link["peak_GBps"]}}
+    sieve_roof = {"kernel": "kvx_sieve_update", "bound": "hbm", "achieved": sieve_gbps_alg, "peak": HBM_PEAK_GBPS,
+                  "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS, "traffic": None, "bytes_per_launch": sb,
+                  "avg_launch_us": sum(sieve_us) / len(timed)}
+    dominant, other = (gather_roof, sieve_roof) if sum(gather_us) >= sum(sieve_us) else (sieve_roof, gather_roof)
+
+    n_timed_steps = args.steps
+    value = rows / (total_ms * 1e-3)
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": n_timed_steps,
+        "warmup": args.warmup,
+        "ms_per_step": total_ms / n_timed_steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32",
+        "data": "synthetic (seeded topK streams, fp16 rows uniform in [-1,1))",
+        "config": {"workload": cfg.name, "req_num": cfg.req_num, "prefill": cfg.prefill, "top_k": cfg.top_k,
+                   "device_buffer_size": cfg.dbs, "miss_ratio": cfg.miss_ratio, "layers": cfg.layers,
+                   "node_num": cfg.node_num, "stripe_rows": cfg.stripe_rows, "row_bytes": cfg.row_bytes,
+                   "stream": cfg.stream, "zipf_s": cfg.zipf_s, "import": "fused" if fused else "per-segment",
+                   "segments": "coherent" if args.coherent else "non-coherent"},
+        "sieve_us_per_layer": {"median": pct(sieve_us, 50), "p99": pct(sieve_us, 99),
+                               "mean": sum(sieve_us) / len(sieve_us)},
+        "gather": {"us_per_layer_median": pct(gather_us, 50), "GBps": link_gbps,
+                   "frac_of_link_peak": link_gbps / link["peak_GBps"], "frac_of_hbm_peak": link_gbps / HBM_PEAK_GBPS,
+                   "rows_per_s": rows / (sum(gather_us) * 1e-6), "rows": rows},
+        "host_link": link,
+        "export": {"bytes": runner.export_bytes, "us": export_us, "GBps": export_gbps},
+        "roofline": dominant,
+        "roofline_other": other,
+        "verify": ok,
+    }
+    if not args.no_cpu:
+        runner.restore(snap)
+        out["cpu_baseline"] = cpu_baseline(runner, plan, args.cpu_sample_s, log)
+    else:
+        out["cpu_baseline"] = None
+    out["wall_s"] = time.perf_counter() - t_start
+    runner.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

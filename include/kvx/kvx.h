@@ -118,6 +118,13 @@ int kvx_host_free(uint64_t addr);
 int kvx_read_overflow(uint64_t *out_value);
 int kvx_clear_overflow(void);
 
+/* Measurement utility, no counterpart in the reference: copy `bytes`
+ * (multiple of 16, both addresses 16-byte aligned) from src to dst with a
+ * grid-stride 16-byte streaming kernel on `stream`.  With src in a pinned
+ * host segment it measures the zero-copy host-link read rate; with both in
+ * HBM it is the known-size copy used to calibrate traffic counters. */
+int kvx_stream_copy(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream);
+
 /* Which SIEVE kernel variant the last kvx_sieve_update launched
  * (0 = LDS-staged, 1 = HBM-resident).  For tests and benchmarks. */
 int kvx_last_sieve_variant(void);

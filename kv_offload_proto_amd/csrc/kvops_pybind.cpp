@@ -154,4 +154,10 @@ PYBIND11_MODULE(_kvops, m)
     });
     m.def("clear_overflow", []() { Check(kvx_clear_overflow()); });
     m.def("last_sieve_variant", []() { return kvx_last_sieve_variant(); });
+    m.def(
+        "stream_copy",
+        [](uint64_t dst, uint64_t src, uint64_t nbytes, uint64_t stream) {
+            Check(kvx_stream_copy(dst, src, nbytes, stream));
+        },
+        py::arg("dst"), py::arg("src"), py::arg("nbytes"), py::arg("stream") = 0);
 }

@@ -580,4 +580,16 @@ int kvx_clear_overflow(void)
 
 int kvx_last_sieve_variant(void) { return g.lastSieveVariant; }
 
+int kvx_stream_copy(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream)
+{
+    return Guarded([&] {
+        EnsureInited();
+        if (bytes % 16 != 0) throw Error("stream_copy: bytes must be a multiple of 16");
+        CheckAligned16(dst, "stream_copy: dst");
+        CheckAligned16(src, "stream_copy: src");
+        if (bytes == 0) return;
+        hipCheck(kvx::launch_stream_copy(dst, src, bytes, AsStream(stream)), "stream_copy launch");
+    });
+}
+
 }  // extern "C"

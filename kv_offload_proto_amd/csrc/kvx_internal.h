@@ -64,6 +64,7 @@ struct GatherPlan {
 };
 hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t overflowSlot,
                          hipStream_t stream);
+hipError_t launch_stream_copy(uint64_t dst, uint64_t src, uint64_t bytes, hipStream_t stream);
 hipError_t launch_export(const KvcScatterAllArgs &a, const RowScratch &scr, uint64_t overflowSlot,
                          hipStream_t stream);
 

@@ -298,7 +298,33 @@ __global__ __launch_bounds__(256) void kvx_export_alllayer(ExportParams P)
     }
 }
 
+// Plain streaming copy, 16 B per lane, kUnroll chunks in flight per lane.
+__global__ __launch_bounds__(256) void kvx_stream_copy(u32x4 *dst, const u32x4 *src, uint64_t n16)
+{
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
+        u32x4 v[kUnroll];
+#pragma unroll
+        for (int j = 0; j < kUnroll; ++j) v[j] = __builtin_nontemporal_load(src + i + j * stride);
+#pragma unroll
+        for (int j = 0; j < kUnroll; ++j) __builtin_nontemporal_store(v[j], dst + i + j * stride);
+    }
+    for (; i < n16; i += stride) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 }  // namespace
+
+hipError_t launch_stream_copy(uint64_t dst, uint64_t src, uint64_t bytes, hipStream_t stream)
+{
+    const uint64_t n16 = bytes / 16;
+    uint64_t blocks = (n16 + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(kvx_stream_copy, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream,
+                       reinterpret_cast<u32x4 *>(dst), reinterpret_cast<const u32x4 *>(src), n16);
+    return hipGetLastError();
+}
 
 hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t overflowSlot, hipStream_t stream)
 {

@@ -32,6 +32,16 @@ def ref_batch(rng, req_num, top_k, prefill, dbs, miss_ratio):
     return batch
 
 
+def _top_order(key, n, width):
+    """Column indices of the `width` largest keys per row, largest first
+    (only the first n are guaranteed; the rest follow in descending order)."""
+    if n <= 0:
+        return np.zeros((key.shape[0], width), dtype=np.int64)
+    part = np.argpartition(-key, n - 1, axis=1)[:, :width] if n < key.shape[1] else np.argsort(-key, axis=1)[:, :width]
+    sub = np.take_along_axis(key, part, axis=1)
+    return np.take_along_axis(part, np.argsort(-sub, axis=1, kind="stable"), axis=1)
+
+
 def state_batch(rng, tokens_rows, prefill, top_k, miss_ratio, zipf_s=None, miss_pool=None):
     """tokens_rows: [req, >=dbs] int32 resident tokens per request (-1 = empty).
 
@@ -74,19 +84,18 @@ def state_batch(rng, tokens_rows, prefill, top_k, miss_ratio, zipf_s=None, miss_
         rank = np.cumsum(resident[:, ::-1], axis=1)[:, ::-1] - 1  # 0 = newest resident position
         w = (np.maximum(rank, 0).astype(np.float64) + 1.0) ** (-float(zipf_s))
         hkey = np.where(resident, lu[1] / w, -np.inf)
-    morder = np.argsort(-mkey, axis=1, kind="stable")
-    horder = np.argsort(-hkey, axis=1, kind="stable")
+    take = min(top_k, prefill)
+    horder = _top_order(hkey, int(n_hit.max(initial=0)), take)
+    morder = _top_order(mkey, int(n_miss.max(initial=0)), take)
     out = np.full((req, top_k), -1, dtype=np.int64)
     col = np.arange(top_k)
     hsel = col[None, :] < n_hit[:, None]
     msel = (col[None, :] >= n_hit[:, None]) & (col[None, :] < (n_hit + n_miss)[:, None])
-    take = min(top_k, prefill)
     hpad = np.full((req, top_k), -1, dtype=np.int64)
-    hpad[:, :take] = horder[:, :take]
-    mpad = np.full((req, top_k), -1, dtype=np.int64)
+    hpad[:, :take] = horder
     idx = np.clip(col[None, :] - n_hit[:, None], 0, top_k - 1)
     mtake = np.full((req, top_k), -1, dtype=np.int64)
-    mtake[:, :take] = morder[:, :take]
+    mtake[:, :take] = morder
     mpad = np.take_along_axis(mtake, idx, axis=1)
     out[hsel] = hpad[hsel]
     out[msel] = mpad[msel]
