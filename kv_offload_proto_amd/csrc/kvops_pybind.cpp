@@ -154,6 +154,7 @@ PYBIND11_MODULE(_kvops, m)
     });
     m.def("clear_overflow", []() { Check(kvx_clear_overflow()); });
     m.def("last_sieve_variant", []() { return kvx_last_sieve_variant(); });
+    m.def("sieve_force_variant", [](int variant) { Check(kvx_sieve_force_variant(variant)); }, py::arg("variant"));
     m.def(
         "stream_copy",
         [](uint64_t dst, uint64_t src, uint64_t nbytes, uint64_t stream) {

@@ -37,6 +37,7 @@ struct State {
     kvx::RowScratch scratch{};
     uint32_t epoch = 0;
     int lastSieveVariant = -1;
+    int forcedSieveVariant = -1;
 };
 
 State g;
@@ -218,8 +219,9 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         int lds = 0;
         hipCheck(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_id),
                  "hipDeviceGetAttribute(LDS)");
-        g.ldsLimit = static_cast<size_t>(lds) - 64;  // room for the kernel's static LDS
+        g.ldsLimit = static_cast<size_t>(lds) - 256;  // room for the kernels' static LDS
         hipCheck(kvx::sieve_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS)");
+        hipCheck(kvx::sieve_fast_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS fast)");
         void *c = nullptr;
         constexpr size_t kTable = 64 * 8 * sizeof(uint32_t);
         hipCheck(hipMalloc(&c, 2 * kTable + 64), "hipMalloc(counters)");
@@ -466,15 +468,28 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         a.reqsPerCore = static_cast<uint32_t>(rpc);
         a.htSize = static_cast<uint32_t>(htSize);
         a.poolSize = pool_size;
+        // Variant: 2 = parallel LDS kernel, 0 = sequential LDS kernel, 1 = sequential HBM-resident.
         const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
                            visited_stride_b;
-        const int variant = lds <= g.ldsLimit ? 0 : 1;
+        const size_t ldsFast = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
+                                                visited_stride_b).total;
+        const bool fastOk = ldsFast <= g.ldsLimit && top_k < 0x3FFF &&
+                            static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535;
+        int variant = fastOk ? 2 : (lds <= g.ldsLimit ? 0 : 1);
+        if (g.forcedSieveVariant == 0 && lds <= g.ldsLimit) variant = 0;
+        if (g.forcedSieveVariant == 1) variant = 1;
+        if (g.forcedSieveVariant == 2 && fastOk) variant = 2;
         a.reserved = static_cast<uint32_t>(variant);
         g.lastSieveVariant = variant;
         if (max_num_reqs == 0) return;
-        hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), variant, variant == 0 ? lds : 0,
-                                          AsStream(stream)),
-                 "hisp_sieve_update launch");
+        if (variant == 2) {
+            hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow), ldsFast, AsStream(stream)),
+                     "hisp_sieve_update launch");
+        } else {
+            hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), variant,
+                                              variant == 0 ? lds : 0, AsStream(stream)),
+                     "hisp_sieve_update launch");
+        }
     });
 }
 
@@ -579,6 +594,14 @@ int kvx_clear_overflow(void)
 }
 
 int kvx_last_sieve_variant(void) { return g.lastSieveVariant; }
+
+int kvx_sieve_force_variant(int variant)
+{
+    return Guarded([&] {
+        if (variant < -1 || variant > 2) throw Error("sieve_force_variant: variant must be -1, 0, 1 or 2");
+        g.forcedSieveVariant = variant;
+    });
+}
 
 int kvx_stream_copy(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream)
 {

@@ -47,12 +47,51 @@ struct RowScratch {
     uint32_t *tickets;         // [4] last-block tickets (gather, export)
 };
 
+// ---------------------------------------------------------------------------
+// LDS layout of the parallel SIEVE kernel (byte offsets, 16-byte aligned):
+// the state row, then per-position, per-slot, per-event and per-cell scratch.
+// ---------------------------------------------------------------------------
+constexpr int kFastThreads = 1024;
+
+struct FastLayout {
+    uint32_t tok, ht, vis, ptok, pinf, vt, cpos, evslot, evold, cvlist, kcell, kstart, ber, bg, bm, total;
+};
+
+__host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
+
+__host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint32_t htSize, uint32_t topK,
+                                                           uint32_t visStrideB)
+{
+    FastLayout l{};
+    uint32_t o = 0;
+    l.tok = o;    o += align16(padded * 4u);
+    l.ht = o;     o += align16(htSize * 2u);
+    l.vis = o;    o += align16(visStrideB);
+    l.ptok = o;   o += align16(topK * 4u);
+    l.pinf = o;   o += align16(topK * 4u);
+    l.vt = o;     o += align16(padded * 2u);
+    l.cpos = o;   o += align16(topK * 2u);
+    l.evslot = o; o += align16(topK * 2u);
+    l.evold = o;  o += align16(topK * 2u);
+    l.cvlist = o; o += align16(topK * 2u);
+    l.kcell = o;  o += align16(topK * 4u);
+    l.kstart = o; o += align16(topK * 4u);
+    l.ber = o;    o += align16(htSize / 8u);
+    l.bg = o;     o += align16(htSize / 8u);
+    l.bm = o;     o += align16(htSize / 8u);
+    l.total = o;
+    return l;
+}
+
 // Launchers (implemented next to their kernels).
 hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int variant,
                                size_t ldsBytes, hipStream_t stream);
 hipError_t launch_sieve_ht_init(const HispSieveHtInitArgs &a, uint64_t overflowSlot, size_t ldsBytes,
                                 hipStream_t stream);
 hipError_t sieve_set_lds_limit(size_t bytes);
+hipError_t sieve_fast_set_lds_limit(size_t bytes);
+hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes,
+                                    hipStream_t stream);
 
 struct GatherPlan {
     KvcGatherArgs a;               // args of the first (or only) segment

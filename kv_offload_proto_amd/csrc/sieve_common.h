@@ -1,0 +1,174 @@
+// Device helpers shared by the SIEVE kernels: the state format of
+// hisp_kernel_common.h (uint16 table entries = slot+1, Knuth hash, linear
+// probing, Algorithm R deletion, visited bitmap) and the exact sequential
+// recurrence of hisp_sieve_update.cpp:115-163.
+#pragma once
+
+#include "kvx_internal.h"
+
+namespace kvx {
+namespace sieve {
+
+struct Guard {
+    uint64_t code = 0;
+};
+
+// Token held by the slot an entry points at.  An entry past the tokens row
+// can only come from a corrupted table; it reads as the empty token (-1)
+// instead of touching memory outside the row.
+__device__ __forceinline__ int32_t tok_at(const int32_t *tok, uint32_t e, int32_t ntok)
+{
+    return (static_cast<int32_t>(e) - 1 < ntok) ? tok[static_cast<int32_t>(e) - 1] : -1;
+}
+
+__device__ __forceinline__ int32_t ht_find(const uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t token,
+                                           int32_t mask, Guard &g)
+{
+    int32_t idx = static_cast<int32_t>(ht_hash(token)) & mask;
+    for (int32_t n = 0; n <= mask; ++n) {
+        const uint16_t e = ht[idx];
+        if (e == 0) return -1;
+        if (tok_at(tok, e, ntok) == token) return static_cast<int32_t>(e) - 1;
+        idx = (idx + 1) & mask;
+    }
+    g.code = kOverflowProbe;
+    return -1;
+}
+
+// Insert token -> slot; a present token keeps its first slot
+// (hisp_kernel_common.h:46-61, :97-112).
+__device__ __forceinline__ void ht_insert(uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t token,
+                                          int32_t slot, int32_t mask, Guard &g)
+{
+    int32_t idx = static_cast<int32_t>(ht_hash(token)) & mask;
+    for (int32_t n = 0; n <= mask; ++n) {
+        const uint16_t e = ht[idx];
+        if (e == 0) {
+            ht[idx] = static_cast<uint16_t>(slot + 1);
+            return;
+        }
+        if (tok_at(tok, e, ntok) == token) return;
+        idx = (idx + 1) & mask;
+    }
+    g.code = kOverflowProbe;
+}
+
+// Backward-shift erase, Knuth 6.4 Algorithm R (hisp_kernel_common.h:64-94).
+__device__ __forceinline__ void ht_erase(uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t token,
+                                         int32_t mask, Guard &g)
+{
+    int32_t idx = static_cast<int32_t>(ht_hash(token)) & mask;
+    int32_t n = 0;
+    for (;; ++n) {
+        if (n > mask) {
+            g.code = kOverflowProbe;
+            return;
+        }
+        const uint16_t e = ht[idx];
+        if (e == 0) return;
+        if (tok_at(tok, e, ntok) == token) break;
+        idx = (idx + 1) & mask;
+    }
+    int32_t j = idx, i = idx;
+    for (n = 0;; ++n) {
+        if (n > mask) {
+            g.code = kOverflowProbe;
+            return;
+        }
+        i = (i + 1) & mask;
+        const uint16_t e = ht[i];
+        if (e == 0) break;
+        const int32_t home = static_cast<int32_t>(ht_hash(tok_at(tok, e, ntok))) & mask;
+        const bool move = (j < i) ? (home <= j || home > i) : (home <= j && home > i);
+        if (move) {
+            ht[j] = e;
+            j = i;
+        }
+    }
+    ht[j] = 0;
+}
+
+__device__ __forceinline__ int vis_get(const uint8_t *v, int32_t s) { return (v[s >> 3] >> (s & 7)) & 1; }
+__device__ __forceinline__ void vis_set(uint8_t *v, int32_t s)
+{
+    v[s >> 3] = static_cast<uint8_t>(v[s >> 3] | (1u << (s & 7)));
+}
+__device__ __forceinline__ void vis_clear(uint8_t *v, int32_t s)
+{
+    v[s >> 3] = static_cast<uint8_t>(v[s >> 3] & ~(1u << (s & 7)));
+}
+
+__device__ __forceinline__ void report_overflow(uint64_t slot, uint64_t code)
+{
+    if (slot != 0 && code != 0) {
+        atomicCAS(reinterpret_cast<unsigned long long *>(slot), 0ull, static_cast<unsigned long long>(code));
+    }
+}
+
+// The per-position recurrence of hisp_sieve_update.cpp:115-163 for one batch
+// row, run by a single lane.  Returns true when a miss modified tokens/ht.
+__device__ bool sieve_row_sequential(const int32_t *rt, int32_t *rs, int8_t *rm, int32_t topK, int32_t seqLen,
+                                     int32_t prefill, int32_t dbs, int32_t padded, int32_t mask, int32_t *tok,
+                                     uint8_t *vis, uint16_t *ht, int32_t &hand, Guard &g)
+{
+    bool dirty = false;
+    for (int32_t k = 0; k < topK; ++k) {
+        const int32_t tp = rt[k];
+        if (g.code != 0 || tp < 0 || tp >= seqLen) {  // past a bound violation the row reads as invalid
+            rs[k] = -1;
+            rm[k] = 0;
+            continue;
+        }
+        if (tp >= prefill) {
+            rs[k] = padded + (tp - prefill);
+            rm[k] = 0;
+            continue;
+        }
+        const int32_t hit = ht_find(ht, tok, padded, tp, mask, g);
+        if (hit >= 0) {
+            rs[k] = hit;
+            rm[k] = 0;
+            vis_set(vis, hit);
+            continue;
+        }
+        int32_t h = hand;
+        int32_t swept = 0;
+        while (vis_get(vis, h) != 0) {
+            vis_clear(vis, h);
+            if (++h == dbs) h = 0;
+            if (++swept > dbs) {
+                g.code = kOverflowSweep;
+                break;
+            }
+        }
+        const int32_t old = tok[h];
+        if (old >= 0) ht_erase(ht, tok, padded, old, mask, g);
+        ht_insert(ht, tok, padded, tp, h, mask, g);
+        dirty = true;
+        rs[k] = h;
+        rm[k] = 1;
+        tok[h] = tp;
+        vis_set(vis, h);
+        hand = (h + 1 == dbs) ? 0 : h + 1;
+    }
+    return dirty;
+}
+
+// Copy n bytes (multiple of 16, both sides 16-byte aligned) with the block.
+__device__ __forceinline__ void block_copy16(void *dst, const void *src, uint32_t n)
+{
+    const uint4 *s = static_cast<const uint4 *>(src);
+    uint4 *d = static_cast<uint4 *>(dst);
+    for (uint32_t i = threadIdx.x; i < n / 16u; i += blockDim.x) d[i] = s[i];
+}
+
+__device__ __forceinline__ void write_dummy_row(int32_t *rs, int8_t *rm, int32_t topK)
+{
+    for (int32_t k = threadIdx.x; k < topK; k += blockDim.x) {
+        rs[k] = -1;
+        rm[k] = 0;
+    }
+}
+
+}  // namespace sieve
+}  // namespace kvx

@@ -42,6 +42,8 @@ class DevSieve:
         sl = slice(None) if layer is None else slice(layer, layer + 1)
         np.testing.assert_array_equal(self.tokens.cpu().numpy()[sl], st.tokens[sl])
         np.testing.assert_array_equal(self.vis.cpu().numpy()[sl], st.vis[sl])
-        np.testing.assert_array_equal(self.hand.cpu().numpy()[sl], st.hand[sl])
+        # element 0 is the hand; element 1 may carry the parallel kernel's
+        # canonical-state flag (elements 1..15 are unused by the reference)
+        np.testing.assert_array_equal(self.hand.cpu().numpy()[sl][..., 0], st.hand[sl][..., 0])
         if check_ht:
             np.testing.assert_array_equal(self.ht.cpu().numpy().view(np.uint16)[sl], st.ht[sl])

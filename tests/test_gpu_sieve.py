@@ -131,3 +131,101 @@ def test_sieve_validation_messages(kvops):
         with pytest.raises(RuntimeError, match=msg):
             kvops.sieve_update(**kw)
     kvops.sieve_update(**base)  # max_num_reqs == 0: nothing to launch
+
+
+def _random_state_stream(rng, st, K, prefill, seq_extra=4, miss_frac=None):
+    """Mixed batch like the fast-path fuzz: resident hits in random order,
+    non-resident misses, a few invalid/extension positions and duplicates."""
+    req = st.pool_size
+    miss_frac = rng.random() if miss_frac is None else miss_frac
+    out = np.empty((req, K), dtype=np.int32)
+    for r in range(req):
+        tok = st.tokens[0, r, :st.dbs]
+        res = tok[tok >= 0]
+        row = np.where(rng.random(K) < miss_frac, rng.integers(0, prefill, K),
+                       res[rng.integers(0, len(res), K)] if len(res) else rng.integers(0, prefill, K))
+        junk = rng.random(K) < 0.03
+        row[junk] = rng.integers(-3, prefill + seq_extra + 3, junk.sum())
+        dup = rng.random(K) < 0.05
+        row[dup] = row[rng.integers(0, K, dup.sum())]
+        out[r] = row
+    return out
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_sieve_fast_kernel_parity_mid(kvops, seed):
+    """The parallel kernel (variant 2) at mid sizes with conversion-heavy
+    streams: full state, including the exact table layout, after every step."""
+    rng = np.random.default_rng(900 + seed)
+    dbs = int(rng.integers(300, 1500))
+    K = int(rng.integers(64, 700))
+    prefill = dbs + int(rng.integers(1, 4000))
+    req = 6
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    variants = set()
+    for step in range(6):
+        batch = _random_state_stream(rng, st, K, prefill)
+        seq = np.full(req, prefill + 2)
+        e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+        g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+        variants.add(kvops.last_sieve_variant())
+        np.testing.assert_array_equal(g_miss, e_miss, err_msg="seed {} step {}".format(seed, step))
+        np.testing.assert_array_equal(g_slots, e_slots, err_msg="seed {} step {}".format(seed, step))
+        dev.assert_state_equal()
+    assert variants == {2}
+    assert kvops.read_overflow() == 0
+
+
+def test_sieve_fast_kernel_parity_dsa_scale(kvops):
+    """DSA-decode shapes (64 requests, topK 2048, 4096 slots, Zipf recency
+    hits, 20% misses) over two layers and three steps."""
+    from kv_offload_proto_amd.xds.configs import CONFIGS
+
+    cfg = CONFIGS[2]
+    L = 2
+    st = orc.SieveState(L, cfg.req_num, cfg.dbs, cfg.top_k)
+    for r in range(cfg.req_num):
+        st.admit(r, cfg.prefill)
+    dev = DevSieve(st)
+    rng = np.random.default_rng(cfg.seed)
+    req_pool = np.arange(cfg.req_num)
+    seq = np.full(cfg.req_num, cfg.prefill)
+    for step in range(3):
+        for layer in range(L):
+            batch = streams.state_batch(rng, st.tokens[layer, :, :cfg.dbs], cfg.prefill, cfg.top_k, cfg.miss_ratio,
+                                        zipf_s=cfg.zipf_s)
+            e_slots, e_miss = st.update(layer, batch, req_pool, seq, cfg.req_num)
+            g_slots, g_miss, _ = dev.update(kvops, layer, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
+            assert kvops.last_sieve_variant() == 2
+            np.testing.assert_array_equal(g_miss, e_miss)
+            np.testing.assert_array_equal(g_slots, e_slots)
+        dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_sieve_variants_agree(kvops, variant):
+    """Sequential LDS (0), sequential HBM-resident (1) and parallel (2) kernels
+    give the oracle's results on the same inputs."""
+    rng = np.random.default_rng(77)
+    dbs, K, prefill, req = 700, 300, 3000, 4
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(variant)
+    try:
+        for step in range(5):
+            batch = _random_state_stream(rng, st, K, prefill)
+            seq = np.full(req, prefill + 3)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == variant
+            np.testing.assert_array_equal(g_miss, e_miss)
+            np.testing.assert_array_equal(g_slots, e_slots)
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
