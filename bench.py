@@ -78,8 +78,22 @@ def measure_link_peak(runner, mib, log):
         best = max(best, m / (e0.elapsed_time(e1) * 1e-3) / 1e9)
     res["zero_copy_read_GBps"] = best
     res["peak_GBps"] = max(res["memcpy_h2d_GBps"], res["zero_copy_read_GBps"])
-    log("[bench] host link: memcpy H2D {:.1f} GB/s, zero-copy read {:.1f} GB/s".format(
-        res["memcpy_h2d_GBps"], res["zero_copy_read_GBps"]))
+    # HBM -> HBM copy of the same size with the same streaming kernel: the
+    # known-size copy that calibrates FETCH_SIZE / WRITE_SIZE readings
+    src = torch.empty(n, dtype=torch.uint8, device=runner.dev)
+    src.fill_(3)
+    best = 0.0
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        _kvops.stream_copy(dst.data_ptr(), src.data_ptr(), n, stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = max(best, 2 * n / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    res["hbm_copy_GBps"] = best
+    del src
+    log("[bench] host link: memcpy H2D {:.1f} GB/s, zero-copy read {:.1f} GB/s; HBM copy {:.0f} GB/s (read+write)".format(
+        res["memcpy_h2d_GBps"], res["zero_copy_read_GBps"], res["hbm_copy_GBps"]))
     del dst, pinned
     return res
 
