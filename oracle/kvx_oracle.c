@@ -15,7 +15,7 @@
  *                       tests/test_oracle_hash.py against brute-force invariants
  *                       (every live key findable, no stray entries, table ==
  *                       live keys re-inserted in insertion order).
- *   orc_sieve_update    test_sieve_oracle.py literals (tests/golden/sieve_kat.json),
+ *   orc_sieve_update    test_sieve_oracle.py literals (tests/golden/reference_kats.json),
  *                       an independent dict model (tests/sieve_model.py), ring
  *                       CLOCK invariants.
  *   orc_sieve_ht_init   invariants + equality with orc_ht_insert replay.
