@@ -107,6 +107,27 @@ def sieve_bytes(cfg, padded, vis_stride, ht_size, dirty_reqs):
     return cfg.req_num * per_req + dirty_reqs * (padded * 4 + ht_size * 2)
 
 
+# Counter profiles committed for a workload: HBM bytes per dispatch, from
+# FETCH_SIZE and WRITE_SIZE runs scaled by a known-size copy.
+TRAFFIC_PROFILES = {"c2-dsa-decode": "profiles/pmc_traffic_dsa_decode.md"}
+
+
+def load_traffic(workload):
+    """{kernel: bytes per dispatch} from the workload's counter profile, or {}."""
+    rel = TRAFFIC_PROFILES.get(workload)
+    if rel is None:
+        return {}, None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), rel)
+    if not os.path.exists(path):
+        return {}, None
+    out = {}
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes":
+            out[f[1]] = float(f[2])
+    return out, rel
+
+
 def cpu_baseline(runner, plan, budget_s, log):
     """The C oracle (oracle/liboracle.so) replaying the same batches from the
     same initial state on one host core, SIEVE + import, for about budget_s."""
@@ -252,14 +273,23 @@ def main():
     link_gbps = rows * cfg.row_bytes / (sum(gather_us) * 1e-6) / 1e9
     sb = sieve_bytes(cfg, c.padded_buffer_size, c.visited_stride_b, c.ht_size, cfg.req_num)
     sieve_gbps_alg = sb * len(timed) / (sum(sieve_us) * 1e-6) / 1e9
+    traffic, traffic_src = load_traffic(cfg.name)
+
+    def traffic_of(*kernels):
+        if not all(k in traffic for k in kernels):
+            return None
+        return sum(traffic[k] for k in kernels)
+
     gather_roof = {"kernel": "kvx_gather_prep+kvx_gather_copy", "bound": "hbm", "achieved": gather_gbps_alg,
-                   "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gather_gbps_alg / HBM_PEAK_GBPS, "traffic": None,
+                   "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gather_gbps_alg / HBM_PEAK_GBPS,
+                   "traffic": traffic_of("kvx_gather_prep", "kvx_gather_copy"), "traffic_source": traffic_src,
                    "bytes_per_launch": sum(gather_bytes) / len(timed),
                    "avg_launch_us": sum(gather_us) / len(timed),
                    "link": {"achieved": link_gbps, "peak": link["peak_GBps"], "unit": "GB/s",
                             "frac": link_gbps / link["peak_GBps"]}}
     sieve_roof = {"kernel": "kvx_sieve_update", "bound": "hbm", "achieved": sieve_gbps_alg, "peak": HBM_PEAK_GBPS,
-                  "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS, "traffic": None, "bytes_per_launch": sb,
+                  "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS,
+                  "traffic": traffic_of("kvx_sieve_update_fast"), "traffic_source": traffic_src, "bytes_per_launch": sb,
                   "avg_launch_us": sum(sieve_us) / len(timed)}
     dominant, other = (gather_roof, sieve_roof) if sum(gather_us) >= sum(sieve_us) else (sieve_roof, gather_roof)
 
