@@ -54,31 +54,38 @@ struct RowScratch {
 constexpr int kFastThreads = 1024;
 
 struct FastLayout {
-    uint32_t tok, ht, vis, ptok, pinf, vt, cpos, evslot, evold, cvlist, kcell, kstart, ber, bg, bm, total;
+    uint32_t tok, ht, vis, ptok, pinf, vt, candPre, evslot, evold, cvlist, eseq, tb, smA, smB, ber, bg, bm, bnew,
+        total;
 };
 
 __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
 
+// LDS regions of the parallel SIEVE kernel for one batch row.  ptok+pinf and
+// smA+smB are each contiguous and reused as 64-bit arrays of topK entries in
+// the table-update phase.
 __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint32_t htSize, uint32_t topK,
                                                            uint32_t visStrideB)
 {
     FastLayout l{};
     uint32_t o = 0;
-    l.tok = o;    o += align16(padded * 4u);
-    l.ht = o;     o += align16(htSize * 2u);
-    l.vis = o;    o += align16(visStrideB);
-    l.ptok = o;   o += align16(topK * 4u);
-    l.pinf = o;   o += align16(topK * 4u);
-    l.vt = o;     o += align16(padded * 2u);
-    l.cpos = o;   o += align16(topK * 2u);
-    l.evslot = o; o += align16(topK * 2u);
-    l.evold = o;  o += align16(topK * 2u);
-    l.cvlist = o; o += align16(topK * 2u);
-    l.kcell = o;  o += align16(topK * 4u);
-    l.kstart = o; o += align16(topK * 4u);
-    l.ber = o;    o += align16(htSize / 8u);
-    l.bg = o;     o += align16(htSize / 8u);
-    l.bm = o;     o += align16(htSize / 8u);
+    l.tok = o;     o += align16(padded * 4u);
+    l.ht = o;      o += align16(htSize * 2u);
+    l.vis = o;     o += align16(visStrideB);
+    l.ptok = o;    o += align16(topK * 4u);
+    l.pinf = o;    o += align16(topK * 4u);
+    l.vt = o;      o += align16(padded * 2u);
+    l.candPre = o; o += align16((topK + 1u) * 2u);
+    l.evslot = o;  o += align16(topK * 2u);
+    l.evold = o;   o += align16(topK * 2u);
+    l.cvlist = o;  o += align16(topK * 2u);
+    l.eseq = o;    o += align16(topK * 2u);
+    l.tb = o;      o += align16((topK + 1u) * 2u);
+    l.smA = o;     o += align16(topK * 4u);
+    l.smB = o;     o += align16(topK * 4u);
+    l.ber = o;     o += align16(htSize / 8u);
+    l.bg = o;      o += align16(htSize / 8u);
+    l.bm = o;      o += align16(htSize / 8u);
+    l.bnew = o;    o += align16(htSize / 8u);
     l.total = o;
     return l;
 }

@@ -2,34 +2,51 @@
 //
 // Same results as the sequential recurrence of hisp_sieve_update.cpp:115-163
 // (slots, is_miss, tokens, visited bitmap, hand and the hash table's exact
-// layout), computed by one 512-lane workgroup per batch row with the state
-// row staged in LDS:
+// layout), computed by one 1024-lane workgroup per batch row with the state
+// row staged in LDS.
 //
-//  A  classify every topK position against the pre-step table in parallel:
-//     invalid, decode-extension, hit on slot s0, or candidate miss;
-//  B  first occurrence of each candidate token (provisional table entries
-//     holding padded+1+position, min position wins), then compact the
-//     first occurrences in position order; per slot, the first hit time;
-//  C  one wave walks the hand over the ring against the misses in time
-//     order: slot s is passed (its bit cleared) at miss time p when it was
-//     visited before the step or first hit before p, otherwise it is evicted.
-//     Evicting a slot whose old token is hit later turns that later position
-//     into a miss (a "conversion", queued in a small heap).  A walk that
-//     would pass a slot twice (hand wraps within the step) falls back to the
-//     sequential recurrence on the same LDS state;
-//  D  outputs and visited bits from the walk's per-slot marks;
-//  E  hash table: erase the evicted tokens cluster by cluster (Algorithm R
-//     deletions commute), then insert the new tokens: a tentative parallel
-//     placement fixes the final occupied cells (independent of order), and
-//     each final cluster holding several new tokens is redone in time order
-//     by one lane.  Linear probing with Algorithm R leaves the table equal to
-//     inserting the live keys in insertion order, so the result is the
-//     sequential one.
+// Events are the positions that need a slot: the first occurrence of each
+// token that is not resident (a candidate miss), and every hit whose token
+// the hand evicted earlier in the same step (a conversion).  Within one step
+// the hand passes each slot at most once (a wrap falls back), so a slot's fate
+// depends only on its class:
+//   S0  visited before the step: passed;
+//   SN  not visited and not hit this step: evicted by the event the hand
+//       serves when it arrives;
+//   SM  not visited, first hit at position k: evicted iff the hand arrives
+//       while serving an event earlier than k (then the hit at k converts).
+// With j(u) = the number of evictions before ring offset u, the hand reaches
+// u while serving event j(u), and an SM slot is evicted iff more than j(u)
+// events precede k.  Events before k are the candidates before k (a prefix
+// count) plus the conversions made so far, so only the SM slots need a
+// sequential pass, and it touches nothing but counters.  Everything else --
+// classification, dedup, the event sequence, marks, outputs, visited bits --
+// is prefix sums and scatters.
 //
-// Preconditions for the fast path, checked in the kernel: the table indexes
-// exactly the non-negative tokens of slots [0, dbs) (each found at its own
-// slot), padded + 1 + topK <= 65535, topK < 16383.  Otherwise the sequential
-// recurrence runs on the staged state.
+// Phases:
+//   stage    tokens/table/visited/topK row into LDS; table consistency check
+//   classify hit / candidate / invalid / decode-extension per position; the
+//            first hit time of every slot (LDS min)
+//   dedup    provisional table entries padded+1+k, smallest k wins
+//   compact  candidate prefix counts per position
+//   ring     classes per ring offset from the hand, SM list with its counts
+//   decide   one wave: SM slots in ring order, 64 at a time, speculating that
+//            none is evicted and correcting at each eviction
+//   events   the merged event sequence (a prefix scan over positions)
+//   marks    per ring offset: evicted at event p / passed at event p
+//   outputs  slots, is_miss, visited bits
+//   table    erase the evicted tokens (Algorithm R deletions commute when
+//            each cluster is done right to left), insert the new tokens with
+//            a tentative parallel placement (the occupied cells do not depend
+//            on order) and redo, in event order, every final cluster that
+//            holds more than one new token.  Linear probing with Algorithm R
+//            leaves the table equal to inserting the live keys in insertion
+//            order, so the result is the sequential table byte for byte.
+//
+// Preconditions, checked in the kernel: the table indexes exactly the
+// non-negative tokens of slots [0, dbs) (each found at its own slot),
+// padded + 1 + topK <= 65535, topK < 16383, no hand wrap within the step.
+// Otherwise the row is restaged from HBM and the sequential recurrence runs.
 #include "kvx_internal.h"
 #include "sieve_common.h"
 
@@ -42,44 +59,30 @@ constexpr int NT = kFastThreads;
 constexpr int NWAVES = NT / 64;
 
 constexpr uint32_t CLS_INV = 0u, CLS_EXT = 1u, CLS_HIT = 2u, CLS_CAND = 3u;
+constexpr uint32_t INF_CONV = 1u << 29;  // a hit position that became a conversion
 constexpr uint16_t VT_NONE = 0xFFFF, VT_EVICTED = 0x8000, VT_PASSED = 0x4000, VT_NOCONV = 0x3FFF;
-// sieve_hand[row][1]: set when this kernel left the row's state canonical
+// sieve_hand[row][1]: set when this kernel left the row's table consistent
 constexpr int32_t kCanonFlag = 0x4B565843;
 
 // Phase timestamps for profiling builds (-DKVX_SIEVE_PHASE_STAMPS): thread 0
 // of each workgroup records clock64() at phase boundaries into kvx_dbg_stamps.
 #ifdef KVX_SIEVE_PHASE_STAMPS
 __device__ unsigned long long kvx_dbg_stamps[1024][16];
-#define STAMP(i)                                                                      \
-    do {                                                                              \
-        if (tid == 0 && bid < 1024) kvx_dbg_stamps[bid][i] = clock64();               \
-    } while (0)
-__device__ unsigned long long kvx_dbg_walk[1024][64];  // per window: clock64 << 16 | events so far
-#define WALK_STAMP(w, nev)                                                                          \
-    do {                                                                                            \
-        if (lane == 0 && bid < 1024 && (w) < 64)                                                    \
-            kvx_dbg_walk[bid][(w)] = (static_cast<unsigned long long>(clock64()) << 16) | (nev);   \
-    } while (0)
-#define STAMP_SYNC(i)    \
-    do {                 \
-        __syncthreads(); \
-        STAMP(i);        \
+#define STAMP(i)                                                        \
+    do {                                                                \
+        if (tid == 0 && bid < 1024) kvx_dbg_stamps[bid][i] = clock64(); \
     } while (0)
 #else
-#define WALK_STAMP(w, nev) \
-    do {                   \
-    } while (0)
-#define STAMP_SYNC(i) \
-    do {              \
-    } while (0)
 #define STAMP(i) \
     do {         \
     } while (0)
 #endif
 
 struct Misc {
-    int32_t nTok, nEnt, bad, M, nConv, uEnd, nEv, wrap, nMulti, ovf;
-    int32_t waveTot[NWAVES];
+    int32_t nTok, nEnt, bad, ovf, late;
+    int32_t M, nSM, T, nConv, N, smDone, uEnd, nTakes, nMulti;
+    uint32_t wt0[NWAVES];
+    uint32_t wt1[NWAVES];
 };
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
@@ -87,6 +90,55 @@ __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 __device__ __forceinline__ uint32_t readlane(uint32_t v, int l)
 {
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m, uint32_t lane)
+{
+    return static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o));
+    return v;
+}
+
+// Exclusive prefix over the workgroup of per-thread values whose set bits all
+// lie in `bits` (small counts: one ballot per bit), in thread order.  Returns
+// the prefix and the total; ends with a barrier, after which `wt` is free.
+__device__ __forceinline__ uint32_t block_exscan(uint32_t v, uint32_t bits, uint32_t *wt, uint32_t &total)
+{
+    const uint32_t lane = lane_id();
+    const int wave = static_cast<int>(threadIdx.x >> 6);
+    uint32_t pre = 0, tot = 0;
+    while (bits != 0u) {
+        const int b = __builtin_ctz(bits);
+        bits &= bits - 1u;
+        const uint64_t bal = __ballot((v >> b) & 1u);
+        pre += lanes_below(bal, lane) << b;
+        tot += static_cast<uint32_t>(__popcll(bal)) << b;
+    }
+    if (lane == 0) wt[wave] = tot;
+    __syncthreads();
+    uint32_t off = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) {
+        const uint32_t c = wt[w];
+        off += (w < wave) ? c : 0u;
+        all += c;
+    }
+    total = all;
+    __syncthreads();
+    return off + pre;
+}
+
+// Bit mask covering the values 0..n.
+__host__ __device__ __forceinline__ uint32_t bits_for(uint32_t n)
+{
+    uint32_t m = 1u;
+    while (m < n + 1u && m != 0x80000000u) m = (m << 1) | 1u;
+    return m;
 }
 
 // 16-bit LDS min via a CAS on the containing word.
@@ -148,38 +200,31 @@ __device__ void rdel_at(uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t 
     ht[j] = 0;
 }
 
-// Copy n bytes (multiple of 16) with the workgroup, 4 chunks in flight per lane.
+// Copy n bytes (multiple of 16) with the workgroup, four 16-byte chunks in
+// flight per lane.
 __device__ __forceinline__ void wg_copy16(void *dst, const void *src, uint32_t n)
 {
     const uint4 *s = static_cast<const uint4 *>(src);
     uint4 *d = static_cast<uint4 *>(dst);
     const uint32_t n16 = n / 16u;
-    for (uint32_t i = threadIdx.x; i < n16; i += 4u * NT) {
-        uint4 v[4];
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            if (i + j * NT < n16) v[j] = s[i + j * NT];
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            if (i + j * NT < n16) d[i + j * NT] = v[j];
-        }
+    uint32_t i = threadIdx.x;
+    for (; i + 3u * NT < n16; i += 4u * NT) {
+        const uint4 a = s[i];
+        const uint4 b = s[i + NT];
+        const uint4 c = s[i + 2u * NT];
+        const uint4 e = s[i + 3u * NT];
+        d[i] = a;
+        d[i + NT] = b;
+        d[i + 2u * NT] = c;
+        d[i + 3u * NT] = e;
     }
+    for (; i < n16; i += NT) d[i] = s[i];
 }
 
-__device__ __forceinline__ uint32_t bpermute(uint32_t v, uint32_t srcLane)
+__device__ __forceinline__ int32_t ring_slot(int32_t hand0, int32_t u, int32_t dbs)
 {
-    return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(srcLane << 2), static_cast<int>(v)));
-}
-
-__device__ __forceinline__ uint32_t writelane(uint32_t old, uint32_t v, int l)
-{
-    return (lane_id() == static_cast<uint32_t>(l)) ? v : old;
-}
-
-__device__ __forceinline__ uint32_t lanes_below(uint64_t m, uint32_t lane)
-{
-    return static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+    const int32_t s = hand0 + u;
+    return s >= dbs ? s - dbs : s;
 }
 
 __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveUpdateArgs> L)
@@ -232,15 +277,23 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *pinf = reinterpret_cast<uint32_t *>(smem + lay.pinf);
     uint16_t *vt = reinterpret_cast<uint16_t *>(smem + lay.vt);
     uint32_t *vt32 = reinterpret_cast<uint32_t *>(smem + lay.vt);
-    uint16_t *cpos = reinterpret_cast<uint16_t *>(smem + lay.cpos);
+    uint16_t *candPre = reinterpret_cast<uint16_t *>(smem + lay.candPre);
     uint16_t *evslot = reinterpret_cast<uint16_t *>(smem + lay.evslot);
     uint16_t *evold = reinterpret_cast<uint16_t *>(smem + lay.evold);
     uint16_t *cvlist = reinterpret_cast<uint16_t *>(smem + lay.cvlist);
-    uint32_t *kcell = reinterpret_cast<uint32_t *>(smem + lay.kcell);
-    uint32_t *kstart = reinterpret_cast<uint32_t *>(smem + lay.kstart);
+    uint16_t *eseq = reinterpret_cast<uint16_t *>(smem + lay.eseq);
+    uint16_t *tb = reinterpret_cast<uint16_t *>(smem + lay.tb);
+    uint32_t *smA = reinterpret_cast<uint32_t *>(smem + lay.smA);  // ring offset | k << 16
+    uint32_t *smB = reinterpret_cast<uint32_t *>(smem + lay.smB);  // SN before | candidates before k << 16
     uint32_t *ber = reinterpret_cast<uint32_t *>(smem + lay.ber);
     uint32_t *bg = reinterpret_cast<uint32_t *>(smem + lay.bg);
     uint32_t *bm = reinterpret_cast<uint32_t *>(smem + lay.bm);
+    uint32_t *bnew = reinterpret_cast<uint32_t *>(smem + lay.bnew);
+    // table-update phase reuse of dead regions
+    uint32_t *kcell = smA;                                                   // erase cell / new token per event
+    uint32_t *lead = smB;                                                    // erase leader flag per event
+    uint64_t *mlist = reinterpret_cast<uint64_t *>(smem + lay.ptok);        // multi-cluster keys
+    uint64_t *msort = reinterpret_cast<uint64_t *>(smem + lay.smA);         // the same, sorted
 
     // ---- stage the state row and the topK row
     STAMP(0);
@@ -248,9 +301,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     wg_copy16(ht, gHt, static_cast<uint32_t>(H) * 2u);
     wg_copy16(vis, gVis, static_cast<uint32_t>(visStrideB));
     for (int32_t k = tid; k < K; k += NT) ptok[k] = rt[k];
-    for (int32_t i = tid; i < 3 * (H >> 5); i += NT) ber[i] = 0u;  // ber, bg, bm are contiguous
+    for (int32_t i = tid; i < 4 * (H >> 5); i += NT) ber[i] = 0u;  // ber, bg, bm, bnew are contiguous
     if (tid == 0) {
-        ms.nTok = ms.nEnt = ms.bad = ms.M = ms.nConv = ms.uEnd = ms.nEv = ms.wrap = ms.nMulti = ms.ovf = 0;
+        ms.nTok = ms.nEnt = ms.bad = ms.ovf = ms.late = 0;
+        ms.M = ms.nSM = ms.T = ms.nConv = ms.N = ms.smDone = ms.uEnd = ms.nTakes = ms.nMulti = 0;
     }
     int32_t hand0 = gHand[0];
     if (hand0 < 0 || hand0 >= dbs) hand0 = 0;  // hisp_sieve_update.cpp:108-111
@@ -258,25 +312,31 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     __syncthreads();
     STAMP(1);
 
-    // ---- canonical state: the table indexes exactly the non-negative tokens of
-    // [0, dbs), each at its own slot.  A row last written by this kernel carries
+    // ---- consistency: the table indexes exactly the non-negative tokens of
+    // [0, dbs), each at its own slot.  A row this kernel wrote last carries
     // the flag, and then only the counts are rechecked.
     {
         Guard g;
-        int32_t nTok = 0, nEnt = 0, bad = 0;
+        uint32_t nTok = 0, nEnt = 0, bad = 0;
         for (int32_t s = tid; s < dbs; s += NT) {
             const int32_t t = tok[s];
             if (t < 0) continue;
             ++nTok;
-            if (!flagged && ht_find(ht, tok, padded, t, mask, g) != s) bad = 1;
+            if (!flagged && ht_find(ht, tok, padded, t, mask, g) != s) bad = 1u;
         }
         for (int32_t c = tid; c < (H >> 1); c += NT) {
             const uint32_t w = ht32[c];
             nEnt += ((w & 0xFFFFu) != 0u) + ((w >> 16) != 0u);
         }
-        if (nTok) atomicAdd(&ms.nTok, nTok);
-        if (nEnt) atomicAdd(&ms.nEnt, nEnt);
-        if (bad || g.code) atomicOr(&ms.bad, 1);
+        nTok = wave_sum(nTok);
+        nEnt = wave_sum(nEnt);
+        const bool anyBad = __ballot(bad != 0u || g.code != 0) != 0ull;
+        if (lane == 0) {
+            atomicAdd(&ms.nTok, static_cast<int32_t>(nTok));
+            atomicAdd(&ms.nEnt, static_cast<int32_t>(nEnt));
+            if (anyBad) atomicOr(&ms.bad, 1);
+        }
+        for (int32_t s = tid; s < dbs; s += NT) vt[s] = vis_get(vis, s) ? 0 : VT_NONE;
     }
     __syncthreads();
     const bool canonical = ms.bad == 0 && ms.nTok == ms.nEnt;
@@ -284,9 +344,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     STAMP(2);
 
     if (fast) {
-        // ---- A: classify positions; first hit per slot
-        for (int32_t s = tid; s < dbs; s += NT) vt[s] = vis_get(vis, s) ? 0 : VT_NONE;
-        __syncthreads();
+        // ---- classify positions; first hit time per slot
         {
             Guard g;
             for (int32_t k = tid; k < K; k += NT) {
@@ -311,7 +369,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         __syncthreads();
         STAMP(3);
-        // ---- B: provisional entries padded+1+k; the smallest position of a token wins its cell
+        // ---- dedup: provisional entries padded+1+k; the smallest position of a token wins its cell
         for (int32_t k = tid; k < K; k += NT) {
             if ((pinf[k] >> 30) != CLS_CAND) continue;
             const int32_t t = ptok[k];
@@ -348,8 +406,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (!done) atomicOr(&ms.ovf, 1);
         }
         __syncthreads();
-        STAMP(4);
-        // first occurrence of each candidate token (read back its provisional entry)
+        // read back the first occurrence of each candidate token and its cell
         for (int32_t k = tid; k < K; k += NT) {
             if ((pinf[k] >> 30) != CLS_CAND) continue;
             const int32_t t = ptok[k];
@@ -357,208 +414,219 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             for (int32_t n = 0; n <= mask; ++n) {
                 const uint32_t e = ht[idx];
                 if (e > static_cast<uint32_t>(padded) && ptok[e - padded - 1] == t) {
-                    pinf[k] = (CLS_CAND << 30) | (e - padded - 1);
+                    const uint32_t k1 = e - static_cast<uint32_t>(padded) - 1u;
+                    pinf[k] = (CLS_CAND << 30) | k1;
+                    if (k1 == static_cast<uint32_t>(k)) kcell[k] = static_cast<uint32_t>(idx);
                     break;
                 }
                 idx = (idx + 1) & mask;
             }
         }
         __syncthreads();
-        // drop every provisional entry: the table is the pre-step table again
-        for (int32_t c = tid; c < H; c += NT) {
-            if (ht[c] > static_cast<uint32_t>(padded)) ht[c] = 0;
+        // drop the provisional entries (one per first occurrence): the table is the pre-step table again
+        for (int32_t k = tid; k < K; k += NT) {
+            const uint32_t inf = pinf[k];
+            if ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ht[kcell[k]] = 0;
         }
-        // compact first occurrences in position order into cpos (contiguous chunk per lane)
+        STAMP(4);
+        // ---- candidate prefix counts per position (contiguous chunk per lane)
         {
             const int32_t P = (K + NT - 1) / NT;
             const int32_t k0 = tid * P;
-            uint32_t cnt = 0;
+            uint32_t cnt = 0, fl = 0;
             for (int32_t i = 0; i < P; ++i) {
                 const int32_t k = k0 + i;
                 if (k < K) {
                     const uint32_t inf = pinf[k];
-                    cnt += ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ? 1u : 0u;
+                    const uint32_t f = ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ? 1u : 0u;
+                    fl |= f << i;
+                    cnt += f;
                 }
             }
-            uint32_t pre = 0, wsum = 0;
-            for (int b = 0; b < 5; ++b) {
-                const uint64_t bal = __ballot((cnt >> b) & 1u);
-                pre += lanes_below(bal, lane) << b;
-                wsum += static_cast<uint32_t>(__popcll(bal)) << b;
-            }
-            if (lane == 0) ms.waveTot[wave] = static_cast<int32_t>(wsum);
-            __syncthreads();
-            uint32_t off = 0, tot = 0;
-            for (int w = 0; w < NWAVES; ++w) {
-                const uint32_t c = static_cast<uint32_t>(ms.waveTot[w]);
-                off += (w < wave) ? c : 0u;
-                tot += c;
-            }
-            uint32_t m = off + pre;
+            uint32_t M;
+            uint32_t pre = block_exscan(cnt, bits_for(static_cast<uint32_t>(P)), ms.wt0, M);
             for (int32_t i = 0; i < P; ++i) {
                 const int32_t k = k0 + i;
                 if (k < K) {
-                    const uint32_t inf = pinf[k];
-                    if ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) {
-                        cpos[m++] = static_cast<uint16_t>(k);
-                    }
+                    candPre[k] = static_cast<uint16_t>(pre);
+                    pre += (fl >> i) & 1u;
                 }
             }
-            if (tid == 0) ms.M = static_cast<int32_t>(tot);
+            if (tid == 0) {
+                candPre[K] = static_cast<uint16_t>(M);
+                ms.M = static_cast<int32_t>(M);
+            }
         }
         __syncthreads();
         STAMP(5);
         if (ms.ovf) fast = false;
     }
 
+    // ---- ring classes per offset from the hand (contiguous chunk per lane)
+    const int32_t Q = (dbs + NT - 1) / NT;
+    const int32_t u0 = tid * Q;
+    uint64_t snM = 0, smM = 0;
+    uint32_t preSN = 0, preSM = 0;
     if (fast) {
-        // ---- C: the hand walk, wave 0, in registers.  Per event: the next time
-        // p (candidate or pending conversion), the first slot at or after the
-        // cursor whose threshold exceeds p.  Windows of 64 slots; marks, event
-        // records and conversion records go to LDS once per 64.
-        const int32_t M = ms.M;
-        if (wave == 0) {
-            int32_t cb = 0;
-            uint32_t cwin = (static_cast<int32_t>(lane) < M) ? cpos[lane] : 0xFFFFu;
-            int32_t ic = 0;
-            uint32_t pend = 0xFFFFu;  // pending conversion times, sorted across lanes
-            int32_t nPend = 0;
-            int32_t base = 0;
-            bool valid = static_cast<int32_t>(lane) < dbs;
-            int32_t sl = hand0 + static_cast<int32_t>(lane);
-            if (sl >= dbs) sl -= dbs;
-            if (!valid) sl = 0;
-            uint32_t vtl = valid ? vt[sl] : 0u;
-            uint64_t takemask = 0, geMask = ~0ull;
-            int32_t cursor = 0, ntakes = 0;
-            uint32_t rtime = 0;
-            uint32_t accP = 0, accU = 0;
-            int32_t nacc = 0;
-            uint32_t cvT = 0, cvS = 0;
-            int32_t ncvAcc = 0, nConv = 0, nEv = 0;
-            bool wrap = false;
-            WALK_STAMP(0, 0);
-
-            auto flush_window = [&](uint32_t pcur) {
-                const uint32_t rank = lanes_below(takemask, lane);
-                const uint32_t nxt = bpermute(rtime, rank & 63u);
-                const uint32_t ptime = (rank < static_cast<uint32_t>(ntakes)) ? nxt : pcur;
-                const bool taken = (takemask >> lane) & 1ull;
-                const uint16_t mark =
-                    taken ? static_cast<uint16_t>(VT_EVICTED | (vtl != VT_NONE ? vtl - 1u : VT_NOCONV))
-                          : static_cast<uint16_t>(VT_PASSED | ptime);
-                if (valid && static_cast<int32_t>(lane) < cursor) vt[sl] = mark;
-            };
-            auto load_window = [&]() {
-                valid = base + static_cast<int32_t>(lane) < dbs;
-                sl = hand0 + base + static_cast<int32_t>(lane);
-                if (sl >= dbs) sl -= dbs;
-                if (!valid) sl = 0;
-                vtl = valid ? vt[sl] : 0u;
-                takemask = 0;
-                geMask = ~0ull;
-                cursor = 0;
-                ntakes = 0;
-            };
-            auto flush_events = [&]() {
-                if (static_cast<int32_t>(lane) < nacc) {
-                    int32_t s = hand0 + static_cast<int32_t>(accU);
-                    if (s >= dbs) s -= dbs;
-                    evslot[accP] = static_cast<uint16_t>(s);
-                }
-                nacc = 0;
-            };
-            auto flush_conv = [&]() {
-                if (static_cast<int32_t>(lane) < ncvAcc) {
-                    evold[cvT] = static_cast<uint16_t>(cvS);
-                    cvlist[nConv - ncvAcc + static_cast<int32_t>(lane)] = static_cast<uint16_t>(cvT);
-                }
-                ncvAcc = 0;
-            };
-
-            while (ic < M || nPend > 0) {
-                const uint32_t pc = (ic < M) ? readlane(cwin, ic - cb) : 0xFFFFu;
-                const uint32_t pm = (nPend > 0) ? readlane(pend, 0) : 0xFFFFu;
-                const bool conv = pm < pc;
-                const uint32_t p = conv ? pm : pc;
-                uint64_t m = __ballot(vtl > p) & geMask;
-                while (m == 0) {  // the rest of this window is passed at time p
-                    cursor = 64;
-                    flush_window(p);
-                    base += 64;
-                    WALK_STAMP(base >> 6, nEv);
-                    if (base >= dbs) {
-                        wrap = true;
-                        break;
-                    }
-                    load_window();
-                    m = __ballot(vtl > p);
-                }
-                if (wrap) break;
-                const int l = __builtin_ctzll(m);
-                const uint32_t v = readlane(vtl, l);
-                takemask |= 1ull << l;
-                geMask = (l == 63) ? 0ull : (~0ull << (l + 1));
-                cursor = l + 1;
-                rtime = writelane(rtime, p, ntakes);
-                ++ntakes;
-                accP = writelane(accP, p, nacc);
-                accU = writelane(accU, static_cast<uint32_t>(base + l), nacc);
-                ++nacc;
-                if (nacc == 64) flush_events();
-                ++nEv;
-                if (conv) {
-                    const uint32_t nx = bpermute(pend, (lane + 1u) & 63u);
-                    pend = (lane == 63u) ? 0xFFFFu : nx;
-                    --nPend;
-                } else {
-                    ++ic;
-                    if (ic - cb == 64) {
-                        cb += 64;
-                        cwin = (cb + static_cast<int32_t>(lane) < M) ? cpos[cb + lane] : 0xFFFFu;
-                    }
-                }
-                if (v != VT_NONE) {  // the evicted token is hit later this step: that hit becomes a miss
-                    const uint32_t t = v - 1u;
-                    const uint32_t pv = bpermute(pend, (lane - 1u) & 63u);
-                    pend = (pend < t) ? pend : ((lane == 0u || pv < t) ? t : pv);
-                    if (++nPend > 64) {
-                        wrap = true;  // more pending conversions than lanes: sequential path
-                        break;
-                    }
-                    cvT = writelane(cvT, t, ncvAcc);
-                    cvS = writelane(cvS, readlane(static_cast<uint32_t>(sl), l), ncvAcc);
-                    ++ncvAcc;
-                    ++nConv;
-                    if (ncvAcc == 64) flush_conv();
-                }
-                if (cursor == 64) {
-                    flush_window(0u);
-                    base += 64;
-                    WALK_STAMP(base >> 6, nEv);
-                    load_window();
-                }
+        for (int32_t j = 0; j < Q; ++j) {
+            const int32_t u = u0 + j;
+            if (u >= dbs) break;
+            const uint16_t v = vt[ring_slot(hand0, u, dbs)];
+            if (v == VT_NONE) snM |= 1ull << j;
+            else if (v != 0) smM |= 1ull << j;
+        }
+        const uint32_t cSN = static_cast<uint32_t>(__popcll(snM)), cSM = static_cast<uint32_t>(__popcll(smM));
+        const uint32_t qb = bits_for(static_cast<uint32_t>(Q));
+        uint32_t tot;
+        const uint32_t pre = block_exscan(cSN | (cSM << 16), qb | (qb << 16), ms.wt0, tot);
+        preSN = pre & 0xFFFFu;
+        preSM = pre >> 16;
+        uint32_t nsn = preSN, nsm = preSM;
+        for (int32_t j = 0; j < Q; ++j) {
+            const int32_t u = u0 + j;
+            if (u >= dbs) break;
+            if ((snM >> j) & 1ull) {
+                ++nsn;
+            } else if ((smM >> j) & 1ull) {
+                const uint32_t k = static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)]) - 1u;
+                smA[nsm] = static_cast<uint32_t>(u) | (k << 16);
+                smB[nsm] = nsn | (static_cast<uint32_t>(candPre[k]) << 16);
+                ++nsm;
             }
-            if (!wrap) {
-                flush_window(0u);
-                flush_events();
-                flush_conv();
+        }
+        if (tid == 0) ms.nSM = static_cast<int32_t>(tot >> 16);
+        __syncthreads();
+        STAMP(6);
+
+        // ---- decide the SM slots, one wave, 64 at a time.  need = the event
+        // index being served when the hand arrives; cnt = events before k.
+        if (wave == 0) {
+            const int32_t nSM = ms.nSM;
+            int32_t T = 0, nConv = 0, Mtot = ms.M, done = 0;
+            bool ended = false;
+            for (int32_t b0 = 0; b0 < nSM && !ended; b0 += 64) {
+                const int32_t i = b0 + static_cast<int32_t>(lane);
+                const bool inb = i < nSM;
+                const uint32_t ea = inb ? smA[i] : 0u;
+                const uint32_t eb = inb ? smB[i] : 0u;
+                const uint32_t k = ea >> 16;
+                int32_t need = static_cast<int32_t>(eb & 0xFFFFu) + T;
+                int32_t cnt = static_cast<int32_t>(eb >> 16);
+                for (int32_t j = 0; j < nConv; ++j) cnt += (static_cast<uint32_t>(cvlist[j]) < k) ? 1 : 0;
+                uint64_t active = __ballot(inb);
+                uint64_t takenM = 0;
+                const int32_t T0 = T;
+                for (;;) {
+                    const uint64_t tk = __ballot(cnt > need) & active;
+                    const uint64_t ur = __ballot(need >= Mtot) & active;
+                    const uint64_t any = tk | ur;
+                    if (any == 0ull) break;
+                    const int f = __builtin_ctzll(any);
+                    if ((ur >> f) & 1ull) {  // the events run out before this slot: the walk ends
+                        ended = true;
+                        break;
+                    }
+                    takenM |= 1ull << f;
+                    const uint32_t t = readlane(k, f);
+                    const uint32_t uf = readlane(ea & 0xFFFFu, f);
+                    if (lane == 0) {
+                        evold[t] = static_cast<uint16_t>(ring_slot(hand0, static_cast<int32_t>(uf), dbs));
+                        cvlist[nConv] = static_cast<uint16_t>(t);
+                    }
+                    ++T;
+                    ++nConv;
+                    ++Mtot;
+                    active &= (f == 63) ? 0ull : (~0ull << (f + 1));
+                    if (static_cast<int>(lane) > f) {
+                        need += 1;
+                        cnt += (k > t) ? 1 : 0;
+                    }
+                }
+                if (inb) {
+                    tb[i] = static_cast<uint16_t>((T0 + static_cast<int32_t>(lanes_below(takenM, lane))) |
+                                                  (((takenM >> lane) & 1ull) ? 0x8000 : 0));
+                }
+                done = (b0 + 64 < nSM) ? b0 + 64 : nSM;
             }
             if (lane == 0) {
-                ms.wrap = wrap ? 1 : 0;
+                ms.T = T;
                 ms.nConv = nConv;
-                ms.nEv = nEv;
-                ms.uEnd = base + cursor;
+                ms.N = Mtot;
+                ms.smDone = nSM < done ? nSM : done;
             }
         }
         __syncthreads();
-        STAMP(6);
-        if (ms.wrap) fast = false;
+        STAMP(7);
+        {
+            const int32_t nSM = ms.nSM, T = ms.T, nConv = ms.nConv;
+            for (int32_t i = ms.smDone + tid; i <= nSM; i += NT) tb[i] = static_cast<uint16_t>(T);
+            for (int32_t j = tid; j < nConv; j += NT) pinf[cvlist[j]] |= INF_CONV;
+        }
+        __syncthreads();
+        // ---- the event sequence: candidates' first occurrences and conversions in position order
+        {
+            const int32_t P = (K + NT - 1) / NT;
+            const int32_t k0 = tid * P;
+            uint32_t cnt = 0, fl = 0;
+            for (int32_t i = 0; i < P; ++i) {
+                const int32_t k = k0 + i;
+                if (k < K) {
+                    const uint32_t inf = pinf[k];
+                    const uint32_t c = inf >> 30;
+                    const uint32_t f = ((c == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ||
+                                        (c == CLS_HIT && (inf & INF_CONV)))
+                                           ? 1u
+                                           : 0u;
+                    fl |= f << i;
+                    cnt += f;
+                }
+            }
+            uint32_t tot;
+            uint32_t pre = block_exscan(cnt, bits_for(static_cast<uint32_t>(P)), ms.wt0, tot);
+            for (int32_t i = 0; i < P; ++i) {
+                if ((fl >> i) & 1u) eseq[pre++] = static_cast<uint16_t>(k0 + i);
+            }
+            if (tid == 0 && static_cast<int32_t>(tot) != ms.N) ms.ovf = 1;
+        }
+        __syncthreads();
+        STAMP(8);
+        // ---- marks per ring offset: evicted by event p, or passed while serving event p
+        {
+            const int32_t N = ms.N;
+            uint32_t nsn2 = preSN, nsm2 = preSM, ntk = 0;
+            for (int32_t j = 0; j < Q; ++j) {
+                const int32_t u = u0 + j;
+                if (u >= dbs) break;
+                const int32_t s = ring_slot(hand0, u, dbs);
+                const bool isSN = (snM >> j) & 1ull, isSM = (smM >> j) & 1ull;
+                const uint32_t tbv = tb[nsm2];
+                const int32_t r = static_cast<int32_t>(nsn2 + (tbv & 0x7FFFu));
+                if (r < N) {
+                    const uint32_t p = eseq[r];
+                    if (isSN || (isSM && (tbv & 0x8000u))) {
+                        evslot[p] = static_cast<uint16_t>(s);
+                        vt[s] = isSM ? static_cast<uint16_t>(VT_EVICTED | (vt[s] - 1u))
+                                     : static_cast<uint16_t>(VT_EVICTED | VT_NOCONV);
+                        ++ntk;
+                        if (r == N - 1) ms.uEnd = u + 1;
+                    } else {
+                        vt[s] = static_cast<uint16_t>(VT_PASSED | p);
+                    }
+                }
+                nsn2 += isSN ? 1u : 0u;
+                nsm2 += isSM ? 1u : 0u;
+            }
+            ntk = wave_sum(ntk);
+            if (lane == 0 && ntk) atomicAdd(&ms.nTakes, static_cast<int32_t>(ntk));
+        }
+        __syncthreads();
+        STAMP(9);
+        if (ms.nTakes != ms.N || ms.ovf) fast = false;  // the hand would wrap within the step
     }
 
     if (fast) {
-        const int32_t M = ms.M, uEnd = ms.uEnd, nEv = ms.nEv;
-        // ---- D: outputs and visited bits
+        const int32_t N = ms.N, uEnd = ms.uEnd;
+        // ---- outputs and visited bits
         for (int32_t k = tid; k < K; k += NT) {
             const uint32_t inf = pinf[k];
             const uint32_t cls = inf >> 30;
@@ -585,13 +653,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             rm[k] = miss;
         }
         for (int32_t u = tid; u < uEnd; u += NT) {
-            int32_t s = hand0 + u;
-            if (s >= dbs) s -= dbs;
+            const int32_t s = ring_slot(hand0, u, dbs);
             atomicAnd(vis32 + (s >> 5), ~(1u << (s & 31)));
         }
         __syncthreads();
-        for (int32_t i = tid; i < nEv; i += NT) {
-            const uint32_t s = evslot[i < M ? cpos[i] : cvlist[i - M]];
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t s = evslot[eseq[i]];
             atomicOr(vis32 + (s >> 5), 1u << (s & 31u));
         }
         for (int32_t k = tid; k < K; k += NT) {
@@ -603,12 +670,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if ((v & VT_PASSED) && static_cast<uint32_t>(k) <= (v & VT_NOCONV)) continue;
             atomicOr(vis32 + (s0 >> 5), 1u << (s0 & 31u));
         }
-        STAMP_SYNC(7);
+        __syncthreads();
+        STAMP(10);
 
-        // ---- E1: erase the evicted tokens (pre-step tokens give the homes)
+        // ---- table: erase the evicted tokens (pre-step tokens give the homes)
         Guard g;
-        for (int32_t i = tid; i < nEv; i += NT) {
-            const uint32_t s = evslot[i < M ? cpos[i] : cvlist[i - M]];
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t s = evslot[eseq[i]];
             const int32_t old = tok[s];
             uint32_t cell = 0xFFFFFFFFu;
             if (old >= 0) {
@@ -626,24 +694,24 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             kcell[i] = cell;
         }
         __syncthreads();
-        for (int32_t i = tid; i < nEv; i += NT) {  // leader: rightmost marked cell of its cluster
+        for (int32_t i = tid; i < N; i += NT) {  // leader: rightmost marked cell of its cluster
             const uint32_t c = kcell[i];
-            uint32_t leader = 0;
+            uint32_t ld = 0;
             if (c != 0xFFFFFFFFu) {
-                leader = 1;
+                ld = 1;
                 int32_t x = (static_cast<int32_t>(c) + 1) & mask;
                 for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
                     if (bit_get(ber, x)) {
-                        leader = 0;
+                        ld = 0;
                         break;
                     }
                 }
             }
-            kstart[i] = leader;
+            lead[i] = ld;
         }
         __syncthreads();
-        for (int32_t i = tid; i < nEv; i += NT) {
-            if (!kstart[i]) continue;
+        for (int32_t i = tid; i < N; i += NT) {
+            if (!lead[i]) continue;
             const int32_t c = static_cast<int32_t>(kcell[i]);
             rdel_at(ht, tok, padded, c, mask, g);
             int32_t x = (c - 1) & mask;
@@ -652,112 +720,105 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         __syncthreads();
-        STAMP(8);
+        STAMP(11);
         // ---- token update: read every new token first (conversions re-insert a pre-step token)
-        for (int32_t i = tid; i < nEv; i += NT) {
-            const uint32_t t = i < M ? cpos[i] : cvlist[i - M];
-            kcell[i] = static_cast<uint32_t>(i < M ? ptok[t] : tok[evold[t]]);
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t p = eseq[i];
+            kcell[i] = static_cast<uint32_t>((pinf[p] >> 30) == CLS_CAND ? ptok[p] : tok[evold[p]]);
         }
         __syncthreads();
-        for (int32_t i = tid; i < nEv; i += NT) tok[evslot[i < M ? cpos[i] : cvlist[i - M]]] = static_cast<int32_t>(kcell[i]);
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t s = evslot[eseq[i]];
+            tok[s] = static_cast<int32_t>(kcell[i]);
+        }
         __syncthreads();
-        // ---- E2: inserts.  Tentative placement (the final occupied cells do not depend on order)
-        for (int32_t i = tid; i < nEv; i += NT) {
-            const uint32_t s = evslot[i < M ? cpos[i] : cvlist[i - M]];
+        // ---- inserts: tentative placement (the final occupied cells do not depend on order)
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t s = evslot[eseq[i]];
             const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(tok[s])) & mask, mask,
                                           static_cast<uint16_t>(s + 1u));
             if (c < 0) g.code = kOverflowProbe;
-            kcell[i] = static_cast<uint32_t>(c);
+            else atomicOr(bnew + (c >> 5), 1u << (c & 31));
         }
         __syncthreads();
-        for (int32_t i = tid; i < nEv; i += NT) {  // final cluster of each new key
-            const uint32_t s = evslot[i < M ? cpos[i] : cvlist[i - M]];
+        // final cluster of each new key (its start); clusters with two or more new keys are redone
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t s = evslot[eseq[i]];
             int32_t st = static_cast<int32_t>(ht_hash(tok[s])) & mask;
             for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
-            kstart[i] = static_cast<uint32_t>(st);
             const uint32_t bit = 1u << (st & 31);
             const uint32_t old = atomicOr(bg + (st >> 5), bit);
             if (old & bit) atomicOr(bm + (st >> 5), bit);
         }
         __syncthreads();
-        STAMP(9);
-        uint32_t *mlist = pinf;  // positions' info is no longer needed
-        for (int32_t i = tid; i < nEv; i += NT) {
-            if (bit_get(bm, kstart[i])) mlist[atomicAdd(&ms.nMulti, 1)] = static_cast<uint32_t>(i);
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t p = eseq[i];
+            const uint32_t s = evslot[p];
+            int32_t st = static_cast<int32_t>(ht_hash(tok[s])) & mask;
+            for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
+            if (bit_get(bm, static_cast<uint32_t>(st))) {
+                const int32_t q = atomicAdd(&ms.nMulti, 1);
+                mlist[q] = (static_cast<uint64_t>(st) << 32) | (static_cast<uint64_t>(p) << 16) | s;
+            }
         }
         __syncthreads();
+        STAMP(12);
         const int32_t nMulti = ms.nMulti;
-        for (int32_t q = tid; q < nMulti; q += NT) {  // one lane per multi-key cluster redoes it in time order
-            const uint32_t i = mlist[q];
-            const uint32_t st = kstart[i];
-            const uint32_t ti = i < static_cast<uint32_t>(M) ? cpos[i] : cvlist[i - M];
-            uint32_t grp[32];
-            uint32_t tms[32];
-            int32_t ng = 0;
-            bool lead = true, big = false;
-            for (int32_t r = 0; r < nMulti; ++r) {
-                const uint32_t o = mlist[r];
-                if (kstart[o] != st) continue;
-                const uint32_t to = o < static_cast<uint32_t>(M) ? cpos[o] : cvlist[o - M];
-                if (to < ti) {
-                    lead = false;
-                    break;
-                }
-                if (ng < 32) {
-                    grp[ng] = o;
-                    tms[ng] = to;
-                    ++ng;
-                } else {
-                    big = true;
-                }
+        for (int32_t q = tid; q < nMulti; q += NT) {  // sort by (cluster start, event time)
+            const uint64_t key = mlist[q];
+            int32_t r = 0;
+            for (int32_t j = 0; j < nMulti; ++j) r += (mlist[j] < key) ? 1 : 0;
+            msort[r] = key;
+        }
+        __syncthreads();
+        for (int32_t q = tid; q < nMulti; q += NT) {  // the first key of each cluster redoes it in time order
+            const uint64_t key = msort[q];
+            const uint32_t st = static_cast<uint32_t>(key >> 32);
+            if (q > 0 && static_cast<uint32_t>(msort[q - 1] >> 32) == st) continue;
+            int32_t end = static_cast<int32_t>(st);
+            for (int32_t n = 0; n < H && ht[end] != 0; ++n) end = (end + 1) & mask;
+            for (int32_t x = static_cast<int32_t>(st); x != end; x = (x + 1) & mask) {
+                if (bit_get(bnew, static_cast<uint32_t>(x))) ht[x] = 0;
             }
-            if (!lead) continue;
-            if (big) {
-                g.code = kOverflowProbe;  // cannot happen below load 1/2 with topK <= 16383 in practice
-                continue;
-            }
-            for (int32_t x = 1; x < ng; ++x) {  // insertion sort by time
-                const uint32_t go = grp[x], tt = tms[x];
-                int32_t y = x - 1;
-                while (y >= 0 && tms[y] > tt) {
-                    grp[y + 1] = grp[y];
-                    tms[y + 1] = tms[y];
-                    --y;
-                }
-                grp[y + 1] = go;
-                tms[y + 1] = tt;
-            }
-            for (int32_t x = 0; x < ng; ++x) ht[kcell[grp[x]]] = 0;
-            for (int32_t x = 0; x < ng; ++x) {
-                const uint32_t s = evslot[tms[x]];
+            for (int32_t r = q; r < nMulti && static_cast<uint32_t>(msort[r] >> 32) == st; ++r) {
+                const uint32_t s = static_cast<uint32_t>(msort[r] & 0xFFFFu);
                 int32_t idx = static_cast<int32_t>(ht_hash(tok[s])) & mask;
                 for (int32_t n = 0; n < H && ht[idx] != 0; ++n) idx = (idx + 1) & mask;
                 ht[idx] = static_cast<uint16_t>(s + 1u);
             }
         }
-        if (g.code) report_overflow(L.overflowSlot, g.code);
+        if (g.code) atomicOr(&ms.late, 1);
         __syncthreads();
-        STAMP(10);
-        // ---- write back
-        wg_copy16(gVis, vis, static_cast<uint32_t>(visStrideB));
-        if (nEv > 0) {
-            wg_copy16(gTok, tok, static_cast<uint32_t>(padded) * 4u);
-            wg_copy16(gHt, ht, static_cast<uint32_t>(H) * 2u);
-        }
-        if (tid == 0) {
-            int32_t hd = hand0;
-            if (nEv > 0) {
-                hd = hand0 + uEnd;
-                while (hd >= dbs) hd -= dbs;
+        STAMP(13);
+        if (!ms.late) {
+            // ---- write back
+            wg_copy16(gVis, vis, static_cast<uint32_t>(visStrideB));
+            if (N > 0) {
+                wg_copy16(gTok, tok, static_cast<uint32_t>(padded) * 4u);
+                wg_copy16(gHt, ht, static_cast<uint32_t>(H) * 2u);
             }
-            gHand[0] = hd;
-            gHand[1] = kCanonFlag;
+            if (tid == 0) {
+                int32_t hd = hand0;
+                if (N > 0) {
+                    hd = hand0 + uEnd;
+                    while (hd >= dbs) hd -= dbs;
+                }
+                gHand[0] = hd;
+                gHand[1] = kCanonFlag;
+            }
+            STAMP(14);
+            return;
         }
-        STAMP_SYNC(11);
-        return;
+        fast = false;
     }
 
-    // ---- fallback: the sequential recurrence on the staged (pre-step) state
+    // ---- fallback: restage the pre-step row from HBM (nothing has been
+    // written back) and run the sequential recurrence on it
+    __syncthreads();
+    wg_copy16(tok, gTok, static_cast<uint32_t>(padded) * 4u);
+    wg_copy16(ht, gHt, static_cast<uint32_t>(H) * 2u);
+    wg_copy16(vis, gVis, static_cast<uint32_t>(visStrideB));
+    __syncthreads();
     __shared__ int32_t s_dirty;
     if (tid == 0) {
         int32_t hand = hand0;
@@ -795,13 +856,6 @@ hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overf
 }  // namespace kvx
 
 #ifdef KVX_SIEVE_PHASE_STAMPS
-extern "C" int kvx_dbg_read_walk(unsigned long long *out, int rows)
-{
-    if (rows > 1024) rows = 1024;
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(kvx::kvx_dbg_walk), sizeof(unsigned long long) * 64 * rows, 0,
-                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
-}
-
 extern "C" int kvx_dbg_read_stamps(unsigned long long *out, int rows)
 {
     if (rows > 1024) rows = 1024;
