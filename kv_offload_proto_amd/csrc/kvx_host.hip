@@ -120,6 +120,24 @@ void EnsureWinScratch(uint64_t entries)
     g.epoch = 0;
 }
 
+// Grow-only gather row list (source and destination addresses per row).
+void EnsureListScratch(uint64_t entries)
+{
+    if (g.scratch.listCap >= entries) return;
+    const uint64_t cap = std::max<uint64_t>(entries, 65536);
+    if (g.scratch.listSrc != nullptr) {
+        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        hipCheck(hipFree(g.scratch.listSrc), "hipFree");
+        g.scratch.listSrc = g.scratch.listDst = nullptr;
+        g.scratch.listCap = 0;
+    }
+    void *p = nullptr;
+    hipCheck(hipMalloc(&p, 2 * cap * sizeof(uint64_t)), "hipMalloc(gather list)");
+    g.scratch.listSrc = static_cast<uint64_t *>(p);
+    g.scratch.listDst = g.scratch.listSrc + cap;
+    g.scratch.listCap = cap;
+}
+
 uint32_t NextEpoch(hipStream_t stream)
 {
     if (++g.epoch == 0) {  // tags of 2^32 calls ago could alias: clear and restart
@@ -188,6 +206,7 @@ void DoGather(const GatherCall &c)
 
     const uint64_t need = static_cast<uint64_t>(c.maxNumReqs - 1) * plan.spanRows + 65536ull;
     EnsureWinScratch(need);
+    EnsureListScratch(positions);
     hipStream_t st = AsStream(c.stream);
     plan.epoch = NextEpoch(st);
     if (c.fused) {
@@ -229,6 +248,7 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         g.scratch.counters = static_cast<uint32_t *>(c);
         g.scratch.errs = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + kTable);
         g.scratch.tickets = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + 2 * kTable);
+        g.scratch.listCount = g.scratch.tickets + 8;
         g.inited = true;
     });
 }
@@ -532,6 +552,7 @@ int kvx_close(void)
         if (g.overflow != nullptr) (void)hipFree(g.overflow);
         g.overflow = nullptr;
         if (g.scratch.win != nullptr) (void)hipFree(g.scratch.win);
+        if (g.scratch.listSrc != nullptr) (void)hipFree(g.scratch.listSrc);
         if (g.scratch.counters != nullptr) (void)hipFree(g.scratch.counters);
         g.scratch = kvx::RowScratch{};
         {

@@ -45,6 +45,10 @@ struct RowScratch {
     uint32_t *counters;        // [64 nodes][8 status words] queued counts
     uint32_t *errs;            // [64 nodes][8 status words] first error code
     uint32_t *tickets;         // [4] last-block tickets (gather, export)
+    uint64_t *listSrc;         // gather row list: source byte addresses
+    uint64_t *listDst;         // gather row list: destination byte addresses
+    uint64_t listCap;          // capacity of the row list
+    uint32_t *listCount;       // rows listed by the current gather
 };
 
 // ---------------------------------------------------------------------------

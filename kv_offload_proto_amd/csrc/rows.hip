@@ -5,9 +5,11 @@
 // kvc_scatter_rows_alllayer.cpp:11-67 of the reference, with the row
 // ownership of kv_layout.h.  The reference moves each row with one HCOMM
 // ReadNbi/WriteNbi; here the host segments are pinned host memory mapped
-// into the device address space, and each wave moves up to 64 rows at a time
-// as 16-byte chunks, 8 chunks in flight per lane, so hundreds of kilobytes of
-// host-link reads are outstanding across the grid.
+// into the device address space.  The import runs in three launches:
+// winners (the last miss position per destination row), a dense list of the
+// rows to move (with the reference's queued counts), and the copy, where
+// each wave moves 64 listed rows at a time as 16-byte chunks, 8 chunks in
+// flight per lane, so megabytes of host-link reads stay outstanding.
 //
 // Completion: the last workgroup to finish (atomicInc ticket) stores the
 // status words with a system-scope release, after every workgroup fenced its
@@ -20,6 +22,7 @@ namespace {
 
 constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kUnroll = 8;         // 16-byte chunks in flight per lane
+constexpr int kGroup = 8;          // 64-position chunks a wave lists per row-list atomic
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -27,6 +30,9 @@ struct GatherExtra {
     uint64_t segBases[64];
     unsigned long long *win;
     uint64_t winEntries;
+    uint64_t *listSrc;     // rows to move: source and destination byte addresses
+    uint64_t *listDst;
+    uint32_t *listCount;
     uint32_t *counters;
     uint32_t *errs;
     uint32_t *tickets;
@@ -69,8 +75,8 @@ __device__ __forceinline__ void store_status(uint64_t addr, uint64_t word)
     __hip_atomic_store(reinterpret_cast<uint64_t *>(addr), word, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Copy `n` rows whose byte addresses sit in src[0..n), dst[0..n) (LDS, per
-// wave) with the whole wave: chunk c covers bytes [16*(c%cpr), +16) of row
+// Copy `n` rows whose byte addresses sit in src[0..n), dst[0..n) (LDS or
+// global) with the whole wave: chunk c covers bytes [16*(c%cpr), +16) of row
 // c/cpr.  kUnroll loads are issued before their stores.
 __device__ __forceinline__ void wave_copy_rows(const uint64_t *src, const uint64_t *dst, uint32_t n, uint32_t cpr)
 {
@@ -121,6 +127,7 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
     if (blockIdx.x == 0) {
         const uint32_t n0 = x.fused ? 0u : a.myNode;
         const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
+        if (threadIdx.x == 0) *x.listCount = 0u;
         for (uint32_t i = threadIdx.x; i < (n1 - n0) * 8u; i += blockDim.x) {
             x.counters[n0 * 8u + i] = 0u;
             x.errs[n0 * 8u + i] = 0u;
@@ -149,20 +156,19 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
     }
 }
 
-// Pass 2: copy the winners owned by the node(s) of this call, count the
-// reference's queued rows per (node, status word), last workgroup reports.
-__global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
+// Pass 2: list the winners owned by the node(s) of this call and count the
+// reference's queued rows per (node, status word).  Each wave takes kGroup
+// chunks of 64 positions at a time and appends their rows with one atomic;
+// counts are summed per workgroup in LDS and flushed once.
+__global__ __launch_bounds__(256) void kvx_gather_list(GatherParams P)
 {
-    __shared__ uint64_t sSrc[kWaves][64];
-    __shared__ uint64_t sDst[kWaves][64];
-    __shared__ int sLast;
+    __shared__ uint32_t sCnt[64 * 8];
     const KvcGatherArgs &a = P.l.a;
     const GatherExtra &x = P.x;
     const int wave = threadIdx.x / 64;
     const uint32_t lane = static_cast<uint32_t>(lane_id());
     const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
     const int64_t total = static_cast<int64_t>(numReal) * a.topK;
-    const uint32_t cpr = a.rowBytes / 16u;
     const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
     const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
     const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
@@ -170,59 +176,85 @@ __global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
     const int64_t *hostBase = reinterpret_cast<const int64_t *>(a.reqHostBase);
     const unsigned long long tagHi = static_cast<unsigned long long>(x.epoch) << 32;
     const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
+    for (uint32_t i = threadIdx.x; i < 64u * 8u; i += blockDim.x) sCnt[i] = 0u;
+    __syncthreads();
 
-    for (int64_t chunk = static_cast<int64_t>(blockIdx.x) * kWaves + wave; chunk * 64 < total;
-         chunk += static_cast<int64_t>(gridDim.x) * kWaves) {
-        const int64_t p = chunk * 64 + lane;
-        bool owned = false, copy = false;
-        uint32_t key = 0;
-        uint64_t src = 0, dst = 0;
-        if (p < total && miss[p] != 0) {
-            const int32_t t = topk[p], s = slots[p];
-            const int64_t bid = p / a.topK;
-            if (t >= 0 && s >= 0 && pool[bid] >= 0) {
-                const uint32_t row = static_cast<uint32_t>(hostBase[bid] + t);  // kvc_gather_rows.cpp:69-73
-                const uint32_t node = kvx_node_of(row, a.stripeRows, a.nodeNum);
-                owned = x.fused ? (node < a.nodeNum) : (node == a.myNode);
-                if (owned) {
-                    key = node * 8u + static_cast<uint32_t>(static_cast<uint64_t>(p) / ppc);
-                    bool winner = true;
-                    if (s < 65536) {
-                        const uint64_t d = win_index(bid, s, x.spanRows);
-                        if (d < x.winEntries) winner = (x.win[d] == (tagHi | static_cast<unsigned long long>(p)));
+    const int64_t chunks = (total + 63) / 64;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWaves;
+    for (int64_t g0 = static_cast<int64_t>(blockIdx.x) * kWaves + wave; g0 < chunks; g0 += waves * kGroup) {
+        uint64_t src[kGroup], dst[kGroup], cm[kGroup];
+        uint32_t nAll = 0;
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            const int64_t p = (g0 + j * waves) * 64 + lane;
+            bool copy = false;
+            src[j] = dst[j] = 0;
+            if (p < total && miss[p] != 0) {
+                const int32_t t = topk[p], s = slots[p];
+                const int64_t bid = p / a.topK;
+                if (t >= 0 && s >= 0 && pool[bid] >= 0) {
+                    const uint32_t row = static_cast<uint32_t>(hostBase[bid] + t);  // kvc_gather_rows.cpp:69-73
+                    const uint32_t node = kvx_node_of(row, a.stripeRows, a.nodeNum);
+                    const bool owned = x.fused ? (node < a.nodeNum) : (node == a.myNode);
+                    if (owned) {
+                        const uint32_t key = node * 8u + static_cast<uint32_t>(static_cast<uint64_t>(p) / ppc);
+                        atomicAdd(&sCnt[key], 1u);
+                        bool winner = true;
+                        if (s < 65536) {
+                            const uint64_t d = win_index(bid, s, x.spanRows);
+                            if (d < x.winEntries) winner = (x.win[d] == (tagHi | static_cast<unsigned long long>(p)));
+                        }
+                        const uint64_t segBase = x.fused ? x.segBases[node] : a.segBase;
+                        const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
+                        if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
+                            atomicCAS(&x.errs[key], 0u, row_error_code(static_cast<uint64_t>(p)));
+                            winner = false;
+                        }
+                        copy = winner;
+                        src[j] = segBase + (static_cast<uint64_t>(a.layerOffsetRows) + segRow) * a.rowBytes;
+                        dst[j] = a.hotRowBase + (static_cast<uint64_t>(s) +
+                                                 static_cast<uint64_t>(bid) * a.hotReqStrideRows) * a.rowBytes;
                     }
-                    const uint64_t segBase = x.fused ? x.segBases[node] : a.segBase;
-                    const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
-                    if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
-                        atomicCAS(&x.errs[key], 0u, row_error_code(static_cast<uint64_t>(p)));
-                        winner = false;
-                    }
-                    copy = winner;
-                    src = segBase + (static_cast<uint64_t>(a.layerOffsetRows) + segRow) * a.rowBytes;
-                    dst = a.hotRowBase +
-                          (static_cast<uint64_t>(s) + static_cast<uint64_t>(bid) * a.hotReqStrideRows) * a.rowBytes;
                 }
             }
+            cm[j] = __ballot(copy);
+            nAll += static_cast<uint32_t>(__popcll(cm[j]));
         }
-        // queued counts, one atomic per distinct (node, status word) in the wave
-        uint64_t rem = __ballot(owned);
-        while (rem != 0) {
-            const int leader = __ffsll(static_cast<long long>(rem)) - 1;
-            const uint32_t k = __shfl(key, leader);
-            const uint64_t same = __ballot(owned && key == k);
-            if (lane == static_cast<uint32_t>(leader)) atomicAdd(&x.counters[k], static_cast<uint32_t>(__popcll(same)));
-            rem &= ~same;
+        if (nAll == 0) continue;
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(x.listCount, nAll);
+        base = __shfl(base, 0);
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            if ((cm[j] >> lane) & 1ull) {
+                const uint32_t at = base + static_cast<uint32_t>(__popcll(cm[j] & ((1ull << lane) - 1ull)));
+                x.listSrc[at] = src[j];
+                x.listDst[at] = dst[j];
+            }
+            base += static_cast<uint32_t>(__popcll(cm[j]));
         }
-        const uint64_t cmask = __ballot(copy);
-        if (cmask == 0) continue;
-        const uint32_t rank = static_cast<uint32_t>(__popcll(cmask & ((1ull << lane) - 1ull)));
-        if (copy) {
-            sSrc[wave][rank] = src;
-            sDst[wave][rank] = dst;
-        }
-        wave_sync_lds();
-        wave_copy_rows(sSrc[wave], sDst[wave], static_cast<uint32_t>(__popcll(cmask)), cpr);
-        wave_sync_lds();
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < 64u * 8u; i += blockDim.x) {
+        if (sCnt[i] != 0u) atomicAdd(&x.counters[i], sCnt[i]);
+    }
+}
+
+// Pass 3: move the listed rows, 64 per wave task; the last workgroup reports.
+__global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
+{
+    __shared__ int sLast;
+    const KvcGatherArgs &a = P.l.a;
+    const GatherExtra &x = P.x;
+    const int wave = threadIdx.x / 64;
+    const uint32_t cpr = a.rowBytes / 16u;
+    const uint32_t n = *x.listCount;
+    const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
+    const int64_t total = static_cast<int64_t>(numReal) * a.topK;
+    const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
+    for (uint32_t r0 = (blockIdx.x * kWaves + wave) * 64u; r0 < n; r0 += gridDim.x * kWaves * 64u) {
+        const uint32_t nr = (n - r0 < 64u) ? n - r0 : 64u;
+        wave_copy_rows(x.listSrc + r0, x.listDst + r0, nr, cpr);
     }
 
     __threadfence();
@@ -336,6 +368,9 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     }
     P.x.win = scr.win;
     P.x.winEntries = scr.winEntries;
+    P.x.listSrc = scr.listSrc;
+    P.x.listDst = scr.listDst;
+    P.x.listCount = scr.listCount;
     P.x.counters = scr.counters;
     P.x.errs = scr.errs;
     P.x.tickets = scr.tickets;
@@ -350,9 +385,16 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     hipLaunchKernelGGL(kvx_gather_prep, dim3(static_cast<uint32_t>(prepBlocks)), dim3(256), 0, stream, P);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    uint64_t listBlocks = (positions + 64ull * kWaves * kGroup - 1ull) / (64ull * kWaves * kGroup);
+    if (listBlocks < 1) listBlocks = 1;
+    if (listBlocks > 1024) listBlocks = 1024;
+    hipLaunchKernelGGL(kvx_gather_list, dim3(static_cast<uint32_t>(listBlocks)), dim3(256), 0, stream, P);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // one 64-row task per wave covers every listed row of a full batch
     uint64_t copyBlocks = (positions + 64ull * kWaves - 1ull) / (64ull * kWaves);
     if (copyBlocks < 1) copyBlocks = 1;
-    if (copyBlocks > 4096) copyBlocks = 4096;
+    if (copyBlocks > 1024) copyBlocks = 1024;
     hipLaunchKernelGGL(kvx_gather_copy, dim3(static_cast<uint32_t>(copyBlocks)), dim3(256), 0, stream, P);
     return hipGetLastError();
 }
