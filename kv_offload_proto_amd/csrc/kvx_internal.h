@@ -58,8 +58,8 @@ struct RowScratch {
 constexpr int kFastThreads = 1024;
 
 struct FastLayout {
-    uint32_t tok, ht, vis, ptok, pinf, vt, candPre, evslot, evold, cvlist, eseq, tb, smA, smB, ber, bg, bm, bnew,
-        total;
+    uint32_t tok, ht, vis, ptok, pinf, vt, candPre, evslot, evold, cvlist, eseq, tb, smA, smB, kst, vset, ber, bg,
+        bm, bnew, total;
 };
 
 __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
@@ -86,6 +86,8 @@ __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint
     l.tb = o;      o += align16((topK + 1u) * 2u);
     l.smA = o;     o += align16(topK * 4u);
     l.smB = o;     o += align16(topK * 4u);
+    l.kst = o;     o += align16(topK * 4u);
+    l.vset = o;    o += align16(visStrideB);
     l.ber = o;     o += align16(htSize / 8u);
     l.bg = o;      o += align16(htSize / 8u);
     l.bm = o;      o += align16(htSize / 8u);

@@ -59,7 +59,6 @@ constexpr int NT = kFastThreads;
 constexpr int NWAVES = NT / 64;
 
 constexpr uint32_t CLS_INV = 0u, CLS_EXT = 1u, CLS_HIT = 2u, CLS_CAND = 3u;
-constexpr uint32_t INF_CONV = 1u << 29;  // a hit position that became a conversion
 constexpr uint16_t VT_NONE = 0xFFFF, VT_EVICTED = 0x8000, VT_PASSED = 0x4000, VT_NOCONV = 0x3FFF;
 // sieve_hand[row][1]: set when this kernel left the row's table consistent
 constexpr int32_t kCanonFlag = 0x4B565843;
@@ -80,17 +79,12 @@ __device__ unsigned long long kvx_dbg_stamps[1024][16];
 
 struct Misc {
     int32_t nTok, nEnt, bad, ovf, late;
-    int32_t M, nSM, T, nConv, N, smDone, uEnd, nTakes, nMulti;
+    int32_t M, nSM, T, nConv, N, nUnd, nRest, uEnd, nTakes, nMulti;
     uint32_t wt0[NWAVES];
     uint32_t wt1[NWAVES];
 };
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
-
-__device__ __forceinline__ uint32_t readlane(uint32_t v, int l)
-{
-    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
-}
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m, uint32_t lane)
 {
@@ -280,63 +274,101 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint16_t *candPre = reinterpret_cast<uint16_t *>(smem + lay.candPre);
     uint16_t *evslot = reinterpret_cast<uint16_t *>(smem + lay.evslot);
     uint16_t *evold = reinterpret_cast<uint16_t *>(smem + lay.evold);
-    uint16_t *cvlist = reinterpret_cast<uint16_t *>(smem + lay.cvlist);
+    uint16_t *smKp = reinterpret_cast<uint16_t *>(smem + lay.cvlist);  // k of SM slots that can be evicted, else 0
     uint16_t *eseq = reinterpret_cast<uint16_t *>(smem + lay.eseq);
     uint16_t *tb = reinterpret_cast<uint16_t *>(smem + lay.tb);
     uint32_t *smA = reinterpret_cast<uint32_t *>(smem + lay.smA);  // ring offset | k << 16
     uint32_t *smB = reinterpret_cast<uint32_t *>(smem + lay.smB);  // SN before | candidates before k << 16
+    uint32_t *kst = reinterpret_cast<uint32_t *>(smem + lay.kst);
+    uint32_t *vset = reinterpret_cast<uint32_t *>(smem + lay.vset);
     uint32_t *ber = reinterpret_cast<uint32_t *>(smem + lay.ber);
     uint32_t *bg = reinterpret_cast<uint32_t *>(smem + lay.bg);
     uint32_t *bm = reinterpret_cast<uint32_t *>(smem + lay.bm);
     uint32_t *bnew = reinterpret_cast<uint32_t *>(smem + lay.bnew);
-    // table-update phase reuse of dead regions
-    uint32_t *kcell = smA;                                                   // erase cell / new token per event
-    uint32_t *lead = smB;                                                    // erase leader flag per event
-    uint64_t *mlist = reinterpret_cast<uint64_t *>(smem + lay.ptok);        // multi-cluster keys
-    uint64_t *msort = reinterpret_cast<uint64_t *>(smem + lay.smA);         // the same, sorted
+    // reuse of regions whose earlier contents are dead by then
+    uint32_t *pcell = smA;                                             // dedup: provisional cell per position
+    uint16_t *posSM = evslot;                                          // decide: SM index + 1 per first-hit position
+    uint32_t *undl = kst;                                              // decide: undecided SM indices
+    uint32_t *ecell = smA;                                             // table: erase cell (| leader bit) per event
+    uint32_t *ntokv = smB;                                             // table: new token per event
+    uint64_t *mlist = reinterpret_cast<uint64_t *>(smem + lay.ptok);  // multi-cluster keys
+    uint64_t *msort = reinterpret_cast<uint64_t *>(smem + lay.smA);   // the same, sorted
 
-    // ---- stage the state row and the topK row
+    // ---- stage the state row and the topK row; count live tokens and table entries
     STAMP(0);
-    wg_copy16(tok, gTok, static_cast<uint32_t>(padded) * 4u);
-    wg_copy16(ht, gHt, static_cast<uint32_t>(H) * 2u);
-    wg_copy16(vis, gVis, static_cast<uint32_t>(visStrideB));
-    for (int32_t k = tid; k < K; k += NT) ptok[k] = rt[k];
-    for (int32_t i = tid; i < 4 * (H >> 5); i += NT) ber[i] = 0u;  // ber, bg, bm, bnew are contiguous
-    if (tid == 0) {
-        ms.nTok = ms.nEnt = ms.bad = ms.ovf = ms.late = 0;
-        ms.M = ms.nSM = ms.T = ms.nConv = ms.N = ms.smDone = ms.uEnd = ms.nTakes = ms.nMulti = 0;
-    }
     int32_t hand0 = gHand[0];
     if (hand0 < 0 || hand0 >= dbs) hand0 = 0;  // hisp_sieve_update.cpp:108-111
     const bool flagged = gHand[1] == kCanonFlag;
-    __syncthreads();
+    {
+        const int32_t nt = padded >> 2, nh = H >> 3, nv = visStrideB >> 4;  // 16-byte chunks
+        const int32_t nAll = nt + nh + nv;
+        const uint4 *sT = reinterpret_cast<const uint4 *>(gTok);
+        const uint4 *sH = reinterpret_cast<const uint4 *>(gHt);
+        const uint4 *sV = reinterpret_cast<const uint4 *>(gVis);
+        uint32_t nTok = 0, nEnt = 0;
+        int32_t t0 = 0, t1 = 0;
+        const bool h0 = tid < K, h1 = tid + NT < K;
+        if (h0) t0 = rt[tid];
+        if (h1) t1 = rt[tid + NT];
+        for (int32_t c0 = tid; c0 < nAll; c0 += 4 * NT) {
+            uint4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int32_t c = c0 + j * NT;
+                if (c < nt) v[j] = sT[c];
+                else if (c < nt + nh) v[j] = sH[c - nt];
+                else if (c < nAll) v[j] = sV[c - nt - nh];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int32_t c = c0 + j * NT;
+                if (c < nt) {
+                    reinterpret_cast<uint4 *>(tok)[c] = v[j];
+                    const int32_t s0 = c * 4;
+                    nTok += (s0 < dbs && static_cast<int32_t>(v[j].x) >= 0) + (s0 + 1 < dbs && static_cast<int32_t>(v[j].y) >= 0) +
+                            (s0 + 2 < dbs && static_cast<int32_t>(v[j].z) >= 0) + (s0 + 3 < dbs && static_cast<int32_t>(v[j].w) >= 0);
+                } else if (c < nt + nh) {
+                    reinterpret_cast<uint4 *>(ht)[c - nt] = v[j];
+                    const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) nEnt += ((w4[q] & 0xFFFFu) != 0u) + ((w4[q] >> 16) != 0u);
+                } else if (c < nAll) {
+                    reinterpret_cast<uint4 *>(vis)[c - nt - nh] = v[j];
+                }
+            }
+        }
+        if (h0) ptok[tid] = t0;
+        if (h1) ptok[tid + NT] = t1;
+        for (int32_t k = tid + 2 * NT; k < K; k += NT) ptok[k] = rt[k];
+        const int32_t nz = (visStrideB >> 2) + 4 * (H >> 5);  // vset, ber, bg, bm, bnew are contiguous
+        for (int32_t i = tid; i < nz; i += NT) vset[i] = 0u;
+        for (int32_t k = tid; k < K; k += NT) evslot[k] = 0;  // SM index + 1 by first-hit position
+        nTok = wave_sum(nTok);
+        nEnt = wave_sum(nEnt);
+        if (tid == 0) {
+            ms.nTok = ms.nEnt = ms.bad = ms.ovf = ms.late = 0;
+            ms.M = ms.nSM = ms.T = ms.nConv = ms.N = ms.nUnd = ms.nRest = ms.uEnd = ms.nTakes = ms.nMulti = 0;
+        }
+        __syncthreads();
+        if (lane == 0) {
+            atomicAdd(&ms.nTok, static_cast<int32_t>(nTok));
+            atomicAdd(&ms.nEnt, static_cast<int32_t>(nEnt));
+        }
+    }
     STAMP(1);
 
     // ---- consistency: the table indexes exactly the non-negative tokens of
     // [0, dbs), each at its own slot.  A row this kernel wrote last carries
-    // the flag, and then only the counts are rechecked.
-    {
+    // the flag, and then only the counts are checked.
+    for (int32_t s = tid; s < dbs; s += NT) vt[s] = vis_get(vis, s) ? 0 : VT_NONE;
+    if (!flagged) {
         Guard g;
-        uint32_t nTok = 0, nEnt = 0, bad = 0;
+        bool bad = false;
         for (int32_t s = tid; s < dbs; s += NT) {
             const int32_t t = tok[s];
-            if (t < 0) continue;
-            ++nTok;
-            if (!flagged && ht_find(ht, tok, padded, t, mask, g) != s) bad = 1u;
+            if (t >= 0 && ht_find(ht, tok, padded, t, mask, g) != s) bad = true;
         }
-        for (int32_t c = tid; c < (H >> 1); c += NT) {
-            const uint32_t w = ht32[c];
-            nEnt += ((w & 0xFFFFu) != 0u) + ((w >> 16) != 0u);
-        }
-        nTok = wave_sum(nTok);
-        nEnt = wave_sum(nEnt);
-        const bool anyBad = __ballot(bad != 0u || g.code != 0) != 0ull;
-        if (lane == 0) {
-            atomicAdd(&ms.nTok, static_cast<int32_t>(nTok));
-            atomicAdd(&ms.nEnt, static_cast<int32_t>(nEnt));
-            if (anyBad) atomicOr(&ms.bad, 1);
-        }
-        for (int32_t s = tid; s < dbs; s += NT) vt[s] = vis_get(vis, s) ? 0 : VT_NONE;
+        if (__ballot(bad || g.code != 0) != 0ull && lane == 0) atomicOr(&ms.bad, 1);
     }
     __syncthreads();
     const bool canonical = ms.bad == 0 && ms.nTok == ms.nEnt;
@@ -344,7 +376,11 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     STAMP(2);
 
     if (fast) {
-        // ---- classify positions; first hit time per slot
+        // ---- classify every position and deduplicate the candidates in one
+        // probe: a hit stops at its entry (provisional entries only fill empty
+        // cells, never the probe path of a resident token); a miss stops at
+        // its token's provisional entry padded+1+k (smallest k wins) or claims
+        // the first empty cell with one
         {
             Guard g;
             for (int32_t k = tid; k < K; k += NT) {
@@ -355,12 +391,50 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 } else if (t >= prefill) {
                     inf = CLS_EXT << 30;
                 } else {
-                    const int32_t s0 = ht_find(ht, tok, padded, t, mask, g);
-                    if (s0 >= 0) {
-                        inf = (CLS_HIT << 30) | static_cast<uint32_t>(s0);
-                        lds_min16(vt32, static_cast<uint32_t>(s0), static_cast<uint16_t>(k + 1));
-                    } else {
-                        inf = CLS_CAND << 30;
+                    const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
+                    int32_t idx = static_cast<int32_t>(ht_hash(t)) & mask;
+                    inf = 0xFFFFFFFFu;
+                    for (int32_t n = 0; n <= mask; ++n) {
+                        uint32_t *w = ht32 + (idx >> 1);
+                        const uint32_t sh = (static_cast<uint32_t>(idx) & 1u) * 16u;
+                        uint32_t old = *reinterpret_cast<volatile uint32_t *>(w);
+                        bool next = false;
+                        for (;;) {
+                            const uint32_t cur = (old >> sh) & 0xFFFFu;
+                            if (cur == 0u) {
+                                const uint32_t prev = atomicCAS(w, old, old | (v << sh));
+                                if (prev == old) {
+                                    inf = CLS_CAND << 30;
+                                    pcell[k] = static_cast<uint32_t>(idx);
+                                    break;
+                                }
+                                old = prev;
+                            } else if (cur <= static_cast<uint32_t>(padded)) {
+                                if (tok[cur - 1u] == t) {
+                                    inf = (CLS_HIT << 30) | (cur - 1u);
+                                    lds_min16(vt32, cur - 1u, static_cast<uint16_t>(k + 1));
+                                } else {
+                                    next = true;
+                                }
+                                break;
+                            } else if (ptok[cur - static_cast<uint32_t>(padded) - 1u] == t) {
+                                pcell[k] = static_cast<uint32_t>(idx);
+                                inf = CLS_CAND << 30;
+                                if (v >= cur) break;
+                                const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
+                                if (prev == old) break;
+                                old = prev;
+                            } else {
+                                next = true;
+                                break;
+                            }
+                        }
+                        if (!next) break;
+                        idx = (idx + 1) & mask;
+                    }
+                    if (inf == 0xFFFFFFFFu) {
+                        g.code = kOverflowProbe;
+                        inf = CLS_INV << 30;
                     }
                 }
                 pinf[k] = inf;
@@ -369,67 +443,16 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         __syncthreads();
         STAMP(3);
-        // ---- dedup: provisional entries padded+1+k; the smallest position of a token wins its cell
+        // the first occurrence of each candidate token: its cell's final value
         for (int32_t k = tid; k < K; k += NT) {
             if ((pinf[k] >> 30) != CLS_CAND) continue;
-            const int32_t t = ptok[k];
-            const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
-            int32_t idx = static_cast<int32_t>(ht_hash(t)) & mask;
-            bool done = false;
-            for (int32_t n = 0; n <= mask && !done; ++n) {
-                uint32_t *w = ht32 + (idx >> 1);
-                const uint32_t sh = (static_cast<uint32_t>(idx) & 1u) * 16u;
-                uint32_t old = *reinterpret_cast<volatile uint32_t *>(w);
-                for (;;) {
-                    const uint32_t cur = (old >> sh) & 0xFFFFu;
-                    uint32_t nw;
-                    if (cur == 0u) {
-                        nw = old | (v << sh);
-                    } else if (cur > static_cast<uint32_t>(padded) && ptok[cur - padded - 1] == t) {
-                        if (v >= cur) {
-                            done = true;
-                            break;
-                        }
-                        nw = (old & ~(0xFFFFu << sh)) | (v << sh);
-                    } else {
-                        break;  // another key: next cell
-                    }
-                    const uint32_t prev = atomicCAS(w, old, nw);
-                    if (prev == old) {
-                        done = true;
-                        break;
-                    }
-                    old = prev;
-                }
-                idx = (idx + 1) & mask;
-            }
-            if (!done) atomicOr(&ms.ovf, 1);
+            const uint32_t e = ht[pcell[k]];
+            pinf[k] = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
         }
         __syncthreads();
-        // read back the first occurrence of each candidate token and its cell
-        for (int32_t k = tid; k < K; k += NT) {
-            if ((pinf[k] >> 30) != CLS_CAND) continue;
-            const int32_t t = ptok[k];
-            int32_t idx = static_cast<int32_t>(ht_hash(t)) & mask;
-            for (int32_t n = 0; n <= mask; ++n) {
-                const uint32_t e = ht[idx];
-                if (e > static_cast<uint32_t>(padded) && ptok[e - padded - 1] == t) {
-                    const uint32_t k1 = e - static_cast<uint32_t>(padded) - 1u;
-                    pinf[k] = (CLS_CAND << 30) | k1;
-                    if (k1 == static_cast<uint32_t>(k)) kcell[k] = static_cast<uint32_t>(idx);
-                    break;
-                }
-                idx = (idx + 1) & mask;
-            }
-        }
-        __syncthreads();
-        // drop the provisional entries (one per first occurrence): the table is the pre-step table again
-        for (int32_t k = tid; k < K; k += NT) {
-            const uint32_t inf = pinf[k];
-            if ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ht[kcell[k]] = 0;
-        }
         STAMP(4);
-        // ---- candidate prefix counts per position (contiguous chunk per lane)
+        // ---- candidate prefix counts per position (contiguous chunk per
+        // lane); first occurrences drop their provisional entries
         {
             const int32_t P = (K + NT - 1) / NT;
             const int32_t k0 = tid * P;
@@ -439,6 +462,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if (k < K) {
                     const uint32_t inf = pinf[k];
                     const uint32_t f = ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ? 1u : 0u;
+                    if (f) ht[pcell[k]] = 0;
                     fl |= f << i;
                     cnt += f;
                 }
@@ -457,8 +481,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 ms.M = static_cast<int32_t>(M);
             }
         }
-        __syncthreads();
-        STAMP(5);
         if (ms.ovf) fast = false;
     }
 
@@ -468,6 +490,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint64_t snM = 0, smM = 0;
     uint32_t preSN = 0, preSM = 0;
     if (fast) {
+        __syncthreads();  // candPre complete
+        STAMP(5);
         for (int32_t j = 0; j < Q; ++j) {
             const int32_t u = u0 + j;
             if (u >= dbs) break;
@@ -478,7 +502,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const uint32_t cSN = static_cast<uint32_t>(__popcll(snM)), cSM = static_cast<uint32_t>(__popcll(smM));
         const uint32_t qb = bits_for(static_cast<uint32_t>(Q));
         uint32_t tot;
-        const uint32_t pre = block_exscan(cSN | (cSM << 16), qb | (qb << 16), ms.wt0, tot);
+        const uint32_t pre = block_exscan(cSN | (cSM << 16), qb | (qb << 16), ms.wt1, tot);
         preSN = pre & 0xFFFFu;
         preSM = pre >> 16;
         uint32_t nsn = preSN, nsm = preSM;
@@ -489,8 +513,11 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 ++nsn;
             } else if ((smM >> j) & 1ull) {
                 const uint32_t k = static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)]) - 1u;
+                const uint32_t cc = candPre[k];
                 smA[nsm] = static_cast<uint32_t>(u) | (k << 16);
-                smB[nsm] = nsn | (static_cast<uint32_t>(candPre[k]) << 16);
+                smB[nsm] = nsn | (cc << 16);
+                smKp[nsm] = (cc > nsn) ? static_cast<uint16_t>(k) : static_cast<uint16_t>(0);
+                posSM[k] = static_cast<uint16_t>(nsm + 1u);
                 ++nsm;
             }
         }
@@ -498,95 +525,146 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         __syncthreads();
         STAMP(6);
 
-        // ---- decide the SM slots, one wave, 64 at a time.  need = the event
-        // index being served when the hand arrives; cnt = events before k.
-        if (wave == 0) {
-            const int32_t nSM = ms.nSM;
-            int32_t T = 0, nConv = 0, Mtot = ms.M, done = 0;
-            bool ended = false;
-            for (int32_t b0 = 0; b0 < nSM && !ended; b0 += 64) {
-                const int32_t i = b0 + static_cast<int32_t>(lane);
-                const bool inb = i < nSM;
-                const uint32_t ea = inb ? smA[i] : 0u;
-                const uint32_t eb = inb ? smB[i] : 0u;
-                const uint32_t k = ea >> 16;
-                int32_t need = static_cast<int32_t>(eb & 0xFFFFu) + T;
-                int32_t cnt = static_cast<int32_t>(eb >> 16);
-                for (int32_t j = 0; j < nConv; ++j) cnt += (static_cast<uint32_t>(cvlist[j]) < k) ? 1 : 0;
-                uint64_t active = __ballot(inb);
-                uint64_t takenM = 0;
-                const int32_t T0 = T;
-                for (;;) {
-                    const uint64_t tk = __ballot(cnt > need) & active;
-                    const uint64_t ur = __ballot(need >= Mtot) & active;
-                    const uint64_t any = tk | ur;
-                    if (any == 0ull) break;
-                    const int f = __builtin_ctzll(any);
-                    if ((ur >> f) & 1ull) {  // the events run out before this slot: the walk ends
-                        ended = true;
-                        break;
+        // ---- decide the SM slots.  In ring order, slot i (k_i, need0_i = SN
+        // slots before it, cc_i = candidates before k_i) is evicted iff the
+        // events before k_i outnumber the event being served on arrival:
+        //   cc_i + #{evicted j < i: k_j < k_i} > need0_i + #{evicted j < i},
+        // i.e. a_i = cc_i - need0_i - 1 >= D_i = #{evicted j < i: k_j > k_i}.
+        // a_i < 0: passed.  a_i >= U_i = #{j < i: a_j >= 0, k_j > k_i} (a
+        // bound on D_i): evicted.  The rest (rare) are settled in ring order
+        // by one wave.  A slot with need0_i >= M lies past the walk's end.
+        {
+            const int32_t nSM = ms.nSM, M = ms.M;
+            for (int32_t i = tid; i < nSM; i += NT) {
+                const uint32_t eb = smB[i];
+                const int32_t need0 = static_cast<int32_t>(eb & 0xFFFFu);
+                const int32_t ai = static_cast<int32_t>(eb >> 16) - need0 - 1;
+                uint16_t dec = 0;  // 0 passed, 1 evicted, 2 undecided
+                if (need0 < M && ai >= 0) {
+                    const uint32_t ki = smA[i] >> 16;
+                    int32_t U = 0;
+                    int32_t j = 0;
+                    for (; j + 8 <= i; j += 8) {
+                        uint32_t kk[8];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) kk[q] = smKp[j + q];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) U += (kk[q] > ki) ? 1 : 0;
                     }
-                    takenM |= 1ull << f;
-                    const uint32_t t = readlane(k, f);
-                    const uint32_t uf = readlane(ea & 0xFFFFu, f);
-                    if (lane == 0) {
-                        evold[t] = static_cast<uint16_t>(ring_slot(hand0, static_cast<int32_t>(uf), dbs));
-                        cvlist[nConv] = static_cast<uint16_t>(t);
-                    }
-                    ++T;
-                    ++nConv;
-                    ++Mtot;
-                    active &= (f == 63) ? 0ull : (~0ull << (f + 1));
-                    if (static_cast<int>(lane) > f) {
-                        need += 1;
-                        cnt += (k > t) ? 1 : 0;
-                    }
+                    for (; j < i; ++j) U += (static_cast<uint32_t>(smKp[j]) > ki) ? 1 : 0;
+                    dec = (ai >= U) ? 1 : 2;
+                    if (dec == 2) undl[atomicAdd(&ms.nUnd, 1)] = static_cast<uint32_t>(i);
                 }
-                if (inb) {
-                    tb[i] = static_cast<uint16_t>((T0 + static_cast<int32_t>(lanes_below(takenM, lane))) |
-                                                  (((takenM >> lane) & 1ull) ? 0x8000 : 0));
-                }
-                done = (b0 + 64 < nSM) ? b0 + 64 : nSM;
-            }
-            if (lane == 0) {
-                ms.T = T;
-                ms.nConv = nConv;
-                ms.N = Mtot;
-                ms.smDone = nSM < done ? nSM : done;
+                tb[i] = dec;
             }
         }
         __syncthreads();
         STAMP(7);
+        // undecided slots, one wave each: count the evictions already settled
+        // before them (L) and the undecided ones before them with a larger k
+        // (X); with X == 0, D = L exactly.  A concurrent settle of j < i reads
+        // either as undecided (counted in X) or settled (counted exactly):
+        // both are safe.
         {
-            const int32_t nSM = ms.nSM, T = ms.T, nConv = ms.nConv;
-            for (int32_t i = ms.smDone + tid; i <= nSM; i += NT) tb[i] = static_cast<uint16_t>(T);
-            for (int32_t j = tid; j < nConv; j += NT) pinf[cvlist[j]] |= INF_CONV;
+            const int32_t nUnd = ms.nUnd;
+            for (int32_t e = wave; e < nUnd; e += NWAVES) {
+                const int32_t i = static_cast<int32_t>(undl[e]);
+                const uint32_t ki = smA[i] >> 16;
+                uint32_t lx = 0;
+                for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
+                    const uint16_t dj = tb[j];
+                    if (dj != 0 && (smA[j] >> 16) > ki) lx += (dj == 1) ? 1u : 0x10000u;
+                }
+                lx = wave_sum(lx);
+                if (lane == 0) {
+                    if ((lx >> 16) == 0u) {
+                        const uint32_t eb = smB[i];
+                        const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
+                        tb[i] = (ai >= static_cast<int32_t>(lx & 0xFFFFu)) ? 1 : 0;
+                    } else {
+                        atomicAdd(&ms.nRest, 1);
+                    }
+                }
+            }
         }
         __syncthreads();
-        // ---- the event sequence: candidates' first occurrences and conversions in position order
+        if (ms.nRest > 0 && wave == 0) {  // the rest, in ring order
+            const int32_t nSM = ms.nSM;
+            for (int32_t c = 0; c < nSM; c += 64) {
+                uint64_t und = __ballot(c + static_cast<int32_t>(lane) < nSM && tb[c + lane] == 2);
+                while (und != 0ull) {
+                    const int f = __builtin_ctzll(und);
+                    und &= und - 1ull;
+                    const int32_t i = c + f;
+                    const uint32_t ki = smA[i] >> 16;
+                    const uint32_t eb = smB[i];
+                    const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
+                    uint32_t d = 0;
+                    for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
+                        d += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
+                    }
+                    d = wave_sum(d);
+                    if (lane == 0) tb[i] = (ai >= static_cast<int32_t>(d)) ? 1 : 0;
+                }
+            }
+        }
+        __syncthreads();
+        // ---- one scan for both the eviction prefix over the SM list and the
+        // event sequence over positions (candidates' first occurrences and
+        // conversions -- first hits of evicted SM slots -- in position order)
         {
-            const int32_t P = (K + NT - 1) / NT;
-            const int32_t k0 = tid * P;
-            uint32_t cnt = 0, fl = 0;
-            for (int32_t i = 0; i < P; ++i) {
-                const int32_t k = k0 + i;
+            const int32_t nSM = ms.nSM;
+            const int32_t Ps = (nSM + NT - 1) / NT, i0 = tid * Ps;
+            const int32_t Pk = (K + NT - 1) / NT, k0 = tid * Pk;
+            uint32_t cs = 0, fs = 0, ce = 0, fe = 0;
+            for (int32_t q = 0; q < Ps; ++q) {
+                const int32_t i = i0 + q;
+                if (i < nSM && tb[i] == 1) {
+                    fs |= 1u << q;
+                    ++cs;
+                    const uint32_t ea = smA[i];
+                    evold[ea >> 16] = static_cast<uint16_t>(ring_slot(hand0, static_cast<int32_t>(ea & 0xFFFFu), dbs));
+                }
+            }
+            for (int32_t q = 0; q < Pk; ++q) {
+                const int32_t k = k0 + q;
                 if (k < K) {
                     const uint32_t inf = pinf[k];
                     const uint32_t c = inf >> 30;
-                    const uint32_t f = ((c == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ||
-                                        (c == CLS_HIT && (inf & INF_CONV)))
-                                           ? 1u
-                                           : 0u;
-                    fl |= f << i;
-                    cnt += f;
+                    bool f = c == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k);
+                    if (c == CLS_HIT) {
+                        const uint32_t sm = posSM[k];
+                        f = sm != 0u && tb[sm - 1u] == 1;
+                    }
+                    if (f) {
+                        fe |= 1u << q;
+                        ++ce;
+                    }
                 }
             }
+            const uint32_t bs = bits_for(static_cast<uint32_t>(Ps)), be = bits_for(static_cast<uint32_t>(Pk));
             uint32_t tot;
-            uint32_t pre = block_exscan(cnt, bits_for(static_cast<uint32_t>(P)), ms.wt0, tot);
-            for (int32_t i = 0; i < P; ++i) {
-                if ((fl >> i) & 1u) eseq[pre++] = static_cast<uint16_t>(k0 + i);
+            const uint32_t pre = block_exscan(cs | (ce << 16), bs | (be << 16), ms.wt0, tot);
+            uint32_t ps = pre & 0xFFFFu, pe = pre >> 16;
+            for (int32_t q = 0; q < Ps; ++q) {
+                const int32_t i = i0 + q;
+                if (i < nSM) {
+                    const uint32_t tk = (fs >> q) & 1u;
+                    tb[i] = static_cast<uint16_t>(ps | (tk << 15));
+                    ps += tk;
+                }
             }
-            if (tid == 0 && static_cast<int32_t>(tot) != ms.N) ms.ovf = 1;
+            for (int32_t q = 0; q < Pk; ++q) {
+                if ((fe >> q) & 1u) eseq[pe++] = static_cast<uint16_t>(k0 + q);
+            }
+            const int32_t T = static_cast<int32_t>(tot & 0xFFFFu);
+            if (tid == 0) {
+                tb[nSM] = static_cast<uint16_t>(T);
+                ms.T = T;
+                ms.nConv = T;
+                ms.N = ms.M + T;
+                if (static_cast<int32_t>(tot >> 16) != ms.M + T) ms.ovf = 1;
+            }
         }
         __syncthreads();
         STAMP(8);
@@ -626,7 +704,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
     if (fast) {
         const int32_t N = ms.N, uEnd = ms.uEnd;
-        // ---- outputs and visited bits
+        Guard g;
+        // ---- outputs; visited bits set this step (into vset); the cell of
+        // each evicted token and each event's new token (conversions
+        // re-insert a pre-step token)
         for (int32_t k = tid; k < K; k += NT) {
             const uint32_t inf = pinf[k];
             const uint32_t cls = inf >> 30;
@@ -643,6 +724,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     miss = (static_cast<uint32_t>(k) == c) ? 1 : 0;
                 } else {
                     slot = static_cast<int32_t>(s0);
+                    if (!(v & VT_PASSED) || static_cast<uint32_t>(k) > (v & VT_NOCONV)) {
+                        atomicOr(vset + (s0 >> 5), 1u << (s0 & 31u));
+                    }
                 }
             } else if (cls == CLS_CAND) {
                 const uint32_t k1 = inf & 0xFFFFu;
@@ -652,31 +736,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             rs[k] = slot;
             rm[k] = miss;
         }
-        for (int32_t u = tid; u < uEnd; u += NT) {
-            const int32_t s = ring_slot(hand0, u, dbs);
-            atomicAnd(vis32 + (s >> 5), ~(1u << (s & 31)));
-        }
-        __syncthreads();
         for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t s = evslot[eseq[i]];
-            atomicOr(vis32 + (s >> 5), 1u << (s & 31u));
-        }
-        for (int32_t k = tid; k < K; k += NT) {
-            const uint32_t inf = pinf[k];
-            if ((inf >> 30) != CLS_HIT) continue;
-            const uint32_t s0 = inf & 0xFFFFu;
-            const uint16_t v = vt[s0];
-            if (v & VT_EVICTED) continue;
-            if ((v & VT_PASSED) && static_cast<uint32_t>(k) <= (v & VT_NOCONV)) continue;
-            atomicOr(vis32 + (s0 >> 5), 1u << (s0 & 31u));
-        }
-        __syncthreads();
-        STAMP(10);
-
-        // ---- table: erase the evicted tokens (pre-step tokens give the homes)
-        Guard g;
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t s = evslot[eseq[i]];
+            const uint32_t p = eseq[i];
+            const uint32_t s = evslot[p];
+            atomicOr(vset + (s >> 5), 1u << (s & 31u));
             const int32_t old = tok[s];
             uint32_t cell = 0xFFFFFFFFu;
             if (old >= 0) {
@@ -691,28 +754,31 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if (cell == 0xFFFFFFFFu) g.code = kOverflowProbe;
                 else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
             }
-            kcell[i] = cell;
+            ecell[i] = cell;
+            ntokv[i] = static_cast<uint32_t>((pinf[p] >> 30) == CLS_CAND ? ptok[p] : tok[evold[p]]);
         }
         __syncthreads();
-        for (int32_t i = tid; i < N; i += NT) {  // leader: rightmost marked cell of its cluster
-            const uint32_t c = kcell[i];
-            uint32_t ld = 0;
-            if (c != 0xFFFFFFFFu) {
-                ld = 1;
-                int32_t x = (static_cast<int32_t>(c) + 1) & mask;
-                for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
-                    if (bit_get(ber, x)) {
-                        ld = 0;
-                        break;
-                    }
+        STAMP(10);
+        // ---- table: erase the evicted tokens; the rightmost marked cell of a
+        // cluster leads it and deletes right to left
+        for (int32_t i = tid; i < N; i += NT) {
+            const uint32_t c = ecell[i];
+            if (c == 0xFFFFFFFFu) continue;
+            bool ld = true;
+            int32_t x = (static_cast<int32_t>(c) + 1) & mask;
+            for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
+                if (bit_get(ber, x)) {
+                    ld = false;
+                    break;
                 }
             }
-            lead[i] = ld;
+            if (ld) ecell[i] = c | 0x80000000u;
         }
         __syncthreads();
         for (int32_t i = tid; i < N; i += NT) {
-            if (!lead[i]) continue;
-            const int32_t c = static_cast<int32_t>(kcell[i]);
+            const uint32_t e = ecell[i];
+            if (e == 0xFFFFFFFFu || !(e & 0x80000000u)) continue;
+            const int32_t c = static_cast<int32_t>(e & 0x7FFFFFFFu);
             rdel_at(ht, tok, padded, c, mask, g);
             int32_t x = (c - 1) & mask;
             for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x - 1) & mask) {
@@ -721,21 +787,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         __syncthreads();
         STAMP(11);
-        // ---- token update: read every new token first (conversions re-insert a pre-step token)
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t p = eseq[i];
-            kcell[i] = static_cast<uint32_t>((pinf[p] >> 30) == CLS_CAND ? ptok[p] : tok[evold[p]]);
-        }
-        __syncthreads();
+        // ---- new tokens; tentative placement (the final occupied cells do not depend on order)
         for (int32_t i = tid; i < N; i += NT) {
             const uint32_t s = evslot[eseq[i]];
-            tok[s] = static_cast<int32_t>(kcell[i]);
-        }
-        __syncthreads();
-        // ---- inserts: tentative placement (the final occupied cells do not depend on order)
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t s = evslot[eseq[i]];
-            const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(tok[s])) & mask, mask,
+            const int32_t t = static_cast<int32_t>(ntokv[i]);
+            tok[s] = t;
+            const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(t)) & mask, mask,
                                           static_cast<uint16_t>(s + 1u));
             if (c < 0) g.code = kOverflowProbe;
             else atomicOr(bnew + (c >> 5), 1u << (c & 31));
@@ -743,56 +800,68 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         __syncthreads();
         // final cluster of each new key (its start); clusters with two or more new keys are redone
         for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t s = evslot[eseq[i]];
-            int32_t st = static_cast<int32_t>(ht_hash(tok[s])) & mask;
+            int32_t st = static_cast<int32_t>(ht_hash(static_cast<int32_t>(ntokv[i]))) & mask;
             for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
+            kst[i] = static_cast<uint32_t>(st);
             const uint32_t bit = 1u << (st & 31);
             const uint32_t old = atomicOr(bg + (st >> 5), bit);
             if (old & bit) atomicOr(bm + (st >> 5), bit);
         }
         __syncthreads();
         for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t p = eseq[i];
-            const uint32_t s = evslot[p];
-            int32_t st = static_cast<int32_t>(ht_hash(tok[s])) & mask;
-            for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
-            if (bit_get(bm, static_cast<uint32_t>(st))) {
+            const uint32_t st = kst[i];
+            if (bit_get(bm, st)) {
+                const uint32_t p = eseq[i];
                 const int32_t q = atomicAdd(&ms.nMulti, 1);
-                mlist[q] = (static_cast<uint64_t>(st) << 32) | (static_cast<uint64_t>(p) << 16) | s;
+                mlist[q] = (static_cast<uint64_t>(st) << 32) | (static_cast<uint64_t>(p) << 16) | evslot[p];
             }
         }
         __syncthreads();
         STAMP(12);
         const int32_t nMulti = ms.nMulti;
-        for (int32_t q = tid; q < nMulti; q += NT) {  // sort by (cluster start, event time)
-            const uint64_t key = mlist[q];
-            int32_t r = 0;
-            for (int32_t j = 0; j < nMulti; ++j) r += (mlist[j] < key) ? 1 : 0;
-            msort[r] = key;
-        }
-        __syncthreads();
-        for (int32_t q = tid; q < nMulti; q += NT) {  // the first key of each cluster redoes it in time order
-            const uint64_t key = msort[q];
-            const uint32_t st = static_cast<uint32_t>(key >> 32);
-            if (q > 0 && static_cast<uint32_t>(msort[q - 1] >> 32) == st) continue;
-            int32_t end = static_cast<int32_t>(st);
-            for (int32_t n = 0; n < H && ht[end] != 0; ++n) end = (end + 1) & mask;
-            for (int32_t x = static_cast<int32_t>(st); x != end; x = (x + 1) & mask) {
-                if (bit_get(bnew, static_cast<uint32_t>(x))) ht[x] = 0;
+        if (nMulti > 0) {
+            for (int32_t q = tid; q < nMulti; q += NT) {  // sort by (cluster start, event time)
+                const uint64_t key = mlist[q];
+                int32_t r = 0;
+                for (int32_t j = 0; j < nMulti; ++j) r += (mlist[j] < key) ? 1 : 0;
+                msort[r] = key;
             }
-            for (int32_t r = q; r < nMulti && static_cast<uint32_t>(msort[r] >> 32) == st; ++r) {
-                const uint32_t s = static_cast<uint32_t>(msort[r] & 0xFFFFu);
-                int32_t idx = static_cast<int32_t>(ht_hash(tok[s])) & mask;
-                for (int32_t n = 0; n < H && ht[idx] != 0; ++n) idx = (idx + 1) & mask;
-                ht[idx] = static_cast<uint16_t>(s + 1u);
+            __syncthreads();
+            for (int32_t q = tid; q < nMulti; q += NT) {  // the first key of each cluster redoes it in time order
+                const uint64_t key = msort[q];
+                const uint32_t st = static_cast<uint32_t>(key >> 32);
+                if (q > 0 && static_cast<uint32_t>(msort[q - 1] >> 32) == st) continue;
+                int32_t end = static_cast<int32_t>(st);
+                for (int32_t n = 0; n < H && ht[end] != 0; ++n) end = (end + 1) & mask;
+                for (int32_t x = static_cast<int32_t>(st); x != end; x = (x + 1) & mask) {
+                    if (bit_get(bnew, static_cast<uint32_t>(x))) ht[x] = 0;
+                }
+                for (int32_t r = q; r < nMulti && static_cast<uint32_t>(msort[r] >> 32) == st; ++r) {
+                    const uint32_t s = static_cast<uint32_t>(msort[r] & 0xFFFFu);
+                    int32_t idx = static_cast<int32_t>(ht_hash(tok[s])) & mask;
+                    for (int32_t n = 0; n < H && ht[idx] != 0; ++n) idx = (idx + 1) & mask;
+                    ht[idx] = static_cast<uint16_t>(s + 1u);
+                }
             }
         }
         if (g.code) atomicOr(&ms.late, 1);
         __syncthreads();
         STAMP(13);
         if (!ms.late) {
-            // ---- write back
-            wg_copy16(gVis, vis, static_cast<uint32_t>(visStrideB));
+            // ---- write back; visited = (staged bits minus the ring range the
+            // hand passed) | bits set this step
+            const int32_t e0 = hand0 + uEnd;  // passed slots: [hand0, e0) then [0, e0 - dbs)
+            for (int32_t w = tid; w < (visStrideB >> 2); w += NT) {
+                const int32_t lo = w * 32;
+                uint32_t clr = 0;
+                if (uEnd > 0) {
+                    const int32_t a0 = max(lo, hand0), a1 = min(lo + 32, min(e0, dbs));
+                    if (a1 > a0) clr |= (a1 - a0 == 32 ? 0xFFFFFFFFu : ((1u << (a1 - a0)) - 1u)) << (a0 - lo);
+                    const int32_t b1 = min(lo + 32, e0 - dbs);
+                    if (b1 > lo) clr |= (b1 - lo == 32 ? 0xFFFFFFFFu : ((1u << (b1 - lo)) - 1u));
+                }
+                reinterpret_cast<uint32_t *>(gVis)[w] = (vis32[w] & ~clr) | vset[w];
+            }
             if (N > 0) {
                 wg_copy16(gTok, tok, static_cast<uint32_t>(padded) * 4u);
                 wg_copy16(gHt, ht, static_cast<uint32_t>(H) * 2u);
