@@ -35,6 +35,8 @@ struct State {
     size_t ldsLimit = 0;            // dynamic LDS per workgroup usable by SIEVE
     std::vector<Alloc> status;      // kvx_alloc_status allocations
     kvx::RowScratch scratch{};
+    int32_t *shadow = nullptr;      // wave-wide SIEVE variant: table shadow
+    uint64_t shadowCells = 0;
     uint32_t epoch = 0;
     int lastSieveVariant = -1;
     int forcedSieveVariant = -1;
@@ -118,6 +120,24 @@ void EnsureWinScratch(uint64_t entries)
     g.scratch.win = static_cast<unsigned long long *>(p);
     g.scratch.winEntries = cap;
     g.epoch = 0;
+}
+
+// Grow-only shadow table (one int32 per hash-table cell per batch row) of the
+// wave-wide HBM SIEVE variant.
+int32_t *EnsureShadow(uint64_t cells)
+{
+    if (g.shadowCells >= cells) return g.shadow;
+    if (g.shadow != nullptr) {
+        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        hipCheck(hipFree(g.shadow), "hipFree");
+        g.shadow = nullptr;
+        g.shadowCells = 0;
+    }
+    void *p = nullptr;
+    hipCheck(hipMalloc(&p, cells * sizeof(int32_t)), "hipMalloc(sieve shadow)");
+    g.shadow = static_cast<int32_t *>(p);
+    g.shadowCells = cells;
+    return g.shadow;
 }
 
 // Grow-only gather row list (source and destination addresses per row).
@@ -488,22 +508,28 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         a.reqsPerCore = static_cast<uint32_t>(rpc);
         a.htSize = static_cast<uint32_t>(htSize);
         a.poolSize = pool_size;
-        // Variant: 2 = parallel LDS kernel, 0 = sequential LDS kernel, 1 = sequential HBM-resident.
+        // Variant: 2 = parallel LDS kernel, 0 = sequential LDS kernel, 3 = sequential
+        // HBM-resident with wave-wide probes (1 = the single-lane HBM kernel, by request only).
         const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
                            visited_stride_b;
         const size_t ldsFast = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
                                                 visited_stride_b).total;
         const bool fastOk = ldsFast <= g.ldsLimit && top_k < 0x3FFF &&
                             static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535;
-        int variant = fastOk ? 2 : (lds <= g.ldsLimit ? 0 : 1);
+        int variant = fastOk ? 2 : (lds <= g.ldsLimit ? 0 : 3);
         if (g.forcedSieveVariant == 0 && lds <= g.ldsLimit) variant = 0;
         if (g.forcedSieveVariant == 1) variant = 1;
         if (g.forcedSieveVariant == 2 && fastOk) variant = 2;
+        if (g.forcedSieveVariant == 3) variant = 3;
         a.reserved = static_cast<uint32_t>(variant);
         g.lastSieveVariant = variant;
         if (max_num_reqs == 0) return;
         if (variant == 2) {
             hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow), ldsFast, AsStream(stream)),
+                     "hisp_sieve_update launch");
+        } else if (variant == 3) {
+            int32_t *shadow = EnsureShadow(static_cast<uint64_t>(max_num_reqs) * static_cast<uint64_t>(htSize));
+            hipCheck(kvx::launch_sieve_update_wave(a, reinterpret_cast<uint64_t>(g.overflow), shadow, AsStream(stream)),
                      "hisp_sieve_update launch");
         } else {
             hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), variant,
@@ -553,6 +579,9 @@ int kvx_close(void)
         g.overflow = nullptr;
         if (g.scratch.win != nullptr) (void)hipFree(g.scratch.win);
         if (g.scratch.listSrc != nullptr) (void)hipFree(g.scratch.listSrc);
+        if (g.shadow != nullptr) (void)hipFree(g.shadow);
+        g.shadow = nullptr;
+        g.shadowCells = 0;
         if (g.scratch.counters != nullptr) (void)hipFree(g.scratch.counters);
         g.scratch = kvx::RowScratch{};
         {
@@ -619,7 +648,7 @@ int kvx_last_sieve_variant(void) { return g.lastSieveVariant; }
 int kvx_sieve_force_variant(int variant)
 {
     return Guarded([&] {
-        if (variant < -1 || variant > 2) throw Error("sieve_force_variant: variant must be -1, 0, 1 or 2");
+        if (variant < -1 || variant > 3) throw Error("sieve_force_variant: variant must be -1, 0, 1, 2 or 3");
         g.forcedSieveVariant = variant;
     });
 }

@@ -103,6 +103,8 @@ hipError_t launch_sieve_ht_init(const HispSieveHtInitArgs &a, uint64_t overflowS
                                 hipStream_t stream);
 hipError_t sieve_set_lds_limit(size_t bytes);
 hipError_t sieve_fast_set_lds_limit(size_t bytes);
+hipError_t launch_sieve_update_wave(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,
+                                    hipStream_t stream);
 hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes,
                                     hipStream_t stream);
 

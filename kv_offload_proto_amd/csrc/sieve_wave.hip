@@ -1,0 +1,255 @@
+// SIEVE update for rows whose state does not fit LDS (variant 3).
+//
+// One workgroup per batch row, state in HBM, updated in place.  The positions
+// are processed in order -- the exact recurrence of hisp_sieve_update.cpp:
+// 115-163 -- but every inner loop runs 64 cells or slots at a time on one
+// wave: a probe reads 64 consecutive table cells and picks the first empty or
+// matching one with a ballot, the hand sweep tests 64 visited bits at once,
+// and Algorithm R's backward shift walks the cluster 64 cells per step,
+// taking the moves in order with ballots.  Probes compare tokens through a
+// per-launch shadow of the table (cell -> token of its entry, built by the
+// whole workgroup first), so one probe step is two coalesced row reads
+// instead of a chain of dependent slot lookups.  Long probe runs (adversarial
+// keys that share home buckets) therefore cost runs/64 memory round trips.
+#include "kvx_internal.h"
+#include "sieve_common.h"
+
+namespace kvx {
+namespace {
+
+using namespace sieve;
+
+constexpr int WT = 256;  // all threads build the shadow; wave 0 runs the recurrence
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+struct Row {
+    uint16_t *ht;
+    int32_t *ct;  // shadow: token of the entry in each cell, -1 for empty
+    int32_t *tok;
+    uint32_t *vis32;
+    int32_t mask, dbs, padded;
+};
+
+__device__ __forceinline__ void wave_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup"); }
+
+// State reads see the L2 copy (agent-scope loads skip the CU's L1), so a
+// value another lane stored or an atomic changed a moment ago is never stale.
+__device__ __forceinline__ uint16_t ld16(const uint16_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld32(const int32_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ldu32(const uint32_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// First cell at or after idx (cyclic) that is empty or holds `token`
+// (hisp_kernel_common.h:29-61); -1 after the whole table.  *entry receives
+// the cell's entry.
+__device__ int32_t probe(const Row &r, int32_t idx, int32_t token, bool &found, uint32_t &entry, Guard &g)
+{
+    const uint32_t lane = lane_id();
+    for (int32_t base = 0; base <= r.mask; base += 64) {
+        const int32_t c = (idx + base + static_cast<int32_t>(lane)) & r.mask;
+        const uint16_t e = ld16(r.ht + c);
+        const int32_t t = ld32(r.ct + c);
+        const uint64_t hit = __ballot(e != 0 && t == token);
+        const uint64_t any = hit | __ballot(e == 0);
+        if (any != 0ull) {
+            const int f = __builtin_ctzll(any);
+            found = (hit >> f) & 1ull;
+            entry = static_cast<uint32_t>(__shfl(static_cast<int>(e), f));
+            return (idx + base + f) & r.mask;
+        }
+    }
+    g.code = kOverflowProbe;
+    found = false;
+    return -1;
+}
+
+// Algorithm R from the hole at cell j (hisp_kernel_common.h:64-94): an entry
+// at i moves into j unless its home lies cyclically in (j, i].
+__device__ void shift_from(const Row &r, int32_t j, Guard &g)
+{
+    const uint32_t lane = lane_id();
+    const int32_t start = j;
+    for (int32_t base = 1; base <= r.mask; base += 64) {
+        const int32_t i = (start + base + static_cast<int32_t>(lane)) & r.mask;
+        const uint16_t e = ld16(r.ht + i);
+        const int32_t t = ld32(r.ct + i);
+        const int32_t home = (e != 0) ? static_cast<int32_t>(ht_hash(t)) & r.mask : 0;
+        uint64_t active = ~0ull;
+        for (;;) {
+            const bool mv = (j < i) ? (home <= j || home > i) : (home <= j && home > i);
+            const uint64_t m = __ballot(e == 0 || mv) & active;
+            if (m == 0ull) break;
+            const int f = __builtin_ctzll(m);
+            const bool stop = __shfl(static_cast<int>(e), f) == 0;
+            if (stop) {
+                if (lane == 0) {
+                    r.ht[j] = 0;
+                    r.ct[j] = -1;
+                }
+                wave_fence();
+                return;
+            }
+            if (static_cast<int>(lane) == f) {
+                r.ht[j] = e;
+                r.ct[j] = t;
+            }
+            wave_fence();
+            j = __shfl(i, f);
+            active = (f == 63) ? 0ull : (~0ull << (f + 1));
+        }
+    }
+    g.code = kOverflowProbe;
+}
+
+__global__ __launch_bounds__(WT) void kvx_sieve_update_wave(KvxLaunch<HispSieveUpdateArgs> L, int32_t *shadow)
+{
+    const HispSieveUpdateArgs &a = L.a;
+    const int32_t K = static_cast<int32_t>(a.topK);
+    const int32_t dbs = static_cast<int32_t>(a.deviceBufferSize);
+    const int32_t padded = static_cast<int32_t>(a.paddedBufferSize);
+    const int32_t visStrideB = static_cast<int32_t>(a.visitedStrideB);
+    const int32_t maxNumReqs = static_cast<int32_t>(a.maxNumReqs);
+    const int32_t H = static_cast<int32_t>(a.htSize);
+    const int32_t poolSize = static_cast<int32_t>(a.poolSize);
+    const int32_t bid = blockIdx.x;
+    if (bid >= maxNumReqs) return;
+
+    int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
+    if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
+    int32_t *rs = reinterpret_cast<int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
+    int8_t *rm = reinterpret_cast<int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
+    if (bid >= numReal) {
+        write_dummy_row(rs, rm, K);
+        return;
+    }
+    const int64_t reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
+    if (reqIdx < 0 || reqIdx >= poolSize) {
+        write_dummy_row(rs, rm, K);
+        return;
+    }
+    const int32_t seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
+    const int32_t prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
+    const int32_t *rt = reinterpret_cast<const int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    Row r;
+    r.tok = reinterpret_cast<int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
+    r.vis32 = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(a.deviceBufferVisited) + reqIdx * visStrideB);
+    r.ht = reinterpret_cast<uint16_t *>(a.deviceBufferHt) + reqIdx * H;
+    r.ct = shadow + static_cast<int64_t>(bid) * H;
+    r.mask = H - 1;
+    r.dbs = dbs;
+    r.padded = padded;
+    int32_t *gHand = reinterpret_cast<int32_t *>(a.sieveHand) + reqIdx * kHandStride;
+
+    // shadow of the table: token of each cell's entry
+    for (int32_t c = threadIdx.x; c < H; c += WT) {
+        const uint16_t e = r.ht[c];
+        r.ct[c] = (e != 0) ? tok_at(r.tok, e, padded) : -1;
+    }
+    __threadfence_block();
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+
+    const uint32_t lane = lane_id();
+    int32_t hand = gHand[0];
+    if (hand < 0 || hand >= dbs) hand = 0;  // hisp_sieve_update.cpp:108-111
+    const int32_t width = dbs < 64 ? dbs : 64;  // slots per sweep step (no slot twice in one step)
+    Guard g;
+    for (int32_t k0 = 0; k0 < K; k0 += 64) {
+        const int32_t myT = (k0 + static_cast<int32_t>(lane) < K) ? rt[k0 + lane] : 0;
+        int32_t mySlot = -1;
+        int32_t myMiss = 0;
+        const int32_t kn = (K - k0 < 64) ? K - k0 : 64;
+        for (int32_t kk = 0; kk < kn; ++kk) {
+            const int32_t tp = __shfl(myT, kk);
+            int32_t slot = -1;
+            int32_t miss = 0;
+            if (g.code != 0 || tp < 0 || tp >= seqLen) {  // past a bound violation the row reads as invalid
+            } else if (tp >= prefill) {
+                slot = padded + (tp - prefill);
+            } else {
+                const int32_t home = static_cast<int32_t>(ht_hash(tp)) & r.mask;
+                bool found = false;
+                uint32_t e = 0;
+                const int32_t cell = probe(r, home, tp, found, e, g);
+                if (cell < 0) {
+                } else if (found) {
+                    slot = static_cast<int32_t>(e) - 1;
+                    if (lane == 0) atomicOr(r.vis32 + (slot >> 5), 1u << (slot & 31));
+                    wave_fence();
+                } else {
+                    // the hand passes visited slots, clearing them, and stops at the first unvisited one
+                    int32_t h = -1;
+                    for (int32_t base = 0; base <= 2 * dbs && h < 0; base += width) {
+                        const bool on = static_cast<int32_t>(lane) < width;
+                        const int32_t s = (hand + base + static_cast<int32_t>(lane)) % dbs;
+                        const bool v = on && ((ldu32(r.vis32 + (s >> 5)) >> (s & 31)) & 1u);
+                        const uint64_t unv = __ballot(on && !v);
+                        const int f = unv ? __builtin_ctzll(unv) : 64;
+                        if (static_cast<int>(lane) < f && v) atomicAnd(r.vis32 + (s >> 5), ~(1u << (s & 31)));
+                        wave_fence();
+                        if (f < 64) h = __shfl(s, f);
+                    }
+                    if (h < 0) {
+                        g.code = kOverflowSweep;
+                    } else {
+                        const int32_t old = ld32(r.tok + h);
+                        if (old >= 0) {  // erase the evicted token
+                            bool f2 = false;
+                            uint32_t e2 = 0;
+                            const int32_t c2 = probe(r, static_cast<int32_t>(ht_hash(old)) & r.mask, old, f2, e2, g);
+                            if (c2 >= 0 && f2) shift_from(r, c2, g);
+                        }
+                        bool f3 = false;
+                        uint32_t e3 = 0;
+                        const int32_t c3 = probe(r, home, tp, f3, e3, g);
+                        if (c3 >= 0 && !f3 && lane == 0) {
+                            r.ht[c3] = static_cast<uint16_t>(h + 1);
+                            r.ct[c3] = tp;
+                        }
+                        if (lane == 0) {
+                            r.tok[h] = tp;
+                            atomicOr(r.vis32 + (h >> 5), 1u << (h & 31));
+                        }
+                        wave_fence();
+                        slot = h;
+                        miss = 1;
+                        hand = (h + 1 == dbs) ? 0 : h + 1;
+                    }
+                }
+            }
+            if (static_cast<int32_t>(lane) == kk) {
+                mySlot = slot;
+                myMiss = miss;
+            }
+        }
+        if (static_cast<int32_t>(lane) < kn) {
+            rs[k0 + lane] = mySlot;
+            rm[k0 + lane] = static_cast<int8_t>(myMiss);
+        }
+    }
+    if (lane == 0) {
+        gHand[0] = hand;
+        report_overflow(L.overflowSlot, g.code);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_sieve_update_wave(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,
+                                    hipStream_t stream)
+{
+    KvxLaunch<HispSieveUpdateArgs> L{a, overflowSlot};
+    hipLaunchKernelGGL(kvx_sieve_update_wave, dim3(a.maxNumReqs), dim3(WT), 0, stream, L, shadow);
+    return hipGetLastError();
+}
+
+}  // namespace kvx

@@ -78,10 +78,12 @@ def test_sieve_state_stream_parity_all_layers(kvops):
     dev.assert_state_equal()
 
 
+@pytest.mark.parametrize("variant", [-1, 3])
 @pytest.mark.parametrize("seed", range(6))
-def test_sieve_defensive_cases_parity(kvops, seed):
+def test_sieve_defensive_cases_parity(kvops, seed, variant):
     """Padding rows, out-of-range pool rows, num_real > max, dirty hands,
-    invalid and decode-extension positions, duplicates, tiny buffers (wrap)."""
+    invalid and decode-extension positions, duplicates, tiny buffers (wrap);
+    automatic variant and the wave-wide HBM kernel."""
     rng = np.random.default_rng(500 + seed)
     dbs = int(rng.integers(1, 70))
     top_k = int(rng.integers(1, 90))
@@ -92,6 +94,15 @@ def test_sieve_defensive_cases_parity(kvops, seed):
         st.admit(r, prefills[r])
     st.hand[0, 1, 0] = dbs + 3
     dev = DevSieve(st)
+    kvops.sieve_force_variant(variant)
+    try:
+        _defensive_steps(kvops, rng, st, dev, pool, max_reqs, prefills, top_k, seed)
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
+def _defensive_steps(kvops, rng, st, dev, pool, max_reqs, prefills, top_k, seed):
     for step in range(5):
         rows = list(rng.permutation(pool))[: int(rng.integers(1, pool + 1))]
         req_pool = rows + [-1] * (max_reqs - len(rows))
@@ -110,7 +121,6 @@ def test_sieve_defensive_cases_parity(kvops, seed):
         np.testing.assert_array_equal(g_miss, e_miss, err_msg="seed {} step {}".format(seed, step))
         np.testing.assert_array_equal(g_slots, e_slots, err_msg="seed {} step {}".format(seed, step))
         dev.assert_state_equal()
-    assert kvops.read_overflow() == 0
 
 
 def test_sieve_validation_messages(kvops):
@@ -206,10 +216,10 @@ def test_sieve_fast_kernel_parity_dsa_scale(kvops):
     assert kvops.read_overflow() == 0
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_sieve_variants_agree(kvops, variant):
-    """Sequential LDS (0), sequential HBM-resident (1) and parallel (2) kernels
-    give the oracle's results on the same inputs."""
+    """Sequential LDS (0), single-lane HBM (1), parallel (2) and wave-wide HBM
+    (3) kernels give the oracle's results on the same inputs."""
     rng = np.random.default_rng(77)
     dbs, K, prefill, req = 700, 300, 3000, 4
     st = orc.SieveState(1, req, dbs, K)
@@ -229,3 +239,50 @@ def test_sieve_variants_agree(kvops, variant):
             dev.assert_state_equal()
     finally:
         kvops.sieve_force_variant(-1)
+
+
+def test_sieve_config3_parity(kvops):
+    """Large-batch decode shapes (256 requests, topK 2048, 8192 slots, 10%
+    misses): two steps, full state after each."""
+    cfg = CONFIGS[3]
+    st = orc.SieveState(1, cfg.req_num, cfg.dbs, cfg.top_k)
+    for r in range(cfg.req_num):
+        st.admit(r, cfg.prefill)
+    dev = DevSieve(st)
+    rng = np.random.default_rng(cfg.seed)
+    req_pool = np.arange(cfg.req_num)
+    seq = np.full(cfg.req_num, cfg.prefill)
+    for step in range(2):
+        batch = streams.state_batch(rng, st.tokens[0, :, :cfg.dbs], cfg.prefill, cfg.top_k, cfg.miss_ratio)
+        e_slots, e_miss = st.update(0, batch, req_pool, seq, cfg.req_num)
+        g_slots, g_miss, _ = dev.update(kvops, 0, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
+        np.testing.assert_array_equal(g_miss, e_miss)
+        np.testing.assert_array_equal(g_slots, e_slots)
+        dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
+
+
+def test_sieve_config4_parity(kvops):
+    """The slot-limit stress shapes (4 requests, 65518 slots, topK 8192, a
+    262144-entry table kept in HBM) with adversarial keys whose Knuth hashes
+    share 4096 home buckets: the first step (thousands of evictions inside
+    one long probe run) and the next, full state after each."""
+    cfg = CONFIGS[4]
+    st = orc.SieveState(1, cfg.req_num, cfg.dbs, cfg.top_k)
+    for r in range(cfg.req_num):
+        st.admit(r, cfg.prefill)
+    dev = DevSieve(st)
+    rng = np.random.default_rng(cfg.seed)
+    pool = streams.adversarial_pool(cfg.prefill, 4096)
+    req_pool = np.arange(cfg.req_num)
+    seq = np.full(cfg.req_num, cfg.prefill)
+    for step in range(2):
+        batch = streams.state_batch(rng, st.tokens[0, :, :cfg.dbs], cfg.prefill, cfg.top_k, cfg.miss_ratio,
+                                    miss_pool=pool)
+        e_slots, e_miss = st.update(0, batch, req_pool, seq, cfg.req_num)
+        g_slots, g_miss, _ = dev.update(kvops, 0, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
+        assert kvops.last_sieve_variant() == 3
+        np.testing.assert_array_equal(g_miss, e_miss)
+        np.testing.assert_array_equal(g_slots, e_slots)
+        dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
