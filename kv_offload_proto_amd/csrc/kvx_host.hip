@@ -508,24 +508,31 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         a.reqsPerCore = static_cast<uint32_t>(rpc);
         a.htSize = static_cast<uint32_t>(htSize);
         a.poolSize = pool_size;
-        // Variant: 2 = parallel LDS kernel, 0 = sequential LDS kernel, 3 = sequential
-        // HBM-resident with wave-wide probes (1 = the single-lane HBM kernel, by request only).
+        // Variant: 2 = parallel LDS kernel, 4 = the same with the compact LDS layout (token
+        // hashes in LDS, tokens in HBM), 0 = sequential LDS kernel, 3 = sequential HBM-resident
+        // with wave-wide probes (1 = the single-lane HBM kernel, by request only).
         const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
                            visited_stride_b;
+        const bool fastShape = top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535;
         const size_t ldsFast = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
-                                                visited_stride_b).total;
-        const bool fastOk = ldsFast <= g.ldsLimit && top_k < 0x3FFF &&
-                            static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535;
-        int variant = fastOk ? 2 : (lds <= g.ldsLimit ? 0 : 3);
+                                                visited_stride_b, false).total;
+        const size_t ldsCompact = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
+                                                   visited_stride_b, true).total;
+        const bool fastOk = fastShape && ldsFast <= g.ldsLimit;
+        const bool compactOk = fastShape && ldsCompact <= g.ldsLimit && lds <= g.ldsLimit;
+        int variant = fastOk ? 2 : (compactOk ? 4 : (lds <= g.ldsLimit ? 0 : 3));
         if (g.forcedSieveVariant == 0 && lds <= g.ldsLimit) variant = 0;
         if (g.forcedSieveVariant == 1) variant = 1;
         if (g.forcedSieveVariant == 2 && fastOk) variant = 2;
         if (g.forcedSieveVariant == 3) variant = 3;
+        if (g.forcedSieveVariant == 4 && compactOk) variant = 4;
         a.reserved = static_cast<uint32_t>(variant);
         g.lastSieveVariant = variant;
         if (max_num_reqs == 0) return;
-        if (variant == 2) {
-            hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow), ldsFast, AsStream(stream)),
+        if (variant == 2 || variant == 4) {
+            hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow),
+                                                   variant == 2 ? ldsFast : std::max(ldsCompact, lds), variant == 4,
+                                                   AsStream(stream)),
                      "hisp_sieve_update launch");
         } else if (variant == 3) {
             int32_t *shadow = EnsureShadow(static_cast<uint64_t>(max_num_reqs) * static_cast<uint64_t>(htSize));
@@ -648,7 +655,7 @@ int kvx_last_sieve_variant(void) { return g.lastSieveVariant; }
 int kvx_sieve_force_variant(int variant)
 {
     return Guarded([&] {
-        if (variant < -1 || variant > 3) throw Error("sieve_force_variant: variant must be -1, 0, 1, 2 or 3");
+        if (variant < -1 || variant > 4) throw Error("sieve_force_variant: variant must be -1 or 0..4");
         g.forcedSieveVariant = variant;
     });
 }

@@ -66,32 +66,50 @@ __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 1
 
 // LDS regions of the parallel SIEVE kernel for one batch row.  ptok+pinf and
 // smA+smB are each contiguous and reused as 64-bit arrays of topK entries in
-// the table-update phase.
+// the table-update phase.  In the compact form (rows whose full layout does
+// not fit) the tokens row is replaced by the 16-bit Knuth hash of each slot's
+// token (full tokens stay in HBM), and regions with disjoint lifetimes share
+// memory: tb with candPre, eseq with the SM k list (cvlist), and the four
+// table bitmaps with vt.
 __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint32_t htSize, uint32_t topK,
-                                                           uint32_t visStrideB)
+                                                           uint32_t visStrideB, bool compact = false)
 {
     FastLayout l{};
     uint32_t o = 0;
-    l.tok = o;     o += align16(padded * 4u);
+    const uint32_t bmBytes = htSize / 8u;
+    l.tok = o;     o += align16(padded * (compact ? 2u : 4u));
     l.ht = o;      o += align16(htSize * 2u);
     l.vis = o;     o += align16(visStrideB);
     l.ptok = o;    o += align16(topK * 4u);
     l.pinf = o;    o += align16(topK * 4u);
-    l.vt = o;      o += align16(padded * 2u);
+    l.vt = o;
+    o += compact ? align16(padded * 2u > 4u * bmBytes ? padded * 2u : 4u * bmBytes) : align16(padded * 2u);
     l.candPre = o; o += align16((topK + 1u) * 2u);
     l.evslot = o;  o += align16(topK * 2u);
     l.evold = o;   o += align16(topK * 2u);
     l.cvlist = o;  o += align16(topK * 2u);
-    l.eseq = o;    o += align16(topK * 2u);
-    l.tb = o;      o += align16((topK + 1u) * 2u);
+    if (compact) {
+        l.eseq = l.cvlist;
+        l.tb = l.candPre;
+    } else {
+        l.eseq = o;    o += align16(topK * 2u);
+        l.tb = o;      o += align16((topK + 1u) * 2u);
+    }
     l.smA = o;     o += align16(topK * 4u);
     l.smB = o;     o += align16(topK * 4u);
     l.kst = o;     o += align16(topK * 4u);
     l.vset = o;    o += align16(visStrideB);
-    l.ber = o;     o += align16(htSize / 8u);
-    l.bg = o;      o += align16(htSize / 8u);
-    l.bm = o;      o += align16(htSize / 8u);
-    l.bnew = o;    o += align16(htSize / 8u);
+    if (compact) {
+        l.ber = l.vt;
+        l.bg = l.vt + bmBytes;
+        l.bm = l.vt + 2u * bmBytes;
+        l.bnew = l.vt + 3u * bmBytes;
+    } else {
+        l.ber = o;     o += align16(bmBytes);
+        l.bg = o;      o += align16(bmBytes);
+        l.bm = o;      o += align16(bmBytes);
+        l.bnew = o;    o += align16(bmBytes);
+    }
     l.total = o;
     return l;
 }
@@ -106,7 +124,7 @@ hipError_t sieve_fast_set_lds_limit(size_t bytes);
 hipError_t launch_sieve_update_wave(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,
                                     hipStream_t stream);
 hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes,
-                                    hipStream_t stream);
+                                    bool compact, hipStream_t stream);
 
 struct GatherPlan {
     KvcGatherArgs a;               // args of the first (or only) segment

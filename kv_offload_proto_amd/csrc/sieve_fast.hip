@@ -172,8 +172,10 @@ __device__ __forceinline__ int32_t lds_claim16(uint32_t *w32, int32_t idx, int32
 
 __device__ __forceinline__ bool bit_get(const uint32_t *b, uint32_t i) { return (b[i >> 5] >> (i & 31u)) & 1u; }
 
-// Algorithm R deletion of the entry at cell c (homes from the tokens row).
-__device__ void rdel_at(uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t c, int32_t mask, Guard &g)
+// Algorithm R deletion of the entry at cell c (homes from the tokens row, or
+// from the per-slot token hashes in the compact form).
+template <bool kC>
+__device__ void rdel_at(uint16_t *ht, const void *tokv, int32_t ntok, int32_t c, int32_t mask, Guard &g)
 {
     int32_t j = c, i = c;
     for (int32_t n = 0;; ++n) {
@@ -184,7 +186,13 @@ __device__ void rdel_at(uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t 
         i = (i + 1) & mask;
         const uint16_t e = ht[i];
         if (e == 0) break;
-        const int32_t home = static_cast<int32_t>(ht_hash(tok_at(tok, e, ntok))) & mask;
+        int32_t home;
+        if constexpr (kC) {
+            const uint16_t *hv = static_cast<const uint16_t *>(tokv);
+            home = static_cast<int32_t>((static_cast<int32_t>(e) - 1 < ntok) ? hv[e - 1u] : ht_hash(-1)) & mask;
+        } else {
+            home = static_cast<int32_t>(ht_hash(tok_at(static_cast<const int32_t *>(tokv), e, ntok))) & mask;
+        }
         const bool move = (j < i) ? (home <= j || home > i) : (home <= j && home > i);
         if (move) {
             ht[j] = e;
@@ -221,6 +229,7 @@ __device__ __forceinline__ int32_t ring_slot(int32_t hand0, int32_t u, int32_t d
     return s >= dbs ? s - dbs : s;
 }
 
+template <bool kC>
 __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveUpdateArgs> L)
 {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -261,8 +270,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint16_t *gHt = reinterpret_cast<uint16_t *>(a.deviceBufferHt) + reqIdx * H;
     int32_t *gHand = reinterpret_cast<int32_t *>(a.sieveHand) + reqIdx * kHandStride;
 
-    const FastLayout lay = fast_layout(padded, H, K, visStrideB);
-    int32_t *tok = reinterpret_cast<int32_t *>(smem + lay.tok);
+    const FastLayout lay = fast_layout(padded, H, K, visStrideB, kC);
+    int32_t *tok = reinterpret_cast<int32_t *>(smem + lay.tok);    // full form: tokens
+    uint16_t *hv = reinterpret_cast<uint16_t *>(smem + lay.tok);   // compact form: token hashes
+    // token of slot s equals t (th = its hash); the compact form checks the
+    // hash in LDS and confirms with the HBM row
+    auto tok_is = [&](uint32_t s, int32_t t, uint32_t th) -> bool {
+        if constexpr (kC) return hv[s] == th && gTok[s] == t;
+        else return tok[s] == t;
+    };
+    auto tok_hash = [&](uint32_t s) -> uint32_t {
+        if constexpr (kC) return hv[s];
+        else return ht_hash(tok[s]);
+    };
     uint16_t *ht = reinterpret_cast<uint16_t *>(smem + lay.ht);
     uint32_t *ht32 = reinterpret_cast<uint32_t *>(smem + lay.ht);
     uint8_t *vis = smem + lay.vis;
@@ -323,7 +343,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             for (int j = 0; j < 4; ++j) {
                 const int32_t c = c0 + j * NT;
                 if (c < nt) {
-                    reinterpret_cast<uint4 *>(tok)[c] = v[j];
+                    if constexpr (kC) {
+                        const uint32_t a0 = ht_hash(static_cast<int32_t>(v[j].x)), a1 = ht_hash(static_cast<int32_t>(v[j].y));
+                        const uint32_t a2 = ht_hash(static_cast<int32_t>(v[j].z)), a3 = ht_hash(static_cast<int32_t>(v[j].w));
+                        reinterpret_cast<uint2 *>(hv)[c] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
+                    } else {
+                        reinterpret_cast<uint4 *>(tok)[c] = v[j];
+                    }
                     const int32_t s0 = c * 4;
                     nTok += (s0 < dbs && static_cast<int32_t>(v[j].x) >= 0) + (s0 + 1 < dbs && static_cast<int32_t>(v[j].y) >= 0) +
                             (s0 + 2 < dbs && static_cast<int32_t>(v[j].z) >= 0) + (s0 + 3 < dbs && static_cast<int32_t>(v[j].w) >= 0);
@@ -340,7 +366,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if (h0) ptok[tid] = t0;
         if (h1) ptok[tid + NT] = t1;
         for (int32_t k = tid + 2 * NT; k < K; k += NT) ptok[k] = rt[k];
-        const int32_t nz = (visStrideB >> 2) + 4 * (H >> 5);  // vset, ber, bg, bm, bnew are contiguous
+        // vset (and in the full form ber, bg, bm, bnew) are contiguous
+        const int32_t nz = (visStrideB >> 2) + (kC ? 0 : 4 * (H >> 5));
         for (int32_t i = tid; i < nz; i += NT) vset[i] = 0u;
         for (int32_t k = tid; k < K; k += NT) evslot[k] = 0;  // SM index + 1 by first-hit position
         nTok = wave_sum(nTok);
@@ -365,8 +392,20 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         Guard g;
         bool bad = false;
         for (int32_t s = tid; s < dbs; s += NT) {
-            const int32_t t = tok[s];
-            if (t >= 0 && ht_find(ht, tok, padded, t, mask, g) != s) bad = true;
+            const int32_t t = kC ? gTok[s] : tok[s];
+            if (t < 0) continue;
+            const uint32_t th = ht_hash(t);
+            int32_t idx = static_cast<int32_t>(th) & mask, found = -1;
+            for (int32_t n = 0; n <= mask; ++n) {
+                const uint16_t e = ht[idx];
+                if (e == 0) break;
+                if (static_cast<int32_t>(e) - 1 < padded && tok_is(e - 1u, t, th)) {
+                    found = static_cast<int32_t>(e) - 1;
+                    break;
+                }
+                idx = (idx + 1) & mask;
+            }
+            if (found != s) bad = true;
         }
         if (__ballot(bad || g.code != 0) != 0ull && lane == 0) atomicOr(&ms.bad, 1);
     }
@@ -392,7 +431,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     inf = CLS_EXT << 30;
                 } else {
                     const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
-                    int32_t idx = static_cast<int32_t>(ht_hash(t)) & mask;
+                    const uint32_t th = ht_hash(t);
+                    int32_t idx = static_cast<int32_t>(th) & mask;
                     inf = 0xFFFFFFFFu;
                     for (int32_t n = 0; n <= mask; ++n) {
                         uint32_t *w = ht32 + (idx >> 1);
@@ -410,7 +450,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                                 }
                                 old = prev;
                             } else if (cur <= static_cast<uint32_t>(padded)) {
-                                if (tok[cur - 1u] == t) {
+                                if (tok_is(cur - 1u, t, th)) {
                                     inf = (CLS_HIT << 30) | (cur - 1u);
                                     lds_min16(vt32, cur - 1u, static_cast<uint16_t>(k + 1));
                                 } else {
@@ -740,7 +780,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             const uint32_t p = eseq[i];
             const uint32_t s = evslot[p];
             atomicOr(vset + (s >> 5), 1u << (s & 31u));
-            const int32_t old = tok[s];
+            const int32_t old = kC ? gTok[s] : tok[s];
             uint32_t cell = 0xFFFFFFFFu;
             if (old >= 0) {
                 int32_t idx = static_cast<int32_t>(ht_hash(old)) & mask;
@@ -752,12 +792,22 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     idx = (idx + 1) & mask;
                 }
                 if (cell == 0xFFFFFFFFu) g.code = kOverflowProbe;
-                else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+                else if (!kC) atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
             }
             ecell[i] = cell;
-            ntokv[i] = static_cast<uint32_t>((pinf[p] >> 30) == CLS_CAND ? ptok[p] : tok[evold[p]]);
+            const uint32_t src = evold[p];
+            ntokv[i] = static_cast<uint32_t>((pinf[p] >> 30) == CLS_CAND ? ptok[p] : (kC ? gTok[src] : tok[src]));
         }
         __syncthreads();
+        if constexpr (kC) {  // the bitmaps share vt's memory: clear them now that vt is read
+            for (int32_t i = tid; i < 4 * (H >> 5); i += NT) ber[i] = 0u;
+            __syncthreads();
+            for (int32_t i = tid; i < N; i += NT) {
+                const uint32_t cell = ecell[i];
+                if (cell != 0xFFFFFFFFu) atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+            }
+            __syncthreads();
+        }
         STAMP(10);
         // ---- table: erase the evicted tokens; the rightmost marked cell of a
         // cluster leads it and deletes right to left
@@ -779,10 +829,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             const uint32_t e = ecell[i];
             if (e == 0xFFFFFFFFu || !(e & 0x80000000u)) continue;
             const int32_t c = static_cast<int32_t>(e & 0x7FFFFFFFu);
-            rdel_at(ht, tok, padded, c, mask, g);
+            rdel_at<kC>(ht, smem + lay.tok, padded, c, mask, g);
             int32_t x = (c - 1) & mask;
             for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x - 1) & mask) {
-                if (bit_get(ber, x)) rdel_at(ht, tok, padded, x, mask, g);
+                if (bit_get(ber, x)) rdel_at<kC>(ht, smem + lay.tok, padded, x, mask, g);
             }
         }
         __syncthreads();
@@ -791,7 +841,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         for (int32_t i = tid; i < N; i += NT) {
             const uint32_t s = evslot[eseq[i]];
             const int32_t t = static_cast<int32_t>(ntokv[i]);
-            tok[s] = t;
+            if constexpr (kC) {
+                hv[s] = static_cast<uint16_t>(ht_hash(t));
+                gTok[s] = t;
+            } else {
+                tok[s] = t;
+            }
             const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(t)) & mask, mask,
                                           static_cast<uint16_t>(s + 1u));
             if (c < 0) g.code = kOverflowProbe;
@@ -838,7 +893,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
                 for (int32_t r = q; r < nMulti && static_cast<uint32_t>(msort[r] >> 32) == st; ++r) {
                     const uint32_t s = static_cast<uint32_t>(msort[r] & 0xFFFFu);
-                    int32_t idx = static_cast<int32_t>(ht_hash(tok[s])) & mask;
+                    int32_t idx = static_cast<int32_t>(tok_hash(s)) & mask;
                     for (int32_t n = 0; n < H && ht[idx] != 0; ++n) idx = (idx + 1) & mask;
                     ht[idx] = static_cast<uint16_t>(s + 1u);
                 }
@@ -863,7 +918,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 reinterpret_cast<uint32_t *>(gVis)[w] = (vis32[w] & ~clr) | vset[w];
             }
             if (N > 0) {
-                wg_copy16(gTok, tok, static_cast<uint32_t>(padded) * 4u);
+                if constexpr (!kC) wg_copy16(gTok, tok, static_cast<uint32_t>(padded) * 4u);  // compact: written in place
                 wg_copy16(gHt, ht, static_cast<uint32_t>(H) * 2u);
             }
             if (tid == 0) {
@@ -878,31 +933,41 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             STAMP(14);
             return;
         }
+        if constexpr (kC) {
+            // the compact form has already written the new tokens to HBM; a
+            // late bound violation only comes from a corrupted table
+            if (tid == 0) report_overflow(L.overflowSlot, kOverflowProbe);
+            return;
+        }
         fast = false;
     }
 
     // ---- fallback: restage the pre-step row from HBM (nothing has been
     // written back) and run the sequential recurrence on it
     __syncthreads();
-    wg_copy16(tok, gTok, static_cast<uint32_t>(padded) * 4u);
-    wg_copy16(ht, gHt, static_cast<uint32_t>(H) * 2u);
-    wg_copy16(vis, gVis, static_cast<uint32_t>(visStrideB));
+    int32_t *tokF = reinterpret_cast<int32_t *>(smem);
+    uint16_t *htF = reinterpret_cast<uint16_t *>(smem + static_cast<size_t>(padded) * 4u);
+    uint8_t *visF = smem + static_cast<size_t>(padded) * 4u + static_cast<size_t>(H) * 2u;
+    wg_copy16(tokF, gTok, static_cast<uint32_t>(padded) * 4u);
+    wg_copy16(htF, gHt, static_cast<uint32_t>(H) * 2u);
+    wg_copy16(visF, gVis, static_cast<uint32_t>(visStrideB));
     __syncthreads();
     __shared__ int32_t s_dirty;
     if (tid == 0) {
         int32_t hand = hand0;
         Guard g;
-        const bool dirty = sieve_row_sequential(rt, rs, rm, K, seqLen, prefill, dbs, padded, mask, tok, vis, ht, hand, g);
+        const bool dirty =
+            sieve_row_sequential(rt, rs, rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
         gHand[0] = hand;
         gHand[1] = (canonical && g.code == 0) ? kCanonFlag : 0;
         s_dirty = dirty ? 1 : 0;
         report_overflow(L.overflowSlot, g.code);
     }
     __syncthreads();
-    wg_copy16(gVis, vis, static_cast<uint32_t>(visStrideB));
+    wg_copy16(gVis, visF, static_cast<uint32_t>(visStrideB));
     if (s_dirty) {
-        wg_copy16(gTok, tok, static_cast<uint32_t>(padded) * 4u);
-        wg_copy16(gHt, ht, static_cast<uint32_t>(H) * 2u);
+        wg_copy16(gTok, tokF, static_cast<uint32_t>(padded) * 4u);
+        wg_copy16(gHt, htF, static_cast<uint32_t>(H) * 2u);
     }
 }
 
@@ -910,15 +975,22 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
 hipError_t sieve_fast_set_lds_limit(size_t bytes)
 {
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update_fast),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update_fast<false>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update_fast<true>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
 }
 
-hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes,
+hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes, bool compact,
                                     hipStream_t stream)
 {
     KvxLaunch<HispSieveUpdateArgs> L{a, overflowSlot};
-    hipLaunchKernelGGL(kvx_sieve_update_fast, dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    if (compact) {
+        hipLaunchKernelGGL(kvx_sieve_update_fast<true>, dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    } else {
+        hipLaunchKernelGGL(kvx_sieve_update_fast<false>, dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    }
     return hipGetLastError();
 }
 

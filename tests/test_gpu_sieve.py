@@ -216,10 +216,11 @@ def test_sieve_fast_kernel_parity_dsa_scale(kvops):
     assert kvops.read_overflow() == 0
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
 def test_sieve_variants_agree(kvops, variant):
-    """Sequential LDS (0), single-lane HBM (1), parallel (2) and wave-wide HBM
-    (3) kernels give the oracle's results on the same inputs."""
+    """Sequential LDS (0), single-lane HBM (1), parallel (2), wave-wide HBM (3)
+    and parallel compact-layout (4) kernels give the oracle's results on the
+    same inputs."""
     rng = np.random.default_rng(77)
     dbs, K, prefill, req = 700, 300, 3000, 4
     st = orc.SieveState(1, req, dbs, K)
@@ -243,7 +244,8 @@ def test_sieve_variants_agree(kvops, variant):
 
 def test_sieve_config3_parity(kvops):
     """Large-batch decode shapes (256 requests, topK 2048, 8192 slots, 10%
-    misses): two steps, full state after each."""
+    misses; the parallel kernel's compact LDS layout): two steps, full state
+    after each."""
     cfg = CONFIGS[3]
     st = orc.SieveState(1, cfg.req_num, cfg.dbs, cfg.top_k)
     for r in range(cfg.req_num):
@@ -256,6 +258,7 @@ def test_sieve_config3_parity(kvops):
         batch = streams.state_batch(rng, st.tokens[0, :, :cfg.dbs], cfg.prefill, cfg.top_k, cfg.miss_ratio)
         e_slots, e_miss = st.update(0, batch, req_pool, seq, cfg.req_num)
         g_slots, g_miss, _ = dev.update(kvops, 0, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
+        assert kvops.last_sieve_variant() == 4
         np.testing.assert_array_equal(g_miss, e_miss)
         np.testing.assert_array_equal(g_slots, e_slots)
         dev.assert_state_equal()
