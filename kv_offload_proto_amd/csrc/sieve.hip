@@ -9,8 +9,10 @@
 // (tokens padded*4 B, hash table htSize*2 B, visited visStrideB B) is staged
 // in LDS when it fits the per-workgroup LDS limit (160 KiB on gfx950) and
 // written back at the end; otherwise the kernel works on the HBM-resident row
-// in place.  Within the row, positions are processed in order by one lane,
-// which is the exact sequential recurrence of the reference.
+// in place.  Within the row, positions are processed in order -- the exact
+// sequential recurrence of the reference -- by one wave whose probes, sweeps
+// and shifts take 64 cells or slots per step (LDS-staged), or by one lane
+// (HBM-resident).
 #include "kvx_internal.h"
 #include "sieve_common.h"
 
@@ -70,7 +72,20 @@ __global__ __launch_bounds__(256) void kvx_sieve_update(KvxLaunch<HispSieveUpdat
         __syncthreads();
     }
 
-    if (threadIdx.x == 0) {
+    if (kLds && htSize > kSmallTable) {
+        if (threadIdx.x < 64) {  // one wave: 64 cells/slots per probe, sweep and shift step
+            int32_t hand = *gHand;
+            if (hand < 0 || hand >= dbs) hand = 0;  // (:108-111)
+            Guard g;
+            const bool dirty =
+                sieve_row_wave(rt, rs, rm, topK, seqLen, prefill, dbs, padded, htSize - 1, tok, vis, ht, hand, g);
+            if (threadIdx.x == 0) {
+                *gHand = hand;
+                s_dirty = dirty ? 1 : 0;
+                report_overflow(L.overflowSlot, g.code);
+            }
+        }
+    } else if (threadIdx.x == 0) {
         int32_t hand = *gHand;
         if (hand < 0 || hand >= dbs) hand = 0;  // (:108-111)
         Guard g;

@@ -13,6 +13,10 @@ struct Guard {
     uint64_t code = 0;
 };
 
+// Tables up to this many cells run the in-order recurrence on one lane (short
+// probe runs); larger ones use a whole wave per probe, sweep and shift step.
+constexpr int32_t kSmallTable = 4096;
+
 // Token held by the slot an entry points at.  An entry past the tokens row
 // can only come from a corrupted table; it reads as the empty token (-1)
 // instead of touching memory outside the row.
@@ -150,6 +154,138 @@ __device__ bool sieve_row_sequential(const int32_t *rt, int32_t *rs, int8_t *rm,
         tok[h] = tp;
         vis_set(vis, h);
         hand = (h + 1 == dbs) ? 0 : h + 1;
+    }
+    return dirty;
+}
+
+// The same recurrence run by one whole wave on an LDS-staged row: each probe
+// reads 64 consecutive cells and takes the first empty or matching one with a
+// ballot, the hand sweep tests 64 visited bits at once, and Algorithm R's
+// backward shift walks 64 cells per step, taking the moves in order.  Every
+// lane of the wave calls it (uniform control flow); same results as
+// sieve_row_sequential.
+__device__ __forceinline__ int32_t wave_probe_lds(const uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t idx,
+                                                  int32_t token, int32_t mask, bool &found, uint32_t &entry, Guard &g)
+{
+    const int32_t lane = static_cast<int32_t>(__lane_id());
+    for (int32_t base = 0; base <= mask; base += 64) {
+        const int32_t c = (idx + base + lane) & mask;
+        const uint16_t e = ht[c];
+        const bool hitL = e != 0 && tok_at(tok, e, ntok) == token;
+        const uint64_t hit = __ballot(hitL);
+        const uint64_t any = hit | __ballot(e == 0);
+        if (any != 0ull) {
+            const int f = __builtin_ctzll(any);
+            found = (hit >> f) & 1ull;
+            entry = static_cast<uint32_t>(__shfl(static_cast<int>(e), f));
+            return (idx + base + f) & mask;
+        }
+    }
+    g.code = kOverflowProbe;
+    found = false;
+    return -1;
+}
+
+__device__ __forceinline__ void wave_shift_lds(uint16_t *ht, const int32_t *tok, int32_t ntok, int32_t j,
+                                               int32_t mask, Guard &g)
+{
+    const int32_t lane = static_cast<int32_t>(__lane_id());
+    const int32_t start = j;
+    for (int32_t base = 1; base <= mask; base += 64) {
+        const int32_t i = (start + base + lane) & mask;
+        const uint16_t e = ht[i];
+        const int32_t home = (e != 0) ? static_cast<int32_t>(ht_hash(tok_at(tok, e, ntok))) & mask : 0;
+        uint64_t active = ~0ull;
+        for (;;) {
+            const bool mv = (j < i) ? (home <= j || home > i) : (home <= j && home > i);
+            const uint64_t m = __ballot(e == 0 || mv) & active;
+            if (m == 0ull) break;
+            const int f = __builtin_ctzll(m);
+            if (__shfl(static_cast<int>(e), f) == 0) {
+                if (lane == 0) ht[j] = 0;
+                return;
+            }
+            if (lane == f) ht[j] = e;
+            j = __shfl(i, f);
+            active = (f == 63) ? 0ull : (~0ull << (f + 1));
+        }
+    }
+    g.code = kOverflowProbe;
+}
+
+__device__ bool sieve_row_wave(const int32_t *rt, int32_t *rs, int8_t *rm, int32_t topK, int32_t seqLen,
+                               int32_t prefill, int32_t dbs, int32_t padded, int32_t mask, int32_t *tok, uint8_t *vis,
+                               uint16_t *ht, int32_t &hand, Guard &g)
+{
+    const int32_t lane = static_cast<int32_t>(__lane_id());
+    uint32_t *vis32 = reinterpret_cast<uint32_t *>(vis);
+    const int32_t width = dbs < 64 ? dbs : 64;  // slots per sweep step (no slot twice in one step)
+    bool dirty = false;
+    for (int32_t k0 = 0; k0 < topK; k0 += 64) {
+        const int32_t myT = (k0 + lane < topK) ? rt[k0 + lane] : 0;
+        int32_t mySlot = -1, myMiss = 0;
+        const int32_t kn = (topK - k0 < 64) ? topK - k0 : 64;
+        for (int32_t kk = 0; kk < kn; ++kk) {
+            const int32_t tp = __shfl(myT, kk);
+            int32_t slot = -1, miss = 0;
+            if (g.code != 0 || tp < 0 || tp >= seqLen) {  // past a bound violation the row reads as invalid
+            } else if (tp >= prefill) {
+                slot = padded + (tp - prefill);
+            } else {
+                const int32_t home = static_cast<int32_t>(ht_hash(tp)) & mask;
+                bool found = false;
+                uint32_t e = 0;
+                const int32_t cell = wave_probe_lds(ht, tok, padded, home, tp, mask, found, e, g);
+                if (cell < 0) {
+                } else if (found) {
+                    slot = static_cast<int32_t>(e) - 1;
+                    if (lane == 0) vis_set(vis, slot);
+                } else {
+                    int32_t h = -1;
+                    for (int32_t base = 0; base <= 2 * dbs && h < 0; base += width) {
+                        const bool on = lane < width;
+                        const int32_t s = (hand + base + lane) % dbs;
+                        const bool v = on && vis_get(vis, s);
+                        const uint64_t unv = __ballot(on && !v);
+                        const int f = unv ? __builtin_ctzll(unv) : 64;
+                        if (lane < f && v) atomicAnd(vis32 + (s >> 5), ~(1u << (s & 31)));
+                        if (f < 64) h = __shfl(s, f);
+                    }
+                    if (h < 0) {
+                        g.code = kOverflowSweep;
+                    } else {
+                        const int32_t old = tok[h];
+                        if (old >= 0) {
+                            bool f2 = false;
+                            uint32_t e2 = 0;
+                            const int32_t c2 = wave_probe_lds(ht, tok, padded, static_cast<int32_t>(ht_hash(old)) & mask,
+                                                              old, mask, f2, e2, g);
+                            if (c2 >= 0 && f2) wave_shift_lds(ht, tok, padded, c2, mask, g);
+                        }
+                        bool f3 = false;
+                        uint32_t e3 = 0;
+                        const int32_t c3 = wave_probe_lds(ht, tok, padded, home, tp, mask, f3, e3, g);
+                        if (c3 >= 0 && !f3 && lane == 0) ht[c3] = static_cast<uint16_t>(h + 1);
+                        if (lane == 0) {
+                            tok[h] = tp;
+                            vis_set(vis, h);
+                        }
+                        dirty = true;
+                        slot = h;
+                        miss = 1;
+                        hand = (h + 1 == dbs) ? 0 : h + 1;
+                    }
+                }
+            }
+            if (lane == kk) {
+                mySlot = slot;
+                myMiss = miss;
+            }
+        }
+        if (lane < kn) {
+            rs[k0 + lane] = mySlot;
+            rm[k0 + lane] = static_cast<int8_t>(myMiss);
+        }
     }
     return dirty;
 }

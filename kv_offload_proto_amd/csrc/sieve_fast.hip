@@ -953,15 +953,21 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     wg_copy16(visF, gVis, static_cast<uint32_t>(visStrideB));
     __syncthreads();
     __shared__ int32_t s_dirty;
-    if (tid == 0) {
+    if (wave == 0) {  // the in-order recurrence: one lane for small tables, else 64 cells/slots per step
         int32_t hand = hand0;
         Guard g;
-        const bool dirty =
-            sieve_row_sequential(rt, rs, rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
-        gHand[0] = hand;
-        gHand[1] = (canonical && g.code == 0) ? kCanonFlag : 0;
-        s_dirty = dirty ? 1 : 0;
-        report_overflow(L.overflowSlot, g.code);
+        bool dirty = false;
+        if (H <= kSmallTable) {
+            if (lane == 0) dirty = sieve_row_sequential(rt, rs, rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
+        } else {
+            dirty = sieve_row_wave(rt, rs, rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
+        }
+        if (lane == 0) {
+            gHand[0] = hand;
+            gHand[1] = (canonical && g.code == 0) ? kCanonFlag : 0;
+            s_dirty = dirty ? 1 : 0;
+            report_overflow(L.overflowSlot, g.code);
+        }
     }
     __syncthreads();
     wg_copy16(gVis, visF, static_cast<uint32_t>(visStrideB));

@@ -289,3 +289,52 @@ def test_sieve_config4_parity(kvops):
         np.testing.assert_array_equal(g_slots, e_slots)
         dev.assert_state_equal()
     assert kvops.read_overflow() == 0
+
+
+def test_sieve_wrap_fallback_large_table(kvops):
+    """More misses than slots (the hand wraps within a step) on a table above
+    4096 cells: the parallel kernel hands the row to the in-order recurrence
+    run by a whole wave."""
+    rng = np.random.default_rng(31)
+    dbs, K, prefill, req = 600, 1800, 20000, 3
+    st = orc.SieveState(1, req, dbs, K)
+    assert st.ht_size > 4096
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    for step in range(3):
+        batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.7)
+        seq = np.full(req, prefill + 2)
+        e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+        g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+        assert kvops.last_sieve_variant() == 2
+        np.testing.assert_array_equal(g_miss, e_miss)
+        np.testing.assert_array_equal(g_slots, e_slots)
+        dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
+
+
+def test_sieve_sequential_lds_wave_path(kvops):
+    """The sequential LDS kernel on a table above 4096 cells (one wave per
+    probe, sweep and shift step): large-batch decode shapes, one step."""
+    cfg = CONFIGS[3]
+    req = 32
+    st = orc.SieveState(1, req, cfg.dbs, cfg.top_k)
+    assert st.ht_size > 4096
+    for r in range(req):
+        st.admit(r, cfg.prefill)
+    dev = DevSieve(st)
+    rng = np.random.default_rng(5)
+    kvops.sieve_force_variant(0)
+    try:
+        for step in range(2):
+            batch = streams.state_batch(rng, st.tokens[0, :, :cfg.dbs], cfg.prefill, cfg.top_k, 0.3)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), np.full(req, cfg.prefill), req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), np.full(req, cfg.prefill), req, req,
+                                            cfg.top_k)
+            assert kvops.last_sieve_variant() == 0
+            np.testing.assert_array_equal(g_miss, e_miss)
+            np.testing.assert_array_equal(g_slots, e_slots)
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
