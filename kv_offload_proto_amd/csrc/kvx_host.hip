@@ -513,7 +513,9 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         // with wave-wide probes (1 = the single-lane HBM kernel, by request only).
         const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
                            visited_stride_b;
-        const bool fastShape = top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535;
+        const bool fastShape = top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535 &&
+                               device_buffer_size <= 64u * kvx::kFastThreads &&
+                               top_k <= 32u * kvx::kFastThreads;
         const size_t ldsFast = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
                                                 visited_stride_b, false).total;
         const size_t ldsCompact = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
@@ -526,12 +528,19 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         if (g.forcedSieveVariant == 2 && fastOk) variant = 2;
         if (g.forcedSieveVariant == 3) variant = 3;
         if (g.forcedSieveVariant == 4 && compactOk) variant = 4;
-        a.reserved = static_cast<uint32_t>(variant);
+        // the parallel kernel's direct token -> slot map takes the LDS left over
+        // (rows whose prefill exceeds it probe the table instead)
+        uint32_t invCap = 0;
+        size_t ldsLaunch = variant == 2 ? ldsFast : std::max(ldsCompact, lds);
+        if (variant == 2 && g.ldsLimit > ldsFast) {
+            invCap = static_cast<uint32_t>(std::min<size_t>((g.ldsLimit - ldsFast) / 2, 65536)) & ~15u;
+            ldsLaunch = ldsFast + static_cast<size_t>(invCap) * 2;
+        }
+        a.reserved = static_cast<uint32_t>(variant) | (invCap << 8);
         g.lastSieveVariant = variant;
         if (max_num_reqs == 0) return;
         if (variant == 2 || variant == 4) {
-            hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow),
-                                                   variant == 2 ? ldsFast : std::max(ldsCompact, lds), variant == 4,
+            hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow), ldsLaunch, variant == 4,
                                                    AsStream(stream)),
                      "hisp_sieve_update launch");
         } else if (variant == 3) {

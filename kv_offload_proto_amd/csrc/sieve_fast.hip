@@ -71,9 +71,17 @@ __device__ unsigned long long kvx_dbg_stamps[1024][16];
     do {                                                                \
         if (tid == 0 && bid < 1024) kvx_dbg_stamps[bid][i] = clock64(); \
     } while (0)
+__device__ unsigned long long kvx_dbg_sub[1024][16];
+#define SUBSTAMP(i)                                                   \
+    do {                                                              \
+        if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = clock64();  \
+    } while (0)
 #else
 #define STAMP(i) \
     do {         \
+    } while (0)
+#define SUBSTAMP(i) \
+    do {            \
     } while (0)
 #endif
 
@@ -305,6 +313,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *bg = reinterpret_cast<uint32_t *>(smem + lay.bg);
     uint32_t *bm = reinterpret_cast<uint32_t *>(smem + lay.bm);
     uint32_t *bnew = reinterpret_cast<uint32_t *>(smem + lay.bnew);
+    // direct token -> slot map for rows whose prefill fits the LDS left over
+    // (after the layout): 0 = not resident, slot+1 when resident,
+    // padded+1+k for a candidate's first position k
+    const int32_t invCap = static_cast<int32_t>(a.reserved >> 8);
+    const bool direct = !kC && prefill > 0 && prefill <= invCap;
+    uint16_t *inv = reinterpret_cast<uint16_t *>(smem + lay.total);
+    uint32_t *inv32 = reinterpret_cast<uint32_t *>(smem + lay.total);
     // reuse of regions whose earlier contents are dead by then
     uint32_t *pcell = smA;                                             // dedup: provisional cell per position
     uint16_t *posSM = evslot;                                          // decide: SM index + 1 per first-hit position
@@ -363,6 +378,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
             }
         }
+        SUBSTAMP(4);
         if (h0) ptok[tid] = t0;
         if (h1) ptok[tid + NT] = t1;
         for (int32_t k = tid + 2 * NT; k < K; k += NT) ptok[k] = rt[k];
@@ -370,6 +386,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const int32_t nz = (visStrideB >> 2) + (kC ? 0 : 4 * (H >> 5));
         for (int32_t i = tid; i < nz; i += NT) vset[i] = 0u;
         for (int32_t k = tid; k < K; k += NT) evslot[k] = 0;  // SM index + 1 by first-hit position
+        if (direct) {
+            for (int32_t i = tid; i < (prefill + 1) >> 1; i += NT) inv32[i] = 0u;
+        }
         nTok = wave_sum(nTok);
         nEnt = wave_sum(nEnt);
         if (tid == 0) {
@@ -387,7 +406,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // ---- consistency: the table indexes exactly the non-negative tokens of
     // [0, dbs), each at its own slot.  A row this kernel wrote last carries
     // the flag, and then only the counts are checked.
-    for (int32_t s = tid; s < dbs; s += NT) vt[s] = vis_get(vis, s) ? 0 : VT_NONE;
+    for (int32_t s = tid; s < dbs; s += NT) {
+        vt[s] = vis_get(vis, s) ? 0 : VT_NONE;
+        if (direct) {
+            const int32_t t = tok[s];
+            if (t >= 0 && t < prefill) inv[t] = static_cast<uint16_t>(s + 1);
+        }
+    }
     if (!flagged) {
         Guard g;
         bool bad = false;
@@ -429,6 +454,25 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     inf = CLS_INV << 30;
                 } else if (t >= prefill) {
                     inf = CLS_EXT << 30;
+                } else if (direct) {
+                    const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
+                    uint32_t *w = inv32 + (t >> 1);
+                    const uint32_t sh = (static_cast<uint32_t>(t) & 1u) * 16u;
+                    uint32_t old = *reinterpret_cast<volatile uint32_t *>(w);
+                    const uint32_t e0 = (old >> sh) & 0xFFFFu;
+                    if (e0 != 0u && e0 <= static_cast<uint32_t>(padded)) {
+                        inf = (CLS_HIT << 30) | (e0 - 1u);
+                        lds_min16(vt32, e0 - 1u, static_cast<uint16_t>(k + 1));
+                    } else {
+                        inf = CLS_CAND << 30;
+                        for (;;) {  // keep the smallest position of the token
+                            const uint32_t cur = (old >> sh) & 0xFFFFu;
+                            if (cur != 0u && cur <= v) break;
+                            const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
+                            if (prev == old) break;
+                            old = prev;
+                        }
+                    }
                 } else {
                     const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
                     const uint32_t th = ht_hash(t);
@@ -481,12 +525,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             if (g.code) atomicOr(&ms.ovf, 1);
         }
+        SUBSTAMP(3);
         __syncthreads();
         STAMP(3);
         // the first occurrence of each candidate token: its cell's final value
         for (int32_t k = tid; k < K; k += NT) {
             if ((pinf[k] >> 30) != CLS_CAND) continue;
-            const uint32_t e = ht[pcell[k]];
+            const uint32_t e = direct ? inv[ptok[k]] : ht[pcell[k]];
             pinf[k] = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
         }
         __syncthreads();
@@ -502,7 +547,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if (k < K) {
                     const uint32_t inf = pinf[k];
                     const uint32_t f = ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ? 1u : 0u;
-                    if (f) ht[pcell[k]] = 0;
+                    if (f && !direct) ht[pcell[k]] = 0;
                     fl |= f << i;
                     cnt += f;
                 }
@@ -539,10 +584,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (v == VT_NONE) snM |= 1ull << j;
             else if (v != 0) smM |= 1ull << j;
         }
+        SUBSTAMP(0);
         const uint32_t cSN = static_cast<uint32_t>(__popcll(snM)), cSM = static_cast<uint32_t>(__popcll(smM));
         const uint32_t qb = bits_for(static_cast<uint32_t>(Q));
         uint32_t tot;
         const uint32_t pre = block_exscan(cSN | (cSM << 16), qb | (qb << 16), ms.wt1, tot);
+        SUBSTAMP(1);
         preSN = pre & 0xFFFFu;
         preSM = pre >> 16;
         uint32_t nsn = preSN, nsm = preSM;
@@ -562,6 +609,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (tid == 0) ms.nSM = static_cast<int32_t>(tot >> 16);
+        SUBSTAMP(2);
         __syncthreads();
         STAMP(6);
 
@@ -598,6 +646,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 tb[i] = dec;
             }
         }
+        SUBSTAMP(5);
         __syncthreads();
         STAMP(7);
         // undecided slots, one wave each: count the evictions already settled
@@ -627,7 +676,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
             }
         }
+        SUBSTAMP(6);
         __syncthreads();
+        SUBSTAMP(7);
         if (ms.nRest > 0 && wave == 0) {  // the rest, in ring order
             const int32_t nSM = ms.nSM;
             for (int32_t c = 0; c < nSM; c += 64) {
@@ -1003,6 +1054,13 @@ hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overf
 }  // namespace kvx
 
 #ifdef KVX_SIEVE_PHASE_STAMPS
+extern "C" int kvx_dbg_read_sub(unsigned long long *out, int rows)
+{
+    if (rows > 1024) rows = 1024;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(kvx::kvx_dbg_sub), sizeof(unsigned long long) * 16 * rows, 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+
 extern "C" int kvx_dbg_read_stamps(unsigned long long *out, int rows)
 {
     if (rows > 1024) rows = 1024;
