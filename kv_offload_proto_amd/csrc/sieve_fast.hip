@@ -108,7 +108,8 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t v)
 
 // Exclusive prefix over the workgroup of per-thread values whose set bits all
 // lie in `bits` (small counts: one ballot per bit), in thread order.  Returns
-// the prefix and the total; ends with a barrier, after which `wt` is free.
+// the prefix and the total.  `wt` is read after the call returns: the next
+// use of the same `wt` must come after another barrier.
 __device__ __forceinline__ uint32_t block_exscan(uint32_t v, uint32_t bits, uint32_t *wt, uint32_t &total)
 {
     const uint32_t lane = lane_id();
@@ -131,7 +132,6 @@ __device__ __forceinline__ uint32_t block_exscan(uint32_t v, uint32_t bits, uint
         all += c;
     }
     total = all;
-    __syncthreads();
     return off + pre;
 }
 
@@ -529,12 +529,15 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         __syncthreads();
         STAMP(3);
         // the first occurrence of each candidate token: its cell's final value
-        for (int32_t k = tid; k < K; k += NT) {
-            if ((pinf[k] >> 30) != CLS_CAND) continue;
-            const uint32_t e = direct ? inv[ptok[k]] : ht[pcell[k]];
-            pinf[k] = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
+        // (with the direct map, read in the compaction pass below)
+        if (!direct) {
+            for (int32_t k = tid; k < K; k += NT) {
+                if ((pinf[k] >> 30) != CLS_CAND) continue;
+                const uint32_t e = ht[pcell[k]];
+                pinf[k] = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
+            }
+            __syncthreads();
         }
-        __syncthreads();
         STAMP(4);
         // ---- candidate prefix counts per position (contiguous chunk per
         // lane); first occurrences drop their provisional entries
@@ -545,7 +548,11 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             for (int32_t i = 0; i < P; ++i) {
                 const int32_t k = k0 + i;
                 if (k < K) {
-                    const uint32_t inf = pinf[k];
+                    uint32_t inf = pinf[k];
+                    if (direct && (inf >> 30) == CLS_CAND) {
+                        inf = (CLS_CAND << 30) | (static_cast<uint32_t>(inv[ptok[k]]) - static_cast<uint32_t>(padded) - 1u);
+                        pinf[k] = inf;
+                    }
                     const uint32_t f = ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ? 1u : 0u;
                     if (f && !direct) ht[pcell[k]] = 0;
                     fl |= f << i;
