@@ -391,10 +391,12 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     hipLaunchKernelGGL(kvx_gather_list, dim3(static_cast<uint32_t>(listBlocks)), dim3(256), 0, stream, P);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // one 64-row task per wave covers every listed row of a full batch
+    // 64-row tasks, grid-stride; 512 waves keep enough 16-byte reads in
+    // flight for the host link, and few workgroups keep the completion
+    // ticket cheap
     uint64_t copyBlocks = (positions + 64ull * kWaves - 1ull) / (64ull * kWaves);
     if (copyBlocks < 1) copyBlocks = 1;
-    if (copyBlocks > 1024) copyBlocks = 1024;
+    if (copyBlocks > 128) copyBlocks = 128;
     hipLaunchKernelGGL(kvx_gather_copy, dim3(static_cast<uint32_t>(copyBlocks)), dim3(256), 0, stream, P);
     return hipGetLastError();
 }
