@@ -223,9 +223,10 @@ def main():
     log("[bench] {}: setup {:.1f} s (HBM pool + {} pinned segments of {:.2f} GiB)".format(
         cfg.name, runner.setup_s, cfg.node_num, runner.pool.pool.segments[0].size_bytes / 2**30))
     export_us = runner.export_prefill()
-    export_gbps = runner.export_bytes / (export_us * 1e-6) / 1e9
-    log("[bench] prefill export: {} rows x {} layers = {} B in {:.1f} us ({:.1f} GB/s)".format(
-        cfg.host_reqs * cfg.prefill, cfg.layers, runner.export_bytes, export_us, export_gbps))
+    export_gbps = runner.export_moved_bytes / (export_us * 1e-6) / 1e9
+    log("[bench] prefill export: {} rows x {} layers ({} B of rows, {} B moved) in {:.1f} us ({:.1f} GB/s moved)".format(
+        cfg.host_reqs * cfg.prefill, cfg.layers, runner.export_bytes, runner.export_moved_bytes, export_us,
+        export_gbps))
     runner.admit_all()
     link = measure_link_peak(runner, args.link_mib, log)
 
@@ -275,14 +276,21 @@ def main():
     sieve_gbps_alg = sb * len(timed) / (sum(sieve_us) * 1e-6) / 1e9
     traffic, traffic_src = load_traffic(cfg.name)
 
-    def traffic_of(*kernels):
-        if not all(k in traffic for k in kernels):
-            return None
-        return sum(traffic[k] for k in kernels)
+    def traffic_of(*prefixes):
+        """Summed bytes per dispatch of the profiled kernels named by each
+        prefix (a template kernel is listed with its arguments), or None."""
+        total = 0.0
+        for pre in prefixes:
+            hits = [v for k, v in traffic.items() if k == pre or k.startswith(pre + "<")]
+            if not hits:
+                return None
+            total += sum(hits)
+        return total
 
-    gather_roof = {"kernel": "kvx_gather_prep+kvx_gather_copy", "bound": "hbm", "achieved": gather_gbps_alg,
+    gather_kernels = ("kvx_gather_prep", "kvx_gather_list", "kvx_gather_copy")
+    gather_roof = {"kernel": "+".join(gather_kernels), "bound": "hbm", "achieved": gather_gbps_alg,
                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gather_gbps_alg / HBM_PEAK_GBPS,
-                   "traffic": traffic_of("kvx_gather_prep", "kvx_gather_copy"), "traffic_source": traffic_src,
+                   "traffic": traffic_of(*gather_kernels), "traffic_source": traffic_src,
                    "bytes_per_launch": sum(gather_bytes) / len(timed),
                    "avg_launch_us": sum(gather_us) / len(timed),
                    "link": {"achieved": link_gbps, "peak": link["peak_GBps"], "unit": "GB/s",
@@ -319,7 +327,8 @@ def main():
                    "frac_of_link_peak": link_gbps / link["peak_GBps"], "frac_of_hbm_peak": link_gbps / HBM_PEAK_GBPS,
                    "rows_per_s": rows / (sum(gather_us) * 1e-6), "rows": rows},
         "host_link": link,
-        "export": {"bytes": runner.export_bytes, "us": export_us, "GBps": export_gbps},
+        "export": {"row_bytes_total": runner.export_bytes, "bytes_moved": runner.export_moved_bytes,
+                   "us": export_us, "GBps_moved": export_gbps},
         "roofline": dominant,
         "roofline_other": other,
         "verify": ok,

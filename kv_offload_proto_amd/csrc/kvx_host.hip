@@ -258,7 +258,7 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         int lds = 0;
         hipCheck(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_id),
                  "hipDeviceGetAttribute(LDS)");
-        g.ldsLimit = static_cast<size_t>(lds) - 256;  // room for the kernels' static LDS
+        g.ldsLimit = static_cast<size_t>(lds) - 512;  // room for the kernels' static LDS (under 512 B)
         hipCheck(kvx::sieve_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS)");
         hipCheck(kvx::sieve_fast_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS fast)");
         void *c = nullptr;
@@ -514,8 +514,7 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
                            visited_stride_b;
         const bool fastShape = top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535 &&
-                               device_buffer_size <= 64u * kvx::kFastThreads &&
-                               top_k <= 32u * kvx::kFastThreads;
+                               device_buffer_size <= 32u * kvx::kFastThreads && htSize <= 32768;
         const size_t ldsFast = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
                                                 visited_stride_b, false).total;
         const size_t ldsCompact = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,

@@ -55,61 +55,51 @@ struct RowScratch {
 // LDS layout of the parallel SIEVE kernel (byte offsets, 16-byte aligned):
 // the state row, then per-position, per-slot, per-event and per-cell scratch.
 // ---------------------------------------------------------------------------
-constexpr int kFastThreads = 1024;
+#ifndef KVX_FAST_THREADS
+#define KVX_FAST_THREADS 1024
+#endif
+constexpr int kFastThreads = KVX_FAST_THREADS;
 
 struct FastLayout {
-    uint32_t tok, ht, vis, ptok, pinf, vt, candPre, evslot, evold, cvlist, eseq, tb, smA, smB, kst, vset, ber, bg,
-        bm, bnew, total;
+    uint32_t tok, ht, vis, ptok, pinf, vt, evslot, smKp, eseq, tb, smA, smB, vset, ber, occ, cmask, emask, smask,
+        total;
 };
 
 __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
 
-// LDS regions of the parallel SIEVE kernel for one batch row.  ptok+pinf and
-// smA+smB are each contiguous and reused as 64-bit arrays of topK entries in
-// the table-update phase.  In the compact form (rows whose full layout does
-// not fit) the tokens row is replaced by the 16-bit Knuth hash of each slot's
-// token (full tokens stay in HBM), and regions with disjoint lifetimes share
-// memory: tb with candPre, eseq with the SM k list (cvlist), and the four
-// table bitmaps with vt.
+// LDS regions of the parallel SIEVE kernel for one batch row.  Regions with
+// disjoint lifetimes share memory (the kernel names the aliases): the SM k
+// list with the conversions' old slots, the event sequence with the list of
+// undecided SM slots, and the SM list with the per-event cells and tokens.
+// In the compact form (rows whose full layout does not fit) the tokens row is
+// replaced by the Knuth hash of each slot's token (full tokens stay in HBM).
+// cmask/emask/smask hold one 64-bit ballot per (wave, 1024-entry block).
 __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint32_t htSize, uint32_t topK,
                                                            uint32_t visStrideB, bool compact = false)
 {
     FastLayout l{};
     uint32_t o = 0;
     const uint32_t bmBytes = htSize / 8u;
+    const uint32_t blocks = (topK + kFastThreads - 1u) / kFastThreads;
+    const uint32_t maskBytes = blocks * (kFastThreads / 64u) * 8u;
     l.tok = o;     o += align16(padded * (compact ? 2u : 4u));
     l.ht = o;      o += align16(htSize * 2u);
     l.vis = o;     o += align16(visStrideB);
     l.ptok = o;    o += align16(topK * 4u);
     l.pinf = o;    o += align16(topK * 4u);
-    l.vt = o;
-    o += compact ? align16(padded * 2u > 4u * bmBytes ? padded * 2u : 4u * bmBytes) : align16(padded * 2u);
-    l.candPre = o; o += align16((topK + 1u) * 2u);
+    l.vt = o;      o += align16(padded * 2u);
     l.evslot = o;  o += align16(topK * 2u);
-    l.evold = o;   o += align16(topK * 2u);
-    l.cvlist = o;  o += align16(topK * 2u);
-    if (compact) {
-        l.eseq = l.cvlist;
-        l.tb = l.candPre;
-    } else {
-        l.eseq = o;    o += align16(topK * 2u);
-        l.tb = o;      o += align16((topK + 1u) * 2u);
-    }
+    l.smKp = o;    o += align16(topK * 2u + 16u);
+    l.eseq = o;    o += align16(topK * 2u);
+    l.tb = o;      o += align16((topK + 1u) * 2u);
     l.smA = o;     o += align16(topK * 4u);
     l.smB = o;     o += align16(topK * 4u);
-    l.kst = o;     o += align16(topK * 4u);
     l.vset = o;    o += align16(visStrideB);
-    if (compact) {
-        l.ber = l.vt;
-        l.bg = l.vt + bmBytes;
-        l.bm = l.vt + 2u * bmBytes;
-        l.bnew = l.vt + 3u * bmBytes;
-    } else {
-        l.ber = o;     o += align16(bmBytes);
-        l.bg = o;      o += align16(bmBytes);
-        l.bm = o;      o += align16(bmBytes);
-        l.bnew = o;    o += align16(bmBytes);
-    }
+    l.ber = o;     o += align16(bmBytes);
+    l.occ = o;     o += align16(bmBytes);
+    l.cmask = o;   o += maskBytes;
+    l.emask = o;   o += maskBytes;
+    l.smask = o;   o += maskBytes;
     l.total = o;
     return l;
 }

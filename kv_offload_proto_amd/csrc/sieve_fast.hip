@@ -23,30 +23,38 @@
 // classification, dedup, the event sequence, marks, outputs, visited bits --
 // is prefix sums and scatters.
 //
-// Phases:
-//   stage    tokens/table/visited/topK row into LDS; table consistency check
+// Phases (one barrier each unless noted):
+//   stage    tokens/table/visited/topK row into LDS, per-slot visited flags,
+//            the table's occupancy bitmap and (when the prefill fits) a
+//            direct token -> slot map; table consistency check (first step)
 //   classify hit / candidate / invalid / decode-extension per position; the
-//            first hit time of every slot (LDS min)
-//   dedup    provisional table entries padded+1+k, smallest k wins
-//   compact  candidate prefix counts per position
-//   ring     classes per ring offset from the hand, SM list with its counts
-//   decide   one wave: SM slots in ring order, 64 at a time, speculating that
-//            none is evicted and correcting at each eviction
-//   events   the merged event sequence (a prefix scan over positions)
-//   marks    per ring offset: evicted at event p / passed at event p
-//   outputs  slots, is_miss, visited bits
-//   table    erase the evicted tokens (Algorithm R deletions commute when
-//            each cluster is done right to left), insert the new tokens with
-//            a tentative parallel placement (the occupied cells do not depend
-//            on order) and redo, in event order, every final cluster that
-//            holds more than one new token.  Linear probing with Algorithm R
-//            leaves the table equal to inserting the live keys in insertion
-//            order, so the result is the sequential table byte for byte.
+//            first hit time of every slot (LDS min); candidate dedup (smallest
+//            position per token) through the direct map or provisional
+//            table entries
+//   scan     ballots of the candidates' first occurrences and a prefix scan
+//            of the ring classes; the SM slots before the M-th SN slot
+//   decide   per SM slot, bounds that settle almost all of them in parallel;
+//            the rest in ring order
+//   events   eviction prefix over the SM slots and the event sequence in
+//            position order, both from ballot masks
+//   marks    per ring offset: evicted at event p / passed at event p, the
+//            evicted token's table cell, each event's slot and new token
+//   outputs  slots, is_miss, visited bits; erase the evicted tokens
+//            (Algorithm R deletions commute when each pre-step cluster is
+//            done right to left by its rightmost marked cell)
+//   insert   tentative parallel placement of the new tokens (the occupied
+//            cells do not depend on order), entries naming the event; a key
+//            alone in its final cluster takes its cell, and the earliest key
+//            of every other cluster redoes it in event order.  Linear probing
+//            with Algorithm R leaves the table equal to inserting the live
+//            keys in insertion order, so the result is the sequential table
+//            byte for byte.
 //
-// Preconditions, checked in the kernel: the table indexes exactly the
-// non-negative tokens of slots [0, dbs) (each found at its own slot),
-// padded + 1 + topK <= 65535, topK < 16383, no hand wrap within the step.
-// Otherwise the row is restaged from HBM and the sequential recurrence runs.
+// Shape preconditions, checked by the launcher: padded + 1 + topK <= 65535,
+// topK < 16383, dbs <= 32 * 1024, htSize <= 32768.  State preconditions,
+// checked in the kernel: the table indexes exactly the non-negative tokens of
+// slots [0, dbs) (each found at its own slot), no hand wrap within the step;
+// otherwise the row is restaged from HBM and the sequential recurrence runs.
 #include "kvx_internal.h"
 #include "sieve_common.h"
 
@@ -55,11 +63,19 @@ namespace {
 
 using namespace sieve;
 
+// Global-memory pointers carry their address space, so the compiler emits
+// global rather than flat instructions: flat ones also count against the LDS
+// wait counter and stall the LDS work that follows them.
+#define KVX_G __attribute__((address_space(1)))
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 16-byte chunk
+
 constexpr int NT = kFastThreads;
 constexpr int NWAVES = NT / 64;
 
 constexpr uint32_t CLS_INV = 0u, CLS_EXT = 1u, CLS_HIT = 2u, CLS_CAND = 3u;
 constexpr uint16_t VT_NONE = 0xFFFF, VT_EVICTED = 0x8000, VT_PASSED = 0x4000, VT_NOCONV = 0x3FFF;
+constexpr uint16_t HV_EMPTY = 0xFFFF;  // compact form: slot without a token (hashes are masked below 2^15)
+constexpr uint32_t NOCELL = 0xFFFFu;   // evicted slot without a table entry
 // sieve_hand[row][1]: set when this kernel left the row's table consistent
 constexpr int32_t kCanonFlag = 0x4B565843;
 
@@ -76,7 +92,15 @@ __device__ unsigned long long kvx_dbg_sub[1024][16];
     do {                                                              \
         if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = clock64();  \
     } while (0)
+__device__ unsigned long long kvx_dbg_w[64][16][16];
+#define WSTAMP(i)                                                          \
+    do {                                                                   \
+        if (lane == 0 && bid < 64) kvx_dbg_w[bid][wave][i] = clock64();    \
+    } while (0)
 #else
+#define WSTAMP(i) \
+    do {          \
+    } while (0)
 #define STAMP(i) \
     do {         \
     } while (0)
@@ -86,10 +110,11 @@ __device__ unsigned long long kvx_dbg_sub[1024][16];
 #endif
 
 struct Misc {
-    int32_t nTok, nEnt, bad, ovf, late;
-    int32_t M, nSM, T, nConv, N, nUnd, nRest, uEnd, nTakes, nMulti;
-    uint32_t wt0[NWAVES];
-    uint32_t wt1[NWAVES];
+    int32_t bad, ovf, late, nSM, nUnd, nRest, uEnd, nTakes;
+    uint32_t wtok[NWAVES];
+    uint32_t went[NWAVES];
+    uint32_t wring[NWAVES];
+    uint32_t wcand[NWAVES];
 };
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
@@ -106,35 +131,6 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t v)
     return v;
 }
 
-// Exclusive prefix over the workgroup of per-thread values whose set bits all
-// lie in `bits` (small counts: one ballot per bit), in thread order.  Returns
-// the prefix and the total.  `wt` is read after the call returns: the next
-// use of the same `wt` must come after another barrier.
-__device__ __forceinline__ uint32_t block_exscan(uint32_t v, uint32_t bits, uint32_t *wt, uint32_t &total)
-{
-    const uint32_t lane = lane_id();
-    const int wave = static_cast<int>(threadIdx.x >> 6);
-    uint32_t pre = 0, tot = 0;
-    while (bits != 0u) {
-        const int b = __builtin_ctz(bits);
-        bits &= bits - 1u;
-        const uint64_t bal = __ballot((v >> b) & 1u);
-        pre += lanes_below(bal, lane) << b;
-        tot += static_cast<uint32_t>(__popcll(bal)) << b;
-    }
-    if (lane == 0) wt[wave] = tot;
-    __syncthreads();
-    uint32_t off = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < NWAVES; ++w) {
-        const uint32_t c = wt[w];
-        off += (w < wave) ? c : 0u;
-        all += c;
-    }
-    total = all;
-    return off + pre;
-}
-
 // Bit mask covering the values 0..n.
 __host__ __device__ __forceinline__ uint32_t bits_for(uint32_t n)
 {
@@ -143,12 +139,49 @@ __host__ __device__ __forceinline__ uint32_t bits_for(uint32_t n)
     return m;
 }
 
+// Exclusive prefix counts over 64-bit ballot masks mk[e], e = block *
+// NWAVES + wave (so entry e covers items 64e..64e+63 of a lane-strided
+// index), computed by every wave for itself: lane L sums g consecutive
+// entries.  Set up and query with the whole wave active.
+struct MaskPrefix {
+    const uint64_t *mk;
+    int32_t g;
+    uint32_t ex;     // prefix of this lane's first entry
+    uint32_t total;  // set bits in all entries
+
+    __device__ __forceinline__ void init(const uint64_t *m, int32_t nE, uint32_t lane)
+    {
+        mk = m;
+        g = (nE + 63) >> 6;
+        if (g < 1) g = 1;
+        const int32_t e0 = static_cast<int32_t>(lane) * g;
+        uint32_t s = 0;
+        for (int32_t x = e0; x < e0 + g && x < nE; ++x) s += static_cast<uint32_t>(__popcll(mk[x]));
+        uint32_t incl = s;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), o));
+            if (static_cast<int>(lane) >= o) incl += t;
+        }
+        ex = incl - s;
+        total = static_cast<uint32_t>(__shfl(static_cast<int>(incl), 63));
+    }
+    // set bits before bit `bit` of entry e
+    __device__ __forceinline__ uint32_t before(int32_t e, uint32_t bit) const
+    {
+        const int32_t L = e / g;
+        uint32_t c = static_cast<uint32_t>(__shfl(static_cast<int>(ex), L));
+        for (int32_t x = L * g; x < e; ++x) c += static_cast<uint32_t>(__popcll(mk[x]));
+        return c + static_cast<uint32_t>(__popcll(mk[e] & ((1ull << bit) - 1ull)));
+    }
+};
+
 // 16-bit LDS min via a CAS on the containing word.
 __device__ __forceinline__ void lds_min16(uint32_t *w32, uint32_t i, uint16_t v)
 {
     uint32_t *w = w32 + (i >> 1);
     const uint32_t sh = (i & 1u) * 16u;
-    uint32_t old = *reinterpret_cast<volatile uint32_t *>(w);
+    uint32_t old = *w;  // a stale value only costs a CAS retry
     for (;;) {
         const uint32_t cur = (old >> sh) & 0xFFFFu;
         if (cur <= v) return;
@@ -166,7 +199,7 @@ __device__ __forceinline__ int32_t lds_claim16(uint32_t *w32, int32_t idx, int32
     for (int32_t n = 0; n <= mask; ++n) {
         uint32_t *w = w32 + (idx >> 1);
         const uint32_t sh = (static_cast<uint32_t>(idx) & 1u) * 16u;
-        uint32_t old = *reinterpret_cast<volatile uint32_t *>(w);
+        uint32_t old = *w;
         for (;;) {
             if (((old >> sh) & 0xFFFFu) != 0u) break;
             const uint32_t prev = atomicCAS(w, old, old | (static_cast<uint32_t>(v) << sh));
@@ -211,18 +244,17 @@ __device__ void rdel_at(uint16_t *ht, const void *tokv, int32_t ntok, int32_t c,
 }
 
 // Copy n bytes (multiple of 16) with the workgroup, four 16-byte chunks in
-// flight per lane.
-__device__ __forceinline__ void wg_copy16(void *dst, const void *src, uint32_t n)
+// flight per lane.  D and S are v4u in the LDS or global address space.
+template <typename D, typename S>
+__device__ __forceinline__ void wg_copy16(D *d, S *s, uint32_t n)
 {
-    const uint4 *s = static_cast<const uint4 *>(src);
-    uint4 *d = static_cast<uint4 *>(dst);
     const uint32_t n16 = n / 16u;
     uint32_t i = threadIdx.x;
     for (; i + 3u * NT < n16; i += 4u * NT) {
-        const uint4 a = s[i];
-        const uint4 b = s[i + NT];
-        const uint4 c = s[i + 2u * NT];
-        const uint4 e = s[i + 3u * NT];
+        const v4u a = s[i];
+        const v4u b = s[i + NT];
+        const v4u c = s[i + 2u * NT];
+        const v4u e = s[i + 3u * NT];
         d[i] = a;
         d[i + NT] = b;
         d[i + 2u * NT] = c;
@@ -257,40 +289,30 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const int32_t wave = tid >> 6;
     if (bid >= maxNumReqs) return;
 
-    int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
+    int32_t numReal = *(KVX_G const int32_t *)(a.numReal);
     if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
-    int32_t *rs = reinterpret_cast<int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
-    int8_t *rm = reinterpret_cast<int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
+    KVX_G int32_t *rs = (KVX_G int32_t *)(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
+    KVX_G int8_t *rm = (KVX_G int8_t *)(a.isMiss) + static_cast<int64_t>(bid) * K;
     if (bid >= numReal) {
-        write_dummy_row(rs, rm, K);
+        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
-    const int64_t reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
+    const int64_t reqIdx = ((KVX_G const int64_t *)(a.reqPoolIndices))[bid];
     if (reqIdx < 0 || reqIdx >= poolSize) {
-        write_dummy_row(rs, rm, K);
+        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
-    const int32_t seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
-    const int32_t prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
-    const int32_t *rt = reinterpret_cast<const int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
-    int32_t *gTok = reinterpret_cast<int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
-    uint8_t *gVis = reinterpret_cast<uint8_t *>(a.deviceBufferVisited) + reqIdx * visStrideB;
-    uint16_t *gHt = reinterpret_cast<uint16_t *>(a.deviceBufferHt) + reqIdx * H;
-    int32_t *gHand = reinterpret_cast<int32_t *>(a.sieveHand) + reqIdx * kHandStride;
+    const int32_t seqLen = ((KVX_G const int32_t *)(a.seqLens))[bid];
+    const int32_t prefill = ((KVX_G const int32_t *)(a.prefillLens))[reqIdx];
+    KVX_G const int32_t *rt = (KVX_G const int32_t *)(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    KVX_G int32_t *gTok = (KVX_G int32_t *)(a.deviceBufferTokens) + reqIdx * padded;
+    KVX_G uint8_t *gVis = (KVX_G uint8_t *)(a.deviceBufferVisited) + reqIdx * visStrideB;
+    KVX_G uint16_t *gHt = (KVX_G uint16_t *)(a.deviceBufferHt) + reqIdx * H;
+    KVX_G int32_t *gHand = (KVX_G int32_t *)(a.sieveHand) + reqIdx * kHandStride;
 
     const FastLayout lay = fast_layout(padded, H, K, visStrideB, kC);
     int32_t *tok = reinterpret_cast<int32_t *>(smem + lay.tok);    // full form: tokens
-    uint16_t *hv = reinterpret_cast<uint16_t *>(smem + lay.tok);   // compact form: token hashes
-    // token of slot s equals t (th = its hash); the compact form checks the
-    // hash in LDS and confirms with the HBM row
-    auto tok_is = [&](uint32_t s, int32_t t, uint32_t th) -> bool {
-        if constexpr (kC) return hv[s] == th && gTok[s] == t;
-        else return tok[s] == t;
-    };
-    auto tok_hash = [&](uint32_t s) -> uint32_t {
-        if constexpr (kC) return hv[s];
-        else return ht_hash(tok[s]);
-    };
+    uint16_t *hv = reinterpret_cast<uint16_t *>(smem + lay.tok);   // compact form: masked token hashes
     uint16_t *ht = reinterpret_cast<uint16_t *>(smem + lay.ht);
     uint32_t *ht32 = reinterpret_cast<uint32_t *>(smem + lay.ht);
     uint8_t *vis = smem + lay.vis;
@@ -299,37 +321,57 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *pinf = reinterpret_cast<uint32_t *>(smem + lay.pinf);
     uint16_t *vt = reinterpret_cast<uint16_t *>(smem + lay.vt);
     uint32_t *vt32 = reinterpret_cast<uint32_t *>(smem + lay.vt);
-    uint16_t *candPre = reinterpret_cast<uint16_t *>(smem + lay.candPre);
     uint16_t *evslot = reinterpret_cast<uint16_t *>(smem + lay.evslot);
-    uint16_t *evold = reinterpret_cast<uint16_t *>(smem + lay.evold);
-    uint16_t *smKp = reinterpret_cast<uint16_t *>(smem + lay.cvlist);  // k of SM slots that can be evicted, else 0
+    uint16_t *smKp = reinterpret_cast<uint16_t *>(smem + lay.smKp);  // k of SM slots that can be evicted, else 0
     uint16_t *eseq = reinterpret_cast<uint16_t *>(smem + lay.eseq);
     uint16_t *tb = reinterpret_cast<uint16_t *>(smem + lay.tb);
     uint32_t *smA = reinterpret_cast<uint32_t *>(smem + lay.smA);  // ring offset | k << 16
     uint32_t *smB = reinterpret_cast<uint32_t *>(smem + lay.smB);  // SN before | candidates before k << 16
-    uint32_t *kst = reinterpret_cast<uint32_t *>(smem + lay.kst);
     uint32_t *vset = reinterpret_cast<uint32_t *>(smem + lay.vset);
-    uint32_t *ber = reinterpret_cast<uint32_t *>(smem + lay.ber);
-    uint32_t *bg = reinterpret_cast<uint32_t *>(smem + lay.bg);
-    uint32_t *bm = reinterpret_cast<uint32_t *>(smem + lay.bm);
-    uint32_t *bnew = reinterpret_cast<uint32_t *>(smem + lay.bnew);
+    uint32_t *ber = reinterpret_cast<uint32_t *>(smem + lay.ber);   // cells of evicted tokens
+    uint32_t *occ = reinterpret_cast<uint32_t *>(smem + lay.occ);   // occupied cells of the pre-step table
+    uint8_t *occ8 = smem + lay.occ;
+    uint64_t *cmask = reinterpret_cast<uint64_t *>(smem + lay.cmask);  // first occurrences of candidates
+    uint64_t *emask = reinterpret_cast<uint64_t *>(smem + lay.emask);  // event positions
+    uint64_t *smask = reinterpret_cast<uint64_t *>(smem + lay.smask);  // evicted SM slots
     // direct token -> slot map for rows whose prefill fits the LDS left over
-    // (after the layout): 0 = not resident, slot+1 when resident,
-    // padded+1+k for a candidate's first position k
+    // (after the layout).  It is not cleared: an entry is trusted only when it
+    // checks out -- slot+1 of a slot holding the token, or padded+1+k of a
+    // position k holding it (a candidate's first position, smallest k wins).
     const int32_t invCap = static_cast<int32_t>(a.reserved >> 8);
     const bool direct = !kC && prefill > 0 && prefill <= invCap;
     uint16_t *inv = reinterpret_cast<uint16_t *>(smem + lay.total);
     uint32_t *inv32 = reinterpret_cast<uint32_t *>(smem + lay.total);
     // reuse of regions whose earlier contents are dead by then
-    uint32_t *pcell = smA;                                             // dedup: provisional cell per position
-    uint16_t *posSM = evslot;                                          // decide: SM index + 1 per first-hit position
-    uint32_t *undl = kst;                                              // decide: undecided SM indices
-    uint32_t *ecell = smA;                                             // table: erase cell (| leader bit) per event
-    uint32_t *ntokv = smB;                                             // table: new token per event
-    uint64_t *mlist = reinterpret_cast<uint64_t *>(smem + lay.ptok);  // multi-cluster keys
-    uint64_t *msort = reinterpret_cast<uint64_t *>(smem + lay.smA);   // the same, sorted
+    uint32_t *pcell = smA;                                   // classify: provisional cell per position
+    uint16_t *posSM = evslot;                                // SM index + 1 per first-hit position
+    uint16_t *undl = eseq;                                   // decide: undecided SM indices
+    uint16_t *evold = smKp;                                  // conversions: the slot evicted before the hit
+    uint32_t *ecell = smA;                                   // per event: table cell | slot << 16
+    int32_t *ntokv = reinterpret_cast<int32_t *>(smB);       // per event: the token inserted
 
-    // ---- stage the state row and the topK row; count live tokens and table entries
+    // token of slot s equals t (th = its hash); the compact form checks the
+    // hash in LDS and confirms with the HBM row
+    auto tok_is = [&](uint32_t s, int32_t t, uint32_t th) -> bool {
+        if constexpr (kC) return hv[s] == (th & static_cast<uint32_t>(mask)) && gTok[s] == t;
+        else return tok[s] == t;
+    };
+    auto slot_live = [&](int32_t s) -> bool {
+        if constexpr (kC) return hv[s] != HV_EMPTY;
+        else return tok[s] >= 0;
+    };
+    auto slot_home = [&](int32_t s) -> int32_t {
+        if constexpr (kC) return static_cast<int32_t>(hv[s]) & mask;
+        else return static_cast<int32_t>(ht_hash(tok[s])) & mask;
+    };
+
+    const int32_t P = (K + NT - 1) / NT;    // positions per lane: k = tid + q * NT
+    const int32_t Q = (dbs + NT - 1) / NT;  // ring offsets per lane: u = tid * Q + j
+    const int32_t u0 = tid * Q;
+
+    // ---- stage the state row and the topK row; visited flags per slot (vt),
+    // the direct map, the table's occupancy bitmap; count live tokens and
+    // table entries
     STAMP(0);
     int32_t hand0 = gHand[0];
     if (hand0 < 0 || hand0 >= dbs) hand0 = 0;  // hisp_sieve_update.cpp:108-111
@@ -337,84 +379,93 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     {
         const int32_t nt = padded >> 2, nh = H >> 3, nv = visStrideB >> 4;  // 16-byte chunks
         const int32_t nAll = nt + nh + nv;
-        const uint4 *sT = reinterpret_cast<const uint4 *>(gTok);
-        const uint4 *sH = reinterpret_cast<const uint4 *>(gHt);
-        const uint4 *sV = reinterpret_cast<const uint4 *>(gVis);
+        KVX_G const v4u *sT = (KVX_G const v4u *)gTok;
+        KVX_G const v4u *sH = (KVX_G const v4u *)gHt;
+        KVX_G const v4u *sV = (KVX_G const v4u *)gVis;
         uint32_t nTok = 0, nEnt = 0;
         int32_t t0 = 0, t1 = 0;
         const bool h0 = tid < K, h1 = tid + NT < K;
         if (h0) t0 = rt[tid];
         if (h1) t1 = rt[tid + NT];
         for (int32_t c0 = tid; c0 < nAll; c0 += 4 * NT) {
-            uint4 v[4];
+            v4u v[4];
+            uint32_t vb[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int32_t c = c0 + j * NT;
-                if (c < nt) v[j] = sT[c];
-                else if (c < nt + nh) v[j] = sH[c - nt];
-                else if (c < nAll) v[j] = sV[c - nt - nh];
+                if (c < nt) {
+                    v[j] = sT[c];
+                    vb[j] = gVis[c >> 1];  // the 8 visited bits of slots 8(c/2)..
+                } else if (c < nt + nh) {
+                    v[j] = sH[c - nt];
+                } else if (c < nAll) {
+                    v[j] = sV[c - nt - nh];
+                }
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int32_t c = c0 + j * NT;
                 if (c < nt) {
+                    const int32_t tt[4] = {static_cast<int32_t>(v[j].x), static_cast<int32_t>(v[j].y),
+                                           static_cast<int32_t>(v[j].z), static_cast<int32_t>(v[j].w)};
                     if constexpr (kC) {
-                        const uint32_t a0 = ht_hash(static_cast<int32_t>(v[j].x)), a1 = ht_hash(static_cast<int32_t>(v[j].y));
-                        const uint32_t a2 = ht_hash(static_cast<int32_t>(v[j].z)), a3 = ht_hash(static_cast<int32_t>(v[j].w));
-                        reinterpret_cast<uint2 *>(hv)[c] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
-                    } else {
-                        reinterpret_cast<uint4 *>(tok)[c] = v[j];
-                    }
-                    const int32_t s0 = c * 4;
-                    nTok += (s0 < dbs && static_cast<int32_t>(v[j].x) >= 0) + (s0 + 1 < dbs && static_cast<int32_t>(v[j].y) >= 0) +
-                            (s0 + 2 < dbs && static_cast<int32_t>(v[j].z) >= 0) + (s0 + 3 < dbs && static_cast<int32_t>(v[j].w) >= 0);
-                } else if (c < nt + nh) {
-                    reinterpret_cast<uint4 *>(ht)[c - nt] = v[j];
-                    const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+                        uint32_t hh[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) nEnt += ((w4[q] & 0xFFFFu) != 0u) + ((w4[q] >> 16) != 0u);
+                        for (int i = 0; i < 4; ++i) hh[i] = tt[i] < 0 ? HV_EMPTY : (ht_hash(tt[i]) & static_cast<uint32_t>(mask));
+                        reinterpret_cast<uint2 *>(hv)[c] = make_uint2(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16));
+                    } else {
+                        reinterpret_cast<v4u *>(tok)[c] = v[j];
+                    }
+                    const uint32_t nib = (vb[j] >> ((c & 1) * 4)) & 0xFu;
+                    vt32[2 * c] = ((nib & 1u) ? 0u : 0xFFFFu) | ((nib & 2u) ? 0u : 0xFFFF0000u);
+                    vt32[2 * c + 1] = ((nib & 4u) ? 0u : 0xFFFFu) | ((nib & 8u) ? 0u : 0xFFFF0000u);
+                    const int32_t s0 = c * 4;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool live = s0 + i < dbs && tt[i] >= 0;
+                        nTok += live ? 1u : 0u;
+                        if (direct && live && tt[i] < prefill) inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
+                    }
+                } else if (c < nt + nh) {
+                    reinterpret_cast<v4u *>(ht)[c - nt] = v[j];
+                    const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+                    uint32_t ob = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        ob |= (((w4[q] & 0xFFFFu) != 0u) ? 1u : 0u) << (2 * q);
+                        ob |= (((w4[q] >> 16) != 0u) ? 1u : 0u) << (2 * q + 1);
+                    }
+                    occ8[c - nt] = static_cast<uint8_t>(ob);
+                    nEnt += static_cast<uint32_t>(__popc(ob));
                 } else if (c < nAll) {
-                    reinterpret_cast<uint4 *>(vis)[c - nt - nh] = v[j];
+                    reinterpret_cast<v4u *>(vis)[c - nt - nh] = v[j];
                 }
             }
         }
-        SUBSTAMP(4);
         if (h0) ptok[tid] = t0;
         if (h1) ptok[tid + NT] = t1;
         for (int32_t k = tid + 2 * NT; k < K; k += NT) ptok[k] = rt[k];
-        // vset (and in the full form ber, bg, bm, bnew) are contiguous
-        const int32_t nz = (visStrideB >> 2) + (kC ? 0 : 4 * (H >> 5));
-        for (int32_t i = tid; i < nz; i += NT) vset[i] = 0u;
-        for (int32_t k = tid; k < K; k += NT) evslot[k] = 0;  // SM index + 1 by first-hit position
-        if (direct) {
-            for (int32_t i = tid; i < (prefill + 1) >> 1; i += NT) inv32[i] = 0u;
-        }
+        for (int32_t i = tid; i < (visStrideB >> 2); i += NT) vset[i] = 0u;
+        for (int32_t i = tid; i < (H >> 5); i += NT) ber[i] = 0u;
+        for (int32_t i = tid; i < ((K + 1) >> 1); i += NT) reinterpret_cast<uint32_t *>(posSM)[i] = 0u;
         nTok = wave_sum(nTok);
         nEnt = wave_sum(nEnt);
-        if (tid == 0) {
-            ms.nTok = ms.nEnt = ms.bad = ms.ovf = ms.late = 0;
-            ms.M = ms.nSM = ms.T = ms.nConv = ms.N = ms.nUnd = ms.nRest = ms.uEnd = ms.nTakes = ms.nMulti = 0;
-        }
-        __syncthreads();
         if (lane == 0) {
-            atomicAdd(&ms.nTok, static_cast<int32_t>(nTok));
-            atomicAdd(&ms.nEnt, static_cast<int32_t>(nEnt));
+            ms.wtok[wave] = nTok;
+            ms.went[wave] = nEnt;
+        }
+        if (tid == 0) {
+            ms.bad = ms.ovf = ms.late = 0;
+            ms.nSM = ms.nUnd = ms.nRest = ms.uEnd = ms.nTakes = 0;
         }
     }
+    __syncthreads();
     STAMP(1);
 
     // ---- consistency: the table indexes exactly the non-negative tokens of
     // [0, dbs), each at its own slot.  A row this kernel wrote last carries
     // the flag, and then only the counts are checked.
-    for (int32_t s = tid; s < dbs; s += NT) {
-        vt[s] = vis_get(vis, s) ? 0 : VT_NONE;
-        if (direct) {
-            const int32_t t = tok[s];
-            if (t >= 0 && t < prefill) inv[t] = static_cast<uint16_t>(s + 1);
-        }
-    }
     if (!flagged) {
-        Guard g;
         bool bad = false;
         for (int32_t s = tid; s < dbs; s += NT) {
             const int32_t t = kC ? gTok[s] : tok[s];
@@ -432,237 +483,272 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             if (found != s) bad = true;
         }
-        if (__ballot(bad || g.code != 0) != 0ull && lane == 0) atomicOr(&ms.bad, 1);
+        if (__ballot(bad) != 0ull && lane == 0) atomicOr(&ms.bad, 1);
+        __syncthreads();
     }
-    __syncthreads();
-    const bool canonical = ms.bad == 0 && ms.nTok == ms.nEnt;
-    bool fast = canonical;
-    STAMP(2);
+    bool fast;
+    {
+        uint32_t sTok = 0, sEnt = 0;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+            sTok += ms.wtok[w];
+            sEnt += ms.went[w];
+        }
+        fast = ms.bad == 0 && sTok == sEnt;
+    }
+    const bool canonical = fast;
 
+    // ---- classify every position; dedup the candidates (smallest position
+    // of each missing token).  With the direct map a hit is an entry that
+    // checks out as the token's slot; otherwise one probe of the table does
+    // both: a hit stops at its entry (provisional entries only fill empty
+    // cells, never the probe path of a resident token), a miss stops at its
+    // token's provisional entry padded+1+k or claims the first empty cell
     if (fast) {
-        // ---- classify every position and deduplicate the candidates in one
-        // probe: a hit stops at its entry (provisional entries only fill empty
-        // cells, never the probe path of a resident token); a miss stops at
-        // its token's provisional entry padded+1+k (smallest k wins) or claims
-        // the first empty cell with one
-        {
-            Guard g;
-            for (int32_t k = tid; k < K; k += NT) {
-                const int32_t t = ptok[k];
-                uint32_t inf;
-                if (t < 0 || t >= seqLen) {
-                    inf = CLS_INV << 30;
-                } else if (t >= prefill) {
-                    inf = CLS_EXT << 30;
-                } else if (direct) {
-                    const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
-                    uint32_t *w = inv32 + (t >> 1);
-                    const uint32_t sh = (static_cast<uint32_t>(t) & 1u) * 16u;
-                    uint32_t old = *reinterpret_cast<volatile uint32_t *>(w);
-                    const uint32_t e0 = (old >> sh) & 0xFFFFu;
-                    if (e0 != 0u && e0 <= static_cast<uint32_t>(padded)) {
-                        inf = (CLS_HIT << 30) | (e0 - 1u);
-                        lds_min16(vt32, e0 - 1u, static_cast<uint16_t>(k + 1));
-                    } else {
-                        inf = CLS_CAND << 30;
-                        for (;;) {  // keep the smallest position of the token
-                            const uint32_t cur = (old >> sh) & 0xFFFFu;
-                            if (cur != 0u && cur <= v) break;
+        Guard g;
+        for (int32_t q = 0; q < P; ++q) {
+            const int32_t k = tid + q * NT;
+            if (k >= K) break;
+            const int32_t t = ptok[k];
+            uint32_t inf;
+            if (t < 0 || t >= seqLen) {
+                inf = CLS_INV << 30;
+            } else if (t >= prefill) {
+                inf = CLS_EXT << 30;
+            } else if (direct) {
+                const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
+                uint32_t *w = inv32 + (t >> 1);
+                const uint32_t sh = (static_cast<uint32_t>(t) & 1u) * 16u;
+                uint32_t old = *w;
+                inf = CLS_CAND << 30;
+                for (;;) {
+                    const uint32_t cur = (old >> sh) & 0xFFFFu;
+                    if (cur - 1u < static_cast<uint32_t>(dbs) && tok[cur - 1u] == t) {
+                        inf = (CLS_HIT << 30) | (cur - 1u);
+                        lds_min16(vt32, cur - 1u, static_cast<uint16_t>(k + 1));
+                        break;
+                    }
+                    const uint32_t kc = cur - static_cast<uint32_t>(padded) - 1u;
+                    if (cur > static_cast<uint32_t>(padded) && kc < static_cast<uint32_t>(K) && cur <= v &&
+                        ptok[kc] == t)
+                        break;  // an earlier position of the token (or this one) holds it
+                    const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
+                    if (prev == old) break;
+                    old = prev;
+                }
+            } else {
+                const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
+                const uint32_t th = ht_hash(t);
+                int32_t idx = static_cast<int32_t>(th) & mask;
+                inf = 0xFFFFFFFFu;
+                for (int32_t n = 0; n <= mask; ++n) {
+                    uint32_t *w = ht32 + (idx >> 1);
+                    const uint32_t sh = (static_cast<uint32_t>(idx) & 1u) * 16u;
+                    uint32_t old = *w;
+                    bool next = false;
+                    for (;;) {
+                        const uint32_t cur = (old >> sh) & 0xFFFFu;
+                        if (cur == 0u) {
+                            const uint32_t prev = atomicCAS(w, old, old | (v << sh));
+                            if (prev == old) {
+                                inf = CLS_CAND << 30;
+                                pcell[k] = static_cast<uint32_t>(idx);
+                                break;
+                            }
+                            old = prev;
+                        } else if (cur <= static_cast<uint32_t>(padded)) {
+                            if (tok_is(cur - 1u, t, th)) {
+                                inf = (CLS_HIT << 30) | (cur - 1u);
+                                lds_min16(vt32, cur - 1u, static_cast<uint16_t>(k + 1));
+                            } else {
+                                next = true;
+                            }
+                            break;
+                        } else if (ptok[cur - static_cast<uint32_t>(padded) - 1u] == t) {
+                            pcell[k] = static_cast<uint32_t>(idx);
+                            inf = CLS_CAND << 30;
+                            if (v >= cur) break;
                             const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
                             if (prev == old) break;
                             old = prev;
+                        } else {
+                            next = true;
+                            break;
                         }
                     }
-                } else {
-                    const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
-                    const uint32_t th = ht_hash(t);
-                    int32_t idx = static_cast<int32_t>(th) & mask;
-                    inf = 0xFFFFFFFFu;
-                    for (int32_t n = 0; n <= mask; ++n) {
-                        uint32_t *w = ht32 + (idx >> 1);
-                        const uint32_t sh = (static_cast<uint32_t>(idx) & 1u) * 16u;
-                        uint32_t old = *reinterpret_cast<volatile uint32_t *>(w);
-                        bool next = false;
-                        for (;;) {
-                            const uint32_t cur = (old >> sh) & 0xFFFFu;
-                            if (cur == 0u) {
-                                const uint32_t prev = atomicCAS(w, old, old | (v << sh));
-                                if (prev == old) {
-                                    inf = CLS_CAND << 30;
-                                    pcell[k] = static_cast<uint32_t>(idx);
-                                    break;
-                                }
-                                old = prev;
-                            } else if (cur <= static_cast<uint32_t>(padded)) {
-                                if (tok_is(cur - 1u, t, th)) {
-                                    inf = (CLS_HIT << 30) | (cur - 1u);
-                                    lds_min16(vt32, cur - 1u, static_cast<uint16_t>(k + 1));
-                                } else {
-                                    next = true;
-                                }
-                                break;
-                            } else if (ptok[cur - static_cast<uint32_t>(padded) - 1u] == t) {
-                                pcell[k] = static_cast<uint32_t>(idx);
-                                inf = CLS_CAND << 30;
-                                if (v >= cur) break;
-                                const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
-                                if (prev == old) break;
-                                old = prev;
-                            } else {
-                                next = true;
-                                break;
-                            }
-                        }
-                        if (!next) break;
-                        idx = (idx + 1) & mask;
-                    }
-                    if (inf == 0xFFFFFFFFu) {
-                        g.code = kOverflowProbe;
-                        inf = CLS_INV << 30;
-                    }
+                    if (!next) break;
+                    idx = (idx + 1) & mask;
                 }
-                pinf[k] = inf;
+                if (inf == 0xFFFFFFFFu) {
+                    g.code = kOverflowProbe;
+                    inf = CLS_INV << 30;
+                }
             }
-            if (g.code) atomicOr(&ms.ovf, 1);
+            pinf[k] = inf;
         }
-        SUBSTAMP(3);
+        if (g.code) atomicOr(&ms.ovf, 1);
         __syncthreads();
-        STAMP(3);
-        // the first occurrence of each candidate token: its cell's final value
-        // (with the direct map, read in the compaction pass below)
+        // probing form: every candidate reads its token's final provisional
+        // entry before the first occurrences drop them
         if (!direct) {
-            for (int32_t k = tid; k < K; k += NT) {
+            for (int32_t q = 0; q < P; ++q) {
+                const int32_t k = tid + q * NT;
+                if (k >= K) break;
                 if ((pinf[k] >> 30) != CLS_CAND) continue;
                 const uint32_t e = ht[pcell[k]];
                 pinf[k] = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
             }
             __syncthreads();
         }
-        STAMP(4);
-        // ---- candidate prefix counts per position (contiguous chunk per
-        // lane); first occurrences drop their provisional entries
-        {
-            const int32_t P = (K + NT - 1) / NT;
-            const int32_t k0 = tid * P;
-            uint32_t cnt = 0, fl = 0;
-            for (int32_t i = 0; i < P; ++i) {
-                const int32_t k = k0 + i;
-                if (k < K) {
-                    uint32_t inf = pinf[k];
-                    if (direct && (inf >> 30) == CLS_CAND) {
-                        inf = (CLS_CAND << 30) | (static_cast<uint32_t>(inv[ptok[k]]) - static_cast<uint32_t>(padded) - 1u);
-                        pinf[k] = inf;
-                    }
-                    const uint32_t f = ((inf >> 30) == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k)) ? 1u : 0u;
-                    if (f && !direct) ht[pcell[k]] = 0;
-                    fl |= f << i;
-                    cnt += f;
-                }
-            }
-            uint32_t M;
-            uint32_t pre = block_exscan(cnt, bits_for(static_cast<uint32_t>(P)), ms.wt0, M);
-            for (int32_t i = 0; i < P; ++i) {
-                const int32_t k = k0 + i;
-                if (k < K) {
-                    candPre[k] = static_cast<uint16_t>(pre);
-                    pre += (fl >> i) & 1u;
-                }
-            }
-            if (tid == 0) {
-                candPre[K] = static_cast<uint16_t>(M);
-                ms.M = static_cast<int32_t>(M);
-            }
-        }
         if (ms.ovf) fast = false;
     }
+    STAMP(2);
 
-    // ---- ring classes per offset from the hand (contiguous chunk per lane)
-    const int32_t Q = (dbs + NT - 1) / NT;
-    const int32_t u0 = tid * Q;
-    uint64_t snM = 0, smM = 0;
-    uint32_t preSN = 0, preSM = 0;
+    // ---- candidates' first occurrences (ballot masks in position order) and
+    // the ring classes per offset from the hand, with one prefix scan; then
+    // the SM list up to the M-th SN slot
+    uint32_t snM = 0, smM = 0, preSN = 0, preSM = 0, M = 0;
     if (fast) {
-        __syncthreads();  // candPre complete
-        STAMP(5);
+        WSTAMP(0);
+        uint32_t cw = 0;
+        for (int32_t q = 0; q < P; ++q) {
+            const int32_t k = tid + q * NT;
+            bool f = false;
+            if (k < K) {
+                const uint32_t inf = pinf[k];
+                if ((inf >> 30) == CLS_CAND) {
+                    uint32_t k1;
+                    if (direct) {
+                        k1 = static_cast<uint32_t>(inv[ptok[k]]) - static_cast<uint32_t>(padded) - 1u;
+                        pinf[k] = (CLS_CAND << 30) | k1;
+                    } else {
+                        k1 = inf & 0xFFFFu;
+                    }
+                    f = k1 == static_cast<uint32_t>(k);
+                    if (f && !direct) ht[pcell[k]] = 0;
+                }
+            }
+            const uint64_t m = __ballot(f);
+            if (lane == 0) cmask[q * NWAVES + wave] = m;
+            cw += static_cast<uint32_t>(__popcll(m));
+        }
+        WSTAMP(1);
         for (int32_t j = 0; j < Q; ++j) {
             const int32_t u = u0 + j;
-            if (u >= dbs) break;
-            const uint16_t v = vt[ring_slot(hand0, u, dbs)];
-            if (v == VT_NONE) snM |= 1ull << j;
-            else if (v != 0) smM |= 1ull << j;
+            if (u < dbs) {
+                const uint16_t v = vt[ring_slot(hand0, u, dbs)];
+                snM |= (v == VT_NONE ? 1u : 0u) << j;
+                smM |= (v != 0 && v != VT_NONE ? 1u : 0u) << j;
+            }
         }
-        SUBSTAMP(0);
-        const uint32_t cSN = static_cast<uint32_t>(__popcll(snM)), cSM = static_cast<uint32_t>(__popcll(smM));
-        const uint32_t qb = bits_for(static_cast<uint32_t>(Q));
-        uint32_t tot;
-        const uint32_t pre = block_exscan(cSN | (cSM << 16), qb | (qb << 16), ms.wt1, tot);
-        SUBSTAMP(1);
+        WSTAMP(2);
+        const uint32_t cSN = static_cast<uint32_t>(__popc(snM)), cSM = static_cast<uint32_t>(__popc(smM));
+        const uint32_t packed = cSN | (cSM << 16);
+        uint32_t bits = bits_for(static_cast<uint32_t>(Q));
+        bits |= bits << 16;
+        uint32_t pre = 0, tot = 0;
+        while (bits != 0u) {
+            const int b = __builtin_ctz(bits);
+            bits &= bits - 1u;
+            const uint64_t bal = __ballot((packed >> b) & 1u);
+            pre += lanes_below(bal, lane) << b;
+            tot += static_cast<uint32_t>(__popcll(bal)) << b;
+        }
+        if (lane == 0) {
+            ms.wring[wave] = tot;
+            ms.wcand[wave] = cw;
+        }
+        WSTAMP(3);
+        __syncthreads();
+        WSTAMP(4);
+        uint32_t off = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+            const uint32_t c = ms.wring[w];
+            off += (w < wave) ? c : 0u;
+            all += c;
+            M += ms.wcand[w];
+        }
+        pre += off;
         preSN = pre & 0xFFFFu;
         preSM = pre >> 16;
-        uint32_t nsn = preSN, nsm = preSM;
-        for (int32_t j = 0; j < Q; ++j) {
-            const int32_t u = u0 + j;
-            if (u >= dbs) break;
-            if ((snM >> j) & 1ull) {
-                ++nsn;
-            } else if ((smM >> j) & 1ull) {
-                const uint32_t k = static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)]) - 1u;
-                const uint32_t cc = candPre[k];
-                smA[nsm] = static_cast<uint32_t>(u) | (k << 16);
-                smB[nsm] = nsn | (cc << 16);
-                smKp[nsm] = (cc > nsn) ? static_cast<uint16_t>(k) : static_cast<uint16_t>(0);
-                posSM[k] = static_cast<uint16_t>(nsm + 1u);
-                ++nsm;
-            }
-        }
-        if (tid == 0) ms.nSM = static_cast<int32_t>(tot >> 16);
-        SUBSTAMP(2);
-        __syncthreads();
-        STAMP(6);
-
-        // ---- decide the SM slots.  In ring order, slot i (k_i, need0_i = SN
-        // slots before it, cc_i = candidates before k_i) is evicted iff the
-        // events before k_i outnumber the event being served on arrival:
-        //   cc_i + #{evicted j < i: k_j < k_i} > need0_i + #{evicted j < i},
-        // i.e. a_i = cc_i - need0_i - 1 >= D_i = #{evicted j < i: k_j > k_i}.
-        // a_i < 0: passed.  a_i >= U_i = #{j < i: a_j >= 0, k_j > k_i} (a
-        // bound on D_i): evicted.  The rest (rare) are settled in ring order
-        // by one wave.  A slot with need0_i >= M lies past the walk's end.
-        {
-            const int32_t nSM = ms.nSM, M = ms.M;
-            for (int32_t i = tid; i < nSM; i += NT) {
-                const uint32_t eb = smB[i];
-                const int32_t need0 = static_cast<int32_t>(eb & 0xFFFFu);
-                const int32_t ai = static_cast<int32_t>(eb >> 16) - need0 - 1;
-                uint16_t dec = 0;  // 0 passed, 1 evicted, 2 undecided
-                if (need0 < M && ai >= 0) {
-                    const uint32_t ki = smA[i] >> 16;
-                    int32_t U = 0;
-                    int32_t j = 0;
-                    for (; j + 8 <= i; j += 8) {
-                        uint32_t kk[8];
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) kk[q] = smKp[j + q];
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) U += (kk[q] > ki) ? 1 : 0;
-                    }
-                    for (; j < i; ++j) U += (static_cast<uint32_t>(smKp[j]) > ki) ? 1 : 0;
-                    dec = (ai >= U) ? 1 : 2;
-                    if (dec == 2) undl[atomicAdd(&ms.nUnd, 1)] = static_cast<uint32_t>(i);
+        if (M > 0) {
+            // only SM slots with fewer than M SN slots before them can be
+            // reached (the SN slots before a slot are all evicted first, and
+            // each conversion is paid by an SM eviction before it): the list
+            // is a prefix of the SM slots in ring order
+            MaskPrefix cp;
+            cp.init(cmask, P * NWAVES, lane);
+            WSTAMP(5);
+            uint32_t nsn = preSN, nsm = preSM;
+            for (int32_t j = 0; j < Q; ++j) {
+                const bool isSM = (smM >> j) & 1u, isSN = (snM >> j) & 1u;
+                const int32_t u = u0 + j;
+                uint32_t k = 0;
+                if (isSM) k = static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)]) - 1u;
+                const uint32_t cc = cp.before(static_cast<int32_t>(k >> 6), k & 63u);
+                if (isSM && nsn < M) {
+                    smA[nsm] = static_cast<uint32_t>(u) | (k << 16);
+                    smB[nsm] = nsn | (cc << 16);
+                    smKp[nsm] = (cc > nsn) ? static_cast<uint16_t>(k) : static_cast<uint16_t>(0);
+                    posSM[k] = static_cast<uint16_t>(nsm + 1u);
                 }
-                tb[i] = dec;
+                if (isSN && ++nsn == M) ms.nSM = static_cast<int32_t>(nsm);
+                nsm += isSM ? 1u : 0u;
             }
+            if (tid == 0 && (all & 0xFFFFu) < M) ms.nSM = static_cast<int32_t>(all >> 16);
         }
-        SUBSTAMP(5);
+        WSTAMP(6);
         __syncthreads();
-        STAMP(7);
+        WSTAMP(7);
+    }
+    STAMP(3);
+
+    // ---- decide the SM slots.  In ring order, slot i (k_i, need0_i = SN
+    // slots before it, cc_i = candidates before k_i) is evicted iff the
+    // events before k_i outnumber the event being served on arrival:
+    //   cc_i + #{evicted j < i: k_j < k_i} > need0_i + #{evicted j < i},
+    // i.e. a_i = cc_i - need0_i - 1 >= D_i = #{evicted j < i: k_j > k_i}.
+    // a_i < 0: passed.  a_i >= U_i = #{j < i: a_j >= 0, k_j > k_i} (a bound
+    // on D_i): evicted.  The rest (rare) are settled in ring order.
+    int32_t nSM = 0;
+    if (fast) {
+        nSM = ms.nSM;
+        int32_t G = 1;  // lanes per SM slot for the U count
+        while (G < 16 && 2 * G * nSM <= NT) G <<= 1;
+        const int32_t part = tid & (G - 1);
+        const uint4 *kp4 = reinterpret_cast<const uint4 *>(smKp);
+        for (int32_t i = tid / G; i < nSM; i += NT / G) {
+            const uint32_t eb = smB[i];
+            const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
+            uint16_t dec = 0;  // 0 passed, 1 evicted, 2 undecided
+            if (ai >= 0) {
+                const uint32_t ki = smA[i] >> 16;
+                uint32_t U = 0;
+                for (int32_t b = part; 8 * b < i; b += G) {
+                    const uint4 x = kp4[b];
+                    const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int32_t j = 8 * b + 2 * q;
+                        U += (j < i && (w4[q] & 0xFFFFu) > ki) ? 1u : 0u;
+                        U += (j + 1 < i && (w4[q] >> 16) > ki) ? 1u : 0u;
+                    }
+                }
+                for (int o = 1; o < G; o <<= 1) U += static_cast<uint32_t>(__shfl_xor(static_cast<int>(U), o));
+                dec = (ai >= static_cast<int32_t>(U)) ? 1 : 2;
+                if (dec == 2 && part == 0) undl[atomicAdd(&ms.nUnd, 1)] = static_cast<uint16_t>(i);
+            }
+            if (part == 0) tb[i] = dec;
+        }
+        __syncthreads();
         // undecided slots, one wave each: count the evictions already settled
         // before them (L) and the undecided ones before them with a larger k
         // (X); with X == 0, D = L exactly.  A concurrent settle of j < i reads
         // either as undecided (counted in X) or settled (counted exactly):
         // both are safe.
-        {
-            const int32_t nUnd = ms.nUnd;
+        const int32_t nUnd = ms.nUnd;
+        if (nUnd > 0) {
             for (int32_t e = wave; e < nUnd; e += NWAVES) {
                 const int32_t i = static_cast<int32_t>(undl[e]);
                 const uint32_t ki = smA[i] >> 16;
@@ -682,131 +768,159 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                 }
             }
-        }
-        SUBSTAMP(6);
-        __syncthreads();
-        SUBSTAMP(7);
-        if (ms.nRest > 0 && wave == 0) {  // the rest, in ring order
-            const int32_t nSM = ms.nSM;
-            for (int32_t c = 0; c < nSM; c += 64) {
-                uint64_t und = __ballot(c + static_cast<int32_t>(lane) < nSM && tb[c + lane] == 2);
-                while (und != 0ull) {
-                    const int f = __builtin_ctzll(und);
-                    und &= und - 1ull;
-                    const int32_t i = c + f;
-                    const uint32_t ki = smA[i] >> 16;
-                    const uint32_t eb = smB[i];
-                    const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
-                    uint32_t d = 0;
-                    for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
-                        d += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
-                    }
-                    d = wave_sum(d);
-                    if (lane == 0) tb[i] = (ai >= static_cast<int32_t>(d)) ? 1 : 0;
-                }
-            }
-        }
-        __syncthreads();
-        // ---- one scan for both the eviction prefix over the SM list and the
-        // event sequence over positions (candidates' first occurrences and
-        // conversions -- first hits of evicted SM slots -- in position order)
-        {
-            const int32_t nSM = ms.nSM;
-            const int32_t Ps = (nSM + NT - 1) / NT, i0 = tid * Ps;
-            const int32_t Pk = (K + NT - 1) / NT, k0 = tid * Pk;
-            uint32_t cs = 0, fs = 0, ce = 0, fe = 0;
-            for (int32_t q = 0; q < Ps; ++q) {
-                const int32_t i = i0 + q;
-                if (i < nSM && tb[i] == 1) {
-                    fs |= 1u << q;
-                    ++cs;
-                    const uint32_t ea = smA[i];
-                    evold[ea >> 16] = static_cast<uint16_t>(ring_slot(hand0, static_cast<int32_t>(ea & 0xFFFFu), dbs));
-                }
-            }
-            for (int32_t q = 0; q < Pk; ++q) {
-                const int32_t k = k0 + q;
-                if (k < K) {
-                    const uint32_t inf = pinf[k];
-                    const uint32_t c = inf >> 30;
-                    bool f = c == CLS_CAND && (inf & 0xFFFFu) == static_cast<uint32_t>(k);
-                    if (c == CLS_HIT) {
-                        const uint32_t sm = posSM[k];
-                        f = sm != 0u && tb[sm - 1u] == 1;
-                    }
-                    if (f) {
-                        fe |= 1u << q;
-                        ++ce;
+            __syncthreads();
+            if (ms.nRest > 0) {  // the rest, in ring order, by one wave
+                if (wave == 0) {
+                    for (int32_t c = 0; c < nSM; c += 64) {
+                        uint64_t und = __ballot(c + static_cast<int32_t>(lane) < nSM && tb[c + lane] == 2);
+                        while (und != 0ull) {
+                            const int f = __builtin_ctzll(und);
+                            und &= und - 1ull;
+                            const int32_t i = c + f;
+                            const uint32_t ki = smA[i] >> 16;
+                            const uint32_t eb = smB[i];
+                            const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
+                            uint32_t d = 0;
+                            for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
+                                d += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
+                            }
+                            d = wave_sum(d);
+                            if (lane == 0) tb[i] = (ai >= static_cast<int32_t>(d)) ? 1 : 0;
+                        }
                     }
                 }
-            }
-            const uint32_t bs = bits_for(static_cast<uint32_t>(Ps)), be = bits_for(static_cast<uint32_t>(Pk));
-            uint32_t tot;
-            const uint32_t pre = block_exscan(cs | (ce << 16), bs | (be << 16), ms.wt0, tot);
-            uint32_t ps = pre & 0xFFFFu, pe = pre >> 16;
-            for (int32_t q = 0; q < Ps; ++q) {
-                const int32_t i = i0 + q;
-                if (i < nSM) {
-                    const uint32_t tk = (fs >> q) & 1u;
-                    tb[i] = static_cast<uint16_t>(ps | (tk << 15));
-                    ps += tk;
-                }
-            }
-            for (int32_t q = 0; q < Pk; ++q) {
-                if ((fe >> q) & 1u) eseq[pe++] = static_cast<uint16_t>(k0 + q);
-            }
-            const int32_t T = static_cast<int32_t>(tot & 0xFFFFu);
-            if (tid == 0) {
-                tb[nSM] = static_cast<uint16_t>(T);
-                ms.T = T;
-                ms.nConv = T;
-                ms.N = ms.M + T;
-                if (static_cast<int32_t>(tot >> 16) != ms.M + T) ms.ovf = 1;
+                __syncthreads();
             }
         }
-        __syncthreads();
-        STAMP(8);
-        // ---- marks per ring offset: evicted by event p, or passed while serving event p
-        {
-            const int32_t N = ms.N;
-            uint32_t nsn2 = preSN, nsm2 = preSM, ntk = 0;
-            for (int32_t j = 0; j < Q; ++j) {
-                const int32_t u = u0 + j;
-                if (u >= dbs) break;
-                const int32_t s = ring_slot(hand0, u, dbs);
-                const bool isSN = (snM >> j) & 1ull, isSM = (smM >> j) & 1ull;
-                const uint32_t tbv = tb[nsm2];
-                const int32_t r = static_cast<int32_t>(nsn2 + (tbv & 0x7FFFu));
-                if (r < N) {
-                    const uint32_t p = eseq[r];
-                    if (isSN || (isSM && (tbv & 0x8000u))) {
-                        evslot[p] = static_cast<uint16_t>(s);
-                        vt[s] = isSM ? static_cast<uint16_t>(VT_EVICTED | (vt[s] - 1u))
-                                     : static_cast<uint16_t>(VT_EVICTED | VT_NOCONV);
-                        ++ntk;
-                        if (r == N - 1) ms.uEnd = u + 1;
-                    } else {
-                        vt[s] = static_cast<uint16_t>(VT_PASSED | p);
-                    }
-                }
-                nsn2 += isSN ? 1u : 0u;
-                nsm2 += isSM ? 1u : 0u;
-            }
-            ntk = wave_sum(ntk);
-            if (lane == 0 && ntk) atomicAdd(&ms.nTakes, static_cast<int32_t>(ntk));
-        }
-        __syncthreads();
-        STAMP(9);
-        if (ms.nTakes != ms.N || ms.ovf) fast = false;  // the hand would wrap within the step
     }
+    STAMP(4);
+
+    // ---- ballots of the evicted SM slots (in ring order) and of the event
+    // positions (candidates' first occurrences and conversions -- first hits
+    // of evicted SM slots); then the eviction prefix per SM slot and the
+    // event sequence in position order
+    int32_t N = 0;
+    if (fast) {
+        const int32_t Ps = (nSM + NT - 1) / NT;
+        for (int32_t q = 0; q < Ps; ++q) {
+            const int32_t i = tid + q * NT;
+            bool tk = false;
+            if (i < nSM && tb[i] == 1) {
+                tk = true;
+                const uint32_t ea = smA[i];
+                evold[ea >> 16] = static_cast<uint16_t>(ring_slot(hand0, static_cast<int32_t>(ea & 0xFFFFu), dbs));
+            }
+            const uint64_t m = __ballot(tk);
+            if (lane == 0) smask[q * NWAVES + wave] = m;
+        }
+        for (int32_t q = 0; q < P; ++q) {
+            const int32_t k = tid + q * NT;
+            bool f = false;
+            if (k < K) {
+                const uint32_t inf = pinf[k];
+                const uint32_t c = inf >> 30;
+                if (c == CLS_CAND) {
+                    f = (inf & 0xFFFFu) == static_cast<uint32_t>(k);
+                } else if (c == CLS_HIT) {
+                    const uint32_t sm = posSM[k];
+                    f = sm != 0u && tb[sm - 1u] == 1;
+                }
+            }
+            const uint64_t m = __ballot(f);
+            if (lane == 0) emask[q * NWAVES + wave] = m;
+        }
+        __syncthreads();
+        MaskPrefix sp;
+        sp.init(smask, Ps * NWAVES, lane);
+        const uint32_t T = sp.total;
+        for (int32_t q = 0; q < Ps; ++q) {
+            const int32_t i = tid + q * NT;
+            const uint32_t pre = sp.before(i >> 6, static_cast<uint32_t>(i) & 63u);
+            if (i < nSM) {
+                const uint32_t tk = static_cast<uint32_t>((smask[i >> 6] >> (i & 63)) & 1ull);
+                tb[i] = static_cast<uint16_t>(pre | (tk << 15));
+            }
+        }
+        if (tid == 0) tb[nSM] = static_cast<uint16_t>(T);
+        MaskPrefix ep;
+        ep.init(emask, P * NWAVES, lane);
+        N = static_cast<int32_t>(M + T);
+        for (int32_t q = 0; q < P; ++q) {
+            const int32_t k = tid + q * NT;
+            const uint32_t pre = ep.before(k >> 6, static_cast<uint32_t>(k) & 63u);
+            if (k < K && ((emask[k >> 6] >> (k & 63)) & 1ull)) eseq[pre] = static_cast<uint16_t>(k);
+        }
+        if (ep.total != static_cast<uint32_t>(N)) fast = false;  // same value in every wave
+        __syncthreads();
+    }
+    STAMP(5);
+
+    // ---- marks per ring offset: evicted by event r (at position p), or
+    // passed while serving event p; each evicted token's table cell (ber),
+    // and each event's slot and new token (a conversion re-inserts the token
+    // of the slot evicted before its hit)
+    if (fast) {
+        Guard g;
+        const uint32_t nSMu = static_cast<uint32_t>(nSM);  // tb[nSM] = T covers the unlisted SM slots
+        uint32_t nsn2 = preSN, nsm2 = preSM < nSMu ? preSM : nSMu, ntk = 0;
+        for (int32_t j = 0; j < Q; ++j) {
+            const int32_t u = u0 + j;
+            if (u >= dbs) break;
+            const int32_t s = ring_slot(hand0, u, dbs);
+            const bool isSN = (snM >> j) & 1u, isSM = (smM >> j) & 1u;
+            const uint32_t tbv = tb[nsm2];
+            const int32_t r = static_cast<int32_t>(nsn2 + (tbv & 0x7FFFu));
+            if (r < N) {
+                const uint32_t p = eseq[r];
+                if (isSN || (isSM && (tbv & 0x8000u))) {
+                    evslot[p] = static_cast<uint16_t>(s);
+                    vt[s] = isSM ? static_cast<uint16_t>(VT_EVICTED | (vt[s] - 1u))
+                                 : static_cast<uint16_t>(VT_EVICTED | VT_NOCONV);
+                    ++ntk;
+                    if (r == N - 1) ms.uEnd = u + 1;
+                    uint32_t cell = NOCELL;
+                    if (slot_live(s)) {
+                        int32_t idx = slot_home(s);
+                        for (int32_t n = 0; n <= mask; ++n) {
+                            const uint32_t e = ht[idx];
+                            if (e == static_cast<uint32_t>(s + 1)) {
+                                cell = static_cast<uint32_t>(idx);
+                                break;
+                            }
+                            if (e == 0u) break;
+                            idx = (idx + 1) & mask;
+                        }
+                        if (cell == NOCELL) g.code = kOverflowProbe;
+                        else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+                    }
+                    ecell[r] = cell | (static_cast<uint32_t>(s) << 16);
+                    if ((pinf[p] >> 30) == CLS_CAND) ntokv[r] = ptok[p];
+                    else ntokv[r] = kC ? gTok[evold[p]] : tok[evold[p]];
+                } else {
+                    vt[s] = static_cast<uint16_t>(VT_PASSED | p);
+                }
+            }
+            nsn2 += isSN ? 1u : 0u;
+            nsm2 += (isSM && nsm2 < nSMu) ? 1u : 0u;
+        }
+        ntk = wave_sum(ntk);
+        if (lane == 0 && ntk) atomicAdd(&ms.nTakes, static_cast<int32_t>(ntk));
+        if (g.code) atomicOr(&ms.ovf, 1);
+        __syncthreads();
+        if (ms.nTakes != N || ms.ovf) fast = false;  // the hand would wrap within the step
+    }
+    STAMP(6);
 
     if (fast) {
-        const int32_t N = ms.N, uEnd = ms.uEnd;
+        const int32_t uEnd = ms.uEnd;
+        const int32_t Pn = (N + NT - 1) / NT;
         Guard g;
-        // ---- outputs; visited bits set this step (into vset); the cell of
-        // each evicted token and each event's new token (conversions
-        // re-insert a pre-step token)
-        for (int32_t k = tid; k < K; k += NT) {
+        // ---- outputs and visited bits set this step (vset); erase the
+        // evicted tokens: the rightmost marked cell of each pre-step cluster
+        // (from the occupancy snapshot) leads it and deletes right to left
+        for (int32_t q = 0; q < P; ++q) {
+            const int32_t k = tid + q * NT;
+            if (k >= K) break;
             const uint32_t inf = pinf[k];
             const uint32_t cls = inf >> 30;
             int32_t slot = -1;
@@ -834,132 +948,114 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             rs[k] = slot;
             rm[k] = miss;
         }
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t p = eseq[i];
-            const uint32_t s = evslot[p];
+        for (int32_t q = 0; q < Pn; ++q) {
+            const int32_t r = tid + q * NT;
+            if (r >= N) break;
+            const uint32_t ec = ecell[r];
+            const uint32_t s = ec >> 16;
             atomicOr(vset + (s >> 5), 1u << (s & 31u));
-            const int32_t old = kC ? gTok[s] : tok[s];
-            uint32_t cell = 0xFFFFFFFFu;
-            if (old >= 0) {
-                int32_t idx = static_cast<int32_t>(ht_hash(old)) & mask;
-                for (int32_t n = 0; n <= mask; ++n) {
-                    if (ht[idx] == s + 1u) {
-                        cell = static_cast<uint32_t>(idx);
-                        break;
-                    }
-                    idx = (idx + 1) & mask;
-                }
-                if (cell == 0xFFFFFFFFu) g.code = kOverflowProbe;
-                else if (!kC) atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
-            }
-            ecell[i] = cell;
-            const uint32_t src = evold[p];
-            ntokv[i] = static_cast<uint32_t>((pinf[p] >> 30) == CLS_CAND ? ptok[p] : (kC ? gTok[src] : tok[src]));
-        }
-        __syncthreads();
-        if constexpr (kC) {  // the bitmaps share vt's memory: clear them now that vt is read
-            for (int32_t i = tid; i < 4 * (H >> 5); i += NT) ber[i] = 0u;
-            __syncthreads();
-            for (int32_t i = tid; i < N; i += NT) {
-                const uint32_t cell = ecell[i];
-                if (cell != 0xFFFFFFFFu) atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
-            }
-            __syncthreads();
-        }
-        STAMP(10);
-        // ---- table: erase the evicted tokens; the rightmost marked cell of a
-        // cluster leads it and deletes right to left
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t c = ecell[i];
-            if (c == 0xFFFFFFFFu) continue;
+            const uint32_t c = ec & 0xFFFFu;
+            if (c == NOCELL) continue;
             bool ld = true;
             int32_t x = (static_cast<int32_t>(c) + 1) & mask;
-            for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
-                if (bit_get(ber, x)) {
+            for (int32_t n = 0; n <= (H >> 5); ++n) {
+                const uint32_t b = static_cast<uint32_t>(x) & 31u, span = 32u - b;
+                const uint32_t o = occ[x >> 5] >> b, eb = ber[x >> 5] >> b;
+                const uint32_t no = ~o;
+                const uint32_t z = no ? static_cast<uint32_t>(__builtin_ctz(no)) : 32u;  // first empty cell
+                const uint32_t below = (z >= 32u) ? 0xFFFFFFFFu : ((1u << z) - 1u);
+                if (eb & below) {
                     ld = false;
                     break;
                 }
+                if (z < span) break;
+                x = (x + static_cast<int32_t>(span)) & mask;
             }
-            if (ld) ecell[i] = c | 0x80000000u;
-        }
-        __syncthreads();
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t e = ecell[i];
-            if (e == 0xFFFFFFFFu || !(e & 0x80000000u)) continue;
-            const int32_t c = static_cast<int32_t>(e & 0x7FFFFFFFu);
-            rdel_at<kC>(ht, smem + lay.tok, padded, c, mask, g);
-            int32_t x = (c - 1) & mask;
-            for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x - 1) & mask) {
-                if (bit_get(ber, x)) rdel_at<kC>(ht, smem + lay.tok, padded, x, mask, g);
+            if (!ld) continue;
+            rdel_at<kC>(ht, smem + lay.tok, padded, static_cast<int32_t>(c), mask, g);
+            int32_t y = (static_cast<int32_t>(c) - 1) & mask;
+            for (int32_t n = 0; n < H && ht[y] != 0; ++n, y = (y - 1) & mask) {
+                if (bit_get(ber, static_cast<uint32_t>(y))) rdel_at<kC>(ht, smem + lay.tok, padded, y, mask, g);
             }
         }
         __syncthreads();
-        STAMP(11);
-        // ---- new tokens; tentative placement (the final occupied cells do not depend on order)
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t s = evslot[eseq[i]];
-            const int32_t t = static_cast<int32_t>(ntokv[i]);
+        STAMP(7);
+        // ---- new tokens; tentative placement (the final occupied cells do
+        // not depend on order), entries padded+1+r name the event
+        for (int32_t q = 0; q < Pn; ++q) {
+            const int32_t r = tid + q * NT;
+            if (r >= N) break;
+            const uint32_t s = ecell[r] >> 16;
+            const int32_t t = ntokv[r];
             if constexpr (kC) {
-                hv[s] = static_cast<uint16_t>(ht_hash(t));
+                hv[s] = static_cast<uint16_t>(ht_hash(t) & static_cast<uint32_t>(mask));
                 gTok[s] = t;
             } else {
                 tok[s] = t;
             }
             const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(t)) & mask, mask,
-                                          static_cast<uint16_t>(s + 1u));
+                                          static_cast<uint16_t>(padded + 1 + r));
             if (c < 0) g.code = kOverflowProbe;
-            else atomicOr(bnew + (c >> 5), 1u << (c & 31));
+            else ecell[r] = static_cast<uint32_t>(c) | (s << 16);
         }
         __syncthreads();
-        // final cluster of each new key (its start); clusters with two or more new keys are redone
-        for (int32_t i = tid; i < N; i += NT) {
-            int32_t st = static_cast<int32_t>(ht_hash(static_cast<int32_t>(ntokv[i]))) & mask;
+        STAMP(8);
+        // ---- final cluster of each new key: alone in it, the key takes its
+        // cell; with others, the earliest event redoes the cluster
+        for (int32_t q = 0; q < Pn; ++q) {
+            const int32_t r = tid + q * NT;
+            if (r >= N) break;
+            const uint32_t ec = ecell[r];
+            const int32_t c = static_cast<int32_t>(ec & 0xFFFFu);
+            int32_t st = c;
             for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
-            kst[i] = static_cast<uint32_t>(st);
-            const uint32_t bit = 1u << (st & 31);
-            const uint32_t old = atomicOr(bg + (st >> 5), bit);
-            if (old & bit) atomicOr(bm + (st >> 5), bit);
+            uint32_t m = 0, mn = 0xFFFFFFFFu;
+            int32_t x = st;
+            for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
+                const uint32_t e = ht[x];
+                if (e > static_cast<uint32_t>(padded)) {
+                    ++m;
+                    mn = min(mn, e);
+                }
+            }
+            if (m == 1u) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
+            else if (mn == static_cast<uint32_t>(padded + 1 + r)) ecell[r] = ec | 0x8000u;
         }
         __syncthreads();
-        for (int32_t i = tid; i < N; i += NT) {
-            const uint32_t st = kst[i];
-            if (bit_get(bm, st)) {
-                const uint32_t p = eseq[i];
-                const int32_t q = atomicAdd(&ms.nMulti, 1);
-                mlist[q] = (static_cast<uint64_t>(st) << 32) | (static_cast<uint64_t>(p) << 16) | evslot[p];
-            }
-        }
-        __syncthreads();
-        STAMP(12);
-        const int32_t nMulti = ms.nMulti;
-        if (nMulti > 0) {
-            for (int32_t q = tid; q < nMulti; q += NT) {  // sort by (cluster start, event time)
-                const uint64_t key = mlist[q];
-                int32_t r = 0;
-                for (int32_t j = 0; j < nMulti; ++j) r += (mlist[j] < key) ? 1 : 0;
-                msort[r] = key;
-            }
-            __syncthreads();
-            for (int32_t q = tid; q < nMulti; q += NT) {  // the first key of each cluster redoes it in time order
-                const uint64_t key = msort[q];
-                const uint32_t st = static_cast<uint32_t>(key >> 32);
-                if (q > 0 && static_cast<uint32_t>(msort[q - 1] >> 32) == st) continue;
-                int32_t end = static_cast<int32_t>(st);
-                for (int32_t n = 0; n < H && ht[end] != 0; ++n) end = (end + 1) & mask;
-                for (int32_t x = static_cast<int32_t>(st); x != end; x = (x + 1) & mask) {
-                    if (bit_get(bnew, static_cast<uint32_t>(x))) ht[x] = 0;
+        STAMP(9);
+        // ---- redo: insert the cluster's new keys in event order.  The cells
+        // still holding padded+1+r' are exactly the ones empty when the next
+        // key is inserted, so key r probes from its home to the first of them
+        // and swaps in; the key it displaces keeps its event number.
+        for (int32_t q = 0; q < Pn; ++q) {
+            const int32_t r = tid + q * NT;
+            if (r >= N) break;
+            const uint32_t ec = ecell[r];
+            if (!(ec & 0x8000u)) continue;
+            int32_t st = static_cast<int32_t>(ec & 0x7FFFu);
+            for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
+            for (int32_t it = 0; it < H; ++it) {
+                uint32_t mn = 0xFFFFFFFFu;
+                int32_t cm = -1;
+                int32_t x = st;
+                for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
+                    const uint32_t e = ht[x];
+                    if (e > static_cast<uint32_t>(padded) && e < mn) {
+                        mn = e;
+                        cm = x;
+                    }
                 }
-                for (int32_t r = q; r < nMulti && static_cast<uint32_t>(msort[r] >> 32) == st; ++r) {
-                    const uint32_t s = static_cast<uint32_t>(msort[r] & 0xFFFFu);
-                    int32_t idx = static_cast<int32_t>(tok_hash(s)) & mask;
-                    for (int32_t n = 0; n < H && ht[idx] != 0; ++n) idx = (idx + 1) & mask;
-                    ht[idx] = static_cast<uint16_t>(s + 1u);
-                }
+                if (cm < 0) break;
+                const uint32_t rr = mn - static_cast<uint32_t>(padded) - 1u;
+                int32_t f = static_cast<int32_t>(ht_hash(ntokv[rr])) & mask;
+                for (int32_t n = 0; n < H && ht[f] <= static_cast<uint32_t>(padded); ++n) f = (f + 1) & mask;
+                ht[cm] = ht[f];
+                ht[f] = static_cast<uint16_t>((ecell[rr] >> 16) + 1u);
             }
         }
         if (g.code) atomicOr(&ms.late, 1);
         __syncthreads();
-        STAMP(13);
+        STAMP(10);
         if (!ms.late) {
             // ---- write back; visited = (staged bits minus the ring range the
             // hand passed) | bits set this step
@@ -973,11 +1069,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     const int32_t b1 = min(lo + 32, e0 - dbs);
                     if (b1 > lo) clr |= (b1 - lo == 32 ? 0xFFFFFFFFu : ((1u << (b1 - lo)) - 1u));
                 }
-                reinterpret_cast<uint32_t *>(gVis)[w] = (vis32[w] & ~clr) | vset[w];
+                ((KVX_G uint32_t *)gVis)[w] = (vis32[w] & ~clr) | vset[w];
             }
             if (N > 0) {
-                if constexpr (!kC) wg_copy16(gTok, tok, static_cast<uint32_t>(padded) * 4u);  // compact: written in place
-                wg_copy16(gHt, ht, static_cast<uint32_t>(H) * 2u);
+                if constexpr (!kC) {  // compact: written in place
+                    wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tok), static_cast<uint32_t>(padded) * 4u);
+                }
+                wg_copy16((KVX_G v4u *)gHt, reinterpret_cast<const v4u *>(ht), static_cast<uint32_t>(H) * 2u);
             }
             if (tid == 0) {
                 int32_t hd = hand0;
@@ -988,7 +1086,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 gHand[0] = hd;
                 gHand[1] = kCanonFlag;
             }
-            STAMP(14);
+            STAMP(11);
             return;
         }
         if constexpr (kC) {
@@ -1006,9 +1104,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     int32_t *tokF = reinterpret_cast<int32_t *>(smem);
     uint16_t *htF = reinterpret_cast<uint16_t *>(smem + static_cast<size_t>(padded) * 4u);
     uint8_t *visF = smem + static_cast<size_t>(padded) * 4u + static_cast<size_t>(H) * 2u;
-    wg_copy16(tokF, gTok, static_cast<uint32_t>(padded) * 4u);
-    wg_copy16(htF, gHt, static_cast<uint32_t>(H) * 2u);
-    wg_copy16(visF, gVis, static_cast<uint32_t>(visStrideB));
+    wg_copy16(reinterpret_cast<v4u *>(tokF), (KVX_G const v4u *)gTok, static_cast<uint32_t>(padded) * 4u);
+    wg_copy16(reinterpret_cast<v4u *>(htF), (KVX_G const v4u *)gHt, static_cast<uint32_t>(H) * 2u);
+    wg_copy16(reinterpret_cast<v4u *>(visF), (KVX_G const v4u *)gVis, static_cast<uint32_t>(visStrideB));
     __syncthreads();
     __shared__ int32_t s_dirty;
     if (wave == 0) {  // the in-order recurrence: one lane for small tables, else 64 cells/slots per step
@@ -1016,9 +1114,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         Guard g;
         bool dirty = false;
         if (H <= kSmallTable) {
-            if (lane == 0) dirty = sieve_row_sequential(rt, rs, rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
+            if (lane == 0) dirty = sieve_row_sequential((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
         } else {
-            dirty = sieve_row_wave(rt, rs, rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
+            dirty = sieve_row_wave((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
         }
         if (lane == 0) {
             gHand[0] = hand;
@@ -1028,10 +1126,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
     }
     __syncthreads();
-    wg_copy16(gVis, visF, static_cast<uint32_t>(visStrideB));
+    wg_copy16((KVX_G v4u *)gVis, reinterpret_cast<const v4u *>(visF), static_cast<uint32_t>(visStrideB));
     if (s_dirty) {
-        wg_copy16(gTok, tokF, static_cast<uint32_t>(padded) * 4u);
-        wg_copy16(gHt, htF, static_cast<uint32_t>(H) * 2u);
+        wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tokF), static_cast<uint32_t>(padded) * 4u);
+        wg_copy16((KVX_G v4u *)gHt, reinterpret_cast<const v4u *>(htF), static_cast<uint32_t>(H) * 2u);
     }
 }
 
@@ -1065,6 +1163,12 @@ extern "C" int kvx_dbg_read_sub(unsigned long long *out, int rows)
 {
     if (rows > 1024) rows = 1024;
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(kvx::kvx_dbg_sub), sizeof(unsigned long long) * 16 * rows, 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+
+extern "C" int kvx_dbg_read_w(unsigned long long *out)
+{
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(kvx::kvx_dbg_w), sizeof(unsigned long long) * 64 * 16 * 16, 0,
                                hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
 }
 

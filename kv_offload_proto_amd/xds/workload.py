@@ -64,7 +64,13 @@ class DecodeRunner:
         self.pool.wait(st)
         torch.cuda.synchronize()
         self.export_us = e0.elapsed_time(e1) * 1e3
-        self.export_bytes = cfg.layers * cfg.host_reqs * cfg.prefill * cfg.row_bytes
+        rows = cfg.host_reqs * cfg.prefill
+        self.export_bytes = cfg.layers * rows * cfg.row_bytes
+        # with S > 1 a stripe's rows share one segment row and only the
+        # stripe's last row lands there (kvc_scatter_rows_alllayer.cpp:34-52,
+        # kvc_common.h:86-89)
+        S = max(1, cfg.stripe_rows)
+        self.export_moved_bytes = cfg.layers * ((rows + S - 1) // S) * cfg.row_bytes
         return self.export_us
 
     def admit_all(self):
