@@ -58,6 +58,9 @@
 #include "kvx_internal.h"
 #include "sieve_common.h"
 
+// the per-lane loops unroll in the fixed-count instantiations only
+#pragma clang diagnostic ignored "-Wpass-failed"
+
 namespace kvx {
 namespace {
 
@@ -119,24 +122,23 @@ struct Misc {
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
-__device__ __forceinline__ uint32_t lanes_below(uint64_t m, uint32_t lane)
+// Inclusive prefix sum over the 64 lanes of a wave from DPP row shifts and
+// row broadcasts (no LDS round trips).  Call with the whole wave active.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x)
 {
-    return static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+    int v = static_cast<int>(x);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+    return static_cast<uint32_t>(v);
 }
 
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o));
-    return v;
-}
-
-// Bit mask covering the values 0..n.
-__host__ __device__ __forceinline__ uint32_t bits_for(uint32_t n)
-{
-    uint32_t m = 1u;
-    while (m < n + 1u && m != 0x80000000u) m = (m << 1) | 1u;
-    return m;
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(v)), 63));
 }
 
 // Exclusive prefix counts over 64-bit ballot masks mk[e], e = block *
@@ -157,14 +159,9 @@ struct MaskPrefix {
         const int32_t e0 = static_cast<int32_t>(lane) * g;
         uint32_t s = 0;
         for (int32_t x = e0; x < e0 + g && x < nE; ++x) s += static_cast<uint32_t>(__popcll(mk[x]));
-        uint32_t incl = s;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t t = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), o));
-            if (static_cast<int>(lane) >= o) incl += t;
-        }
+        const uint32_t incl = wave_incl_scan(s);
         ex = incl - s;
-        total = static_cast<uint32_t>(__shfl(static_cast<int>(incl), 63));
+        total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
     }
     // set bits before bit `bit` of entry e
     __device__ __forceinline__ uint32_t before(int32_t e, uint32_t bit) const
@@ -269,7 +266,12 @@ __device__ __forceinline__ int32_t ring_slot(int32_t hand0, int32_t u, int32_t d
     return s >= dbs ? s - dbs : s;
 }
 
-template <bool kC>
+// kC: compact LDS form.  PM, QM: positions and ring offsets per lane when
+// fixed at compile time (the launcher picks an instantiation whose values
+// equal ceil(topK / NT) and ceil(dbs / NT)); 0 = any shape.  With fixed
+// counts the per-lane loops unroll and the lane's positions, their classes
+// and its ring offsets' first-hit times stay in registers between phases.
+template <bool kC, int PM, int QM>
 __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveUpdateArgs> L)
 {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -365,9 +367,14 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         else return static_cast<int32_t>(ht_hash(tok[s])) & mask;
     };
 
-    const int32_t P = (K + NT - 1) / NT;    // positions per lane: k = tid + q * NT
-    const int32_t Q = (dbs + NT - 1) / NT;  // ring offsets per lane: u = tid * Q + j
+    constexpr bool kFixed = PM > 0 && QM > 0;
+    const int32_t P = kFixed ? PM : (K + NT - 1) / NT;    // positions per lane: k = tid + q * NT
+    const int32_t Q = kFixed ? QM : (dbs + NT - 1) / NT;  // ring offsets per lane: u = tid * Q + j
     const int32_t u0 = tid * Q;
+    constexpr int PR = kFixed ? PM : 1, QR = kFixed ? QM : 1;
+    int32_t tR[PR];    // token of position tid + q * NT
+    uint32_t iR[PR];   // its class word (pinf)
+    uint32_t vR[QR];   // first-hit code (vt) of ring offset u0 + j
 
     // ---- stage the state row and the topK row; visited flags per slot (vt),
     // the direct map, the table's occupancy bitmap; count live tokens and
@@ -445,6 +452,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if (h0) ptok[tid] = t0;
         if (h1) ptok[tid + NT] = t1;
         for (int32_t k = tid + 2 * NT; k < K; k += NT) ptok[k] = rt[k];
+        if constexpr (kFixed) {
+#pragma unroll
+            for (int q = 0; q < PR; ++q) {
+                const int32_t k = tid + q * NT;
+                tR[q] = (q == 0) ? t0 : (q == 1) ? t1 : (k < K ? ptok[k] : 0);
+            }
+        }
         for (int32_t i = tid; i < (visStrideB >> 2); i += NT) vset[i] = 0u;
         for (int32_t i = tid; i < (H >> 5); i += NT) ber[i] = 0u;
         for (int32_t i = tid; i < ((K + 1) >> 1); i += NT) reinterpret_cast<uint32_t *>(posSM)[i] = 0u;
@@ -506,10 +520,11 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // token's provisional entry padded+1+k or claims the first empty cell
     if (fast) {
         Guard g;
+#pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
-            if (k >= K) break;
-            const int32_t t = ptok[k];
+            if (k >= K) continue;
+            const int32_t t = kFixed ? tR[kFixed ? q : 0] : ptok[k];
             uint32_t inf;
             if (t < 0 || t >= seqLen) {
                 inf = CLS_INV << 30;
@@ -585,18 +600,23 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
             }
             pinf[k] = inf;
+            if constexpr (kFixed) iR[q] = inf;
         }
         if (g.code) atomicOr(&ms.ovf, 1);
         __syncthreads();
         // probing form: every candidate reads its token's final provisional
         // entry before the first occurrences drop them
         if (!direct) {
+#pragma unroll
             for (int32_t q = 0; q < P; ++q) {
                 const int32_t k = tid + q * NT;
-                if (k >= K) break;
-                if ((pinf[k] >> 30) != CLS_CAND) continue;
+                if (k >= K) continue;
+                const uint32_t inf = kFixed ? iR[kFixed ? q : 0] : pinf[k];
+                if ((inf >> 30) != CLS_CAND) continue;
                 const uint32_t e = ht[pcell[k]];
-                pinf[k] = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
+                const uint32_t ni = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
+                pinf[k] = ni;
+                if constexpr (kFixed) iR[q] = ni;
             }
             __syncthreads();
         }
@@ -611,16 +631,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     if (fast) {
         WSTAMP(0);
         uint32_t cw = 0;
+#pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
             bool f = false;
             if (k < K) {
-                const uint32_t inf = pinf[k];
+                const uint32_t inf = kFixed ? iR[kFixed ? q : 0] : pinf[k];
                 if ((inf >> 30) == CLS_CAND) {
                     uint32_t k1;
                     if (direct) {
-                        k1 = static_cast<uint32_t>(inv[ptok[k]]) - static_cast<uint32_t>(padded) - 1u;
+                        const int32_t t = kFixed ? tR[kFixed ? q : 0] : ptok[k];
+                        k1 = static_cast<uint32_t>(inv[t]) - static_cast<uint32_t>(padded) - 1u;
                         pinf[k] = (CLS_CAND << 30) | k1;
+                        if constexpr (kFixed) iR[q] = (CLS_CAND << 30) | k1;
                     } else {
                         k1 = inf & 0xFFFFu;
                     }
@@ -633,27 +656,20 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             cw += static_cast<uint32_t>(__popcll(m));
         }
         WSTAMP(1);
+#pragma unroll
         for (int32_t j = 0; j < Q; ++j) {
             const int32_t u = u0 + j;
-            if (u < dbs) {
-                const uint16_t v = vt[ring_slot(hand0, u, dbs)];
-                snM |= (v == VT_NONE ? 1u : 0u) << j;
-                smM |= (v != 0 && v != VT_NONE ? 1u : 0u) << j;
-            }
+            const uint32_t v = (u < dbs) ? vt[ring_slot(hand0, u, dbs)] : 0u;
+            if constexpr (kFixed) vR[j] = v;
+            snM |= (v == VT_NONE ? 1u : 0u) << j;
+            smM |= (v != 0u && v != VT_NONE ? 1u : 0u) << j;
         }
         WSTAMP(2);
         const uint32_t cSN = static_cast<uint32_t>(__popc(snM)), cSM = static_cast<uint32_t>(__popc(smM));
         const uint32_t packed = cSN | (cSM << 16);
-        uint32_t bits = bits_for(static_cast<uint32_t>(Q));
-        bits |= bits << 16;
-        uint32_t pre = 0, tot = 0;
-        while (bits != 0u) {
-            const int b = __builtin_ctz(bits);
-            bits &= bits - 1u;
-            const uint64_t bal = __ballot((packed >> b) & 1u);
-            pre += lanes_below(bal, lane) << b;
-            tot += static_cast<uint32_t>(__popcll(bal)) << b;
-        }
+        const uint32_t incl = wave_incl_scan(packed);
+        uint32_t pre = incl - packed;
+        const uint32_t tot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
         if (lane == 0) {
             ms.wring[wave] = tot;
             ms.wcand[wave] = cw;
@@ -681,11 +697,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             cp.init(cmask, P * NWAVES, lane);
             WSTAMP(5);
             uint32_t nsn = preSN, nsm = preSM;
+#pragma unroll
             for (int32_t j = 0; j < Q; ++j) {
                 const bool isSM = (smM >> j) & 1u, isSN = (snM >> j) & 1u;
                 const int32_t u = u0 + j;
                 uint32_t k = 0;
-                if (isSM) k = static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)]) - 1u;
+                if (isSM) k = (kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)])) - 1u;
                 const uint32_t cc = cp.before(static_cast<int32_t>(k >> 6), k & 63u);
                 if (isSM && nsn < M) {
                     smA[nsm] = static_cast<uint32_t>(u) | (k << 16);
@@ -813,11 +830,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             const uint64_t m = __ballot(tk);
             if (lane == 0) smask[q * NWAVES + wave] = m;
         }
+#pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
             bool f = false;
             if (k < K) {
-                const uint32_t inf = pinf[k];
+                const uint32_t inf = kFixed ? iR[kFixed ? q : 0] : pinf[k];
                 const uint32_t c = inf >> 30;
                 if (c == CLS_CAND) {
                     f = (inf & 0xFFFFu) == static_cast<uint32_t>(k);
@@ -845,6 +863,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         MaskPrefix ep;
         ep.init(emask, P * NWAVES, lane);
         N = static_cast<int32_t>(M + T);
+#pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
             const uint32_t pre = ep.before(k >> 6, static_cast<uint32_t>(k) & 63u);
@@ -863,9 +882,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         Guard g;
         const uint32_t nSMu = static_cast<uint32_t>(nSM);  // tb[nSM] = T covers the unlisted SM slots
         uint32_t nsn2 = preSN, nsm2 = preSM < nSMu ? preSM : nSMu, ntk = 0;
+#pragma unroll
         for (int32_t j = 0; j < Q; ++j) {
             const int32_t u = u0 + j;
-            if (u >= dbs) break;
+            if (u >= dbs) continue;
             const int32_t s = ring_slot(hand0, u, dbs);
             const bool isSN = (snM >> j) & 1u, isSM = (smM >> j) & 1u;
             const uint32_t tbv = tb[nsm2];
@@ -874,7 +894,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 const uint32_t p = eseq[r];
                 if (isSN || (isSM && (tbv & 0x8000u))) {
                     evslot[p] = static_cast<uint16_t>(s);
-                    vt[s] = isSM ? static_cast<uint16_t>(VT_EVICTED | (vt[s] - 1u))
+                    const uint32_t v0 = kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[s]);
+                    vt[s] = isSM ? static_cast<uint16_t>(VT_EVICTED | (v0 - 1u))
                                  : static_cast<uint16_t>(VT_EVICTED | VT_NOCONV);
                     ++ntk;
                     if (r == N - 1) ms.uEnd = u + 1;
@@ -918,15 +939,16 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         // ---- outputs and visited bits set this step (vset); erase the
         // evicted tokens: the rightmost marked cell of each pre-step cluster
         // (from the occupancy snapshot) leads it and deletes right to left
+#pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
-            if (k >= K) break;
-            const uint32_t inf = pinf[k];
+            if (k >= K) continue;
+            const uint32_t inf = kFixed ? iR[kFixed ? q : 0] : pinf[k];
             const uint32_t cls = inf >> 30;
             int32_t slot = -1;
             int8_t miss = 0;
             if (cls == CLS_EXT) {
-                slot = padded + (ptok[k] - prefill);
+                slot = padded + ((kFixed ? tR[kFixed ? q : 0] : ptok[k]) - prefill);
             } else if (cls == CLS_HIT) {
                 const uint32_t s0 = inf & 0xFFFFu;
                 const uint16_t v = vt[s0];
@@ -1135,24 +1157,44 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
 }  // namespace
 
+template <bool kC, int PM, int QM>
+static hipError_t set_limit_one(size_t bytes)
+{
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update_fast<kC, PM, QM>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
 hipError_t sieve_fast_set_lds_limit(size_t bytes)
 {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update_fast<false>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update_fast<true>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    hipError_t e = hipSuccess;
+    if ((e = set_limit_one<false, 0, 0>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<false, 2, 4>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<false, 2, 8>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<true, 0, 0>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<true, 2, 4>(bytes)) != hipSuccess) return e;
+    return set_limit_one<true, 2, 8>(bytes);
+}
+
+template <bool kC>
+static void launch_one(const KvxLaunch<HispSieveUpdateArgs> &L, size_t ldsBytes, hipStream_t stream)
+{
+    const HispSieveUpdateArgs &a = L.a;
+    const uint32_t P = (a.topK + NT - 1) / NT, Q = (a.deviceBufferSize + NT - 1) / NT;
+    if (P == 2 && Q == 4) {
+        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 4>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    } else if (P == 2 && Q == 8) {
+        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 8>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    } else {
+        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 0, 0>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    }
 }
 
 hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes, bool compact,
                                     hipStream_t stream)
 {
     KvxLaunch<HispSieveUpdateArgs> L{a, overflowSlot};
-    if (compact) {
-        hipLaunchKernelGGL(kvx_sieve_update_fast<true>, dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
-    } else {
-        hipLaunchKernelGGL(kvx_sieve_update_fast<false>, dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
-    }
+    if (compact) launch_one<true>(L, ldsBytes, stream);
+    else launch_one<false>(L, ldsBytes, stream);
     return hipGetLastError();
 }
 
