@@ -37,15 +37,16 @@
 //            the rest in ring order
 //   events   eviction prefix over the SM slots and the event sequence in
 //            position order, both from ballot masks
-//   marks    per ring offset: evicted at event p / passed at event p, the
-//            evicted token's table cell, each event's slot and new token
+//   marks    per ring offset: evicted at event p / passed at event p; the
+//            evicted tokens' table cells (looked up with the ring classes
+//            for the SN slots, which are all evicted)
 //   outputs  slots, is_miss, visited bits; erase the evicted tokens
 //            (Algorithm R deletions commute when each pre-step cluster is
 //            done right to left by its rightmost marked cell)
 //   insert   tentative parallel placement of the new tokens (the occupied
 //            cells do not depend on order), entries naming the event; a key
-//            alone in its final cluster takes its cell, and the earliest key
-//            of every other cluster redoes it in event order.  Linear probing
+//            alone in its final cluster takes its cell, and every other
+//            cluster is redone in event order by one wave (a lane per cell).  Linear probing
 //            with Algorithm R leaves the table equal to inserting the live
 //            keys in insertion order, so the result is the sequential table
 //            byte for byte.
@@ -113,7 +114,7 @@ __device__ unsigned long long kvx_dbg_w[64][16][16];
 #endif
 
 struct Misc {
-    int32_t bad, ovf, late, nSM, nUnd, nRest, uEnd, nTakes;
+    int32_t bad, ovf, late, nSM, nUnd, nRest, uEnd, nTakes, nLead;
     uint32_t wtok[NWAVES];
     uint32_t went[NWAVES];
     uint32_t wring[NWAVES];
@@ -162,6 +163,30 @@ struct MaskPrefix {
         const uint32_t incl = wave_incl_scan(s);
         ex = incl - s;
         total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+    }
+    // two prefixes from one scan (16-bit fields) when both fit one entry per lane
+    static __device__ __forceinline__ void init_pair(MaskPrefix &a, const uint64_t *ma, int32_t na, MaskPrefix &b,
+                                                     const uint64_t *mb, int32_t nb, uint32_t lane)
+    {
+        if (na > 64 || nb > 64) {
+            a.init(ma, na, lane);
+            b.init(mb, nb, lane);
+            return;
+        }
+        a.mk = ma;
+        b.mk = mb;
+        a.g = b.g = 1;
+        const int32_t L = static_cast<int32_t>(lane);
+        const uint32_t ca = L < na ? static_cast<uint32_t>(__popcll(ma[L])) : 0u;
+        const uint32_t cb = L < nb ? static_cast<uint32_t>(__popcll(mb[L])) : 0u;
+        const uint32_t packed = ca | (cb << 16);
+        const uint32_t incl = wave_incl_scan(packed);
+        const uint32_t ex = incl - packed;
+        const uint32_t tot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+        a.ex = ex & 0xFFFFu;
+        b.ex = ex >> 16;
+        a.total = tot & 0xFFFFu;
+        b.total = tot >> 16;
     }
     // set bits before bit `bit` of entry e
     __device__ __forceinline__ uint32_t before(int32_t e, uint32_t bit) const
@@ -348,8 +373,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *pcell = smA;                                   // classify: provisional cell per position
     uint16_t *posSM = evslot;                                // SM index + 1 per first-hit position
     uint16_t *undl = eseq;                                   // decide: undecided SM indices
-    uint16_t *evold = smKp;                                  // conversions: the slot evicted before the hit
     uint32_t *ecell = smA;                                   // per event: table cell | slot << 16
+    uint16_t *lead = eseq;                                   // redo: start cell of each multi-key cluster
     int32_t *ntokv = reinterpret_cast<int32_t *>(smB);       // per event: the token inserted
 
     // token of slot s equals t (th = its hash); the compact form checks the
@@ -470,7 +495,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         if (tid == 0) {
             ms.bad = ms.ovf = ms.late = 0;
-            ms.nSM = ms.nUnd = ms.nRest = ms.uEnd = ms.nTakes = 0;
+            ms.nSM = ms.nUnd = ms.nRest = ms.uEnd = ms.nTakes = ms.nLead = 0;
         }
     }
     __syncthreads();
@@ -710,6 +735,27 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     smKp[nsm] = (cc > nsn) ? static_cast<uint16_t>(k) : static_cast<uint16_t>(0);
                     posSM[k] = static_cast<uint16_t>(nsm + 1u);
                 }
+                if (isSN && nsn < M) {
+                    // every SN slot before the M-th is evicted: look up its
+                    // token's cell now (vt of an SN slot is not read again)
+                    const int32_t sl = ring_slot(hand0, u, dbs);
+                    uint32_t cell = NOCELL;
+                    if (slot_live(sl)) {
+                        int32_t idx = slot_home(sl);
+                        for (int32_t n = 0; n <= mask; ++n) {
+                            const uint32_t e = ht[idx];
+                            if (e == static_cast<uint32_t>(sl + 1)) {
+                                cell = static_cast<uint32_t>(idx);
+                                break;
+                            }
+                            if (e == 0u) break;
+                            idx = (idx + 1) & mask;
+                        }
+                        if (cell == NOCELL) atomicOr(&ms.ovf, 1);
+                        else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+                    }
+                    vt[sl] = static_cast<uint16_t>(cell);
+                }
                 if (isSN && ++nsn == M) ms.nSM = static_cast<int32_t>(nsm);
                 nsm += isSM ? 1u : 0u;
             }
@@ -822,11 +868,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
             bool tk = false;
-            if (i < nSM && tb[i] == 1) {
-                tk = true;
-                const uint32_t ea = smA[i];
-                evold[ea >> 16] = static_cast<uint16_t>(ring_slot(hand0, static_cast<int32_t>(ea & 0xFFFFu), dbs));
-            }
+            if (i < nSM && tb[i] == 1) tk = true;
             const uint64_t m = __ballot(tk);
             if (lane == 0) smask[q * NWAVES + wave] = m;
         }
@@ -848,8 +890,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (lane == 0) emask[q * NWAVES + wave] = m;
         }
         __syncthreads();
-        MaskPrefix sp;
-        sp.init(smask, Ps * NWAVES, lane);
+        MaskPrefix sp, ep;
+        MaskPrefix::init_pair(sp, smask, Ps * NWAVES, ep, emask, P * NWAVES, lane);
         const uint32_t T = sp.total;
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
@@ -860,14 +902,17 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (tid == 0) tb[nSM] = static_cast<uint16_t>(T);
-        MaskPrefix ep;
-        ep.init(emask, P * NWAVES, lane);
         N = static_cast<int32_t>(M + T);
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
             const uint32_t pre = ep.before(k >> 6, static_cast<uint32_t>(k) & 63u);
-            if (k < K && ((emask[k >> 6] >> (k & 63)) & 1ull)) eseq[pre] = static_cast<uint16_t>(k);
+            if (k < K && ((emask[k >> 6] >> (k & 63)) & 1ull)) {
+                // the event inserts the position's own token: a candidate's,
+                // or for a conversion the token of the slot its hit lost
+                eseq[pre] = static_cast<uint16_t>(k);
+                ntokv[pre] = kFixed ? tR[kFixed ? q : 0] : ptok[k];
+            }
         }
         if (ep.total != static_cast<uint32_t>(N)) fast = false;  // same value in every wave
         __syncthreads();
@@ -875,9 +920,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     STAMP(5);
 
     // ---- marks per ring offset: evicted by event r (at position p), or
-    // passed while serving event p; each evicted token's table cell (ber),
-    // and each event's slot and new token (a conversion re-inserts the token
-    // of the slot evicted before its hit)
+    // passed while serving event p; each event's slot and the table cell of
+    // the token it evicts (ber)
     if (fast) {
         Guard g;
         const uint32_t nSMu = static_cast<uint32_t>(nSM);  // tb[nSM] = T covers the unlisted SM slots
@@ -894,29 +938,31 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 const uint32_t p = eseq[r];
                 if (isSN || (isSM && (tbv & 0x8000u))) {
                     evslot[p] = static_cast<uint16_t>(s);
-                    const uint32_t v0 = kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[s]);
-                    vt[s] = isSM ? static_cast<uint16_t>(VT_EVICTED | (v0 - 1u))
-                                 : static_cast<uint16_t>(VT_EVICTED | VT_NOCONV);
                     ++ntk;
                     if (r == N - 1) ms.uEnd = u + 1;
-                    uint32_t cell = NOCELL;
-                    if (slot_live(s)) {
-                        int32_t idx = slot_home(s);
-                        for (int32_t n = 0; n <= mask; ++n) {
-                            const uint32_t e = ht[idx];
-                            if (e == static_cast<uint32_t>(s + 1)) {
-                                cell = static_cast<uint32_t>(idx);
-                                break;
+                    uint32_t cell;
+                    if (isSN) {
+                        cell = vt[s];  // looked up with the ring classes
+                    } else {
+                        const uint32_t v0 = kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[s]);
+                        vt[s] = static_cast<uint16_t>(VT_EVICTED | (v0 - 1u));
+                        cell = NOCELL;
+                        if (slot_live(s)) {
+                            int32_t idx = slot_home(s);
+                            for (int32_t n = 0; n <= mask; ++n) {
+                                const uint32_t e = ht[idx];
+                                if (e == static_cast<uint32_t>(s + 1)) {
+                                    cell = static_cast<uint32_t>(idx);
+                                    break;
+                                }
+                                if (e == 0u) break;
+                                idx = (idx + 1) & mask;
                             }
-                            if (e == 0u) break;
-                            idx = (idx + 1) & mask;
+                            if (cell == NOCELL) g.code = kOverflowProbe;
+                            else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
                         }
-                        if (cell == NOCELL) g.code = kOverflowProbe;
-                        else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
                     }
                     ecell[r] = cell | (static_cast<uint32_t>(s) << 16);
-                    if ((pinf[p] >> 30) == CLS_CAND) ntokv[r] = ptok[p];
-                    else ntokv[r] = kC ? gTok[evold[p]] : tok[evold[p]];
                 } else {
                     vt[s] = static_cast<uint16_t>(VT_PASSED | p);
                 }
@@ -1041,38 +1087,69 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
             }
             if (m == 1u) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
-            else if (mn == static_cast<uint32_t>(padded + 1 + r)) ecell[r] = ec | 0x8000u;
+            else if (mn == static_cast<uint32_t>(padded + 1 + r)) lead[atomicAdd(&ms.nLead, 1)] = static_cast<uint16_t>(st);
         }
         __syncthreads();
         STAMP(9);
         // ---- redo: insert the cluster's new keys in event order.  The cells
         // still holding padded+1+r' are exactly the ones empty when the next
         // key is inserted, so key r probes from its home to the first of them
-        // and swaps in; the key it displaces keeps its event number.
-        for (int32_t q = 0; q < Pn; ++q) {
-            const int32_t r = tid + q * NT;
-            if (r >= N) break;
-            const uint32_t ec = ecell[r];
-            if (!(ec & 0x8000u)) continue;
-            int32_t st = static_cast<int32_t>(ec & 0x7FFFu);
-            for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
-            for (int32_t it = 0; it < H; ++it) {
-                uint32_t mn = 0xFFFFFFFFu;
-                int32_t cm = -1;
-                int32_t x = st;
-                for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
-                    const uint32_t e = ht[x];
-                    if (e > static_cast<uint32_t>(padded) && e < mn) {
-                        mn = e;
-                        cm = x;
+        // and swaps in; the key it displaces keeps its event number.  One
+        // wave per cluster, a lane per cell (longer clusters: one lane).
+        const int32_t nLead = ms.nLead;
+        for (int32_t li = wave; li < nLead; li += NWAVES) {
+            const int32_t st = lead[li];
+            const int32_t x = (st + static_cast<int32_t>(lane)) & mask;
+            uint32_t e = ht[x];
+            const uint64_t empt = __ballot(e == 0u);
+            if (empt != 0ull) {
+                const int32_t Lc = __builtin_ctzll(empt);  // cluster length
+                bool un = static_cast<int32_t>(lane) < Lc && e > static_cast<uint32_t>(padded);
+                for (int32_t it = 0; it < 64; ++it) {
+                    uint64_t um = __ballot(un);
+                    if (um == 0ull) break;
+                    uint32_t best = 0xFFFFFFFFu;
+                    int32_t cm = 0;
+                    for (; um != 0ull; um &= um - 1ull) {
+                        const int32_t l = __builtin_ctzll(um);
+                        const uint32_t v = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), l));
+                        if (v < best) {
+                            best = v;
+                            cm = l;
+                        }
+                    }
+                    const uint32_t rr = best - static_cast<uint32_t>(padded) - 1u;
+                    const int32_t hl = ((static_cast<int32_t>(ht_hash(ntokv[rr])) & mask) - st) & mask;
+                    const uint32_t fin = (ecell[rr] >> 16) + 1u;
+                    const uint64_t fm = __ballot(un && static_cast<int32_t>(lane) >= hl);
+                    const int32_t f = fm ? __builtin_ctzll(fm) : cm;  // the home lies in the cluster
+                    const uint32_t ef = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), f));
+                    if (static_cast<int32_t>(lane) == cm) e = ef;
+                    if (static_cast<int32_t>(lane) == f) {
+                        e = fin;
+                        un = false;
                     }
                 }
-                if (cm < 0) break;
-                const uint32_t rr = mn - static_cast<uint32_t>(padded) - 1u;
-                int32_t f = static_cast<int32_t>(ht_hash(ntokv[rr])) & mask;
-                for (int32_t n = 0; n < H && ht[f] <= static_cast<uint32_t>(padded); ++n) f = (f + 1) & mask;
-                ht[cm] = ht[f];
-                ht[f] = static_cast<uint16_t>((ecell[rr] >> 16) + 1u);
+                if (static_cast<int32_t>(lane) < Lc) ht[x] = static_cast<uint16_t>(e);
+            } else if (lane == 0) {
+                for (int32_t it = 0; it < H; ++it) {
+                    uint32_t mn = 0xFFFFFFFFu;
+                    int32_t cm = -1;
+                    int32_t y = st;
+                    for (int32_t n = 0; n < H && ht[y] != 0; ++n, y = (y + 1) & mask) {
+                        const uint32_t ey = ht[y];
+                        if (ey > static_cast<uint32_t>(padded) && ey < mn) {
+                            mn = ey;
+                            cm = y;
+                        }
+                    }
+                    if (cm < 0) break;
+                    const uint32_t rr = mn - static_cast<uint32_t>(padded) - 1u;
+                    int32_t f = static_cast<int32_t>(ht_hash(ntokv[rr])) & mask;
+                    for (int32_t n = 0; n < H && ht[f] <= static_cast<uint32_t>(padded); ++n) f = (f + 1) & mask;
+                    ht[cm] = ht[f];
+                    ht[f] = static_cast<uint16_t>((ecell[rr] >> 16) + 1u);
+                }
             }
         }
         if (g.code) atomicOr(&ms.late, 1);
