@@ -62,7 +62,7 @@ constexpr int kFastThreads = KVX_FAST_THREADS;
 
 struct FastLayout {
     uint32_t tok, ht, vis, ptok, pinf, vt, evslot, smKp, eseq, tb, smA, smB, vset, ber, occ, cmask, emask, smask,
-        total;
+        rsn, rsm, cellOf, total;
 };
 
 __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
@@ -73,7 +73,8 @@ __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 1
 // undecided SM slots, and the SM list with the per-event cells and tokens.
 // In the compact form (rows whose full layout does not fit) the tokens row is
 // replaced by the Knuth hash of each slot's token (full tokens stay in HBM).
-// cmask/emask/smask hold one 64-bit ballot per (wave, 1024-entry block).
+// cmask/emask/smask/rsn/rsm hold one 64-bit ballot per (wave, block of one
+// entry per lane).
 __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint32_t htSize, uint32_t topK,
                                                            uint32_t visStrideB, bool compact = false)
 {
@@ -100,6 +101,10 @@ __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint
     l.cmask = o;   o += maskBytes;
     l.emask = o;   o += maskBytes;
     l.smask = o;   o += maskBytes;
+    const uint32_t ringMaskBytes = (padded + kFastThreads - 1u) / kFastThreads * (kFastThreads / 64u) * 8u;
+    l.rsn = o;     o += ringMaskBytes;
+    l.rsm = o;     o += ringMaskBytes;
+    l.cellOf = o;  o += compact ? 0u : align16(padded * 2u);  // full form: table cell of each slot's entry
     l.total = o;
     return l;
 }

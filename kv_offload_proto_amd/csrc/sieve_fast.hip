@@ -142,24 +142,31 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t v)
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_incl_scan(v)), 63));
 }
 
+// Set bits of m below this lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m)
+{
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+}
+
 // Exclusive prefix counts over 64-bit ballot masks mk[e], e = block *
 // NWAVES + wave (so entry e covers items 64e..64e+63 of a lane-strided
-// index), computed by every wave for itself: lane L sums g consecutive
+// index), computed by every wave for itself: lane L sums 2^lg consecutive
 // entries.  Set up and query with the whole wave active.
 struct MaskPrefix {
     const uint64_t *mk;
-    int32_t g;
+    int32_t lg;
     uint32_t ex;     // prefix of this lane's first entry
     uint32_t total;  // set bits in all entries
 
     __device__ __forceinline__ void init(const uint64_t *m, int32_t nE, uint32_t lane)
     {
         mk = m;
-        g = (nE + 63) >> 6;
-        if (g < 1) g = 1;
-        const int32_t e0 = static_cast<int32_t>(lane) * g;
+        lg = 0;
+        while ((64 << lg) < nE) ++lg;
+        const int32_t e0 = static_cast<int32_t>(lane) << lg;
         uint32_t s = 0;
-        for (int32_t x = e0; x < e0 + g && x < nE; ++x) s += static_cast<uint32_t>(__popcll(mk[x]));
+        for (int32_t x = e0; x < e0 + (1 << lg) && x < nE; ++x) s += static_cast<uint32_t>(__popcll(mk[x]));
         const uint32_t incl = wave_incl_scan(s);
         ex = incl - s;
         total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
@@ -175,7 +182,7 @@ struct MaskPrefix {
         }
         a.mk = ma;
         b.mk = mb;
-        a.g = b.g = 1;
+        a.lg = b.lg = 0;
         const int32_t L = static_cast<int32_t>(lane);
         const uint32_t ca = L < na ? static_cast<uint32_t>(__popcll(ma[L])) : 0u;
         const uint32_t cb = L < nb ? static_cast<uint32_t>(__popcll(mb[L])) : 0u;
@@ -188,12 +195,20 @@ struct MaskPrefix {
         a.total = tot & 0xFFFFu;
         b.total = tot >> 16;
     }
-    // set bits before bit `bit` of entry e
+    // set bits before this lane's bit of entry e (e the same in the whole wave)
+    __device__ __forceinline__ uint32_t own(int32_t e) const
+    {
+        const int32_t L = e >> lg;
+        uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ex), L));
+        for (int32_t x = L << lg; x < e; ++x) c += static_cast<uint32_t>(__popcll(mk[x]));
+        return c + lanes_below(mk[e]);
+    }
+    // set bits before bit `bit` of entry e (any entry per lane)
     __device__ __forceinline__ uint32_t before(int32_t e, uint32_t bit) const
     {
-        const int32_t L = e / g;
+        const int32_t L = e >> lg;
         uint32_t c = static_cast<uint32_t>(__shfl(static_cast<int>(ex), L));
-        for (int32_t x = L * g; x < e; ++x) c += static_cast<uint32_t>(__popcll(mk[x]));
+        for (int32_t x = L << lg; x < e; ++x) c += static_cast<uint32_t>(__popcll(mk[x]));
         return c + static_cast<uint32_t>(__popcll(mk[e] & ((1ull << bit) - 1ull)));
     }
 };
@@ -313,9 +328,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const int32_t bid = blockIdx.x;
     const int32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
-    const int32_t wave = tid >> 6;
+    const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (bid >= maxNumReqs) return;
 
+    WSTAMP(8);
     int32_t numReal = *(KVX_G const int32_t *)(a.numReal);
     if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
     KVX_G int32_t *rs = (KVX_G int32_t *)(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
@@ -324,11 +340,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
+    WSTAMP(9);
     const int64_t reqIdx = ((KVX_G const int64_t *)(a.reqPoolIndices))[bid];
     if (reqIdx < 0 || reqIdx >= poolSize) {
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
+    WSTAMP(10);
     const int32_t seqLen = ((KVX_G const int32_t *)(a.seqLens))[bid];
     const int32_t prefill = ((KVX_G const int32_t *)(a.prefillLens))[reqIdx];
     KVX_G const int32_t *rt = (KVX_G const int32_t *)(a.topkIndices) + static_cast<int64_t>(bid) * K;
@@ -361,6 +379,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint64_t *cmask = reinterpret_cast<uint64_t *>(smem + lay.cmask);  // first occurrences of candidates
     uint64_t *emask = reinterpret_cast<uint64_t *>(smem + lay.emask);  // event positions
     uint64_t *smask = reinterpret_cast<uint64_t *>(smem + lay.smask);  // evicted SM slots
+    uint64_t *rsn = reinterpret_cast<uint64_t *>(smem + lay.rsn);      // SN slots by ring offset
+    uint64_t *rsm = reinterpret_cast<uint64_t *>(smem + lay.rsm);      // SM slots by ring offset
+    uint16_t *cellOf = reinterpret_cast<uint16_t *>(smem + lay.cellOf);  // full form: cell of slot s's entry
     // direct token -> slot map for rows whose prefill fits the LDS left over
     // (after the layout).  It is not cleared: an entry is trusted only when it
     // checks out -- slot+1 of a slot holding the token, or padded+1+k of a
@@ -394,12 +415,11 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
     constexpr bool kFixed = PM > 0 && QM > 0;
     const int32_t P = kFixed ? PM : (K + NT - 1) / NT;    // positions per lane: k = tid + q * NT
-    const int32_t Q = kFixed ? QM : (dbs + NT - 1) / NT;  // ring offsets per lane: u = tid * Q + j
-    const int32_t u0 = tid * Q;
+    const int32_t Q = kFixed ? QM : (dbs + NT - 1) / NT;  // ring offsets per lane: u = tid + j * NT
     constexpr int PR = kFixed ? PM : 1, QR = kFixed ? QM : 1;
     int32_t tR[PR];    // token of position tid + q * NT
     uint32_t iR[PR];   // its class word (pinf)
-    uint32_t vR[QR];   // first-hit code (vt) of ring offset u0 + j
+    uint32_t vR[QR];   // first-hit code (vt) of ring offset tid + j * NT
 
     // ---- stage the state row and the topK row; visited flags per slot (vt),
     // the direct map, the table's occupancy bitmap; count live tokens and
@@ -410,7 +430,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const bool flagged = gHand[1] == kCanonFlag;
     {
         const int32_t nt = padded >> 2, nh = H >> 3, nv = visStrideB >> 4;  // 16-byte chunks
-        const int32_t nAll = nt + nh + nv;
         KVX_G const v4u *sT = (KVX_G const v4u *)gTok;
         KVX_G const v4u *sH = (KVX_G const v4u *)gHt;
         KVX_G const v4u *sV = (KVX_G const v4u *)gVis;
@@ -419,36 +438,46 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const bool h0 = tid < K, h1 = tid + NT < K;
         if (h0) t0 = rt[tid];
         if (h1) t1 = rt[tid + NT];
-        for (int32_t c0 = tid; c0 < nAll; c0 += 4 * NT) {
-            v4u v[4];
-            uint32_t vb[4];
+        // Each region loads into registers of its own, all before the first
+        // use: loads that share a destination register across divergent
+        // branches would each wait for the previous one to land.
+        // pass p: token chunks [2 NT p, 2 NT (p+1)), table chunks [4 NT p, ...),
+        // visited chunks [NT p, ...).  The first pass (all of it for rows up
+        // to 8192 slots) is straight-line code: in a loop the compiler waits
+        // for the previous iteration's loads before reusing their registers.
+        auto stage_pass = [&](int32_t p) __attribute__((always_inline)) {
+            v4u vT[2], vH[4], vV;
+            uint32_t vB[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int32_t c = c0 + j * NT;
-                if (c < nt) {
-                    v[j] = sT[c];
-                    vb[j] = gVis[c >> 1];  // the 8 visited bits of slots 8(c/2)..
-                } else if (c < nt + nh) {
-                    v[j] = sH[c - nt];
-                } else if (c < nAll) {
-                    v[j] = sV[c - nt - nh];
-                }
+            for (int j = 0; j < 2; ++j) {
+                // unconditional (clamped) loads: a load under a branch makes
+                // the compiler wait for it at the branch's end
+                const int32_t c = min(2 * NT * p + tid + j * NT, nt - 1);
+                vT[j] = sT[c];
+                vB[j] = gVis[c >> 1];  // the visited bits of slots 8(c/2)..
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int32_t c = c0 + j * NT;
+                vH[j] = sH[min(4 * NT * p + tid + j * NT, nh - 1)];
+            }
+            const int32_t cv = NT * p + tid;
+            vV = sV[min(cv, nv - 1)];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int32_t c = 2 * NT * p + tid + j * NT;
                 if (c < nt) {
-                    const int32_t tt[4] = {static_cast<int32_t>(v[j].x), static_cast<int32_t>(v[j].y),
-                                           static_cast<int32_t>(v[j].z), static_cast<int32_t>(v[j].w)};
+                    const v4u x = vT[j];
+                    const int32_t tt[4] = {static_cast<int32_t>(x.x), static_cast<int32_t>(x.y),
+                                           static_cast<int32_t>(x.z), static_cast<int32_t>(x.w)};
                     if constexpr (kC) {
                         uint32_t hh[4];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) hh[i] = tt[i] < 0 ? HV_EMPTY : (ht_hash(tt[i]) & static_cast<uint32_t>(mask));
                         reinterpret_cast<uint2 *>(hv)[c] = make_uint2(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16));
                     } else {
-                        reinterpret_cast<v4u *>(tok)[c] = v[j];
+                        reinterpret_cast<v4u *>(tok)[c] = x;
                     }
-                    const uint32_t nib = (vb[j] >> ((c & 1) * 4)) & 0xFu;
+                    const uint32_t nib = (vB[j] >> ((c & 1) * 4)) & 0xFu;
                     vt32[2 * c] = ((nib & 1u) ? 0u : 0xFFFFu) | ((nib & 2u) ? 0u : 0xFFFF0000u);
                     vt32[2 * c + 1] = ((nib & 4u) ? 0u : 0xFFFFu) | ((nib & 8u) ? 0u : 0xFFFF0000u);
                     const int32_t s0 = c * 4;
@@ -458,22 +487,38 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         nTok += live ? 1u : 0u;
                         if (direct && live && tt[i] < prefill) inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
                     }
-                } else if (c < nt + nh) {
-                    reinterpret_cast<v4u *>(ht)[c - nt] = v[j];
-                    const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int32_t c = 4 * NT * p + tid + j * NT;
+                if (c < nh) {
+                    const v4u x = vH[j];
+                    reinterpret_cast<v4u *>(ht)[c] = x;
+                    const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
                     uint32_t ob = 0;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         ob |= (((w4[q] & 0xFFFFu) != 0u) ? 1u : 0u) << (2 * q);
                         ob |= (((w4[q] >> 16) != 0u) ? 1u : 0u) << (2 * q + 1);
                     }
-                    occ8[c - nt] = static_cast<uint8_t>(ob);
+                    occ8[c] = static_cast<uint8_t>(ob);
                     nEnt += static_cast<uint32_t>(__popc(ob));
-                } else if (c < nAll) {
-                    reinterpret_cast<v4u *>(vis)[c - nt - nh] = v[j];
+                    if constexpr (!kC) {  // inverse of the table: the cell of each slot's entry
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const uint32_t lo = w4[q] & 0xFFFFu, hi = w4[q] >> 16;
+                            if (lo - 1u < static_cast<uint32_t>(padded)) cellOf[lo - 1u] = static_cast<uint16_t>(8 * c + 2 * q);
+                            if (hi - 1u < static_cast<uint32_t>(padded)) cellOf[hi - 1u] = static_cast<uint16_t>(8 * c + 2 * q + 1);
+                        }
+                    }
                 }
             }
-        }
+            if (cv < nv) reinterpret_cast<v4u *>(vis)[cv] = vV;
+        };
+        stage_pass(0);
+        for (int32_t p = 1; 2 * NT * p < nt || 4 * NT * p < nh || NT * p < nv; ++p) stage_pass(p);
+        WSTAMP(11);
         if (h0) ptok[tid] = t0;
         if (h1) ptok[tid + NT] = t1;
         for (int32_t k = tid + 2 * NT; k < K; k += NT) ptok[k] = rt[k];
@@ -497,8 +542,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             ms.bad = ms.ovf = ms.late = 0;
             ms.nSM = ms.nUnd = ms.nRest = ms.uEnd = ms.nTakes = ms.nLead = 0;
         }
+        WSTAMP(12);
     }
     __syncthreads();
+    WSTAMP(13);
     STAMP(1);
 
     // ---- consistency: the table indexes exactly the non-negative tokens of
@@ -652,7 +699,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // ---- candidates' first occurrences (ballot masks in position order) and
     // the ring classes per offset from the hand, with one prefix scan; then
     // the SM list up to the M-th SN slot
-    uint32_t snM = 0, smM = 0, preSN = 0, preSM = 0, M = 0;
+    uint32_t snM = 0, smM = 0, M = 0;  // bit j: class of ring offset tid + j * NT
+    MaskPrefix snP, smP;                // SN / SM slots before a ring offset
     if (fast) {
         WSTAMP(0);
         uint32_t cw = 0;
@@ -681,38 +729,30 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             cw += static_cast<uint32_t>(__popcll(m));
         }
         WSTAMP(1);
+        // ring offsets are lane-strided so that the hand's walk (the first
+        // offsets) spreads over all waves
 #pragma unroll
         for (int32_t j = 0; j < Q; ++j) {
-            const int32_t u = u0 + j;
+            const int32_t u = tid + j * NT;
             const uint32_t v = (u < dbs) ? vt[ring_slot(hand0, u, dbs)] : 0u;
             if constexpr (kFixed) vR[j] = v;
-            snM |= (v == VT_NONE ? 1u : 0u) << j;
-            smM |= (v != 0u && v != VT_NONE ? 1u : 0u) << j;
+            const bool sn = u < dbs && v == VT_NONE, sm = u < dbs && v != 0u && v != VT_NONE;
+            snM |= (sn ? 1u : 0u) << j;
+            smM |= (sm ? 1u : 0u) << j;
+            const uint64_t bsn = __ballot(sn), bsm = __ballot(sm);
+            if (lane == 0) {
+                rsn[j * NWAVES + wave] = bsn;
+                rsm[j * NWAVES + wave] = bsm;
+            }
         }
         WSTAMP(2);
-        const uint32_t cSN = static_cast<uint32_t>(__popc(snM)), cSM = static_cast<uint32_t>(__popc(smM));
-        const uint32_t packed = cSN | (cSM << 16);
-        const uint32_t incl = wave_incl_scan(packed);
-        uint32_t pre = incl - packed;
-        const uint32_t tot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
-        if (lane == 0) {
-            ms.wring[wave] = tot;
-            ms.wcand[wave] = cw;
-        }
+        if (lane == 0) ms.wcand[wave] = cw;
         WSTAMP(3);
         __syncthreads();
         WSTAMP(4);
-        uint32_t off = 0, all = 0;
 #pragma unroll
-        for (int w = 0; w < NWAVES; ++w) {
-            const uint32_t c = ms.wring[w];
-            off += (w < wave) ? c : 0u;
-            all += c;
-            M += ms.wcand[w];
-        }
-        pre += off;
-        preSN = pre & 0xFFFFu;
-        preSM = pre >> 16;
+        for (int w = 0; w < NWAVES; ++w) M += ms.wcand[w];
+        MaskPrefix::init_pair(snP, rsn, Q * NWAVES, smP, rsm, Q * NWAVES, lane);
         if (M > 0) {
             // only SM slots with fewer than M SN slots before them can be
             // reached (the SN slots before a slot are all evicted first, and
@@ -721,11 +761,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             MaskPrefix cp;
             cp.init(cmask, P * NWAVES, lane);
             WSTAMP(5);
-            uint32_t nsn = preSN, nsm = preSM;
 #pragma unroll
             for (int32_t j = 0; j < Q; ++j) {
                 const bool isSM = (smM >> j) & 1u, isSN = (snM >> j) & 1u;
-                const int32_t u = u0 + j;
+                const int32_t u = tid + j * NT;
+                const int32_t e = j * NWAVES + wave;
+                const uint32_t nsn = snP.own(e), nsm = smP.own(e);
                 uint32_t k = 0;
                 if (isSM) k = (kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)])) - 1u;
                 const uint32_t cc = cp.before(static_cast<int32_t>(k >> 6), k & 63u);
@@ -735,7 +776,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     smKp[nsm] = (cc > nsn) ? static_cast<uint16_t>(k) : static_cast<uint16_t>(0);
                     posSM[k] = static_cast<uint16_t>(nsm + 1u);
                 }
-                if (isSN && nsn < M) {
+                if (kC && isSN && nsn < M) {
                     // every SN slot before the M-th is evicted: look up its
                     // token's cell now (vt of an SN slot is not read again)
                     const int32_t sl = ring_slot(hand0, u, dbs);
@@ -743,12 +784,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     if (slot_live(sl)) {
                         int32_t idx = slot_home(sl);
                         for (int32_t n = 0; n <= mask; ++n) {
-                            const uint32_t e = ht[idx];
-                            if (e == static_cast<uint32_t>(sl + 1)) {
+                            const uint32_t ev = ht[idx];
+                            if (ev == static_cast<uint32_t>(sl + 1)) {
                                 cell = static_cast<uint32_t>(idx);
                                 break;
                             }
-                            if (e == 0u) break;
+                            if (ev == 0u) break;
                             idx = (idx + 1) & mask;
                         }
                         if (cell == NOCELL) atomicOr(&ms.ovf, 1);
@@ -756,10 +797,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                     vt[sl] = static_cast<uint16_t>(cell);
                 }
-                if (isSN && ++nsn == M) ms.nSM = static_cast<int32_t>(nsm);
-                nsm += isSM ? 1u : 0u;
+                if (isSN && nsn + 1u == M) ms.nSM = static_cast<int32_t>(nsm);
             }
-            if (tid == 0 && (all & 0xFFFFu) < M) ms.nSM = static_cast<int32_t>(all >> 16);
+            if (tid == 0 && snP.total < M) ms.nSM = static_cast<int32_t>(smP.total);
         }
         WSTAMP(6);
         __syncthreads();
@@ -895,7 +935,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const uint32_t T = sp.total;
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
-            const uint32_t pre = sp.before(i >> 6, static_cast<uint32_t>(i) & 63u);
+            const uint32_t pre = sp.own(q * NWAVES + wave);
             if (i < nSM) {
                 const uint32_t tk = static_cast<uint32_t>((smask[i >> 6] >> (i & 63)) & 1ull);
                 tb[i] = static_cast<uint16_t>(pre | (tk << 15));
@@ -906,7 +946,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
-            const uint32_t pre = ep.before(k >> 6, static_cast<uint32_t>(k) & 63u);
+            const uint32_t pre = ep.own(q * NWAVES + wave);
             if (k < K && ((emask[k >> 6] >> (k & 63)) & 1ull)) {
                 // the event inserts the position's own token: a candidate's,
                 // or for a conversion the token of the slot its hit lost
@@ -925,10 +965,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     if (fast) {
         Guard g;
         const uint32_t nSMu = static_cast<uint32_t>(nSM);  // tb[nSM] = T covers the unlisted SM slots
-        uint32_t nsn2 = preSN, nsm2 = preSM < nSMu ? preSM : nSMu, ntk = 0;
+        uint32_t ntk = 0;
 #pragma unroll
         for (int32_t j = 0; j < Q; ++j) {
-            const int32_t u = u0 + j;
+            const int32_t u = tid + j * NT;
+            const int32_t e = j * NWAVES + wave;
+            const uint32_t nsn2 = snP.own(e), nsm2 = min(smP.own(e), nSMu);
             if (u >= dbs) continue;
             const int32_t s = ring_slot(hand0, u, dbs);
             const bool isSN = (snM >> j) & 1u, isSM = (smM >> j) & 1u;
@@ -941,11 +983,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     ++ntk;
                     if (r == N - 1) ms.uEnd = u + 1;
                     uint32_t cell;
-                    if (isSN) {
-                        cell = vt[s];  // looked up with the ring classes
-                    } else {
+                    if (isSM) {
                         const uint32_t v0 = kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[s]);
                         vt[s] = static_cast<uint16_t>(VT_EVICTED | (v0 - 1u));
+                    }
+                    if constexpr (!kC) {
+                        cell = NOCELL;
+                        if (tok[s] >= 0) {
+                            cell = cellOf[s];
+                            atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+                        }
+                    } else if (isSN) {
+                        cell = vt[s];  // looked up with the ring classes
+                    } else {
                         cell = NOCELL;
                         if (slot_live(s)) {
                             int32_t idx = slot_home(s);
@@ -967,8 +1017,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     vt[s] = static_cast<uint16_t>(VT_PASSED | p);
                 }
             }
-            nsn2 += isSN ? 1u : 0u;
-            nsm2 += (isSM && nsm2 < nSMu) ? 1u : 0u;
         }
         ntk = wave_sum(ntk);
         if (lane == 0 && ntk) atomicAdd(&ms.nTakes, static_cast<int32_t>(ntk));
@@ -1247,8 +1295,12 @@ hipError_t sieve_fast_set_lds_limit(size_t bytes)
     if ((e = set_limit_one<false, 0, 0>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<false, 2, 4>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<false, 2, 8>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<false, 4, 8>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<false, 4, 16>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<true, 0, 0>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<true, 2, 4>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<true, 4, 8>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<true, 4, 16>(bytes)) != hipSuccess) return e;
     return set_limit_one<true, 2, 8>(bytes);
 }
 
@@ -1261,6 +1313,10 @@ static void launch_one(const KvxLaunch<HispSieveUpdateArgs> &L, size_t ldsBytes,
         hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 4>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     } else if (P == 2 && Q == 8) {
         hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 8>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    } else if (P == 4 && Q == 8) {
+        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 4, 8>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    } else if (P == 4 && Q == 16) {
+        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 4, 16>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     } else {
         hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 0, 0>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     }
