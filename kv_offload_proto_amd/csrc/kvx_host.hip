@@ -258,7 +258,7 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         int lds = 0;
         hipCheck(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device_id),
                  "hipDeviceGetAttribute(LDS)");
-        g.ldsLimit = static_cast<size_t>(lds) - 512;  // room for the kernels' static LDS (under 512 B)
+        g.ldsLimit = static_cast<size_t>(lds) - 1024;  // room for the kernels' static LDS (under 1 KiB)
         hipCheck(kvx::sieve_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS)");
         hipCheck(kvx::sieve_fast_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS fast)");
         void *c = nullptr;

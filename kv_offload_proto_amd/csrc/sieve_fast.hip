@@ -114,11 +114,13 @@ __device__ unsigned long long kvx_dbg_w[64][16][16];
 #endif
 
 struct Misc {
-    int32_t bad, ovf, late, nSM, nUnd, nRest, uEnd, nTakes, nLead;
+    int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead;
     uint32_t wtok[NWAVES];
     uint32_t went[NWAVES];
     uint32_t wring[NWAVES];
     uint32_t wcand[NWAVES];
+    uint32_t uL[64];  // undecided SM slots in ring order: evictions settled before them with a larger k
+    uint16_t ui[64];  // ... and their SM indices
 };
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
@@ -540,7 +542,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         if (tid == 0) {
             ms.bad = ms.ovf = ms.late = 0;
-            ms.nSM = ms.nUnd = ms.nRest = ms.uEnd = ms.nTakes = ms.nLead = 0;
+            ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = 0;
         }
         WSTAMP(12);
     }
@@ -851,49 +853,68 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         // either as undecided (counted in X) or settled (counted exactly):
         // both are safe.
         const int32_t nUnd = ms.nUnd;
-        if (nUnd > 0) {
+        if (nUnd > 0 && nUnd <= 64) {
+            // undecided slots (few): one wave each counts the evictions
+            // settled in the first pass before it with a larger k (L) and
+            // files it under its rank in ring order; then one wave walks
+            // them in ring order, adding the evictions among the undecided
+            // ones before each: D = L + #{undecided j < i evicted, k_j > k_i}
             for (int32_t e = wave; e < nUnd; e += NWAVES) {
                 const int32_t i = static_cast<int32_t>(undl[e]);
                 const uint32_t ki = smA[i] >> 16;
-                uint32_t lx = 0;
+                uint32_t l = 0;
                 for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
-                    const uint16_t dj = tb[j];
-                    if (dj != 0 && (smA[j] >> 16) > ki) lx += (dj == 1) ? 1u : 0x10000u;
+                    l += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
                 }
-                lx = wave_sum(lx);
+                l = wave_sum(l);
+                const bool before = static_cast<int32_t>(lane) < nUnd && static_cast<int32_t>(undl[lane]) < i;
+                const int32_t rank = __popcll(__ballot(before));
                 if (lane == 0) {
-                    if ((lx >> 16) == 0u) {
+                    ms.uL[rank] = l;
+                    ms.ui[rank] = static_cast<uint16_t>(i);
+                }
+            }
+            __syncthreads();
+            if (wave == 0) {
+                const bool act = static_cast<int32_t>(lane) < nUnd;
+                const int32_t i = act ? static_cast<int32_t>(ms.ui[lane]) : 0;
+                const uint32_t ki = act ? (smA[i] >> 16) : 0u;
+                const uint32_t eb = act ? smB[i] : 0u;
+                const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
+                const uint32_t l = act ? ms.uL[lane] : 0u;
+                uint64_t ev = 0;  // undecided slots found evicted so far (by rank)
+                for (int32_t e = 0; e < nUnd; ++e) {
+                    const uint32_t ke = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ki), e));
+                    const int32_t ae = __builtin_amdgcn_readlane(ai, e);
+                    const uint32_t le = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(l), e));
+                    const uint64_t larger = __ballot(static_cast<int32_t>(lane) < e && ki > ke);
+                    const uint32_t d = le + static_cast<uint32_t>(__popcll(larger & ev));
+                    if (ae >= static_cast<int32_t>(d)) ev |= 1ull << e;
+                }
+                if (act) tb[i] = ((ev >> lane) & 1ull) ? 1 : 0;
+            }
+            __syncthreads();
+        } else if (nUnd > 64) {  // many undecided slots: one wave settles them in ring order
+            if (wave == 0) {
+                for (int32_t c = 0; c < nSM; c += 64) {
+                    uint64_t und = __ballot(c + static_cast<int32_t>(lane) < nSM && tb[c + lane] == 2);
+                    while (und != 0ull) {
+                        const int f = __builtin_ctzll(und);
+                        und &= und - 1ull;
+                        const int32_t i = c + f;
+                        const uint32_t ki = smA[i] >> 16;
                         const uint32_t eb = smB[i];
                         const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
-                        tb[i] = (ai >= static_cast<int32_t>(lx & 0xFFFFu)) ? 1 : 0;
-                    } else {
-                        atomicAdd(&ms.nRest, 1);
+                        uint32_t d = 0;
+                        for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
+                            d += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
+                        }
+                        d = wave_sum(d);
+                        if (lane == 0) tb[i] = (ai >= static_cast<int32_t>(d)) ? 1 : 0;
                     }
                 }
             }
             __syncthreads();
-            if (ms.nRest > 0) {  // the rest, in ring order, by one wave
-                if (wave == 0) {
-                    for (int32_t c = 0; c < nSM; c += 64) {
-                        uint64_t und = __ballot(c + static_cast<int32_t>(lane) < nSM && tb[c + lane] == 2);
-                        while (und != 0ull) {
-                            const int f = __builtin_ctzll(und);
-                            und &= und - 1ull;
-                            const int32_t i = c + f;
-                            const uint32_t ki = smA[i] >> 16;
-                            const uint32_t eb = smB[i];
-                            const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
-                            uint32_t d = 0;
-                            for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
-                                d += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
-                            }
-                            d = wave_sum(d);
-                            if (lane == 0) tb[i] = (ai >= static_cast<int32_t>(d)) ? 1 : 0;
-                        }
-                    }
-                }
-                __syncthreads();
-            }
         }
     }
     STAMP(4);
