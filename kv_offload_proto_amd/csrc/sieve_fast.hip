@@ -157,37 +157,43 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m)
 // entries.  Set up and query with the whole wave active.
 struct MaskPrefix {
     const uint64_t *mk;
+    const uint64_t *mk2;  // optional second array, OR'ed into mk (null: none)
     int32_t lg;
     uint32_t ex;     // prefix of this lane's first entry
     uint32_t total;  // set bits in all entries
 
-    __device__ __forceinline__ void init(const uint64_t *m, int32_t nE, uint32_t lane)
+    __device__ __forceinline__ uint64_t ent(int32_t x) const { return mk2 ? (mk[x] | mk2[x]) : mk[x]; }
+    __device__ __forceinline__ void init(const uint64_t *m, int32_t nE, uint32_t lane, const uint64_t *m2 = nullptr)
     {
         mk = m;
+        mk2 = m2;
         lg = 0;
         while ((64 << lg) < nE) ++lg;
         const int32_t e0 = static_cast<int32_t>(lane) << lg;
         uint32_t s = 0;
-        for (int32_t x = e0; x < e0 + (1 << lg) && x < nE; ++x) s += static_cast<uint32_t>(__popcll(mk[x]));
+        for (int32_t x = e0; x < e0 + (1 << lg) && x < nE; ++x) s += static_cast<uint32_t>(__popcll(ent(x)));
         const uint32_t incl = wave_incl_scan(s);
         ex = incl - s;
         total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
     }
     // two prefixes from one scan (16-bit fields) when both fit one entry per lane
     static __device__ __forceinline__ void init_pair(MaskPrefix &a, const uint64_t *ma, int32_t na, MaskPrefix &b,
-                                                     const uint64_t *mb, int32_t nb, uint32_t lane)
+                                                     const uint64_t *mb, int32_t nb, uint32_t lane,
+                                                     const uint64_t *mb2 = nullptr)
     {
         if (na > 64 || nb > 64) {
             a.init(ma, na, lane);
-            b.init(mb, nb, lane);
+            b.init(mb, nb, lane, mb2);
             return;
         }
         a.mk = ma;
         b.mk = mb;
+        a.mk2 = nullptr;
+        b.mk2 = mb2;
         a.lg = b.lg = 0;
         const int32_t L = static_cast<int32_t>(lane);
-        const uint32_t ca = L < na ? static_cast<uint32_t>(__popcll(ma[L])) : 0u;
-        const uint32_t cb = L < nb ? static_cast<uint32_t>(__popcll(mb[L])) : 0u;
+        const uint32_t ca = L < na ? static_cast<uint32_t>(__popcll(a.ent(L))) : 0u;
+        const uint32_t cb = L < nb ? static_cast<uint32_t>(__popcll(b.ent(L))) : 0u;
         const uint32_t packed = ca | (cb << 16);
         const uint32_t incl = wave_incl_scan(packed);
         const uint32_t ex = incl - packed;
@@ -202,16 +208,16 @@ struct MaskPrefix {
     {
         const int32_t L = e >> lg;
         uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ex), L));
-        for (int32_t x = L << lg; x < e; ++x) c += static_cast<uint32_t>(__popcll(mk[x]));
-        return c + lanes_below(mk[e]);
+        for (int32_t x = L << lg; x < e; ++x) c += static_cast<uint32_t>(__popcll(ent(x)));
+        return c + lanes_below(ent(e));
     }
     // set bits before bit `bit` of entry e (any entry per lane)
     __device__ __forceinline__ uint32_t before(int32_t e, uint32_t bit) const
     {
         const int32_t L = e >> lg;
         uint32_t c = static_cast<uint32_t>(__shfl(static_cast<int>(ex), L));
-        for (int32_t x = L << lg; x < e; ++x) c += static_cast<uint32_t>(__popcll(mk[x]));
-        return c + static_cast<uint32_t>(__popcll(mk[e] & ((1ull << bit) - 1ull)));
+        for (int32_t x = L << lg; x < e; ++x) c += static_cast<uint32_t>(__popcll(ent(x)));
+        return c + static_cast<uint32_t>(__popcll(ent(e) & ((1ull << bit) - 1ull)));
     }
 };
 
@@ -379,7 +385,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *occ = reinterpret_cast<uint32_t *>(smem + lay.occ);   // occupied cells of the pre-step table
     uint8_t *occ8 = smem + lay.occ;
     uint64_t *cmask = reinterpret_cast<uint64_t *>(smem + lay.cmask);  // first occurrences of candidates
-    uint64_t *emask = reinterpret_cast<uint64_t *>(smem + lay.emask);  // event positions
+    uint64_t *emask = reinterpret_cast<uint64_t *>(smem + lay.emask);  // conversion positions
     uint64_t *smask = reinterpret_cast<uint64_t *>(smem + lay.smask);  // evicted SM slots
     uint64_t *rsn = reinterpret_cast<uint64_t *>(smem + lay.rsn);      // SN slots by ring offset
     uint64_t *rsm = reinterpret_cast<uint64_t *>(smem + lay.rsm);      // SM slots by ring offset
@@ -394,7 +400,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *inv32 = reinterpret_cast<uint32_t *>(smem + lay.total);
     // reuse of regions whose earlier contents are dead by then
     uint32_t *pcell = smA;                                   // classify: provisional cell per position
-    uint16_t *posSM = evslot;                                // SM index + 1 per first-hit position
     uint16_t *undl = eseq;                                   // decide: undecided SM indices
     uint32_t *ecell = smA;                                   // per event: table cell | slot << 16
     uint16_t *lead = eseq;                                   // redo: start cell of each multi-key cluster
@@ -533,7 +538,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         for (int32_t i = tid; i < (visStrideB >> 2); i += NT) vset[i] = 0u;
         for (int32_t i = tid; i < (H >> 5); i += NT) ber[i] = 0u;
-        for (int32_t i = tid; i < ((K + 1) >> 1); i += NT) reinterpret_cast<uint32_t *>(posSM)[i] = 0u;
+        for (int32_t i = tid; i < 2 * P * NWAVES; i += NT) emask[i] = 0ull;  // emask, smask (adjacent)
         nTok = wave_sum(nTok);
         nEnt = wave_sum(nEnt);
         if (lane == 0) {
@@ -704,7 +709,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t snM = 0, smM = 0, M = 0;  // bit j: class of ring offset tid + j * NT
     MaskPrefix snP, smP;                // SN / SM slots before a ring offset
     if (fast) {
-        WSTAMP(0);
         uint32_t cw = 0;
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
@@ -730,7 +734,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (lane == 0) cmask[q * NWAVES + wave] = m;
             cw += static_cast<uint32_t>(__popcll(m));
         }
-        WSTAMP(1);
         // ring offsets are lane-strided so that the hand's walk (the first
         // offsets) spreads over all waves
 #pragma unroll
@@ -747,11 +750,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 rsm[j * NWAVES + wave] = bsm;
             }
         }
-        WSTAMP(2);
         if (lane == 0) ms.wcand[wave] = cw;
-        WSTAMP(3);
         __syncthreads();
-        WSTAMP(4);
 #pragma unroll
         for (int w = 0; w < NWAVES; ++w) M += ms.wcand[w];
         MaskPrefix::init_pair(snP, rsn, Q * NWAVES, smP, rsm, Q * NWAVES, lane);
@@ -762,7 +762,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             // is a prefix of the SM slots in ring order
             MaskPrefix cp;
             cp.init(cmask, P * NWAVES, lane);
-            WSTAMP(5);
 #pragma unroll
             for (int32_t j = 0; j < Q; ++j) {
                 const bool isSM = (smM >> j) & 1u, isSN = (snM >> j) & 1u;
@@ -776,7 +775,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     smA[nsm] = static_cast<uint32_t>(u) | (k << 16);
                     smB[nsm] = nsn | (cc << 16);
                     smKp[nsm] = (cc > nsn) ? static_cast<uint16_t>(k) : static_cast<uint16_t>(0);
-                    posSM[k] = static_cast<uint16_t>(nsm + 1u);
                 }
                 if (kC && isSN && nsn < M) {
                     // every SN slot before the M-th is evicted: look up its
@@ -803,9 +801,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             if (tid == 0 && snP.total < M) ms.nSM = static_cast<int32_t>(smP.total);
         }
-        WSTAMP(6);
         __syncthreads();
-        WSTAMP(7);
     }
     STAMP(3);
 
@@ -842,7 +838,14 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
                 for (int o = 1; o < G; o <<= 1) U += static_cast<uint32_t>(__shfl_xor(static_cast<int>(U), o));
                 dec = (ai >= static_cast<int32_t>(U)) ? 1 : 2;
-                if (dec == 2 && part == 0) undl[atomicAdd(&ms.nUnd, 1)] = static_cast<uint16_t>(i);
+                if (part == 0) {
+                    if (dec == 2) {
+                        undl[atomicAdd(&ms.nUnd, 1)] = static_cast<uint16_t>(i);
+                    } else {  // evicted: its first hit converts
+                        atomicOr(reinterpret_cast<unsigned long long *>(smask) + (i >> 6), 1ull << (i & 63));
+                        atomicOr(reinterpret_cast<unsigned long long *>(emask) + (ki >> 6), 1ull << (ki & 63u));
+                    }
+                }
             }
             if (part == 0) tb[i] = dec;
         }
@@ -891,7 +894,14 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     const uint32_t d = le + static_cast<uint32_t>(__popcll(larger & ev));
                     if (ae >= static_cast<int32_t>(d)) ev |= 1ull << e;
                 }
-                if (act) tb[i] = ((ev >> lane) & 1ull) ? 1 : 0;
+                if (act) {
+                    const bool evd = (ev >> lane) & 1ull;
+                    tb[i] = evd ? 1 : 0;
+                    if (evd) {
+                        atomicOr(reinterpret_cast<unsigned long long *>(smask) + (i >> 6), 1ull << (i & 63));
+                        atomicOr(reinterpret_cast<unsigned long long *>(emask) + (ki >> 6), 1ull << (ki & 63u));
+                    }
+                }
             }
             __syncthreads();
         } else if (nUnd > 64) {  // many undecided slots: one wave settles them in ring order
@@ -910,7 +920,14 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                             d += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
                         }
                         d = wave_sum(d);
-                        if (lane == 0) tb[i] = (ai >= static_cast<int32_t>(d)) ? 1 : 0;
+                        if (lane == 0) {
+                            const bool evd = ai >= static_cast<int32_t>(d);
+                            tb[i] = evd ? 1 : 0;
+                            if (evd) {
+                                atomicOr(reinterpret_cast<unsigned long long *>(smask) + (i >> 6), 1ull << (i & 63));
+                                atomicOr(reinterpret_cast<unsigned long long *>(emask) + (ki >> 6), 1ull << (ki & 63u));
+                            }
+                        }
                     }
                 }
             }
@@ -925,50 +942,29 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // event sequence in position order
     int32_t N = 0;
     if (fast) {
+        WSTAMP(0);
         const int32_t Ps = (nSM + NT - 1) / NT;
-        for (int32_t q = 0; q < Ps; ++q) {
-            const int32_t i = tid + q * NT;
-            bool tk = false;
-            if (i < nSM && tb[i] == 1) tk = true;
-            const uint64_t m = __ballot(tk);
-            if (lane == 0) smask[q * NWAVES + wave] = m;
-        }
-#pragma unroll
-        for (int32_t q = 0; q < P; ++q) {
-            const int32_t k = tid + q * NT;
-            bool f = false;
-            if (k < K) {
-                const uint32_t inf = kFixed ? iR[kFixed ? q : 0] : pinf[k];
-                const uint32_t c = inf >> 30;
-                if (c == CLS_CAND) {
-                    f = (inf & 0xFFFFu) == static_cast<uint32_t>(k);
-                } else if (c == CLS_HIT) {
-                    const uint32_t sm = posSM[k];
-                    f = sm != 0u && tb[sm - 1u] == 1;
-                }
-            }
-            const uint64_t m = __ballot(f);
-            if (lane == 0) emask[q * NWAVES + wave] = m;
-        }
-        __syncthreads();
         MaskPrefix sp, ep;
-        MaskPrefix::init_pair(sp, smask, Ps * NWAVES, ep, emask, P * NWAVES, lane);
+        // events: candidates' first occurrences (cmask) and conversions (emask)
+        MaskPrefix::init_pair(sp, smask, Ps * NWAVES, ep, cmask, P * NWAVES, lane, emask);
+        WSTAMP(4);
         const uint32_t T = sp.total;
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
             const uint32_t pre = sp.own(q * NWAVES + wave);
             if (i < nSM) {
-                const uint32_t tk = static_cast<uint32_t>((smask[i >> 6] >> (i & 63)) & 1ull);
+                const uint32_t tk = static_cast<uint32_t>((smask[i >> 6] >> (i & 63)) & 1ull);  // evicted
                 tb[i] = static_cast<uint16_t>(pre | (tk << 15));
             }
         }
         if (tid == 0) tb[nSM] = static_cast<uint16_t>(T);
+        WSTAMP(5);
         N = static_cast<int32_t>(M + T);
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
             const uint32_t pre = ep.own(q * NWAVES + wave);
-            if (k < K && ((emask[k >> 6] >> (k & 63)) & 1ull)) {
+            if (k < K && ((ep.ent(k >> 6) >> (k & 63)) & 1ull)) {
                 // the event inserts the position's own token: a candidate's,
                 // or for a conversion the token of the slot its hit lost
                 eseq[pre] = static_cast<uint16_t>(k);
@@ -976,7 +972,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (ep.total != static_cast<uint32_t>(N)) fast = false;  // same value in every wave
+        WSTAMP(6);
         __syncthreads();
+        WSTAMP(7);
     }
     STAMP(5);
 
