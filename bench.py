@@ -35,6 +35,8 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--verify", action="store_true", help="check the last step's imported rows on the GPU")
     p.add_argument("--link-mib", type=int, default=256)
+    p.add_argument("--sieve-variant", type=int, default=-1,
+                   help="force a SIEVE kernel variant (0-4, see include/kvx/kvx.h); -1 = chosen per shape")
     return p.parse_args()
 
 
@@ -224,6 +226,9 @@ def main():
     cfg = CONFIGS[args.config]
     t_start = time.perf_counter()
     runner = DecodeRunner(cfg, coherent=args.coherent, log=log)
+    if args.sieve_variant >= 0:
+        from kv_offload_proto_amd.kvops_ext import _kvops
+        _kvops.sieve_force_variant(args.sieve_variant)
     log("[bench] {}: setup {:.1f} s (HBM pool + {} pinned segments of {:.2f} GiB)".format(
         cfg.name, runner.setup_s, cfg.node_num, runner.pool.pool.segments[0].size_bytes / 2**30))
     export_us = runner.export_prefill()

@@ -252,8 +252,13 @@ __global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
     const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
     const int64_t total = static_cast<int64_t>(numReal) * a.topK;
     const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
-    for (uint32_t r0 = (blockIdx.x * kWaves + wave) * 64u; r0 < n; r0 += gridDim.x * kWaves * 64u) {
-        const uint32_t nr = (n - r0 < 64u) ? n - r0 : 64u;
+    // tasks of up to 64 rows, smaller when the list is short so that every
+    // wave of the grid has rows in flight
+    const uint32_t waves = gridDim.x * kWaves;
+    uint32_t task = (n + waves - 1u) / waves;
+    task = task < 1u ? 1u : (task > 64u ? 64u : task);
+    for (uint32_t r0 = (blockIdx.x * kWaves + wave) * task; r0 < n; r0 += waves * task) {
+        const uint32_t nr = (n - r0 < task) ? n - r0 : task;
         wave_copy_rows(x.listSrc + r0, x.listDst + r0, nr, cpr);
     }
 
@@ -391,10 +396,9 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     hipLaunchKernelGGL(kvx_gather_list, dim3(static_cast<uint32_t>(listBlocks)), dim3(256), 0, stream, P);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // 64-row tasks, grid-stride; 512 waves keep enough 16-byte reads in
-    // flight for the host link, and few workgroups keep the completion
-    // ticket cheap
-    uint64_t copyBlocks = (positions + 64ull * kWaves - 1ull) / (64ull * kWaves);
+    // grid-stride row tasks; 512 waves keep enough 16-byte reads in flight
+    // for the host link, and few workgroups keep the completion ticket cheap
+    uint64_t copyBlocks = (positions + 63ull) / 64ull;
     if (copyBlocks < 1) copyBlocks = 1;
     if (copyBlocks > 128) copyBlocks = 128;
     hipLaunchKernelGGL(kvx_gather_copy, dim3(static_cast<uint32_t>(copyBlocks)), dim3(256), 0, stream, P);
