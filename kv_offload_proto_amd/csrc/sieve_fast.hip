@@ -814,6 +814,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // on D_i): evicted.  The rest (rare) are settled in ring order.
     int32_t nSM = 0;
     if (fast) {
+        WSTAMP(0);
         nSM = ms.nSM;
         int32_t G = 1;  // lanes per SM slot for the U count
         while (G < 16 && 2 * G * nSM <= NT) G <<= 1;
@@ -849,7 +850,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             if (part == 0) tb[i] = dec;
         }
+        WSTAMP(1);
         __syncthreads();
+        WSTAMP(2);
         // undecided slots, one wave each: count the evictions already settled
         // before them (L) and the undecided ones before them with a larger k
         // (X); with X == 0, D = L exactly.  A concurrent settle of j < i reads
@@ -877,7 +880,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     ms.ui[rank] = static_cast<uint16_t>(i);
                 }
             }
+            WSTAMP(3);
             __syncthreads();
+            WSTAMP(4);
             if (wave == 0) {
                 const bool act = static_cast<int32_t>(lane) < nUnd;
                 const int32_t i = act ? static_cast<int32_t>(ms.ui[lane]) : 0;
@@ -903,7 +908,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                 }
             }
+            WSTAMP(5);
             __syncthreads();
+            WSTAMP(6);
         } else if (nUnd > 64) {  // many undecided slots: one wave settles them in ring order
             if (wave == 0) {
                 for (int32_t c = 0; c < nSM; c += 64) {
@@ -942,12 +949,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // event sequence in position order
     int32_t N = 0;
     if (fast) {
-        WSTAMP(0);
         const int32_t Ps = (nSM + NT - 1) / NT;
         MaskPrefix sp, ep;
         // events: candidates' first occurrences (cmask) and conversions (emask)
         MaskPrefix::init_pair(sp, smask, Ps * NWAVES, ep, cmask, P * NWAVES, lane, emask);
-        WSTAMP(4);
         const uint32_t T = sp.total;
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
@@ -958,7 +963,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (tid == 0) tb[nSM] = static_cast<uint16_t>(T);
-        WSTAMP(5);
         N = static_cast<int32_t>(M + T);
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
@@ -972,9 +976,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (ep.total != static_cast<uint32_t>(N)) fast = false;  // same value in every wave
-        WSTAMP(6);
         __syncthreads();
-        WSTAMP(7);
     }
     STAMP(5);
 
@@ -1314,12 +1316,8 @@ hipError_t sieve_fast_set_lds_limit(size_t bytes)
     if ((e = set_limit_one<false, 0, 0>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<false, 2, 4>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<false, 2, 8>(bytes)) != hipSuccess) return e;
-    if ((e = set_limit_one<false, 4, 8>(bytes)) != hipSuccess) return e;
-    if ((e = set_limit_one<false, 4, 16>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<true, 0, 0>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<true, 2, 4>(bytes)) != hipSuccess) return e;
-    if ((e = set_limit_one<true, 4, 8>(bytes)) != hipSuccess) return e;
-    if ((e = set_limit_one<true, 4, 16>(bytes)) != hipSuccess) return e;
     return set_limit_one<true, 2, 8>(bytes);
 }
 
@@ -1332,10 +1330,6 @@ static void launch_one(const KvxLaunch<HispSieveUpdateArgs> &L, size_t ldsBytes,
         hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 4>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     } else if (P == 2 && Q == 8) {
         hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 8>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
-    } else if (P == 4 && Q == 8) {
-        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 4, 8>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
-    } else if (P == 4 && Q == 16) {
-        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 4, 16>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     } else {
         hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 0, 0>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     }

@@ -31,22 +31,17 @@ struct Row {
     int32_t mask, dbs, padded;
 };
 
+// Workgroup-scope fence: the wave's stores and atomics are complete and
+// visible to its later loads (one CU, one L1).  Taken once per position and
+// where a step reads what an earlier step of the same position wrote, not
+// per move: a shift writes only cells behind the window it reads next.
 __device__ __forceinline__ void wave_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup"); }
 
-// State reads see the L2 copy (agent-scope loads skip the CU's L1), so a
-// value another lane stored or an atomic changed a moment ago is never stale.
-__device__ __forceinline__ uint16_t ld16(const uint16_t *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int32_t ld32(const int32_t *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ldu32(const uint32_t *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+__device__ __forceinline__ uint16_t ld16(const uint16_t *p) { return *p; }
+__device__ __forceinline__ int32_t ld32(const int32_t *p) { return *p; }
+__device__ __forceinline__ uint32_t ldu32(const uint32_t *p) { return *p; }
+
+constexpr int kBatch = 16;  // 64-cell windows loaded together (one memory round trip)
 
 // First cell at or after idx (cyclic) that is empty or holds `token`
 // (hisp_kernel_common.h:29-61); -1 after the whole table.  *entry receives
@@ -54,17 +49,25 @@ __device__ __forceinline__ uint32_t ldu32(const uint32_t *p)
 __device__ int32_t probe(const Row &r, int32_t idx, int32_t token, bool &found, uint32_t &entry, Guard &g)
 {
     const uint32_t lane = lane_id();
-    for (int32_t base = 0; base <= r.mask; base += 64) {
-        const int32_t c = (idx + base + static_cast<int32_t>(lane)) & r.mask;
-        const uint16_t e = ld16(r.ht + c);
-        const int32_t t = ld32(r.ct + c);
-        const uint64_t hit = __ballot(e != 0 && t == token);
-        const uint64_t any = hit | __ballot(e == 0);
-        if (any != 0ull) {
-            const int f = __builtin_ctzll(any);
-            found = (hit >> f) & 1ull;
-            entry = static_cast<uint32_t>(__shfl(static_cast<int>(e), f));
-            return (idx + base + f) & r.mask;
+    for (int32_t base = 0; base <= r.mask; base += 64 * kBatch) {
+        uint16_t e[kBatch];
+        int32_t t[kBatch];
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+            const int32_t c = (idx + base + 64 * q + static_cast<int32_t>(lane)) & r.mask;
+            e[q] = ld16(r.ht + c);
+            t[q] = ld32(r.ct + c);
+        }
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+            const uint64_t hit = __ballot(e[q] != 0 && t[q] == token);
+            const uint64_t any = hit | __ballot(e[q] == 0);
+            if (any != 0ull) {
+                const int f = __builtin_ctzll(any);
+                found = (hit >> f) & 1ull;
+                entry = static_cast<uint32_t>(__shfl(static_cast<int>(e[q]), f));
+                return (idx + base + 64 * q + f) & r.mask;
+            }
         }
     }
     g.code = kOverflowProbe;
@@ -73,41 +76,54 @@ __device__ int32_t probe(const Row &r, int32_t idx, int32_t token, bool &found, 
 }
 
 // Algorithm R from the hole at cell j (hisp_kernel_common.h:64-94): an entry
-// at i moves into j unless its home lies cyclically in (j, i].
-__device__ void shift_from(const Row &r, int32_t j, Guard &g)
+// at i moves into j unless its home lies cyclically in (j, i].  Moves write
+// only cells behind the window being scanned, so the windows ahead can be
+// loaded before the moves are made.
+__device__ int32_t shift_from(const Row &r, int32_t j, Guard &g)
 {
     const uint32_t lane = lane_id();
     const int32_t start = j;
-    for (int32_t base = 1; base <= r.mask; base += 64) {
-        const int32_t i = (start + base + static_cast<int32_t>(lane)) & r.mask;
-        const uint16_t e = ld16(r.ht + i);
-        const int32_t t = ld32(r.ct + i);
-        const int32_t home = (e != 0) ? static_cast<int32_t>(ht_hash(t)) & r.mask : 0;
-        uint64_t active = ~0ull;
-        for (;;) {
-            const bool mv = (j < i) ? (home <= j || home > i) : (home <= j && home > i);
-            const uint64_t m = __ballot(e == 0 || mv) & active;
-            if (m == 0ull) break;
-            const int f = __builtin_ctzll(m);
-            const bool stop = __shfl(static_cast<int>(e), f) == 0;
-            if (stop) {
-                if (lane == 0) {
-                    r.ht[j] = 0;
-                    r.ct[j] = -1;
+    for (int32_t base = 1; base <= r.mask; base += 64 * kBatch) {
+        uint16_t eb[kBatch];
+        int32_t tb[kBatch];
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+            const int32_t c = (start + base + 64 * q + static_cast<int32_t>(lane)) & r.mask;
+            eb[q] = ld16(r.ht + c);
+            tb[q] = ld32(r.ct + c);
+        }
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+            const int32_t i = (start + base + 64 * q + static_cast<int32_t>(lane)) & r.mask;
+            const uint16_t e = eb[q];
+            const int32_t t = tb[q];
+            const int32_t home = (e != 0) ? static_cast<int32_t>(ht_hash(t)) & r.mask : 0;
+            uint64_t active = ~0ull;
+            for (;;) {
+                const bool mv = (j < i) ? (home <= j || home > i) : (home <= j && home > i);
+                const uint64_t m = __ballot(e == 0 || mv) & active;
+                if (m == 0ull) break;
+                const int f = __builtin_ctzll(m);
+                const bool stop = __shfl(static_cast<int>(e), f) == 0;
+                if (stop) {
+                    if (lane == 0) {
+                        r.ht[j] = 0;
+                        r.ct[j] = -1;
+                    }
+                    wave_fence();
+                    return j;
                 }
-                wave_fence();
-                return;
+                if (static_cast<int>(lane) == f) {
+                    r.ht[j] = e;
+                    r.ct[j] = t;
+                }
+                j = __shfl(i, f);
+                active = (f == 63) ? 0ull : (~0ull << (f + 1));
             }
-            if (static_cast<int>(lane) == f) {
-                r.ht[j] = e;
-                r.ct[j] = t;
-            }
-            wave_fence();
-            j = __shfl(i, f);
-            active = (f == 63) ? 0ull : (~0ull << (f + 1));
         }
     }
     g.code = kOverflowProbe;
+    return -1;
 }
 
 __global__ __launch_bounds__(WT) void kvx_sieve_update_wave(KvxLaunch<HispSieveUpdateArgs> L, int32_t *shadow)
@@ -195,23 +211,28 @@ __global__ __launch_bounds__(WT) void kvx_sieve_update_wave(KvxLaunch<HispSieveU
                         const uint64_t unv = __ballot(on && !v);
                         const int f = unv ? __builtin_ctzll(unv) : 64;
                         if (static_cast<int>(lane) < f && v) atomicAnd(r.vis32 + (s >> 5), ~(1u << (s & 31)));
-                        wave_fence();
+                        // a later window of this sweep reads cleared bits only after a full turn
+                        if (base + 2 * width > (base / dbs + 1) * dbs) wave_fence();
                         if (f < 64) h = __shfl(s, f);
                     }
                     if (h < 0) {
                         g.code = kOverflowSweep;
                     } else {
+                        // the first probe stopped at the first empty cell c1 after
+                        // tp's home; an erase empties exactly one cell (its final
+                        // hole), so tp goes there if it lies in [home, c1), else c1
+                        int32_t c3 = cell;
                         const int32_t old = ld32(r.tok + h);
                         if (old >= 0) {  // erase the evicted token
                             bool f2 = false;
                             uint32_t e2 = 0;
                             const int32_t c2 = probe(r, static_cast<int32_t>(ht_hash(old)) & r.mask, old, f2, e2, g);
-                            if (c2 >= 0 && f2) shift_from(r, c2, g);
+                            if (c2 >= 0 && f2) {
+                                const int32_t hole = shift_from(r, c2, g);
+                                if (hole >= 0 && ((hole - home) & r.mask) < ((cell - home) & r.mask)) c3 = hole;
+                            }
                         }
-                        bool f3 = false;
-                        uint32_t e3 = 0;
-                        const int32_t c3 = probe(r, home, tp, f3, e3, g);
-                        if (c3 >= 0 && !f3 && lane == 0) {
+                        if (c3 >= 0 && lane == 0) {
                             r.ht[c3] = static_cast<uint16_t>(h + 1);
                             r.ct[c3] = tp;
                         }
