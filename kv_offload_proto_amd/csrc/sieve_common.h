@@ -17,6 +17,10 @@ struct Guard {
 // probe runs); larger ones use a whole wave per probe, sweep and shift step.
 constexpr int32_t kSmallTable = 4096;
 
+// Value of x in lane l, l the same in the whole wave (a register read, no
+// LDS round trip as a shuffle would take).
+__device__ __forceinline__ int32_t lane_value(int32_t x, int32_t l) { return __builtin_amdgcn_readlane(x, l); }
+
 // Token held by the slot an entry points at.  An entry past the tokens row
 // can only come from a corrupted table; it reads as the empty token (-1)
 // instead of touching memory outside the row.
@@ -177,7 +181,7 @@ __device__ __forceinline__ int32_t wave_probe_lds(const uint16_t *ht, const int3
         if (any != 0ull) {
             const int f = __builtin_ctzll(any);
             found = (hit >> f) & 1ull;
-            entry = static_cast<uint32_t>(__shfl(static_cast<int>(e), f));
+            entry = static_cast<uint32_t>(lane_value(static_cast<int>(e), f));
             return (idx + base + f) & mask;
         }
     }
@@ -201,12 +205,12 @@ __device__ __forceinline__ void wave_shift_lds(uint16_t *ht, const int32_t *tok,
             const uint64_t m = __ballot(e == 0 || mv) & active;
             if (m == 0ull) break;
             const int f = __builtin_ctzll(m);
-            if (__shfl(static_cast<int>(e), f) == 0) {
+            if (lane_value(static_cast<int>(e), f) == 0) {
                 if (lane == 0) ht[j] = 0;
                 return;
             }
             if (lane == f) ht[j] = e;
-            j = __shfl(i, f);
+            j = lane_value(i, f);
             active = (f == 63) ? 0ull : (~0ull << (f + 1));
         }
     }
@@ -226,7 +230,7 @@ __device__ bool sieve_row_wave(const int32_t *rt, int32_t *rs, int8_t *rm, int32
         int32_t mySlot = -1, myMiss = 0;
         const int32_t kn = (topK - k0 < 64) ? topK - k0 : 64;
         for (int32_t kk = 0; kk < kn; ++kk) {
-            const int32_t tp = __shfl(myT, kk);
+            const int32_t tp = lane_value(myT, kk);
             int32_t slot = -1, miss = 0;
             if (g.code != 0 || tp < 0 || tp >= seqLen) {  // past a bound violation the row reads as invalid
             } else if (tp >= prefill) {
@@ -249,7 +253,7 @@ __device__ bool sieve_row_wave(const int32_t *rt, int32_t *rs, int8_t *rm, int32
                         const uint64_t unv = __ballot(on && !v);
                         const int f = unv ? __builtin_ctzll(unv) : 64;
                         if (lane < f && v) atomicAnd(vis32 + (s >> 5), ~(1u << (s & 31)));
-                        if (f < 64) h = __shfl(s, f);
+                        if (f < 64) h = lane_value(s, f);
                     }
                     if (h < 0) {
                         g.code = kOverflowSweep;

@@ -65,7 +65,7 @@ __device__ int32_t probe(const Row &r, int32_t idx, int32_t token, bool &found, 
             if (any != 0ull) {
                 const int f = __builtin_ctzll(any);
                 found = (hit >> f) & 1ull;
-                entry = static_cast<uint32_t>(__shfl(static_cast<int>(e[q]), f));
+                entry = static_cast<uint32_t>(lane_value(static_cast<int>(e[q]), f));
                 return (idx + base + 64 * q + f) & r.mask;
             }
         }
@@ -104,7 +104,7 @@ __device__ int32_t shift_from(const Row &r, int32_t j, Guard &g)
                 const uint64_t m = __ballot(e == 0 || mv) & active;
                 if (m == 0ull) break;
                 const int f = __builtin_ctzll(m);
-                const bool stop = __shfl(static_cast<int>(e), f) == 0;
+                const bool stop = lane_value(static_cast<int>(e), f) == 0;
                 if (stop) {
                     if (lane == 0) {
                         r.ht[j] = 0;
@@ -117,7 +117,7 @@ __device__ int32_t shift_from(const Row &r, int32_t j, Guard &g)
                     r.ht[j] = e;
                     r.ct[j] = t;
                 }
-                j = __shfl(i, f);
+                j = lane_value(i, f);
                 active = (f == 63) ? 0ull : (~0ull << (f + 1));
             }
         }
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(WT) void kvx_sieve_update_wave(KvxLaunch<HispSieveU
         int32_t myMiss = 0;
         const int32_t kn = (K - k0 < 64) ? K - k0 : 64;
         for (int32_t kk = 0; kk < kn; ++kk) {
-            const int32_t tp = __shfl(myT, kk);
+            const int32_t tp = lane_value(myT, kk);
             int32_t slot = -1;
             int32_t miss = 0;
             if (g.code != 0 || tp < 0 || tp >= seqLen) {  // past a bound violation the row reads as invalid
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(WT) void kvx_sieve_update_wave(KvxLaunch<HispSieveU
                         if (static_cast<int>(lane) < f && v) atomicAnd(r.vis32 + (s >> 5), ~(1u << (s & 31)));
                         // a later window of this sweep reads cleared bits only after a full turn
                         if (base + 2 * width > (base / dbs + 1) * dbs) wave_fence();
-                        if (f < 64) h = __shfl(s, f);
+                        if (f < 64) h = lane_value(s, f);
                     }
                     if (h < 0) {
                         g.code = kOverflowSweep;
