@@ -76,7 +76,11 @@ __device__ int32_t probe(const Row &r, int32_t idx, int32_t token, bool &found, 
 }
 
 // Algorithm R from the hole at cell j (hisp_kernel_common.h:64-94): an entry
-// at i moves into j unless its home lies cyclically in (j, i].  Moves write
+// at i moves into the hole j unless its home lies cyclically in (j, i], and
+// then i is the new hole.  Per 64-cell window the chain of movers is found
+// first (each step is one ballot against the current hole, no memory
+// access), then every mover writes its entry into the cell of the mover
+// before it (the window's incoming hole for the first) at once.  Moves write
 // only cells behind the window being scanned, so the windows ahead can be
 // loaded before the moves are made.
 __device__ int32_t shift_from(const Row &r, int32_t j, Guard &g)
@@ -94,31 +98,41 @@ __device__ int32_t shift_from(const Row &r, int32_t j, Guard &g)
         }
 #pragma unroll
         for (int q = 0; q < kBatch; ++q) {
-            const int32_t i = (start + base + 64 * q + static_cast<int32_t>(lane)) & r.mask;
+            const int32_t w0 = (start + base + 64 * q) & r.mask;  // cell of lane 0
+            const int32_t i = (w0 + static_cast<int32_t>(lane)) & r.mask;
             const uint16_t e = eb[q];
             const int32_t t = tb[q];
             const int32_t home = (e != 0) ? static_cast<int32_t>(ht_hash(t)) & r.mask : 0;
-            uint64_t active = ~0ull;
-            for (;;) {
+            const uint64_t empty = __ballot(e == 0);
+            const int32_t jin = j;
+            uint64_t movers = 0;
+            bool stop = false;
+            for (int from = 0; from < 64;) {
                 const bool mv = (j < i) ? (home <= j || home > i) : (home <= j && home > i);
-                const uint64_t m = __ballot(e == 0 || mv) & active;
+                const uint64_t m = __ballot(static_cast<int>(lane) >= from && (e == 0 || mv));
                 if (m == 0ull) break;
                 const int f = __builtin_ctzll(m);
-                const bool stop = lane_value(static_cast<int>(e), f) == 0;
-                if (stop) {
-                    if (lane == 0) {
-                        r.ht[j] = 0;
-                        r.ct[j] = -1;
-                    }
-                    wave_fence();
-                    return j;
+                if ((empty >> f) & 1ull) {
+                    stop = true;
+                    break;
                 }
-                if (static_cast<int>(lane) == f) {
-                    r.ht[j] = e;
-                    r.ct[j] = t;
+                movers |= 1ull << f;
+                j = (w0 + f) & r.mask;
+                from = f + 1;
+            }
+            if ((movers >> lane) & 1ull) {
+                const uint64_t below = movers & ((1ull << lane) - 1ull);
+                const int32_t dst = below ? ((w0 + 63 - __builtin_clzll(below)) & r.mask) : jin;
+                r.ht[dst] = e;
+                r.ct[dst] = t;
+            }
+            if (stop) {
+                if (lane == 0) {
+                    r.ht[j] = 0;
+                    r.ct[j] = -1;
                 }
-                j = lane_value(i, f);
-                active = (f == 63) ? 0ull : (~0ull << (f + 1));
+                wave_fence();
+                return j;
             }
         }
     }
