@@ -1109,10 +1109,29 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 x = (x + static_cast<int32_t>(span)) & mask;
             }
             if (!ld) continue;
-            rdel_at<kC>(ht, smem + lay.tok, padded, static_cast<int32_t>(c), mask, g);
-            int32_t y = (static_cast<int32_t>(c) - 1) & mask;
-            for (int32_t n = 0; n < H && ht[y] != 0; ++n, y = (y - 1) & mask) {
-                if (bit_get(ber, static_cast<uint32_t>(y))) rdel_at<kC>(ht, smem + lay.tok, padded, y, mask, g);
+            // the cluster's marked cells right to left; cells left of a
+            // deletion keep their pre-step contents, so the occupancy
+            // snapshot finds the next marked cell and the cluster's start
+            int32_t y = static_cast<int32_t>(c);
+            for (int32_t n = 0; n <= H; ++n) {
+                rdel_at<kC>(ht, smem + lay.tok, padded, y, mask, g);
+                int32_t nx = -1;
+                int32_t x2 = (y - 1) & mask;  // scan words leftward from x2
+                for (int32_t m = 0; m <= (H >> 5); ++m) {
+                    const uint32_t b = static_cast<uint32_t>(x2) & 31u;
+                    const uint32_t keep = (b == 31u) ? 0xFFFFFFFFu : ((2u << b) - 1u);  // bits 0..b
+                    const uint32_t empt = ~occ[x2 >> 5] & keep, mk = ber[x2 >> 5] & keep;
+                    const int32_t hiE = empt ? 31 - __builtin_clz(empt) : -1;  // cluster start boundary
+                    const uint32_t live = (hiE >= 0) ? (mk & ~((2u << hiE) - 1u)) : mk;
+                    if (live) {
+                        nx = (x2 & ~31) + (31 - __builtin_clz(live));
+                        break;
+                    }
+                    if (hiE >= 0) break;
+                    x2 = ((x2 & ~31) - 1) & mask;
+                }
+                if (nx < 0) break;
+                y = nx;
             }
         }
         __syncthreads();
