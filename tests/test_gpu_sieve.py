@@ -216,6 +216,38 @@ def test_sieve_fast_kernel_parity_dsa_scale(kvops):
     assert kvops.read_overflow() == 0
 
 
+@pytest.mark.parametrize("K,dbs,force", [(2048, 4096, 4), (2500, 3000, -1), (1500, 6000, -1), (1024, 8192, -1),
+                                         (2048, 8192, 4), (64, 4096, -1)])
+def test_sieve_parallel_kernel_shapes(kvops, K, dbs, force):
+    """The parallel kernel's instantiations: positions and ring offsets per
+    lane fixed at (2, 4) / (2, 8), or any shape (P = ceil(topK/1024), Q =
+    ceil(dbs/1024) of 1..8), in the full and the compact LDS form."""
+    rng = np.random.default_rng(K * 7 + dbs)
+    prefill, req = dbs + 5000, 8
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(force)
+    variants = set()
+    try:
+        for step in range(4):
+            batch = _random_state_stream(rng, st, K, prefill)
+            seq = np.full(req, prefill + 3)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            variants.add(kvops.last_sieve_variant())
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert variants <= {2, 4} and len(variants) == 1
+    if force == 4:
+        assert variants == {4}
+    assert kvops.read_overflow() == 0
+
+
 @pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
 def test_sieve_variants_agree(kvops, variant):
     """Sequential LDS (0), single-lane HBM (1), parallel (2), wave-wide HBM (3)
