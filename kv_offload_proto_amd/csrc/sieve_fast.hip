@@ -114,7 +114,7 @@ __device__ unsigned long long kvx_dbg_w[64][16][16];
 #endif
 
 struct Misc {
-    int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead;
+    int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead, nDone;
     uint32_t wtok[NWAVES];
     uint32_t went[NWAVES];
     uint32_t wring[NWAVES];
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         if (tid == 0) {
             ms.bad = ms.ovf = ms.late = 0;
-            ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = 0;
+            ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = 0;
         }
         WSTAMP(12);
     }
@@ -827,6 +827,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (ai >= 0) {
                 const uint32_t ki = smA[i] >> 16;
                 uint32_t U = 0;
+#pragma unroll 2
                 for (int32_t b = part; 8 * b < i; b += G) {
                     const uint4 x = kp4[b];
                     const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
@@ -862,49 +863,56 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if (nUnd > 0 && nUnd <= 64) {
             // undecided slots (few): one wave each counts the evictions
             // settled in the first pass before it with a larger k (L) and
-            // files it under its rank in ring order; then one wave walks
-            // them in ring order, adding the evictions among the undecided
-            // ones before each: D = L + #{undecided j < i evicted, k_j > k_i}
-            for (int32_t e = wave; e < nUnd; e += NWAVES) {
-                const int32_t i = static_cast<int32_t>(undl[e]);
-                const uint32_t ki = smA[i] >> 16;
-                uint32_t l = 0;
-                for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
-                    l += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
+            // files it under its rank in ring order; the last wave to finish
+            // then walks them in ring order, adding the evictions among the
+            // undecided ones before each: D = L + #{undecided j < i evicted, k_j > k_i}
+            if (wave < nUnd) {
+                for (int32_t e = wave; e < nUnd; e += NWAVES) {
+                    const int32_t i = static_cast<int32_t>(undl[e]);
+                    const uint32_t ki = smA[i] >> 16;
+                    uint32_t l = 0;
+                    for (int32_t j = static_cast<int32_t>(lane); j < i; j += 64) {
+                        l += (tb[j] == 1 && (smA[j] >> 16) > ki) ? 1u : 0u;
+                    }
+                    l = wave_sum(l);
+                    const bool before = static_cast<int32_t>(lane) < nUnd && static_cast<int32_t>(undl[lane]) < i;
+                    const int32_t rank = __popcll(__ballot(before));
+                    if (lane == 0) {
+                        ms.uL[rank] = l;
+                        ms.ui[rank] = static_cast<uint16_t>(i);
+                    }
                 }
-                l = wave_sum(l);
-                const bool before = static_cast<int32_t>(lane) < nUnd && static_cast<int32_t>(undl[lane]) < i;
-                const int32_t rank = __popcll(__ballot(before));
+                WSTAMP(3);
+                int32_t old = 0;
                 if (lane == 0) {
-                    ms.uL[rank] = l;
-                    ms.ui[rank] = static_cast<uint16_t>(i);
+                    __threadfence_block();
+                    old = atomicAdd(&ms.nDone, 1);
                 }
-            }
-            WSTAMP(3);
-            __syncthreads();
-            WSTAMP(4);
-            if (wave == 0) {
-                const bool act = static_cast<int32_t>(lane) < nUnd;
-                const int32_t i = act ? static_cast<int32_t>(ms.ui[lane]) : 0;
-                const uint32_t ki = act ? (smA[i] >> 16) : 0u;
-                const uint32_t eb = act ? smB[i] : 0u;
-                const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
-                const uint32_t l = act ? ms.uL[lane] : 0u;
-                uint64_t ev = 0;  // undecided slots found evicted so far (by rank)
-                for (int32_t e = 0; e < nUnd; ++e) {
-                    const uint32_t ke = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ki), e));
-                    const int32_t ae = __builtin_amdgcn_readlane(ai, e);
-                    const uint32_t le = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(l), e));
-                    const uint64_t larger = __ballot(static_cast<int32_t>(lane) < e && ki > ke);
-                    const uint32_t d = le + static_cast<uint32_t>(__popcll(larger & ev));
-                    if (ae >= static_cast<int32_t>(d)) ev |= 1ull << e;
-                }
-                if (act) {
-                    const bool evd = (ev >> lane) & 1ull;
-                    tb[i] = evd ? 1 : 0;
-                    if (evd) {
-                        atomicOr(reinterpret_cast<unsigned long long *>(smask) + (i >> 6), 1ull << (i & 63));
-                        atomicOr(reinterpret_cast<unsigned long long *>(emask) + (ki >> 6), 1ull << (ki & 63u));
+                const int32_t waves = nUnd < NWAVES ? nUnd : NWAVES;
+                if (lane_value(old, 0) == waves - 1) {  // every other wave has filed its slots
+                    __threadfence_block();
+                    const bool act = static_cast<int32_t>(lane) < nUnd;
+                    const int32_t i = act ? static_cast<int32_t>(ms.ui[lane]) : 0;
+                    const uint32_t ki = act ? (smA[i] >> 16) : 0u;
+                    const uint32_t eb = act ? smB[i] : 0u;
+                    const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
+                    const uint32_t l = act ? ms.uL[lane] : 0u;
+                    uint64_t ev = 0;  // undecided slots found evicted so far (by rank)
+                    for (int32_t e = 0; e < nUnd; ++e) {
+                        const uint32_t ke = static_cast<uint32_t>(lane_value(static_cast<int>(ki), e));
+                        const int32_t ae = lane_value(ai, e);
+                        const uint32_t le = static_cast<uint32_t>(lane_value(static_cast<int>(l), e));
+                        const uint64_t larger = __ballot(static_cast<int32_t>(lane) < e && ki > ke);
+                        const uint32_t d = le + static_cast<uint32_t>(__popcll(larger & ev));
+                        if (ae >= static_cast<int32_t>(d)) ev |= 1ull << e;
+                    }
+                    if (act) {
+                        const bool evd = (ev >> lane) & 1ull;
+                        tb[i] = evd ? 1 : 0;
+                        if (evd) {
+                            atomicOr(reinterpret_cast<unsigned long long *>(smask) + (i >> 6), 1ull << (i & 63));
+                            atomicOr(reinterpret_cast<unsigned long long *>(emask) + (ki >> 6), 1ull << (ki & 63u));
+                        }
                     }
                 }
             }
