@@ -513,7 +513,7 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         // with wave-wide probes (1 = the single-lane HBM kernel, by request only).
         const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
                            visited_stride_b;
-        const bool fastShape = top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535 &&
+        const bool fastShape = top_k >= 1 && pool_size >= 1 && top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535 &&
                                device_buffer_size <= 32u * kvx::kFastThreads && htSize <= 32768;
         const size_t ldsFast = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
                                                 visited_stride_b, false).total;

@@ -62,7 +62,7 @@ constexpr int kFastThreads = KVX_FAST_THREADS;
 
 struct FastLayout {
     uint32_t tok, ht, vis, ptok, pinf, vt, evslot, smKp, eseq, tb, smA, smB, vset, ber, occ, cmask, emask, smask,
-        rsn, rsm, cellOf, total;
+        rsn, rsm, total;
 };
 
 __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
@@ -104,7 +104,6 @@ __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint
     const uint32_t ringMaskBytes = (padded + kFastThreads - 1u) / kFastThreads * (kFastThreads / 64u) * 8u;
     l.rsn = o;     o += ringMaskBytes;
     l.rsm = o;     o += ringMaskBytes;
-    l.cellOf = o;  o += compact ? 0u : align16(padded * 2u);  // full form: table cell of each slot's entry
     l.total = o;
     return l;
 }

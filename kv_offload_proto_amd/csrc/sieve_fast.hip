@@ -71,6 +71,10 @@ using namespace sieve;
 // global rather than flat instructions: flat ones also count against the LDS
 // wait counter and stall the LDS work that follows them.
 #define KVX_G __attribute__((address_space(1)))
+// Uniform values this kernel does not write before reading them (lengths,
+// the request index, the hand) load through the constant address space, as
+// scalar loads that need no wave-wide copy into scalar registers.
+#define KVX_C __attribute__((address_space(4)))
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 16-byte chunk
 
 constexpr int NT = kFastThreads;
@@ -203,14 +207,16 @@ struct MaskPrefix {
         a.total = tot & 0xFFFFu;
         b.total = tot >> 16;
     }
-    // set bits before this lane's bit of entry e (e the same in the whole wave)
-    __device__ __forceinline__ uint32_t own(int32_t e) const
+    // set bits before entry e (e the same in the whole wave)
+    __device__ __forceinline__ uint32_t base(int32_t e) const
     {
         const int32_t L = e >> lg;
         uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ex), L));
         for (int32_t x = L << lg; x < e; ++x) c += static_cast<uint32_t>(__popcll(ent(x)));
-        return c + lanes_below(ent(e));
+        return c;
     }
+    // set bits before this lane's bit of entry e (e the same in the whole wave)
+    __device__ __forceinline__ uint32_t own(int32_t e) const { return base(e) + lanes_below(ent(e)); }
     // set bits before bit `bit` of entry e (any entry per lane)
     __device__ __forceinline__ uint32_t before(int32_t e, uint32_t bit) const
     {
@@ -255,8 +261,6 @@ __device__ __forceinline__ int32_t lds_claim16(uint32_t *w32, int32_t idx, int32
     }
     return -1;
 }
-
-__device__ __forceinline__ bool bit_get(const uint32_t *b, uint32_t i) { return (b[i >> 5] >> (i & 31u)) & 1u; }
 
 // Algorithm R deletion of the entry at cell c (homes from the tokens row, or
 // from the per-slot token hashes in the compact form).
@@ -337,10 +341,15 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const int32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (bid >= maxNumReqs) return;
+    // (the grid is exactly maxNumReqs workgroups.)  The pointers are loaded
+    // from the arguments in one batch, ahead of the first branch: fetched on
+    // demand they would each cost a round trip.
+    asm volatile("" : : "s"(a.topkIndices), "s"(a.reqPoolIndices), "s"(a.seqLens), "s"(a.prefillLens),
+                 "s"(a.deviceBufferTokens), "s"(a.deviceBufferVisited), "s"(a.deviceBufferHt), "s"(a.sieveHand),
+                 "s"(a.topKDeviceSlots), "s"(a.isMiss), "s"(a.numReal));
 
     WSTAMP(8);
-    int32_t numReal = *(KVX_G const int32_t *)(a.numReal);
+    int32_t numReal = *(KVX_C const int32_t *)(a.numReal);
     if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
     KVX_G int32_t *rs = (KVX_G int32_t *)(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
     KVX_G int8_t *rm = (KVX_G int8_t *)(a.isMiss) + static_cast<int64_t>(bid) * K;
@@ -349,21 +358,39 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         return;
     }
     WSTAMP(9);
-    const int64_t reqIdx = ((KVX_G const int64_t *)(a.reqPoolIndices))[bid];
-    if (reqIdx < 0 || reqIdx >= poolSize) {
-        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
-        return;
-    }
-    WSTAMP(10);
-    const int32_t seqLen = ((KVX_G const int32_t *)(a.seqLens))[bid];
-    const int32_t prefill = ((KVX_G const int32_t *)(a.prefillLens))[reqIdx];
+    // the batch row's request, length and topK row in one round trip.  An
+    // invalid request index is acted on after staging (row 0, which exists,
+    // is staged meanwhile): an early exit here would let the compiler sink
+    // the loads below it, each then waited for on its own.
+    const int64_t reqRaw = ((KVX_C const int64_t *)(a.reqPoolIndices))[bid];
+    const int32_t seqLen = ((KVX_C const int32_t *)(a.seqLens))[bid];
     KVX_G const int32_t *rt = (KVX_G const int32_t *)(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    // unconditional (clamped, K >= 1 here) loads: a load under a branch makes
+    // the compiler wait for it at the branch's end
+    const bool h0 = tid < K, h1 = tid + NT < K;
+    const int32_t t0 = rt[min(tid, K - 1)], t1 = rt[min(tid + NT, K - 1)];
+    const bool badReq = reqRaw < 0 || reqRaw >= poolSize;
+    const int64_t reqIdx = badReq ? 0 : reqRaw;
+    WSTAMP(10);
+    // direct token -> slot map over the tokens that can be looked up (below
+    // both prefill and seqLen) when they fit the LDS left over after the
+    // layout: 0, slot+1 of the slot holding the token, or padded+1+k for a
+    // missing token first seen at position k (smallest k wins).  Cleared over
+    // min(seqLen, capacity) entries before the state row lands.
+    const FastLayout lay = fast_layout(padded, H, K, visStrideB, kC);
+    const int32_t invCap = static_cast<int32_t>(a.reserved >> 8);
+    uint16_t *inv = reinterpret_cast<uint16_t *>(smem + lay.total);
+    uint32_t *inv32 = reinterpret_cast<uint32_t *>(smem + lay.total);
+    if (!kC && invCap > 0 && seqLen > 0) {
+        const int32_t n16 = (min(seqLen, invCap) + 7) >> 3;
+        for (int32_t i = tid; i < n16; i += NT) reinterpret_cast<v4u *>(inv)[i] = v4u{0u, 0u, 0u, 0u};
+    }
+    int32_t prefill = ((KVX_C const int32_t *)(a.prefillLens))[reqIdx];
     KVX_G int32_t *gTok = (KVX_G int32_t *)(a.deviceBufferTokens) + reqIdx * padded;
     KVX_G uint8_t *gVis = (KVX_G uint8_t *)(a.deviceBufferVisited) + reqIdx * visStrideB;
     KVX_G uint16_t *gHt = (KVX_G uint16_t *)(a.deviceBufferHt) + reqIdx * H;
     KVX_G int32_t *gHand = (KVX_G int32_t *)(a.sieveHand) + reqIdx * kHandStride;
 
-    const FastLayout lay = fast_layout(padded, H, K, visStrideB, kC);
     int32_t *tok = reinterpret_cast<int32_t *>(smem + lay.tok);    // full form: tokens
     uint16_t *hv = reinterpret_cast<uint16_t *>(smem + lay.tok);   // compact form: masked token hashes
     uint16_t *ht = reinterpret_cast<uint16_t *>(smem + lay.ht);
@@ -389,21 +416,16 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint64_t *smask = reinterpret_cast<uint64_t *>(smem + lay.smask);  // evicted SM slots
     uint64_t *rsn = reinterpret_cast<uint64_t *>(smem + lay.rsn);      // SN slots by ring offset
     uint64_t *rsm = reinterpret_cast<uint64_t *>(smem + lay.rsm);      // SM slots by ring offset
-    uint16_t *cellOf = reinterpret_cast<uint16_t *>(smem + lay.cellOf);  // full form: cell of slot s's entry
-    // direct token -> slot map for rows whose prefill fits the LDS left over
-    // (after the layout).  It is not cleared: an entry is trusted only when it
-    // checks out -- slot+1 of a slot holding the token, or padded+1+k of a
-    // position k holding it (a candidate's first position, smallest k wins).
-    const int32_t invCap = static_cast<int32_t>(a.reserved >> 8);
-    const bool direct = !kC && prefill > 0 && prefill <= invCap;
-    uint16_t *inv = reinterpret_cast<uint16_t *>(smem + lay.total);
-    uint32_t *inv32 = reinterpret_cast<uint32_t *>(smem + lay.total);
+    int32_t lim = 0;      // min(prefill, seqLen)
+    bool direct = false;  // the direct map is in use (both set once the row's loads are in flight)
     // reuse of regions whose earlier contents are dead by then
     uint32_t *pcell = smA;                                   // classify: provisional cell per position
     uint16_t *undl = eseq;                                   // decide: undecided SM indices
     uint32_t *ecell = smA;                                   // per event: table cell | slot << 16
     uint16_t *lead = eseq;                                   // redo: start cell of each multi-key cluster
     int32_t *ntokv = reinterpret_cast<int32_t *>(smB);       // per event: the token inserted
+    uint16_t *snList = evslot;                               // scan -> decide: the evicted SN slots in ring order
+    uint16_t *smCell = smKp;                                 // events -> marks: table cell of each evicted SM slot
 
     // token of slot s equals t (th = its hash); the compact form checks the
     // hash in LDS and confirms with the HBM row
@@ -419,6 +441,25 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if constexpr (kC) return static_cast<int32_t>(hv[s]) & mask;
         else return static_cast<int32_t>(ht_hash(tok[s])) & mask;
     };
+    // table cell of slot s's entry (NOCELL for an empty slot), marked in ber
+    auto cell_of = [&](int32_t s) -> uint32_t {
+        uint32_t cell = NOCELL;
+        if (slot_live(s)) {
+            int32_t idx = slot_home(s);
+            for (int32_t n = 0; n <= mask; ++n) {
+                const uint32_t ev = ht[idx];
+                if (ev == static_cast<uint32_t>(s + 1)) {
+                    cell = static_cast<uint32_t>(idx);
+                    break;
+                }
+                if (ev == 0u) break;
+                idx = (idx + 1) & mask;
+            }
+            if (cell == NOCELL) atomicOr(&ms.ovf, 1);
+            else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+        }
+        return cell;
+    };
 
     constexpr bool kFixed = PM > 0 && QM > 0;
     const int32_t P = kFixed ? PM : (K + NT - 1) / NT;    // positions per lane: k = tid + q * NT
@@ -432,19 +473,14 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // the direct map, the table's occupancy bitmap; count live tokens and
     // table entries
     STAMP(0);
-    int32_t hand0 = gHand[0];
-    if (hand0 < 0 || hand0 >= dbs) hand0 = 0;  // hisp_sieve_update.cpp:108-111
-    const bool flagged = gHand[1] == kCanonFlag;
+    int32_t hand0 = ((KVX_C const int32_t *)gHand)[0];
+    int32_t flagw = ((KVX_C const int32_t *)gHand)[1];
     {
         const int32_t nt = padded >> 2, nh = H >> 3, nv = visStrideB >> 4;  // 16-byte chunks
         KVX_G const v4u *sT = (KVX_G const v4u *)gTok;
         KVX_G const v4u *sH = (KVX_G const v4u *)gHt;
         KVX_G const v4u *sV = (KVX_G const v4u *)gVis;
         uint32_t nTok = 0, nEnt = 0;
-        int32_t t0 = 0, t1 = 0;
-        const bool h0 = tid < K, h1 = tid + NT < K;
-        if (h0) t0 = rt[tid];
-        if (h1) t1 = rt[tid + NT];
         // Each region loads into registers of its own, all before the first
         // use: loads that share a destination register across divergent
         // branches would each wait for the previous one to land.
@@ -469,6 +505,15 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             const int32_t cv = NT * p + tid;
             vV = sV[min(cv, nv - 1)];
+            // the direct map's clearing is complete in every wave (the
+            // barrier waits for LDS stores only, the loads stay in flight)
+            // (the scalar values pass through the statement, so that nothing
+            // computed from them is scheduled, and waited for, before the loads)
+            if (p == 0) {
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : "+s"(prefill), "+s"(hand0), "+s"(flagw) : : "memory");
+                lim = min(prefill, seqLen);
+                direct = !kC && lim > 0 && lim <= invCap;
+            }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int32_t c = 2 * NT * p + tid + j * NT;
@@ -492,7 +537,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     for (int i = 0; i < 4; ++i) {
                         const bool live = s0 + i < dbs && tt[i] >= 0;
                         nTok += live ? 1u : 0u;
-                        if (direct && live && tt[i] < prefill) inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
+                        if (direct && live && tt[i] < lim) inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
                     }
                 }
             }
@@ -511,19 +556,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                     occ8[c] = static_cast<uint8_t>(ob);
                     nEnt += static_cast<uint32_t>(__popc(ob));
-                    if constexpr (!kC) {  // inverse of the table: the cell of each slot's entry
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const uint32_t lo = w4[q] & 0xFFFFu, hi = w4[q] >> 16;
-                            if (lo - 1u < static_cast<uint32_t>(padded)) cellOf[lo - 1u] = static_cast<uint16_t>(8 * c + 2 * q);
-                            if (hi - 1u < static_cast<uint32_t>(padded)) cellOf[hi - 1u] = static_cast<uint16_t>(8 * c + 2 * q + 1);
-                        }
-                    }
                 }
             }
             if (cv < nv) reinterpret_cast<v4u *>(vis)[cv] = vV;
         };
         stage_pass(0);
+        if (hand0 < 0 || hand0 >= dbs) hand0 = 0;  // hisp_sieve_update.cpp:108-111
         for (int32_t p = 1; 2 * NT * p < nt || 4 * NT * p < nh || NT * p < nv; ++p) stage_pass(p);
         WSTAMP(11);
         if (h0) ptok[tid] = t0;
@@ -549,11 +587,15 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             ms.bad = ms.ovf = ms.late = 0;
             ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = 0;
         }
-        WSTAMP(12);
     }
     __syncthreads();
     WSTAMP(13);
     STAMP(1);
+    const bool flagged = flagw == kCanonFlag;
+    if (badReq) {  // hisp_sieve_update.cpp:80-87: the row gets the dummy outputs, the state is untouched
+        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
+        return;
+    }
 
     // ---- consistency: the table indexes exactly the non-negative tokens of
     // [0, dbs), each at its own slot.  A row this kernel wrote last carries
@@ -592,12 +634,71 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const bool canonical = fast;
 
     // ---- classify every position; dedup the candidates (smallest position
-    // of each missing token).  With the direct map a hit is an entry that
-    // checks out as the token's slot; otherwise one probe of the table does
-    // both: a hit stops at its entry (provisional entries only fill empty
-    // cells, never the probe path of a resident token), a miss stops at its
-    // token's provisional entry padded+1+k or claims the first empty cell
-    if (fast) {
+    // of each missing token).  With the direct map a hit is an entry naming a
+    // slot, and a missing token keeps the smallest padded+1+k; the steps of a
+    // lane's positions interleave (map words, then first-hit words, then the
+    // updates).  Otherwise one probe of the table does both: a hit stops at
+    // its entry (provisional entries only fill empty cells, never the probe
+    // path of a resident token), a miss stops at its token's provisional
+    // entry padded+1+k or claims the first empty cell
+    if (fast && direct) {
+        constexpr int PB = kFixed ? PM : 1;  // positions handled together
+        for (int32_t q0 = 0; q0 < P; q0 += PB) {
+            int32_t tq[PB];
+            uint32_t wq[PB], inf[PB];
+#pragma unroll
+            for (int b = 0; b < PB; ++b) {
+                const int32_t k = tid + (q0 + b) * NT;
+                const int32_t t = k < K ? (kFixed ? tR[kFixed ? b : 0] : ptok[k]) : -1;
+                tq[b] = t;
+                inf[b] = (t < 0 || t >= seqLen) ? (CLS_INV << 30) : (t >= prefill) ? (CLS_EXT << 30) : 0xFFFFFFFFu;
+                wq[b] = inf[b] == 0xFFFFFFFFu ? inv32[t >> 1] : 0u;
+            }
+#pragma unroll
+            for (int b = 0; b < PB; ++b) {
+                if (inf[b] != 0xFFFFFFFFu) continue;
+                const int32_t k = tid + (q0 + b) * NT, t = tq[b];
+                const uint32_t sh = (static_cast<uint32_t>(t) & 1u) * 16u;
+                uint32_t old = wq[b];
+                const uint32_t cur0 = (old >> sh) & 0xFFFFu;
+                if (cur0 - 1u < static_cast<uint32_t>(dbs)) {
+                    inf[b] = (CLS_HIT << 30) | (cur0 - 1u);
+                    wq[b] = vt32[(cur0 - 1u) >> 1];
+                    continue;
+                }
+                inf[b] = CLS_CAND << 30;
+                const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
+                uint32_t *w = inv32 + (t >> 1);
+                for (;;) {  // the entry stays 0 or provisional: resident entries are written in staging only
+                    const uint32_t cur = (old >> sh) & 0xFFFFu;
+                    if (cur != 0u && cur <= v) break;  // an earlier position of the token holds it
+                    const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
+                    if (prev == old) break;
+                    old = prev;
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < PB; ++b) {
+                const int32_t k = tid + (q0 + b) * NT;
+                if (k >= K) continue;
+                if ((inf[b] >> 30) == CLS_HIT) {  // first hit of the slot: 16-bit min by CAS on its word
+                    const uint32_t s0 = inf[b] & 0xFFFFu;
+                    uint32_t *w = vt32 + (s0 >> 1);
+                    const uint32_t sh = (s0 & 1u) * 16u, v = static_cast<uint32_t>(k + 1);
+                    uint32_t old = wq[b];
+                    for (;;) {
+                        if (((old >> sh) & 0xFFFFu) <= v) break;
+                        const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
+                        if (prev == old) break;
+                        old = prev;
+                    }
+                }
+                pinf[k] = inf[b];
+                if constexpr (kFixed) iR[b] = inf[b];
+            }
+        }
+        __syncthreads();
+    } else if (fast) {
         Guard g;
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
@@ -609,27 +710,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 inf = CLS_INV << 30;
             } else if (t >= prefill) {
                 inf = CLS_EXT << 30;
-            } else if (direct) {
-                const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
-                uint32_t *w = inv32 + (t >> 1);
-                const uint32_t sh = (static_cast<uint32_t>(t) & 1u) * 16u;
-                uint32_t old = *w;
-                inf = CLS_CAND << 30;
-                for (;;) {
-                    const uint32_t cur = (old >> sh) & 0xFFFFu;
-                    if (cur - 1u < static_cast<uint32_t>(dbs) && tok[cur - 1u] == t) {
-                        inf = (CLS_HIT << 30) | (cur - 1u);
-                        lds_min16(vt32, cur - 1u, static_cast<uint16_t>(k + 1));
-                        break;
-                    }
-                    const uint32_t kc = cur - static_cast<uint32_t>(padded) - 1u;
-                    if (cur > static_cast<uint32_t>(padded) && kc < static_cast<uint32_t>(K) && cur <= v &&
-                        ptok[kc] == t)
-                        break;  // an earlier position of the token (or this one) holds it
-                    const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
-                    if (prev == old) break;
-                    old = prev;
-                }
             } else {
                 const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
                 const uint32_t th = ht_hash(t);
@@ -709,6 +789,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t snM = 0, smM = 0, M = 0;  // bit j: class of ring offset tid + j * NT
     MaskPrefix snP, smP;                // SN / SM slots before a ring offset
     if (fast) {
+        WSTAMP(4);
         uint32_t cw = 0;
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
@@ -751,6 +832,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (lane == 0) ms.wcand[wave] = cw;
+        WSTAMP(7);
         __syncthreads();
 #pragma unroll
         for (int w = 0; w < NWAVES; ++w) M += ms.wcand[w];
@@ -762,11 +844,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             // is a prefix of the SM slots in ring order
             MaskPrefix cp;
             cp.init(cmask, P * NWAVES, lane);
+            WSTAMP(14);
 #pragma unroll
             for (int32_t j = 0; j < Q; ++j) {
+                const int32_t e = j * NWAVES + wave;
+                if (snP.base(e) >= M) continue;  // the whole block lies past the M-th SN slot
                 const bool isSM = (smM >> j) & 1u, isSN = (snM >> j) & 1u;
                 const int32_t u = tid + j * NT;
-                const int32_t e = j * NWAVES + wave;
                 const uint32_t nsn = snP.own(e), nsm = smP.own(e);
                 uint32_t k = 0;
                 if (isSM) k = (kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)])) - 1u;
@@ -776,31 +860,15 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     smB[nsm] = nsn | (cc << 16);
                     smKp[nsm] = (cc > nsn) ? static_cast<uint16_t>(k) : static_cast<uint16_t>(0);
                 }
-                if (kC && isSN && nsn < M) {
-                    // every SN slot before the M-th is evicted: look up its
-                    // token's cell now (vt of an SN slot is not read again)
-                    const int32_t sl = ring_slot(hand0, u, dbs);
-                    uint32_t cell = NOCELL;
-                    if (slot_live(sl)) {
-                        int32_t idx = slot_home(sl);
-                        for (int32_t n = 0; n <= mask; ++n) {
-                            const uint32_t ev = ht[idx];
-                            if (ev == static_cast<uint32_t>(sl + 1)) {
-                                cell = static_cast<uint32_t>(idx);
-                                break;
-                            }
-                            if (ev == 0u) break;
-                            idx = (idx + 1) & mask;
-                        }
-                        if (cell == NOCELL) atomicOr(&ms.ovf, 1);
-                        else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
-                    }
-                    vt[sl] = static_cast<uint16_t>(cell);
-                }
+                // every SN slot before the M-th is evicted: listed for the
+                // lookup of its token's table cell
+                if (isSN && nsn < M) snList[nsn] = static_cast<uint16_t>(ring_slot(hand0, u, dbs));
                 if (isSN && nsn + 1u == M) ms.nSM = static_cast<int32_t>(nsm);
             }
             if (tid == 0 && snP.total < M) ms.nSM = static_cast<int32_t>(smP.total);
+            WSTAMP(12);
         }
+        WSTAMP(15);
         __syncthreads();
     }
     STAMP(3);
@@ -860,6 +928,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         // either as undecided (counted in X) or settled (counted exactly):
         // both are safe.
         const int32_t nUnd = ms.nUnd;
+        // the waves not settling undecided slots look up the table cells of
+        // the evicted SN slots meanwhile (all waves, after, when none is free;
+        // with no undecided slots the lookups overlap the events phase, which
+        // does not touch what they write)
+        const int32_t busy = nUnd == 0 ? 0 : nUnd <= 64 ? min(nUnd, NWAVES) : 1;
+        const int32_t nSNev = static_cast<int32_t>(min(M, snP.total));
+        auto sn_cells = [&](int32_t first, int32_t stride) {
+            for (int32_t x = first; x < nSNev; x += stride) {
+                const int32_t sl = snList[x];
+                vt[sl] = static_cast<uint16_t>(cell_of(sl));
+            }
+        };
+        if (wave >= busy) sn_cells(tid - busy * 64, NT - busy * 64);
         if (nUnd > 0 && nUnd <= 64) {
             // undecided slots (few): one wave each counts the evictions
             // settled in the first pass before it with a larger k (L) and
@@ -916,9 +997,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                 }
             }
-            WSTAMP(5);
-            __syncthreads();
-            WSTAMP(6);
         } else if (nUnd > 64) {  // many undecided slots: one wave settles them in ring order
             if (wave == 0) {
                 for (int32_t c = 0; c < nSM; c += 64) {
@@ -946,8 +1024,11 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                 }
             }
-            __syncthreads();
         }
+        if (busy == NWAVES) sn_cells(tid, NT);
+        WSTAMP(5);
+        if (nUnd > 0) __syncthreads();
+        WSTAMP(6);
     }
     STAMP(4);
 
@@ -984,6 +1065,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (ep.total != static_cast<uint32_t>(N)) fast = false;  // same value in every wave
+        // table cells of the evicted SM slots' tokens
+        for (int32_t q = 0; q < Ps; ++q) {
+            const int32_t i = tid + q * NT;
+            if (i < nSM && ((smask[i >> 6] >> (i & 63)) & 1ull)) {
+                smCell[i] = static_cast<uint16_t>(cell_of(ring_slot(hand0, static_cast<int32_t>(smA[i] & 0xFFFFu), dbs)));
+            }
+        }
         __syncthreads();
     }
     STAMP(5);
@@ -999,6 +1087,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         for (int32_t j = 0; j < Q; ++j) {
             const int32_t u = tid + j * NT;
             const int32_t e = j * NWAVES + wave;
+            // with N SN slots before the block, every offset in it has r >= N
+            if (snP.base(e) >= static_cast<uint32_t>(N)) continue;
             const uint32_t nsn2 = snP.own(e), nsm2 = min(smP.own(e), nSMu);
             if (u >= dbs) continue;
             const int32_t s = ring_slot(hand0, u, dbs);
@@ -1011,36 +1101,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     evslot[p] = static_cast<uint16_t>(s);
                     ++ntk;
                     if (r == N - 1) ms.uEnd = u + 1;
-                    uint32_t cell;
                     if (isSM) {
                         const uint32_t v0 = kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[s]);
                         vt[s] = static_cast<uint16_t>(VT_EVICTED | (v0 - 1u));
                     }
-                    if constexpr (!kC) {
-                        cell = NOCELL;
-                        if (tok[s] >= 0) {
-                            cell = cellOf[s];
-                            atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
-                        }
-                    } else if (isSN) {
-                        cell = vt[s];  // looked up with the ring classes
-                    } else {
-                        cell = NOCELL;
-                        if (slot_live(s)) {
-                            int32_t idx = slot_home(s);
-                            for (int32_t n = 0; n <= mask; ++n) {
-                                const uint32_t e = ht[idx];
-                                if (e == static_cast<uint32_t>(s + 1)) {
-                                    cell = static_cast<uint32_t>(idx);
-                                    break;
-                                }
-                                if (e == 0u) break;
-                                idx = (idx + 1) & mask;
-                            }
-                            if (cell == NOCELL) g.code = kOverflowProbe;
-                            else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
-                        }
-                    }
+                    // looked up (and marked in ber) while deciding (SN) or in
+                    // the events phase (SM)
+                    const uint32_t cell = isSN ? static_cast<uint32_t>(vt[s]) : static_cast<uint32_t>(smCell[nsm2]);
                     ecell[r] = cell | (static_cast<uint32_t>(s) << 16);
                 } else {
                     vt[s] = static_cast<uint16_t>(VT_PASSED | p);
@@ -1337,15 +1404,18 @@ static hipError_t set_limit_one(size_t bytes)
                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
 }
 
+// Fixed-count instantiations: topK up to 2048 with 4096 or 8192 slots.
+constexpr int kP1 = 2048 / NT, kQ1 = 4096 / NT, kQ2 = 8192 / NT;
+
 hipError_t sieve_fast_set_lds_limit(size_t bytes)
 {
     hipError_t e = hipSuccess;
     if ((e = set_limit_one<false, 0, 0>(bytes)) != hipSuccess) return e;
-    if ((e = set_limit_one<false, 2, 4>(bytes)) != hipSuccess) return e;
-    if ((e = set_limit_one<false, 2, 8>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<false, kP1, kQ1>(bytes)) != hipSuccess) return e;
+    if ((e = set_limit_one<false, kP1, kQ2>(bytes)) != hipSuccess) return e;
     if ((e = set_limit_one<true, 0, 0>(bytes)) != hipSuccess) return e;
-    if ((e = set_limit_one<true, 2, 4>(bytes)) != hipSuccess) return e;
-    return set_limit_one<true, 2, 8>(bytes);
+    if ((e = set_limit_one<true, kP1, kQ1>(bytes)) != hipSuccess) return e;
+    return set_limit_one<true, kP1, kQ2>(bytes);
 }
 
 template <bool kC>
@@ -1353,10 +1423,10 @@ static void launch_one(const KvxLaunch<HispSieveUpdateArgs> &L, size_t ldsBytes,
 {
     const HispSieveUpdateArgs &a = L.a;
     const uint32_t P = (a.topK + NT - 1) / NT, Q = (a.deviceBufferSize + NT - 1) / NT;
-    if (P == 2 && Q == 4) {
-        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 4>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
-    } else if (P == 2 && Q == 8) {
-        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 2, 8>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    if (P == kP1 && Q == kQ1) {
+        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, kP1, kQ1>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
+    } else if (P == kP1 && Q == kQ2) {
+        hipLaunchKernelGGL((kvx_sieve_update_fast<kC, kP1, kQ2>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     } else {
         hipLaunchKernelGGL((kvx_sieve_update_fast<kC, 0, 0>), dim3(a.maxNumReqs), dim3(NT), ldsBytes, stream, L);
     }
