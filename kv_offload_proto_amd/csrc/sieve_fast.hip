@@ -118,7 +118,7 @@ __device__ unsigned long long kvx_dbg_w[64][16][16];
 #endif
 
 struct Misc {
-    int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead, nDone;
+    int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead, nDone, snNext;
     uint32_t wtok[NWAVES];
     uint32_t went[NWAVES];
     uint32_t wring[NWAVES];
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         }
         if (tid == 0) {
             ms.bad = ms.ovf = ms.late = 0;
-            ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = 0;
+            ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = ms.snNext = 0;
         }
     }
     __syncthreads();
@@ -906,7 +906,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         U += (j + 1 < i && (w4[q] >> 16) > ki) ? 1u : 0u;
                     }
                 }
-                for (int o = 1; o < G; o <<= 1) U += static_cast<uint32_t>(__shfl_xor(static_cast<int>(U), o));
+                // sum over the slot's G lanes (aligned within a row of 16) into its first lane
+                int Ui = static_cast<int>(U);
+                if (G >= 2) Ui += __builtin_amdgcn_update_dpp(0, Ui, 0x101, 0xF, 0xF, true);  // row_shl:1
+                if (G >= 4) Ui += __builtin_amdgcn_update_dpp(0, Ui, 0x102, 0xF, 0xF, true);  // row_shl:2
+                if (G >= 8) Ui += __builtin_amdgcn_update_dpp(0, Ui, 0x104, 0xF, 0xF, true);  // row_shl:4
+                if (G >= 16) Ui += __builtin_amdgcn_update_dpp(0, Ui, 0x108, 0xF, 0xF, true); // row_shl:8
+                U = static_cast<uint32_t>(Ui);
                 dec = (ai >= static_cast<int32_t>(U)) ? 1 : 2;
                 if (part == 0) {
                     if (dec == 2) {
@@ -920,6 +926,75 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (part == 0) tb[i] = dec;
         }
         WSTAMP(1);
+        const int32_t nSNev = static_cast<int32_t>(min(M, snP.total));
+        if (nSM <= 4 * 64) {
+            // short list: the last wave to finish the first pass settles the
+            // undecided slots in ring order from registers (a lane per SM
+            // slot of each 64-slot chunk); every wave then looks up the table
+            // cells of the evicted SN slots, 64 at a time from a shared counter
+            int32_t old = 0;
+            if (lane == 0) {
+                __threadfence_block();
+                old = atomicAdd(&ms.nDone, 1);
+            }
+            if (lane_value(old, 0) == NWAVES - 1) {
+                __threadfence_block();
+                if (ms.nUnd > 0) {
+                    uint32_t kq[4], bq[4];
+                    uint64_t evq[4], undq[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int32_t j = c * 64 + static_cast<int32_t>(lane);
+                        const bool ok = j < nSM;
+                        const uint32_t t = ok ? tb[j] : 0u;
+                        kq[c] = ok ? (smA[j] >> 16) : 0u;
+                        bq[c] = ok ? smB[j] : 0u;
+                        evq[c] = __ballot(t == 1u);
+                        undq[c] = __ballot(t == 2u);
+                    }
+                    WSTAMP(3);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        for (uint64_t und = undq[c]; und != 0ull; und &= und - 1ull) {
+                            const int f = __builtin_ctzll(und);
+                            const uint32_t ki = static_cast<uint32_t>(lane_value(static_cast<int>(kq[c]), f));
+                            const uint32_t eb = static_cast<uint32_t>(lane_value(static_cast<int>(bq[c]), f));
+                            const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
+                            uint32_t d = static_cast<uint32_t>(__popcll(__ballot(kq[c] > ki) & evq[c] & ((1ull << f) - 1ull)));
+#pragma unroll
+                            for (int c2 = 0; c2 < c; ++c2) d += static_cast<uint32_t>(__popcll(__ballot(kq[c2] > ki) & evq[c2]));
+                            if (ai >= static_cast<int32_t>(d)) evq[c] |= 1ull << f;
+                        }
+                    }
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int32_t j = c * 64 + static_cast<int32_t>(lane);
+                        if ((undq[c] >> lane) & 1ull) {
+                            const bool evd = (evq[c] >> lane) & 1ull;
+                            tb[j] = evd ? 1 : 0;
+                            if (evd) {
+                                atomicOr(reinterpret_cast<unsigned long long *>(smask) + (j >> 6), 1ull << (j & 63));
+                                atomicOr(reinterpret_cast<unsigned long long *>(emask) + (kq[c] >> 6), 1ull << (kq[c] & 63u));
+                            }
+                        }
+                    }
+                }
+            }
+            for (;;) {
+                int32_t x0 = 0;
+                if (lane == 0) x0 = atomicAdd(&ms.snNext, 64);
+                x0 = lane_value(x0, 0);
+                if (x0 >= nSNev) break;
+                const int32_t x = x0 + static_cast<int32_t>(lane);
+                if (x < nSNev) {
+                    const int32_t sl = snList[x];
+                    vt[sl] = static_cast<uint16_t>(cell_of(sl));
+                }
+            }
+            WSTAMP(5);
+            __syncthreads();
+            WSTAMP(6);
+        } else {
         __syncthreads();
         WSTAMP(2);
         // undecided slots, one wave each: count the evictions already settled
@@ -933,7 +1008,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         // with no undecided slots the lookups overlap the events phase, which
         // does not touch what they write)
         const int32_t busy = nUnd == 0 ? 0 : nUnd <= 64 ? min(nUnd, NWAVES) : 1;
-        const int32_t nSNev = static_cast<int32_t>(min(M, snP.total));
         auto sn_cells = [&](int32_t first, int32_t stride) {
             for (int32_t x = first; x < nSNev; x += stride) {
                 const int32_t sl = snList[x];
@@ -1026,9 +1100,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (busy == NWAVES) sn_cells(tid, NT);
-        WSTAMP(5);
         if (nUnd > 0) __syncthreads();
-        WSTAMP(6);
+        }
     }
     STAMP(4);
 
