@@ -119,10 +119,8 @@ __device__ unsigned long long kvx_dbg_w[64][16][16];
 
 struct Misc {
     int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead, nDone, snNext;
-    uint32_t wtok[NWAVES];
-    uint32_t went[NWAVES];
-    uint32_t wring[NWAVES];
-    uint32_t wcand[NWAVES];
+    int32_t diff;  // live tokens minus table entries
+    uint32_t M;    // candidates (first occurrences of missing tokens)
     uint32_t uL[64];  // undecided SM slots in ring order: evictions settled before them with a larger k
     uint16_t ui[64];  // ... and their SM indices
 };
@@ -385,6 +383,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const int32_t n16 = (min(seqLen, invCap) + 7) >> 3;
         for (int32_t i = tid; i < n16; i += NT) reinterpret_cast<v4u *>(inv)[i] = v4u{0u, 0u, 0u, 0u};
     }
+    if (tid == 0) {  // ordered before every update by the barrier in the staging pass
+        ms.bad = ms.ovf = ms.late = 0;
+        ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = ms.snNext = 0;
+        ms.diff = 0;
+        ms.M = 0;
+    }
     int32_t prefill = ((KVX_C const int32_t *)(a.prefillLens))[reqIdx];
     KVX_G int32_t *gTok = (KVX_G int32_t *)(a.deviceBufferTokens) + reqIdx * padded;
     KVX_G uint8_t *gVis = (KVX_G uint8_t *)(a.deviceBufferVisited) + reqIdx * visStrideB;
@@ -577,16 +581,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         for (int32_t i = tid; i < (visStrideB >> 2); i += NT) vset[i] = 0u;
         for (int32_t i = tid; i < (H >> 5); i += NT) ber[i] = 0u;
         for (int32_t i = tid; i < 2 * P * NWAVES; i += NT) emask[i] = 0ull;  // emask, smask (adjacent)
-        nTok = wave_sum(nTok);
-        nEnt = wave_sum(nEnt);
-        if (lane == 0) {
-            ms.wtok[wave] = nTok;
-            ms.went[wave] = nEnt;
-        }
-        if (tid == 0) {
-            ms.bad = ms.ovf = ms.late = 0;
-            ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = ms.snNext = 0;
-        }
+        const int32_t dw = static_cast<int32_t>(wave_sum(nTok)) - static_cast<int32_t>(wave_sum(nEnt));
+        if (lane == 0 && dw != 0) atomicAdd(&ms.diff, dw);
     }
     __syncthreads();
     WSTAMP(13);
@@ -621,16 +617,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if (__ballot(bad) != 0ull && lane == 0) atomicOr(&ms.bad, 1);
         __syncthreads();
     }
-    bool fast;
-    {
-        uint32_t sTok = 0, sEnt = 0;
-#pragma unroll
-        for (int w = 0; w < NWAVES; ++w) {
-            sTok += ms.wtok[w];
-            sEnt += ms.went[w];
-        }
-        fast = ms.bad == 0 && sTok == sEnt;
-    }
+    bool fast = ms.bad == 0 && ms.diff == 0;
     const bool canonical = fast;
 
     // ---- classify every position; dedup the candidates (smallest position
@@ -831,11 +818,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 rsm[j * NWAVES + wave] = bsm;
             }
         }
-        if (lane == 0) ms.wcand[wave] = cw;
+        if (lane == 0 && cw != 0u) atomicAdd(&ms.M, cw);
         WSTAMP(7);
         __syncthreads();
-#pragma unroll
-        for (int w = 0; w < NWAVES; ++w) M += ms.wcand[w];
+        M = ms.M;
         MaskPrefix::init_pair(snP, rsn, Q * NWAVES, smP, rsm, Q * NWAVES, lane);
         if (M > 0) {
             // only SM slots with fewer than M SN slots before them can be
@@ -895,13 +881,23 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (ai >= 0) {
                 const uint32_t ki = smA[i] >> 16;
                 uint32_t U = 0;
+                const int32_t nb = i >> 3;  // blocks of 8 entirely before i
 #pragma unroll 2
-                for (int32_t b = part; 8 * b < i; b += G) {
+                for (int32_t b = part; b < nb; b += G) {
                     const uint4 x = kp4[b];
                     const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const int32_t j = 8 * b + 2 * q;
+                        U += ((w4[q] & 0xFFFFu) > ki) ? 1u : 0u;
+                        U += ((w4[q] >> 16) > ki) ? 1u : 0u;
+                    }
+                }
+                if ((i & 7) != 0 && (nb & (G - 1)) == part) {
+                    const uint4 x = kp4[nb];
+                    const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int32_t j = 8 * nb + 2 * q;
                         U += (j < i && (w4[q] & 0xFFFFu) > ki) ? 1u : 0u;
                         U += (j + 1 < i && (w4[q] >> 16) > ki) ? 1u : 0u;
                     }
@@ -1522,6 +1518,13 @@ extern "C" int kvx_dbg_read_sub(unsigned long long *out, int rows)
     if (rows > 1024) rows = 1024;
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(kvx::kvx_dbg_sub), sizeof(unsigned long long) * 16 * rows, 0,
                                hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+
+extern "C" int kvx_dbg_clear_w()
+{
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(kvx::kvx_dbg_w)) != hipSuccess) return -1;
+    return hipMemset(p, 0, sizeof(unsigned long long) * 64 * 16 * 16) == hipSuccess ? 0 : -1;
 }
 
 extern "C" int kvx_dbg_read_w(unsigned long long *out)
