@@ -515,10 +515,10 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
                            visited_stride_b;
         const bool fastShape = top_k >= 1 && pool_size >= 1 && top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535 &&
                                device_buffer_size <= 32u * kvx::kFastThreads && htSize <= 32768;
-        const size_t ldsFast = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
-                                                visited_stride_b, false).total;
-        const size_t ldsCompact = kvx::fast_layout(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
-                                                   visited_stride_b, true).total;
+        const size_t ldsFast = kvx::fast_layout_for(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
+                                                    device_buffer_size, visited_stride_b, false).total;
+        const size_t ldsCompact = kvx::fast_layout_for(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
+                                                       device_buffer_size, visited_stride_b, true).total;
         const bool fastOk = fastShape && ldsFast <= g.ldsLimit;
         const bool compactOk = fastShape && ldsCompact <= g.ldsLimit && lds <= g.ldsLimit;
         int variant = fastOk ? 2 : (compactOk ? 4 : (lds <= g.ldsLimit ? 0 : 3));

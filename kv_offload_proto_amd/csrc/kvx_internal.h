@@ -108,6 +108,65 @@ __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint
     return l;
 }
 
+// Fixed-count instantiations of the parallel kernel (positions and ring
+// offsets per lane): topK up to 2048 with up to 4096 or 8192 slots.
+constexpr int kFixP = 2048 / kFastThreads, kFixQ1 = 4096 / kFastThreads, kFixQ2 = 8192 / kFastThreads;
+
+__host__ __device__ constexpr bool fast_fixed(uint32_t topK, uint32_t dbs, int &pm, int &qm)
+{
+    const uint32_t P = (topK + kFastThreads - 1u) / kFastThreads, Q = (dbs + kFastThreads - 1u) / kFastThreads;
+    pm = static_cast<int>(P);
+    qm = static_cast<int>(Q);
+    return P == static_cast<uint32_t>(kFixP) && (Q == static_cast<uint32_t>(kFixQ1) || Q == static_cast<uint32_t>(kFixQ2));
+}
+
+// Layout of a fixed-count instantiation: the regions sized by topK or dbs
+// take their bounds (PM or QM entries per lane), so their offsets are
+// compile-time constants; the state row (tokens, table, visited bits) and the
+// per-cell bitmaps follow at offsets that depend on padded and htSize.
+template <int PM, int QM>
+__host__ __device__ __forceinline__ FastLayout fast_layout_fixed(uint32_t padded, uint32_t htSize, uint32_t visStrideB,
+                                                                 bool compact)
+{
+    constexpr uint32_t Kx = PM * kFastThreads, Dx = QM * kFastThreads, NW = kFastThreads / 64;
+    FastLayout l{};
+    uint32_t o = 0;
+    l.ptok = o;    o += Kx * 4u;
+    l.pinf = o;    o += Kx * 4u;
+    l.vt = o;      o += Dx * 2u;
+    l.evslot = o;  o += Kx * 2u;
+    l.smKp = o;    o += align16(Kx * 2u + 16u);
+    l.eseq = o;    o += Kx * 2u;
+    l.tb = o;      o += align16((Kx + 1u) * 2u);
+    l.smA = o;     o += Kx * 4u;
+    l.smB = o;     o += Kx * 4u;
+    l.vset = o;    o += align16(Dx / 8u);
+    l.cmask = o;   o += PM * NW * 8u;
+    l.emask = o;   o += PM * NW * 8u;
+    l.smask = o;   o += PM * NW * 8u;
+    l.rsn = o;     o += QM * NW * 8u;
+    l.rsm = o;     o += QM * NW * 8u;
+    l.tok = o;     o += align16(padded * (compact ? 2u : 4u));
+    l.ht = o;      o += align16(htSize * 2u);
+    l.vis = o;     o += align16(visStrideB);
+    l.ber = o;     o += align16(htSize / 8u);
+    l.occ = o;     o += align16(htSize / 8u);
+    l.total = o;
+    return l;
+}
+
+// The layout the launcher and the kernel use for a shape.
+__host__ __device__ __forceinline__ FastLayout fast_layout_for(uint32_t padded, uint32_t htSize, uint32_t topK,
+                                                               uint32_t dbs, uint32_t visStrideB, bool compact)
+{
+    int pm = 0, qm = 0;
+    if (fast_fixed(topK, dbs, pm, qm)) {
+        return qm == kFixQ1 ? fast_layout_fixed<kFixP, kFixQ1>(padded, htSize, visStrideB, compact)
+                            : fast_layout_fixed<kFixP, kFixQ2>(padded, htSize, visStrideB, compact);
+    }
+    return fast_layout(padded, htSize, topK, visStrideB, compact);
+}
+
 // Launchers (implemented next to their kernels).
 hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int variant,
                                size_t ldsBytes, hipStream_t stream);

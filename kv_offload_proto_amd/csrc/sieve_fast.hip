@@ -375,7 +375,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // layout: 0, slot+1 of the slot holding the token, or padded+1+k for a
     // missing token first seen at position k (smallest k wins).  Cleared over
     // min(seqLen, capacity) entries before the state row lands.
-    const FastLayout lay = fast_layout(padded, H, K, visStrideB, kC);
+    constexpr bool kFixed = PM > 0 && QM > 0;
+    // fixed-count instantiations: compile-time offsets for the regions sized by topK and dbs
+    const FastLayout lay = kFixed ? fast_layout_fixed<(kFixed ? PM : 1), (kFixed ? QM : 1)>(padded, H, visStrideB, kC)
+                                  : fast_layout(padded, H, K, visStrideB, kC);
+    // words of the visited bits set this step (bits of slots below dbs)
+    const int32_t vsetWords = kFixed ? QM * NT / 32 : (visStrideB >> 2);
     const int32_t invCap = static_cast<int32_t>(a.reserved >> 8);
     uint16_t *inv = reinterpret_cast<uint16_t *>(smem + lay.total);
     uint32_t *inv32 = reinterpret_cast<uint32_t *>(smem + lay.total);
@@ -465,7 +470,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         return cell;
     };
 
-    constexpr bool kFixed = PM > 0 && QM > 0;
     const int32_t P = kFixed ? PM : (K + NT - 1) / NT;    // positions per lane: k = tid + q * NT
     const int32_t Q = kFixed ? QM : (dbs + NT - 1) / NT;  // ring offsets per lane: u = tid + j * NT
     constexpr int PR = kFixed ? PM : 1, QR = kFixed ? QM : 1;
@@ -534,8 +538,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         reinterpret_cast<v4u *>(tok)[c] = x;
                     }
                     const uint32_t nib = (vB[j] >> ((c & 1) * 4)) & 0xFu;
-                    vt32[2 * c] = ((nib & 1u) ? 0u : 0xFFFFu) | ((nib & 2u) ? 0u : 0xFFFF0000u);
-                    vt32[2 * c + 1] = ((nib & 4u) ? 0u : 0xFFFFu) | ((nib & 8u) ? 0u : 0xFFFF0000u);
+                    if (4 * c < dbs) {  // first-hit codes of the ring's slots
+                        vt32[2 * c] = ((nib & 1u) ? 0u : 0xFFFFu) | ((nib & 2u) ? 0u : 0xFFFF0000u);
+                        vt32[2 * c + 1] = ((nib & 4u) ? 0u : 0xFFFFu) | ((nib & 8u) ? 0u : 0xFFFF0000u);
+                    }
                     const int32_t s0 = c * 4;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -578,7 +584,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 tR[q] = (q == 0) ? t0 : (q == 1) ? t1 : (k < K ? ptok[k] : 0);
             }
         }
-        for (int32_t i = tid; i < (visStrideB >> 2); i += NT) vset[i] = 0u;
+        for (int32_t i = tid; i < vsetWords; i += NT) vset[i] = 0u;
         for (int32_t i = tid; i < (H >> 5); i += NT) ber[i] = 0u;
         for (int32_t i = tid; i < 2 * P * NWAVES; i += NT) emask[i] = 0ull;  // emask, smask (adjacent)
         const int32_t dw = static_cast<int32_t>(wave_sum(nTok)) - static_cast<int32_t>(wave_sum(nEnt));
@@ -776,7 +782,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t snM = 0, smM = 0, M = 0;  // bit j: class of ring offset tid + j * NT
     MaskPrefix snP, smP;                // SN / SM slots before a ring offset
     if (fast) {
-        WSTAMP(4);
         uint32_t cw = 0;
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
@@ -819,7 +824,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (lane == 0 && cw != 0u) atomicAdd(&ms.M, cw);
-        WSTAMP(7);
         __syncthreads();
         M = ms.M;
         MaskPrefix::init_pair(snP, rsn, Q * NWAVES, smP, rsm, Q * NWAVES, lane);
@@ -830,7 +834,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             // is a prefix of the SM slots in ring order
             MaskPrefix cp;
             cp.init(cmask, P * NWAVES, lane);
-            WSTAMP(14);
 #pragma unroll
             for (int32_t j = 0; j < Q; ++j) {
                 const int32_t e = j * NWAVES + wave;
@@ -852,9 +855,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if (isSN && nsn + 1u == M) ms.nSM = static_cast<int32_t>(nsm);
             }
             if (tid == 0 && snP.total < M) ms.nSM = static_cast<int32_t>(smP.total);
-            WSTAMP(12);
         }
-        WSTAMP(15);
         __syncthreads();
     }
     STAMP(3);
@@ -1195,6 +1196,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const int32_t uEnd = ms.uEnd;
         const int32_t Pn = (N + NT - 1) / NT;
         Guard g;
+        WSTAMP(4);
         // ---- outputs and visited bits set this step (vset); erase the
         // evicted tokens: the rightmost marked cell of each pre-step cluster
         // (from the occupancy snapshot) leads it and deletes right to left
@@ -1229,6 +1231,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             rs[k] = slot;
             rm[k] = miss;
         }
+        WSTAMP(7);
         for (int32_t q = 0; q < Pn; ++q) {
             const int32_t r = tid + q * NT;
             if (r >= N) break;
@@ -1278,6 +1281,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 y = nx;
             }
         }
+        WSTAMP(14);
         __syncthreads();
         STAMP(7);
         // ---- new tokens; tentative placement (the final occupied cells do
@@ -1298,6 +1302,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (c < 0) g.code = kOverflowProbe;
             else ecell[r] = static_cast<uint32_t>(c) | (s << 16);
         }
+        WSTAMP(12);
         __syncthreads();
         STAMP(8);
         // ---- final cluster of each new key: alone in it, the key takes its
@@ -1321,6 +1326,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (m == 1u) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
             else if (mn == static_cast<uint32_t>(padded + 1 + r)) lead[atomicAdd(&ms.nLead, 1)] = static_cast<uint16_t>(st);
         }
+        WSTAMP(15);
         __syncthreads();
         STAMP(9);
         // ---- redo: insert the cluster's new keys in event order.  The cells
@@ -1400,7 +1406,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     const int32_t b1 = min(lo + 32, e0 - dbs);
                     if (b1 > lo) clr |= (b1 - lo == 32 ? 0xFFFFFFFFu : ((1u << (b1 - lo)) - 1u));
                 }
-                ((KVX_G uint32_t *)gVis)[w] = (vis32[w] & ~clr) | vset[w];
+                ((KVX_G uint32_t *)gVis)[w] = (vis32[w] & ~clr) | (w < vsetWords ? vset[w] : 0u);
             }
             if (N > 0) {
                 if constexpr (!kC) {  // compact: written in place
@@ -1473,8 +1479,7 @@ static hipError_t set_limit_one(size_t bytes)
                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
 }
 
-// Fixed-count instantiations: topK up to 2048 with 4096 or 8192 slots.
-constexpr int kP1 = 2048 / NT, kQ1 = 4096 / NT, kQ2 = 8192 / NT;
+constexpr int kP1 = kFixP, kQ1 = kFixQ1, kQ2 = kFixQ2;
 
 hipError_t sieve_fast_set_lds_limit(size_t bytes)
 {
