@@ -76,6 +76,7 @@ using namespace sieve;
 // scalar loads that need no wave-wide copy into scalar registers.
 #define KVX_C __attribute__((address_space(4)))
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 16-byte chunk
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));  // two 16-bit lanes of a register
 
 constexpr int NT = kFastThreads;
 constexpr int NWAVES = NT / 64;
@@ -883,16 +884,24 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 const uint32_t ki = smA[i] >> 16;
                 uint32_t U = 0;
                 const int32_t nb = i >> 3;  // blocks of 8 entirely before i
+                // two entries per 32-bit word: saturating k_j - k_i, capped at
+                // 1, summed in 16-bit halves
+                const uint32_t kk = ki | (ki << 16), ones = 0x00010001u;
+                u16x2 acc = {0, 0};
 #pragma unroll 2
                 for (int32_t b = part; b < nb; b += G) {
                     const uint4 x = kp4[b];
                     const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        U += ((w4[q] & 0xFFFFu) > ki) ? 1u : 0u;
-                        U += ((w4[q] >> 16) > ki) ? 1u : 0u;
+                        uint32_t gt;
+                        asm("v_pk_sub_u16 %0, %1, %2 clamp\n\tv_pk_min_u16 %0, %0, %3"
+                            : "=&v"(gt)
+                            : "v"(w4[q]), "v"(kk), "v"(ones));
+                        acc += __builtin_bit_cast(u16x2, gt);
                     }
                 }
+                U += static_cast<uint32_t>(acc.x) + static_cast<uint32_t>(acc.y);
                 if ((i & 7) != 0 && (nb & (G - 1)) == part) {
                     const uint4 x = kp4[nb];
                     const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
@@ -913,7 +922,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 dec = (ai >= static_cast<int32_t>(U)) ? 1 : 2;
                 if (part == 0) {
                     if (dec == 2) {
-                        undl[atomicAdd(&ms.nUnd, 1)] = static_cast<uint16_t>(i);
+                        // (the short list's settle finds them by their mark)
+                        if (nSM > 4 * 64) undl[atomicAdd(&ms.nUnd, 1)] = static_cast<uint16_t>(i);
                     } else {  // evicted: its first hit converts
                         atomicOr(reinterpret_cast<unsigned long long *>(smask) + (i >> 6), 1ull << (i & 63));
                         atomicOr(reinterpret_cast<unsigned long long *>(emask) + (ki >> 6), 1ull << (ki & 63u));
@@ -936,19 +946,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             if (lane_value(old, 0) == NWAVES - 1) {
                 __threadfence_block();
-                if (ms.nUnd > 0) {
-                    uint32_t kq[4], bq[4];
-                    uint64_t evq[4], undq[4];
+                uint32_t kq[4], bq[4];
+                uint64_t evq[4], undq[4];
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const int32_t j = c * 64 + static_cast<int32_t>(lane);
-                        const bool ok = j < nSM;
-                        const uint32_t t = ok ? tb[j] : 0u;
-                        kq[c] = ok ? (smA[j] >> 16) : 0u;
-                        bq[c] = ok ? smB[j] : 0u;
-                        evq[c] = __ballot(t == 1u);
-                        undq[c] = __ballot(t == 2u);
-                    }
+                for (int c = 0; c < 4; ++c) {
+                    const int32_t j = c * 64 + static_cast<int32_t>(lane);
+                    const bool ok = j < nSM;
+                    const uint32_t t = ok ? tb[j] : 0u;
+                    kq[c] = ok ? (smA[j] >> 16) : 0u;
+                    bq[c] = ok ? smB[j] : 0u;
+                    evq[c] = __ballot(t == 1u);
+                    undq[c] = __ballot(t == 2u);
+                }
+                if ((undq[0] | undq[1] | undq[2] | undq[3]) != 0ull) {
                     WSTAMP(3);
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
