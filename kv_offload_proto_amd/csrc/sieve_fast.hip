@@ -538,17 +538,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     } else {
                         reinterpret_cast<v4u *>(tok)[c] = x;
                     }
-                    const uint32_t nib = (vB[j] >> ((c & 1) * 4)) & 0xFu;
-                    if (4 * c < dbs) {  // first-hit codes of the ring's slots
-                        vt32[2 * c] = ((nib & 1u) ? 0u : 0xFFFFu) | ((nib & 2u) ? 0u : 0xFFFF0000u);
-                        vt32[2 * c + 1] = ((nib & 4u) ? 0u : 0xFFFFu) | ((nib & 8u) ? 0u : 0xFFFF0000u);
+                    if (4 * c < dbs) {  // first-hit codes of the ring's slots: 0 visited, 0xFFFF not
+                        const uint32_t nv4 = ~(vB[j] >> ((c & 1) * 4));  // bit i: slot 4c+i not visited
+                        const uint2 code = make_uint2(((nv4 & 1u) | ((nv4 & 2u) << 15)) * 0xFFFFu,
+                                                      (((nv4 >> 2) & 1u) | ((nv4 & 8u) << 13)) * 0xFFFFu);
+                        reinterpret_cast<uint2 *>(vt32)[c] = code;
                     }
-                    const int32_t s0 = c * 4;
+                    const int32_t s0 = c * 4, room = dbs - s0;  // slots of the chunk below dbs: i < room
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const bool live = s0 + i < dbs && tt[i] >= 0;
+                        const bool live = i < room && tt[i] >= 0;
                         nTok += live ? 1u : 0u;
-                        if (direct && live && tt[i] < lim) inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
+                        if (direct && i < room && static_cast<uint32_t>(tt[i]) < static_cast<uint32_t>(lim))
+                            inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
                     }
                 }
             }
@@ -558,13 +560,14 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if (c < nh) {
                     const v4u x = vH[j];
                     reinterpret_cast<v4u *>(ht)[c] = x;
+                    // occupied cells: min(cell, 1) per 16-bit half, the halves'
+                    // bits gathered into bit 2q (low cell) and 2q+1 (high cell)
                     const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
-                    uint32_t ob = 0;
+                    uint32_t m4[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        ob |= (((w4[q] & 0xFFFFu) != 0u) ? 1u : 0u) << (2 * q);
-                        ob |= (((w4[q] >> 16) != 0u) ? 1u : 0u) << (2 * q + 1);
-                    }
+                    for (int q = 0; q < 4; ++q) asm("v_pk_min_u16 %0, %1, %2" : "=v"(m4[q]) : "v"(w4[q]), "v"(0x00010001u));
+                    const uint32_t xo = m4[0] | (m4[1] << 2) | (m4[2] << 4) | (m4[3] << 6);
+                    const uint32_t ob = (xo | (xo >> 15)) & 0xFFu;
                     occ8[c] = static_cast<uint8_t>(ob);
                     nEnt += static_cast<uint32_t>(__popc(ob));
                 }
