@@ -484,6 +484,38 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     STAMP(0);
     int32_t hand0 = ((KVX_C const int32_t *)gHand)[0];
     int32_t flagw = ((KVX_C const int32_t *)gHand)[1];
+    // sieve_hand[row][2]: steps in a row this kernel could not take in parallel
+    int32_t hintw = ((KVX_C const int32_t *)gHand)[2];
+
+    // The in-order recurrence (hisp_sieve_update.cpp:115-163) on a staged copy
+    // of the row, then its write back: one lane for small tables, else 64
+    // cells/slots per step.  canon: the row was consistent before the step.
+    __shared__ int32_t s_dirty;
+    auto run_inorder = [&](int32_t *tokF, uint16_t *htF, uint8_t *visF, bool canon) {
+        if (wave == 0) {
+            int32_t hand = hand0;
+            Guard g;
+            bool dirty = false;
+            if (H <= kSmallTable) {
+                if (lane == 0) dirty = sieve_row_sequential((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
+            } else {
+                dirty = sieve_row_wave((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
+            }
+            if (lane == 0) {
+                gHand[0] = hand;
+                gHand[1] = (canon && g.code == 0) ? kCanonFlag : 0;
+                gHand[2] = min(hintw, (1 << 30)) + 1;
+                s_dirty = dirty ? 1 : 0;
+                report_overflow(L.overflowSlot, g.code);
+            }
+        }
+        __syncthreads();
+        wg_copy16((KVX_G v4u *)gVis, reinterpret_cast<const v4u *>(visF), static_cast<uint32_t>(visStrideB));
+        if (s_dirty) {
+            wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tokF), static_cast<uint32_t>(padded) * 4u);
+            wg_copy16((KVX_G v4u *)gHt, reinterpret_cast<const v4u *>(htF), static_cast<uint32_t>(H) * 2u);
+        }
+    };
     {
         const int32_t nt = padded >> 2, nh = H >> 3, nv = visStrideB >> 4;  // 16-byte chunks
         KVX_G const v4u *sT = (KVX_G const v4u *)gTok;
@@ -519,7 +551,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             // (the scalar values pass through the statement, so that nothing
             // computed from them is scheduled, and waited for, before the loads)
             if (p == 0) {
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : "+s"(prefill), "+s"(hand0), "+s"(flagw) : : "memory");
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : "+s"(prefill), "+s"(hand0), "+s"(flagw), "+s"(hintw)
+                             : : "memory");
                 lim = min(prefill, seqLen);
                 direct = !kC && lim > 0 && lim <= invCap;
             }
@@ -600,6 +633,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const bool flagged = flagw == kCanonFlag;
     if (badReq) {  // hisp_sieve_update.cpp:80-87: the row gets the dummy outputs, the state is untouched
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
+        return;
+    }
+    // A row whose recent steps all wrapped the hand (the parallel form's
+    // bound) tries the parallel form only every 8th step; the other steps
+    // run the in-order recurrence on the row as staged.
+    if (!kC && hintw > 0 && (hintw & 7) != 0) {
+        run_inorder(tok, ht, vis, flagged);
         return;
     }
 
@@ -1435,6 +1475,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
                 gHand[0] = hd;
                 gHand[1] = kCanonFlag;
+                if (hintw != 0) gHand[2] = 0;
             }
             STAMP(11);
             return;
@@ -1458,29 +1499,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     wg_copy16(reinterpret_cast<v4u *>(htF), (KVX_G const v4u *)gHt, static_cast<uint32_t>(H) * 2u);
     wg_copy16(reinterpret_cast<v4u *>(visF), (KVX_G const v4u *)gVis, static_cast<uint32_t>(visStrideB));
     __syncthreads();
-    __shared__ int32_t s_dirty;
-    if (wave == 0) {  // the in-order recurrence: one lane for small tables, else 64 cells/slots per step
-        int32_t hand = hand0;
-        Guard g;
-        bool dirty = false;
-        if (H <= kSmallTable) {
-            if (lane == 0) dirty = sieve_row_sequential((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
-        } else {
-            dirty = sieve_row_wave((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
-        }
-        if (lane == 0) {
-            gHand[0] = hand;
-            gHand[1] = (canonical && g.code == 0) ? kCanonFlag : 0;
-            s_dirty = dirty ? 1 : 0;
-            report_overflow(L.overflowSlot, g.code);
-        }
-    }
-    __syncthreads();
-    wg_copy16((KVX_G v4u *)gVis, reinterpret_cast<const v4u *>(visF), static_cast<uint32_t>(visStrideB));
-    if (s_dirty) {
-        wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tokF), static_cast<uint32_t>(padded) * 4u);
-        wg_copy16((KVX_G v4u *)gHt, reinterpret_cast<const v4u *>(htF), static_cast<uint32_t>(H) * 2u);
-    }
+    run_inorder(tokF, htF, visF, canonical);
 }
 
 }  // namespace
