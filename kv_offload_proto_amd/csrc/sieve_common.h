@@ -295,6 +295,149 @@ __device__ bool sieve_row_wave(const int32_t *rt, int32_t *rs, int8_t *rm, int32
 }
 
 // Copy n bytes (multiple of 16, both sides 16-byte aligned) with the block.
+// The in-order recurrence of hisp_sieve_update.cpp:115-163 for a row of at
+// most 64 slots whose table indexes exactly its non-negative tokens (each
+// at its own slot), with one wave: slot s's token and the cell of its entry
+// in lane s, the visited bits and the hand in scalar registers, and the home
+// of every occupied cell in hmc (htSize entries of LDS scratch, plus 64 for
+// the set-up).  A lookup is a ballot over the lanes (the slot holding the
+// token is the one the table's probe finds), the sweep a few mask
+// operations; an eviction reads one window of 64 cells (entries and homes)
+// for the erase's shifts and one for the insert.  Updates tok, vis and ht in
+// place; returns whether any slot changed.
+__device__ bool sieve_row_regs(const int32_t *rt, int32_t *rs, int8_t *rm, int32_t topK, int32_t seqLen,
+                               int32_t prefill, int32_t dbs, int32_t padded, int32_t mask, int32_t *tok, uint8_t *vis,
+                               uint16_t *ht, uint16_t *hmc, int32_t &hand, Guard &g)
+{
+    const int32_t lane = static_cast<int32_t>(__lane_id());
+    const bool mine = lane < dbs;
+    int32_t tokR = mine ? tok[lane] : -1;
+    const uint64_t all = dbs >= 64 ? ~0ull : ((1ull << dbs) - 1ull);
+    uint64_t vm = __ballot(mine && ((vis[lane >> 3] >> (lane & 7)) & 1));
+    // homes of the occupied cells; the cell of each slot's entry
+    int32_t cellR = -1;
+    {
+        uint16_t *cellF = hmc + mask + 1;
+        for (int32_t c = lane; c <= mask; c += 64) {
+            const uint32_t e = ht[c];
+            if (e - 1u < static_cast<uint32_t>(dbs)) {
+                hmc[c] = static_cast<uint16_t>(ht_hash(tok[e - 1u]) & static_cast<uint32_t>(mask));
+                cellF[e - 1u] = static_cast<uint16_t>(c);
+            }
+        }
+        if (mine && tokR >= 0) cellR = cellF[lane];
+    }
+    int32_t hd = hand;
+    bool dirty = false;
+    for (int32_t k0 = 0; k0 < topK; k0 += 64) {
+        const int32_t kn = (topK - k0 < 64) ? topK - k0 : 64;
+        const int32_t myT = lane < kn ? rt[k0 + lane] : -1;
+        int32_t mySlot = -1, myMiss = 0;
+        for (int32_t kk = 0; kk < kn; ++kk) {
+            const int32_t tp = lane_value(myT, kk);
+            int32_t slot = -1, miss = 0;
+            if (tp < 0 || tp >= seqLen) {
+            } else if (tp >= prefill) {
+                slot = padded + (tp - prefill);
+            } else {
+                const uint64_t hm = __ballot(mine && tokR == tp);
+                if (hm != 0ull) {
+                    slot = __builtin_ctzll(hm);
+                    vm |= 1ull << slot;
+                } else {
+                    // sweep from the hand: visited slots passed are cleared
+                    const uint64_t unv = ~vm & all, from = all & ~((1ull << hd) - 1ull);
+                    int32_t h;
+                    if (unv & from) {
+                        h = __builtin_ctzll(unv & from);
+                        vm &= ~(((1ull << h) - 1ull) & from);
+                    } else if (unv) {
+                        h = __builtin_ctzll(unv);
+                        vm &= ~(from | ((1ull << h) - 1ull));
+                    } else {  // every slot visited: a whole revolution clears them all
+                        h = hd;
+                        vm = 0ull;
+                    }
+                    if (lane_value(tokR, h) >= 0) {
+                        // erase (Algorithm R): entries after the hole move into
+                        // it unless their home lies cyclically in (hole, cell]
+                        const int32_t c = lane_value(cellR, h);
+                        int32_t j = c;
+                        bool closed = false;
+                        for (int32_t base = 1; base <= mask + 1; base += 64) {
+                            const int32_t i = (c + base + lane) & mask;
+                            const uint32_t e = ht[i];
+                            const int32_t hme = hmc[i];
+                            const uint64_t z = __ballot(e == 0u);
+                            const int32_t lim = z ? __builtin_ctzll(z) : 64;
+                            int32_t last = -1;
+                            for (;;) {
+                                const bool mv = lane < lim && lane > last &&
+                                                ((j < i) ? (hme <= j || hme > i) : (hme <= j && hme > i));
+                                const uint64_t cm = __ballot(mv);
+                                if (cm == 0ull) break;
+                                last = __builtin_ctzll(cm);
+                                if (lane == last) {
+                                    ht[j] = static_cast<uint16_t>(e);
+                                    hmc[j] = static_cast<uint16_t>(hme);
+                                }
+                                if (lane == lane_value(static_cast<int32_t>(e), last) - 1) cellR = j;
+                                j = lane_value(i, last);
+                            }
+                            if (z) {
+                                closed = true;
+                                break;
+                            }
+                        }
+                        if (!closed) g.code = kOverflowProbe;
+                        if (lane == 0) ht[j] = 0;
+                    }
+                    // insert: the first empty cell from the new token's home
+                    const int32_t home = static_cast<int32_t>(ht_hash(tp)) & mask;
+                    bool placed = false;
+                    for (int32_t base = 0; base <= mask; base += 64) {
+                        const int32_t i = (home + base + lane) & mask;
+                        const uint64_t z = __ballot(ht[i] == 0u);
+                        if (z) {
+                            const int32_t f = __builtin_ctzll(z);
+                            if (lane == f) {
+                                ht[i] = static_cast<uint16_t>(h + 1);
+                                hmc[i] = static_cast<uint16_t>(home);
+                            }
+                            if (lane == h) cellR = lane_value(i, f);
+                            placed = true;
+                            break;
+                        }
+                    }
+                    if (!placed) g.code = kOverflowProbe;
+                    if (lane == h) tokR = tp;
+                    vm |= 1ull << h;
+                    hd = (h + 1 == dbs) ? 0 : h + 1;
+                    slot = h;
+                    miss = 1;
+                    dirty = true;
+                }
+            }
+            if (lane == kk) {
+                mySlot = slot;
+                myMiss = miss;
+            }
+        }
+        if (lane < kn) {
+            rs[k0 + lane] = mySlot;
+            rm[k0 + lane] = static_cast<int8_t>(myMiss);
+        }
+    }
+    if (mine) tok[lane] = tokR;
+    if (lane < (dbs + 7) / 8) {  // the visited bytes of slots [0, dbs); bits past dbs keep their value
+        const int32_t b0 = lane * 8;
+        const uint32_t keep = (dbs - b0 >= 8) ? 0u : (0xFFu << (dbs - b0)) & 0xFFu;
+        vis[lane] = static_cast<uint8_t>((vis[lane] & keep) | (static_cast<uint32_t>(vm >> b0) & 0xFFu & ~keep));
+    }
+    hand = hd;
+    return dirty;
+}
+
 __device__ __forceinline__ void block_copy16(void *dst, const void *src, uint32_t n)
 {
     const uint4 *s = static_cast<const uint4 *>(src);

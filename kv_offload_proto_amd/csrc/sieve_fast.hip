@@ -488,15 +488,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     int32_t hintw = ((KVX_C const int32_t *)gHand)[2];
 
     // The in-order recurrence (hisp_sieve_update.cpp:115-163) on a staged copy
-    // of the row, then its write back: one lane for small tables, else 64
-    // cells/slots per step.  canon: the row was consistent before the step.
+    // of the row, then its write back: registers for consistent rows of up to
+    // 64 slots, else one lane for small tables, else 64 cells/slots per step.
+    // canon: the row was consistent before the step.
     __shared__ int32_t s_dirty;
     auto run_inorder = [&](int32_t *tokF, uint16_t *htF, uint8_t *visF, bool canon) {
+        STAMP(12);
         if (wave == 0) {
             int32_t hand = hand0;
             Guard g;
             bool dirty = false;
-            if (H <= kSmallTable) {
+            if (canon && dbs <= 64 && invCap >= H + 64) {  // scratch: the direct map's region
+                dirty = sieve_row_regs((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, inv, hand, g);
+            } else if (H <= kSmallTable) {
                 if (lane == 0) dirty = sieve_row_sequential((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
             } else {
                 dirty = sieve_row_wave((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
@@ -509,8 +513,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 report_overflow(L.overflowSlot, g.code);
             }
         }
+        STAMP(13);
         __syncthreads();
         wg_copy16((KVX_G v4u *)gVis, reinterpret_cast<const v4u *>(visF), static_cast<uint32_t>(visStrideB));
+        STAMP(14);
         if (s_dirty) {
             wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tokF), static_cast<uint32_t>(padded) * 4u);
             wg_copy16((KVX_G v4u *)gHt, reinterpret_cast<const v4u *>(htF), static_cast<uint32_t>(H) * 2u);

@@ -370,3 +370,29 @@ def test_sieve_sequential_lds_wave_path(kvops):
             dev.assert_state_equal()
     finally:
         kvops.sieve_force_variant(-1)
+
+
+@pytest.mark.parametrize("dbs,K,prefill", [(64, 64, 256), (37, 100, 300), (16, 48, 12), (64, 200, 90)])
+def test_sieve_small_rows_inorder_paths(kvops, dbs, K, prefill):
+    """Rows of up to 64 slots whose steps wrap the hand: after a wrap the row
+    runs the in-order recurrence in registers, skipping the parallel form for
+    seven steps and retrying it on the eighth; a row whose consistency flag
+    was cleared takes the one-lane recurrence.  Full state after every step
+    (partial visited bytes, empty slots, duplicates, invalid positions)."""
+    rng = np.random.default_rng(dbs * 1000 + K)
+    req = 4
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    for step in range(20):
+        if step == 12:
+            dev.hand[0, 1, 1] = 0  # row 1 no longer known consistent: checked again, one-lane path meanwhile
+        batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.8)
+        seq = np.full(req, prefill + 2)
+        e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+        g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+        np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+        np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+        dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
