@@ -86,7 +86,8 @@ int kvx_export_seg_alllayer(uint64_t channel, uint64_t seg_base, uint32_t per_la
  * informational reqsPerCore field (the grid is one workgroup per batch row).
  * Elements 1 and 2 of each 16-int sieve_hand record (unused by the reference)
  * carry a consistency flag and a count of steps that wrapped the hand;
- * zeroing them is always safe. */
+ * zeroing them is always safe, and a caller that edits a row's tokens or
+ * table outside these calls zeroes element 1. */
 int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t seq_lens,
                      uint64_t prefill_lens, uint64_t device_buffer_tokens,
                      uint64_t device_buffer_visited, uint64_t device_buffer_ht, uint64_t sieve_hand,

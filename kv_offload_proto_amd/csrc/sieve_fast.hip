@@ -643,9 +643,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     }
     // A row whose recent steps all wrapped the hand (the parallel form's
     // bound) tries the parallel form only every 8th step; the other steps
-    // run the in-order recurrence on the row as staged.
+    // run the in-order recurrence on the row as staged (known consistent when
+    // flagged and its entry count matches its live tokens).
     if (!kC && hintw > 0 && (hintw & 7) != 0) {
-        run_inorder(tok, ht, vis, flagged);
+        run_inorder(tok, ht, vis, flagged && ms.diff == 0);
         return;
     }
 

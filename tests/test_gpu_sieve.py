@@ -388,6 +388,22 @@ def test_sieve_small_rows_inorder_paths(kvops, dbs, K, prefill):
     for step in range(20):
         if step == 12:
             dev.hand[0, 1, 1] = 0  # row 1 no longer known consistent: checked again, one-lane path meanwhile
+        if step == 14:
+            # row 2's tokens edited outside the kernel (a duplicated token), the flag cleared as
+            # the interface asks: the row is checked again and takes the exact one-lane recurrence
+            live = np.nonzero(st.tokens[0, 2, :dbs] >= 0)[0]
+            if len(live) >= 2:
+                a_, b_ = int(live[0]), int(live[1])
+                st.tokens[0, 2, a_] = st.tokens[0, 2, b_]
+                dev.tokens[0, 2, a_] = int(st.tokens[0, 2, b_])
+                dev.hand[0, 2, 1] = 0
+        if step == 16:
+            # row 3: one more live token than table entries with the flag still set; the count
+            # check catches it
+            empty = np.nonzero(st.tokens[0, 3, :dbs] < 0)[0]
+            if len(empty):
+                st.tokens[0, 3, int(empty[0])] = prefill - 1
+                dev.tokens[0, 3, int(empty[0])] = prefill - 1
         batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.8)
         seq = np.full(req, prefill + 2)
         e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
