@@ -438,6 +438,83 @@ __device__ bool sieve_row_regs(const int32_t *rt, int32_t *rs, int8_t *rm, int32
     return dirty;
 }
 
+// The hit/miss decisions of the in-order recurrence (hisp_sieve_update.cpp:
+// 115-163) for a row of at most 64 slots whose table indexes exactly its
+// non-negative tokens, in one wave's registers and without the table: a
+// lookup is a ballot over the slots' tokens (slot s in lane s), the sweep a
+// few mask operations on the visited bits.  Writes the outputs; returns the
+// number of misses (events) and, per lane s, the slot's final token and the
+// event that placed it (-1: not evicted this step), with the visited bits of
+// slots [0, dbs) and the hand.  The table is left to the caller: it loses
+// the pre-step token of every evicted slot and gains the final tokens in
+// event order (a token placed and evicted within the step leaves no trace).
+__device__ int32_t sieve_row_regs_decide(const int32_t *rt, int32_t *rs, int8_t *rm, int32_t topK, int32_t seqLen,
+                                         int32_t prefill, int32_t dbs, int32_t padded, const int32_t *tok,
+                                         const uint8_t *vis, int32_t &hand, int32_t &tokFinal, int32_t &lastEv,
+                                         uint64_t &visMask)
+{
+    const int32_t lane = static_cast<int32_t>(__lane_id());
+    const bool mine = lane < dbs;
+    int32_t tokR = mine ? tok[lane] : -1;
+    const uint64_t all = dbs >= 64 ? ~0ull : ((1ull << dbs) - 1ull);
+    uint64_t vm = __ballot(mine && ((vis[lane >> 3] >> (lane & 7)) & 1));
+    int32_t hd = hand, ev = -1, nev = 0;
+    for (int32_t k0 = 0; k0 < topK; k0 += 64) {
+        const int32_t kn = (topK - k0 < 64) ? topK - k0 : 64;
+        const int32_t myT = lane < kn ? rt[k0 + lane] : -1;
+        int32_t mySlot = -1, myMiss = 0;
+        for (int32_t kk = 0; kk < kn; ++kk) {
+            const int32_t tp = lane_value(myT, kk);
+            int32_t slot = -1, miss = 0;
+            if (tp < 0 || tp >= seqLen) {
+            } else if (tp >= prefill) {
+                slot = padded + (tp - prefill);
+            } else {
+                const uint64_t hm = __ballot(mine && tokR == tp);
+                if (hm != 0ull) {
+                    slot = __builtin_ctzll(hm);
+                    vm |= 1ull << slot;
+                } else {
+                    const uint64_t unv = ~vm & all, from = all & ~((1ull << hd) - 1ull);
+                    int32_t h;
+                    if (unv & from) {
+                        h = __builtin_ctzll(unv & from);
+                        vm &= ~(((1ull << h) - 1ull) & from);
+                    } else if (unv) {
+                        h = __builtin_ctzll(unv);
+                        vm &= ~(from | ((1ull << h) - 1ull));
+                    } else {  // every slot visited: a whole revolution clears them all
+                        h = hd;
+                        vm = 0ull;
+                    }
+                    if (lane == h) {
+                        tokR = tp;
+                        ev = nev;
+                    }
+                    ++nev;
+                    vm |= 1ull << h;
+                    hd = (h + 1 == dbs) ? 0 : h + 1;
+                    slot = h;
+                    miss = 1;
+                }
+            }
+            if (lane == kk) {
+                mySlot = slot;
+                myMiss = miss;
+            }
+        }
+        if (lane < kn) {
+            rs[k0 + lane] = mySlot;
+            rm[k0 + lane] = static_cast<int8_t>(myMiss);
+        }
+    }
+    tokFinal = tokR;
+    lastEv = ev;
+    visMask = vm;
+    hand = hd;
+    return nev;
+}
+
 __device__ __forceinline__ void block_copy16(void *dst, const void *src, uint32_t n)
 {
     const uint4 *s = static_cast<const uint4 *>(src);

@@ -119,6 +119,8 @@ __device__ unsigned long long kvx_dbg_w[64][16][16];
 #endif
 
 struct Misc {
+    unsigned long long evMask;  // in-order path: the events that placed a slot's final token
+    int32_t nEv, handOut;
     int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead, nDone, snNext;
     int32_t diff;  // live tokens minus table entries
     uint32_t M;    // candidates (first occurrences of missing tokens)
@@ -394,6 +396,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = ms.snNext = 0;
         ms.diff = 0;
         ms.M = 0;
+        ms.evMask = 0ull;
     }
     int32_t prefill = ((KVX_C const int32_t *)(a.prefillLens))[reqIdx];
     KVX_G int32_t *gTok = (KVX_G int32_t *)(a.deviceBufferTokens) + reqIdx * padded;
@@ -522,6 +525,192 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             wg_copy16((KVX_G v4u *)gHt, reinterpret_cast<const v4u *>(htF), static_cast<uint32_t>(H) * 2u);
         }
     };
+
+    // Restage the pre-step row from HBM (nothing has been written back) and
+    // run the in-order recurrence on it.
+    auto restage_and_run = [&](bool canon) {
+        __syncthreads();
+        int32_t *tokF = reinterpret_cast<int32_t *>(smem);
+        uint16_t *htF = reinterpret_cast<uint16_t *>(smem + static_cast<size_t>(padded) * 4u);
+        uint8_t *visF = smem + static_cast<size_t>(padded) * 4u + static_cast<size_t>(H) * 2u;
+        wg_copy16(reinterpret_cast<v4u *>(tokF), (KVX_G const v4u *)gTok, static_cast<uint32_t>(padded) * 4u);
+        wg_copy16(reinterpret_cast<v4u *>(htF), (KVX_G const v4u *)gHt, static_cast<uint32_t>(H) * 2u);
+        wg_copy16(reinterpret_cast<v4u *>(visF), (KVX_G const v4u *)gVis, static_cast<uint32_t>(visStrideB));
+        __syncthreads();
+        run_inorder(tokF, htF, visF, canon);
+    };
+
+    // ---- table update for Nev events (ecell[r]: the cell of the token the
+    // event's slot loses, NOCELL for none, | slot << 16; ntokv[r]: the token
+    // it gains, in event order): erase the lost tokens -- the rightmost
+    // marked cell (ber) of each pre-step cluster (occ) leads it and deletes
+    // right to left -- then place the gained ones (claims, clusters, redo).
+    // setVset: also mark the events' slots visited in vset.  Sets ms.late on
+    // a bound violation.  Every thread calls it.
+    auto table_update = [&](int32_t Nev, bool setVset) {
+        const int32_t Pn = (Nev + NT - 1) / NT;
+        Guard g;
+        for (int32_t q = 0; q < Pn; ++q) {
+            const int32_t r = tid + q * NT;
+            if (r >= Nev) break;
+            const uint32_t ec = ecell[r];
+            const uint32_t s = ec >> 16;
+            if (setVset) atomicOr(vset + (s >> 5), 1u << (s & 31u));
+            const uint32_t c = ec & 0xFFFFu;
+            if (c == NOCELL) continue;
+            bool ld = true;
+            int32_t x = (static_cast<int32_t>(c) + 1) & mask;
+            for (int32_t n = 0; n <= (H >> 5); ++n) {
+                const uint32_t b = static_cast<uint32_t>(x) & 31u, span = 32u - b;
+                const uint32_t o = occ[x >> 5] >> b, eb = ber[x >> 5] >> b;
+                const uint32_t no = ~o;
+                const uint32_t z = no ? static_cast<uint32_t>(__builtin_ctz(no)) : 32u;  // first empty cell
+                const uint32_t below = (z >= 32u) ? 0xFFFFFFFFu : ((1u << z) - 1u);
+                if (eb & below) {
+                    ld = false;
+                    break;
+                }
+                if (z < span) break;
+                x = (x + static_cast<int32_t>(span)) & mask;
+            }
+            if (!ld) continue;
+            // the cluster's marked cells right to left; cells left of a
+            // deletion keep their pre-step contents, so the occupancy
+            // snapshot finds the next marked cell and the cluster's start
+            int32_t y = static_cast<int32_t>(c);
+            for (int32_t n = 0; n <= H; ++n) {
+                rdel_at<kC>(ht, smem + lay.tok, padded, y, mask, g);
+                int32_t nx = -1;
+                int32_t x2 = (y - 1) & mask;  // scan words leftward from x2
+                for (int32_t m = 0; m <= (H >> 5); ++m) {
+                    const uint32_t b = static_cast<uint32_t>(x2) & 31u;
+                    const uint32_t keep = (b == 31u) ? 0xFFFFFFFFu : ((2u << b) - 1u);  // bits 0..b
+                    const uint32_t empt = ~occ[x2 >> 5] & keep, mk = ber[x2 >> 5] & keep;
+                    const int32_t hiE = empt ? 31 - __builtin_clz(empt) : -1;  // cluster start boundary
+                    const uint32_t live = (hiE >= 0) ? (mk & ~((2u << hiE) - 1u)) : mk;
+                    if (live) {
+                        nx = (x2 & ~31) + (31 - __builtin_clz(live));
+                        break;
+                    }
+                    if (hiE >= 0) break;
+                    x2 = ((x2 & ~31) - 1) & mask;
+                }
+                if (nx < 0) break;
+                y = nx;
+            }
+        }
+        WSTAMP(14);
+        __syncthreads();
+        STAMP(7);
+        // ---- new tokens; tentative placement (the final occupied cells do
+        // not depend on order), entries padded+1+r name the event
+        for (int32_t q = 0; q < Pn; ++q) {
+            const int32_t r = tid + q * NT;
+            if (r >= Nev) break;
+            const uint32_t s = ecell[r] >> 16;
+            const int32_t t = ntokv[r];
+            if constexpr (kC) {
+                hv[s] = static_cast<uint16_t>(ht_hash(t) & static_cast<uint32_t>(mask));
+                gTok[s] = t;
+            } else {
+                tok[s] = t;
+            }
+            const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(t)) & mask, mask,
+                                          static_cast<uint16_t>(padded + 1 + r));
+            if (c < 0) g.code = kOverflowProbe;
+            else ecell[r] = static_cast<uint32_t>(c) | (s << 16);
+        }
+        WSTAMP(12);
+        __syncthreads();
+        STAMP(8);
+        // ---- final cluster of each new key: alone in it, the key takes its
+        // cell; with others, the earliest event redoes the cluster
+        for (int32_t q = 0; q < Pn; ++q) {
+            const int32_t r = tid + q * NT;
+            if (r >= Nev) break;
+            const uint32_t ec = ecell[r];
+            const int32_t c = static_cast<int32_t>(ec & 0xFFFFu);
+            int32_t st = c;
+            for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
+            uint32_t m = 0, mn = 0xFFFFFFFFu;
+            int32_t x = st;
+            for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
+                const uint32_t e = ht[x];
+                if (e > static_cast<uint32_t>(padded)) {
+                    ++m;
+                    mn = min(mn, e);
+                }
+            }
+            if (m == 1u) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
+            else if (mn == static_cast<uint32_t>(padded + 1 + r)) lead[atomicAdd(&ms.nLead, 1)] = static_cast<uint16_t>(st);
+        }
+        WSTAMP(15);
+        __syncthreads();
+        STAMP(9);
+        // ---- redo: insert the cluster's new keys in event order.  The cells
+        // still holding padded+1+r' are exactly the ones empty when the next
+        // key is inserted, so key r probes from its home to the first of them
+        // and swaps in; the key it displaces keeps its event number.  One
+        // wave per cluster, a lane per cell (longer clusters: one lane).
+        const int32_t nLead = ms.nLead;
+        for (int32_t li = wave; li < nLead; li += NWAVES) {
+            const int32_t st = lead[li];
+            const int32_t x = (st + static_cast<int32_t>(lane)) & mask;
+            uint32_t e = ht[x];
+            const uint64_t empt = __ballot(e == 0u);
+            if (empt != 0ull) {
+                const int32_t Lc = __builtin_ctzll(empt);  // cluster length
+                bool un = static_cast<int32_t>(lane) < Lc && e > static_cast<uint32_t>(padded);
+                for (int32_t it = 0; it < 64; ++it) {
+                    uint64_t um = __ballot(un);
+                    if (um == 0ull) break;
+                    uint32_t best = 0xFFFFFFFFu;
+                    int32_t cm = 0;
+                    for (; um != 0ull; um &= um - 1ull) {
+                        const int32_t l = __builtin_ctzll(um);
+                        const uint32_t v = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), l));
+                        if (v < best) {
+                            best = v;
+                            cm = l;
+                        }
+                    }
+                    const uint32_t rr = best - static_cast<uint32_t>(padded) - 1u;
+                    const int32_t hl = ((static_cast<int32_t>(ht_hash(ntokv[rr])) & mask) - st) & mask;
+                    const uint32_t fin = (ecell[rr] >> 16) + 1u;
+                    const uint64_t fm = __ballot(un && static_cast<int32_t>(lane) >= hl);
+                    const int32_t f = fm ? __builtin_ctzll(fm) : cm;  // the home lies in the cluster
+                    const uint32_t ef = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), f));
+                    if (static_cast<int32_t>(lane) == cm) e = ef;
+                    if (static_cast<int32_t>(lane) == f) {
+                        e = fin;
+                        un = false;
+                    }
+                }
+                if (static_cast<int32_t>(lane) < Lc) ht[x] = static_cast<uint16_t>(e);
+            } else if (lane == 0) {
+                for (int32_t it = 0; it < H; ++it) {
+                    uint32_t mn = 0xFFFFFFFFu;
+                    int32_t cm = -1;
+                    int32_t y = st;
+                    for (int32_t n = 0; n < H && ht[y] != 0; ++n, y = (y + 1) & mask) {
+                        const uint32_t ey = ht[y];
+                        if (ey > static_cast<uint32_t>(padded) && ey < mn) {
+                            mn = ey;
+                            cm = y;
+                        }
+                    }
+                    if (cm < 0) break;
+                    const uint32_t rr = mn - static_cast<uint32_t>(padded) - 1u;
+                    int32_t f = static_cast<int32_t>(ht_hash(ntokv[rr])) & mask;
+                    for (int32_t n = 0; n < H && ht[f] <= static_cast<uint32_t>(padded); ++n) f = (f + 1) & mask;
+                    ht[cm] = ht[f];
+                    ht[f] = static_cast<uint16_t>((ecell[rr] >> 16) + 1u);
+                }
+            }
+        }
+        if (g.code) atomicOr(&ms.late, 1);
+        __syncthreads();
+    };
     {
         const int32_t nt = padded >> 2, nh = H >> 3, nv = visStrideB >> 4;  // 16-byte chunks
         KVX_G const v4u *sT = (KVX_G const v4u *)gTok;
@@ -642,11 +831,73 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         return;
     }
     // A row whose recent steps all wrapped the hand (the parallel form's
-    // bound) tries the parallel form only every 8th step; the other steps
+    // bound) retries the parallel form after 8, 16, 32 and then every 64
+    // such steps; the other steps
     // run the in-order recurrence on the row as staged (known consistent when
-    // flagged and its entry count matches its live tokens).
-    if (!kC && hintw > 0 && (hintw & 7) != 0) {
-        run_inorder(tok, ht, vis, flagged && ms.diff == 0);
+    // flagged and its entry count matches its live tokens).  Consistent rows
+    // of up to 64 slots take the recurrence's decisions in one wave's
+    // registers and leave the table to the parallel update: the pre-step
+    // token of every evicted slot leaves, the slots' final tokens arrive in
+    // the order of the events that placed them.
+    const bool retry = (hintw >= 8 && __popc(static_cast<uint32_t>(hintw)) == 1) || (hintw & 63) == 0;
+    if (!kC && hintw > 0 && !retry) {
+        const bool canon = flagged && ms.diff == 0;
+        if (!(canon && dbs <= 64)) {
+            run_inorder(tok, ht, vis, canon);
+            return;
+        }
+        if (wave == 0) {
+            int32_t hand = hand0, tokFin = -1, lastEv = -1;
+            uint64_t vmF = 0;
+            const int32_t nev = sieve_row_regs_decide((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen,
+                                                      prefill, dbs, padded, tok, vis, hand, tokFin, lastEv, vmF);
+            const bool alive = lastEv >= 0;
+            uint32_t rank = 0;  // among the slots' final placements, in event order
+            if (nev <= 64) {
+                if (alive) atomicOr(&ms.evMask, 1ull << lastEv);
+                __threadfence_block();
+                rank = static_cast<uint32_t>(__popcll(ms.evMask & ((1ull << (alive ? lastEv : 0)) - 1ull)));
+            } else {
+                for (int32_t l = 0; l < 64; ++l) {
+                    const int32_t x = lane_value(lastEv, l);
+                    rank += (x >= 0 && x < lastEv) ? 1u : 0u;
+                }
+            }
+            if (alive) {
+                ecell[rank] = cell_of(static_cast<int32_t>(lane)) | (lane << 16);  // the pre-step token's cell
+                ntokv[rank] = tokFin;
+            }
+            if (static_cast<int32_t>(lane) < (dbs + 7) / 8) {  // visited bytes of slots [0, dbs)
+                const int32_t b0 = static_cast<int32_t>(lane) * 8;
+                const uint32_t keep = (dbs - b0 >= 8) ? 0u : (0xFFu << (dbs - b0)) & 0xFFu;
+                vis[lane] = static_cast<uint8_t>((vis[lane] & keep) | (static_cast<uint32_t>(vmF >> b0) & 0xFFu & ~keep));
+            }
+            const uint64_t am = __ballot(alive);
+            if (lane == 0) {
+                ms.nEv = __popcll(am);
+                ms.handOut = hand;
+            }
+        }
+        __syncthreads();
+        STAMP(15);
+        const int32_t nAlive = ms.nEv;
+        table_update(nAlive, false);
+        if (!ms.late && !ms.ovf) {
+            wg_copy16((KVX_G v4u *)gVis, reinterpret_cast<const v4u *>(vis), static_cast<uint32_t>(visStrideB));
+            if (nAlive > 0) {
+                wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tok), static_cast<uint32_t>(padded) * 4u);
+                wg_copy16((KVX_G v4u *)gHt, reinterpret_cast<const v4u *>(ht), static_cast<uint32_t>(H) * 2u);
+            }
+            if (tid == 0) {
+                gHand[0] = ms.handOut;
+                gHand[1] = kCanonFlag;
+                gHand[2] = min(hintw, (1 << 30)) + 1;
+            }
+            return;
+        }
+        // a bound violation (only a corrupted table): nothing written back
+        // but the outputs; the exact recurrence on the row restaged from HBM
+        restage_and_run(false);
         return;
     }
 
@@ -1254,8 +1505,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
     if (fast) {
         const int32_t uEnd = ms.uEnd;
-        const int32_t Pn = (N + NT - 1) / NT;
-        Guard g;
         WSTAMP(4);
         // ---- outputs and visited bits set this step (vset); erase the
         // evicted tokens: the rightmost marked cell of each pre-step cluster
@@ -1292,166 +1541,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             rm[k] = miss;
         }
         WSTAMP(7);
-        for (int32_t q = 0; q < Pn; ++q) {
-            const int32_t r = tid + q * NT;
-            if (r >= N) break;
-            const uint32_t ec = ecell[r];
-            const uint32_t s = ec >> 16;
-            atomicOr(vset + (s >> 5), 1u << (s & 31u));
-            const uint32_t c = ec & 0xFFFFu;
-            if (c == NOCELL) continue;
-            bool ld = true;
-            int32_t x = (static_cast<int32_t>(c) + 1) & mask;
-            for (int32_t n = 0; n <= (H >> 5); ++n) {
-                const uint32_t b = static_cast<uint32_t>(x) & 31u, span = 32u - b;
-                const uint32_t o = occ[x >> 5] >> b, eb = ber[x >> 5] >> b;
-                const uint32_t no = ~o;
-                const uint32_t z = no ? static_cast<uint32_t>(__builtin_ctz(no)) : 32u;  // first empty cell
-                const uint32_t below = (z >= 32u) ? 0xFFFFFFFFu : ((1u << z) - 1u);
-                if (eb & below) {
-                    ld = false;
-                    break;
-                }
-                if (z < span) break;
-                x = (x + static_cast<int32_t>(span)) & mask;
-            }
-            if (!ld) continue;
-            // the cluster's marked cells right to left; cells left of a
-            // deletion keep their pre-step contents, so the occupancy
-            // snapshot finds the next marked cell and the cluster's start
-            int32_t y = static_cast<int32_t>(c);
-            for (int32_t n = 0; n <= H; ++n) {
-                rdel_at<kC>(ht, smem + lay.tok, padded, y, mask, g);
-                int32_t nx = -1;
-                int32_t x2 = (y - 1) & mask;  // scan words leftward from x2
-                for (int32_t m = 0; m <= (H >> 5); ++m) {
-                    const uint32_t b = static_cast<uint32_t>(x2) & 31u;
-                    const uint32_t keep = (b == 31u) ? 0xFFFFFFFFu : ((2u << b) - 1u);  // bits 0..b
-                    const uint32_t empt = ~occ[x2 >> 5] & keep, mk = ber[x2 >> 5] & keep;
-                    const int32_t hiE = empt ? 31 - __builtin_clz(empt) : -1;  // cluster start boundary
-                    const uint32_t live = (hiE >= 0) ? (mk & ~((2u << hiE) - 1u)) : mk;
-                    if (live) {
-                        nx = (x2 & ~31) + (31 - __builtin_clz(live));
-                        break;
-                    }
-                    if (hiE >= 0) break;
-                    x2 = ((x2 & ~31) - 1) & mask;
-                }
-                if (nx < 0) break;
-                y = nx;
-            }
-        }
-        WSTAMP(14);
-        __syncthreads();
-        STAMP(7);
-        // ---- new tokens; tentative placement (the final occupied cells do
-        // not depend on order), entries padded+1+r name the event
-        for (int32_t q = 0; q < Pn; ++q) {
-            const int32_t r = tid + q * NT;
-            if (r >= N) break;
-            const uint32_t s = ecell[r] >> 16;
-            const int32_t t = ntokv[r];
-            if constexpr (kC) {
-                hv[s] = static_cast<uint16_t>(ht_hash(t) & static_cast<uint32_t>(mask));
-                gTok[s] = t;
-            } else {
-                tok[s] = t;
-            }
-            const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(t)) & mask, mask,
-                                          static_cast<uint16_t>(padded + 1 + r));
-            if (c < 0) g.code = kOverflowProbe;
-            else ecell[r] = static_cast<uint32_t>(c) | (s << 16);
-        }
-        WSTAMP(12);
-        __syncthreads();
-        STAMP(8);
-        // ---- final cluster of each new key: alone in it, the key takes its
-        // cell; with others, the earliest event redoes the cluster
-        for (int32_t q = 0; q < Pn; ++q) {
-            const int32_t r = tid + q * NT;
-            if (r >= N) break;
-            const uint32_t ec = ecell[r];
-            const int32_t c = static_cast<int32_t>(ec & 0xFFFFu);
-            int32_t st = c;
-            for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
-            uint32_t m = 0, mn = 0xFFFFFFFFu;
-            int32_t x = st;
-            for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
-                const uint32_t e = ht[x];
-                if (e > static_cast<uint32_t>(padded)) {
-                    ++m;
-                    mn = min(mn, e);
-                }
-            }
-            if (m == 1u) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
-            else if (mn == static_cast<uint32_t>(padded + 1 + r)) lead[atomicAdd(&ms.nLead, 1)] = static_cast<uint16_t>(st);
-        }
-        WSTAMP(15);
-        __syncthreads();
-        STAMP(9);
-        // ---- redo: insert the cluster's new keys in event order.  The cells
-        // still holding padded+1+r' are exactly the ones empty when the next
-        // key is inserted, so key r probes from its home to the first of them
-        // and swaps in; the key it displaces keeps its event number.  One
-        // wave per cluster, a lane per cell (longer clusters: one lane).
-        const int32_t nLead = ms.nLead;
-        for (int32_t li = wave; li < nLead; li += NWAVES) {
-            const int32_t st = lead[li];
-            const int32_t x = (st + static_cast<int32_t>(lane)) & mask;
-            uint32_t e = ht[x];
-            const uint64_t empt = __ballot(e == 0u);
-            if (empt != 0ull) {
-                const int32_t Lc = __builtin_ctzll(empt);  // cluster length
-                bool un = static_cast<int32_t>(lane) < Lc && e > static_cast<uint32_t>(padded);
-                for (int32_t it = 0; it < 64; ++it) {
-                    uint64_t um = __ballot(un);
-                    if (um == 0ull) break;
-                    uint32_t best = 0xFFFFFFFFu;
-                    int32_t cm = 0;
-                    for (; um != 0ull; um &= um - 1ull) {
-                        const int32_t l = __builtin_ctzll(um);
-                        const uint32_t v = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), l));
-                        if (v < best) {
-                            best = v;
-                            cm = l;
-                        }
-                    }
-                    const uint32_t rr = best - static_cast<uint32_t>(padded) - 1u;
-                    const int32_t hl = ((static_cast<int32_t>(ht_hash(ntokv[rr])) & mask) - st) & mask;
-                    const uint32_t fin = (ecell[rr] >> 16) + 1u;
-                    const uint64_t fm = __ballot(un && static_cast<int32_t>(lane) >= hl);
-                    const int32_t f = fm ? __builtin_ctzll(fm) : cm;  // the home lies in the cluster
-                    const uint32_t ef = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), f));
-                    if (static_cast<int32_t>(lane) == cm) e = ef;
-                    if (static_cast<int32_t>(lane) == f) {
-                        e = fin;
-                        un = false;
-                    }
-                }
-                if (static_cast<int32_t>(lane) < Lc) ht[x] = static_cast<uint16_t>(e);
-            } else if (lane == 0) {
-                for (int32_t it = 0; it < H; ++it) {
-                    uint32_t mn = 0xFFFFFFFFu;
-                    int32_t cm = -1;
-                    int32_t y = st;
-                    for (int32_t n = 0; n < H && ht[y] != 0; ++n, y = (y + 1) & mask) {
-                        const uint32_t ey = ht[y];
-                        if (ey > static_cast<uint32_t>(padded) && ey < mn) {
-                            mn = ey;
-                            cm = y;
-                        }
-                    }
-                    if (cm < 0) break;
-                    const uint32_t rr = mn - static_cast<uint32_t>(padded) - 1u;
-                    int32_t f = static_cast<int32_t>(ht_hash(ntokv[rr])) & mask;
-                    for (int32_t n = 0; n < H && ht[f] <= static_cast<uint32_t>(padded); ++n) f = (f + 1) & mask;
-                    ht[cm] = ht[f];
-                    ht[f] = static_cast<uint16_t>((ecell[rr] >> 16) + 1u);
-                }
-            }
-        }
-        if (g.code) atomicOr(&ms.late, 1);
-        __syncthreads();
+        table_update(N, true);
         STAMP(10);
         if (!ms.late) {
             // ---- write back; visited = (staged bits minus the ring range the
@@ -1498,15 +1588,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
     // ---- fallback: restage the pre-step row from HBM (nothing has been
     // written back) and run the sequential recurrence on it
-    __syncthreads();
-    int32_t *tokF = reinterpret_cast<int32_t *>(smem);
-    uint16_t *htF = reinterpret_cast<uint16_t *>(smem + static_cast<size_t>(padded) * 4u);
-    uint8_t *visF = smem + static_cast<size_t>(padded) * 4u + static_cast<size_t>(H) * 2u;
-    wg_copy16(reinterpret_cast<v4u *>(tokF), (KVX_G const v4u *)gTok, static_cast<uint32_t>(padded) * 4u);
-    wg_copy16(reinterpret_cast<v4u *>(htF), (KVX_G const v4u *)gHt, static_cast<uint32_t>(H) * 2u);
-    wg_copy16(reinterpret_cast<v4u *>(visF), (KVX_G const v4u *)gVis, static_cast<uint32_t>(visStrideB));
-    __syncthreads();
-    run_inorder(tokF, htF, visF, canonical);
+    restage_and_run(canonical);
 }
 
 }  // namespace

@@ -375,9 +375,9 @@ def test_sieve_sequential_lds_wave_path(kvops):
 @pytest.mark.parametrize("dbs,K,prefill", [(64, 64, 256), (37, 100, 300), (16, 48, 12), (64, 200, 90)])
 def test_sieve_small_rows_inorder_paths(kvops, dbs, K, prefill):
     """Rows of up to 64 slots whose steps wrap the hand: after a wrap the row
-    runs the in-order recurrence in registers, skipping the parallel form for
-    seven steps and retrying it on the eighth; a row whose consistency flag
-    was cleared takes the one-lane recurrence.  Full state after every step
+    takes the in-order decisions in registers and the parallel table update,
+    retrying the parallel form after 8 and 16 wrapping steps; a row whose
+    consistency flag was cleared takes the one-lane recurrence.  Full state after every step
     (partial visited bytes, empty slots, duplicates, invalid positions)."""
     rng = np.random.default_rng(dbs * 1000 + K)
     req = 4
@@ -385,7 +385,7 @@ def test_sieve_small_rows_inorder_paths(kvops, dbs, K, prefill):
     for r in range(req):
         st.admit(r, prefill)
     dev = DevSieve(st)
-    for step in range(20):
+    for step in range(24):
         if step == 12:
             dev.hand[0, 1, 1] = 0  # row 1 no longer known consistent: checked again, one-lane path meanwhile
         if step == 14:
