@@ -101,15 +101,7 @@ __device__ unsigned long long kvx_dbg_sub[1024][16];
     do {                                                              \
         if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = clock64();  \
     } while (0)
-__device__ unsigned long long kvx_dbg_w[64][16][16];
-#define WSTAMP(i)                                                          \
-    do {                                                                   \
-        if (lane == 0 && bid < 64) kvx_dbg_w[bid][wave][i] = clock64();    \
-    } while (0)
 #else
-#define WSTAMP(i) \
-    do {          \
-    } while (0)
 #define STAMP(i) \
     do {         \
     } while (0)
@@ -349,7 +341,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                  "s"(a.deviceBufferTokens), "s"(a.deviceBufferVisited), "s"(a.deviceBufferHt), "s"(a.sieveHand),
                  "s"(a.topKDeviceSlots), "s"(a.isMiss), "s"(a.numReal));
 
-    WSTAMP(8);
     int32_t numReal = *(KVX_C const int32_t *)(a.numReal);
     if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
     KVX_G int32_t *rs = (KVX_G int32_t *)(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
@@ -358,7 +349,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
-    WSTAMP(9);
     // the batch row's request, length and topK row in one round trip.  An
     // invalid request index is acted on after staging (row 0, which exists,
     // is staged meanwhile): an early exit here would let the compiler sink
@@ -372,7 +362,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const int32_t t0 = rt[min(tid, K - 1)], t1 = rt[min(tid + NT, K - 1)];
     const bool badReq = reqRaw < 0 || reqRaw >= poolSize;
     const int64_t reqIdx = badReq ? 0 : reqRaw;
-    WSTAMP(10);
     // direct token -> slot map over the tokens that can be looked up (below
     // both prefill and seqLen) when they fit the LDS left over after the
     // layout: 0, slot+1 of the slot holding the token, or padded+1+k for a
@@ -599,7 +588,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 y = nx;
             }
         }
-        WSTAMP(14);
         __syncthreads();
         STAMP(7);
         // ---- new tokens; tentative placement (the final occupied cells do
@@ -620,7 +608,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (c < 0) g.code = kOverflowProbe;
             else ecell[r] = static_cast<uint32_t>(c) | (s << 16);
         }
-        WSTAMP(12);
         __syncthreads();
         STAMP(8);
         // ---- final cluster of each new key: alone in it, the key takes its
@@ -644,7 +631,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (m == 1u) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
             else if (mn == static_cast<uint32_t>(padded + 1 + r)) lead[atomicAdd(&ms.nLead, 1)] = static_cast<uint16_t>(st);
         }
-        WSTAMP(15);
         __syncthreads();
         STAMP(9);
         // ---- redo: insert the cluster's new keys in event order.  The cells
@@ -805,7 +791,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         stage_pass(0);
         if (hand0 < 0 || hand0 >= dbs) hand0 = 0;  // hisp_sieve_update.cpp:108-111
         for (int32_t p = 1; 2 * NT * p < nt || 4 * NT * p < nh || NT * p < nv; ++p) stage_pass(p);
-        WSTAMP(11);
         if (h0) ptok[tid] = t0;
         if (h1) ptok[tid + NT] = t1;
         for (int32_t k = tid + 2 * NT; k < K; k += NT) ptok[k] = rt[k];
@@ -823,7 +808,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if (lane == 0 && dw != 0) atomicAdd(&ms.diff, dw);
     }
     __syncthreads();
-    WSTAMP(13);
     STAMP(1);
     const bool flagged = flagw == kCanonFlag;
     if (badReq) {  // hisp_sieve_update.cpp:80-87: the row gets the dummy outputs, the state is untouched
@@ -1171,7 +1155,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // on D_i): evicted.  The rest (rare) are settled in ring order.
     int32_t nSM = 0;
     if (fast) {
-        WSTAMP(0);
         nSM = ms.nSM;
         int32_t G = 1;  // lanes per SM slot for the U count
         while (G < 16 && 2 * G * nSM <= NT) G <<= 1;
@@ -1233,7 +1216,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             if (part == 0) tb[i] = dec;
         }
-        WSTAMP(1);
         const int32_t nSNev = static_cast<int32_t>(min(M, snP.total));
         if (nSM <= 4 * 64) {
             // short list: the last wave to finish the first pass settles the
@@ -1260,7 +1242,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     undq[c] = __ballot(t == 2u);
                 }
                 if ((undq[0] | undq[1] | undq[2] | undq[3]) != 0ull) {
-                    WSTAMP(3);
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         for (uint64_t und = undq[c]; und != 0ull; und &= und - 1ull) {
@@ -1299,12 +1280,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     vt[sl] = static_cast<uint16_t>(cell_of(sl));
                 }
             }
-            WSTAMP(5);
             __syncthreads();
-            WSTAMP(6);
         } else {
         __syncthreads();
-        WSTAMP(2);
         // undecided slots, one wave each: count the evictions already settled
         // before them (L) and the undecided ones before them with a larger k
         // (X); with X == 0, D = L exactly.  A concurrent settle of j < i reads
@@ -1345,7 +1323,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         ms.ui[rank] = static_cast<uint16_t>(i);
                     }
                 }
-                WSTAMP(3);
                 int32_t old = 0;
                 if (lane == 0) {
                     __threadfence_block();
@@ -1505,7 +1482,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
     if (fast) {
         const int32_t uEnd = ms.uEnd;
-        WSTAMP(4);
         // ---- outputs and visited bits set this step (vset); erase the
         // evicted tokens: the rightmost marked cell of each pre-step cluster
         // (from the occupancy snapshot) leads it and deletes right to left
@@ -1540,7 +1516,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             rs[k] = slot;
             rm[k] = miss;
         }
-        WSTAMP(7);
         table_update(N, true);
         STAMP(10);
         if (!ms.late) {
@@ -1643,19 +1618,6 @@ extern "C" int kvx_dbg_read_sub(unsigned long long *out, int rows)
 {
     if (rows > 1024) rows = 1024;
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(kvx::kvx_dbg_sub), sizeof(unsigned long long) * 16 * rows, 0,
-                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
-}
-
-extern "C" int kvx_dbg_clear_w()
-{
-    void *p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(kvx::kvx_dbg_w)) != hipSuccess) return -1;
-    return hipMemset(p, 0, sizeof(unsigned long long) * 64 * 16 * 16) == hipSuccess ? 0 : -1;
-}
-
-extern "C" int kvx_dbg_read_w(unsigned long long *out)
-{
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(kvx::kvx_dbg_w), sizeof(unsigned long long) * 64 * 16 * 16, 0,
                                hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
 }
 
