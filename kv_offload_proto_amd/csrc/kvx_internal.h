@@ -61,8 +61,8 @@ struct RowScratch {
 constexpr int kFastThreads = KVX_FAST_THREADS;
 
 struct FastLayout {
-    uint32_t tok, ht, vis, ptok, pinf, vt, evslot, smKp, eseq, tb, smA, smB, vset, ber, occ, cmask, emask, smask,
-        rsn, rsm, total;
+    uint32_t tok, ht, vis, ptok, pinf, vt, evslot, smKp, eseq, tb, smA, smB, vset, ber, occ, fin, nkb, cmask, emask,
+        smask, rsn, rsm, total;
 };
 
 __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
@@ -74,7 +74,9 @@ __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 1
 // In the compact form (rows whose full layout does not fit) the tokens row is
 // replaced by the Knuth hash of each slot's token (full tokens stay in HBM).
 // cmask/emask/smask/rsn/rsm hold one 64-bit ballot per (wave, block of one
-// entry per lane).
+// entry per lane).  ber, occ, fin and nkb are one bit per table cell: cells
+// of evicted tokens, the pre-step occupancy, the occupancy as the erase and
+// insert phases change it, and the cells new keys claim.
 __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint32_t htSize, uint32_t topK,
                                                            uint32_t visStrideB, bool compact = false)
 {
@@ -104,6 +106,8 @@ __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint
     const uint32_t ringMaskBytes = (padded + kFastThreads - 1u) / kFastThreads * (kFastThreads / 64u) * 8u;
     l.rsn = o;     o += ringMaskBytes;
     l.rsm = o;     o += ringMaskBytes;
+    l.fin = o;     o += align16(bmBytes);
+    l.nkb = o;     o += align16(bmBytes);
     l.total = o;
     return l;
 }
@@ -151,6 +155,15 @@ __host__ __device__ __forceinline__ FastLayout fast_layout_fixed(uint32_t padded
     l.vis = o;     o += align16(visStrideB);
     l.ber = o;     o += align16(htSize / 8u);
     l.occ = o;     o += align16(htSize / 8u);
+    // the two table bitmaps of the insert phases take the per-position
+    // classes' region, which the fixed kernels keep in registers instead
+    if (2u * align16(htSize / 8u) <= Kx * 4u) {
+        l.fin = l.pinf;
+        l.nkb = l.pinf + align16(htSize / 8u);
+    } else {
+        l.fin = o;  o += align16(htSize / 8u);
+        l.nkb = o;  o += align16(htSize / 8u);
+    }
     l.total = o;
     return l;
 }

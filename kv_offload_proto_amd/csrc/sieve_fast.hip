@@ -101,12 +101,19 @@ __device__ unsigned long long kvx_dbg_sub[1024][16];
     do {                                                              \
         if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = clock64();  \
     } while (0)
+#define DBGVAL(i, v)                                                  \
+    do {                                                              \
+        if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = (v);        \
+    } while (0)
 #else
 #define STAMP(i) \
     do {         \
     } while (0)
 #define SUBSTAMP(i) \
     do {            \
+    } while (0)
+#define DBGVAL(i, v) \
+    do {             \
     } while (0)
 #endif
 
@@ -236,29 +243,29 @@ __device__ __forceinline__ void lds_min16(uint32_t *w32, uint32_t i, uint16_t v)
     }
 }
 
-// Claim the first empty cell at or after `idx` with value v (16-bit cells,
-// CAS on words).  Returns the cell, or -1 after a whole-table probe.
-__device__ __forceinline__ int32_t lds_claim16(uint32_t *w32, int32_t idx, int32_t mask, uint16_t v)
+// Claim the first free cell at or after `idx` in an occupancy bitmap (one
+// bit per cell) with an atomic OR per try; a failed try moves to the next
+// free cell the returned word shows.  Bits are only set while claims run, so
+// every cell from idx to the one returned was occupied when passed.  Returns
+// the cell, or -1 after a whole-table probe.
+__device__ __forceinline__ int32_t lds_claim_bit(uint32_t *bm, int32_t idx, int32_t mask)
 {
     for (int32_t n = 0; n <= mask; ++n) {
-        uint32_t *w = w32 + (idx >> 1);
-        const uint32_t sh = (static_cast<uint32_t>(idx) & 1u) * 16u;
-        uint32_t old = *w;
-        for (;;) {
-            if (((old >> sh) & 0xFFFFu) != 0u) break;
-            const uint32_t prev = atomicCAS(w, old, old | (static_cast<uint32_t>(v) << sh));
-            if (prev == old) return idx;
-            old = prev;
-        }
-        idx = (idx + 1) & mask;
+        const uint32_t b = static_cast<uint32_t>(idx) & 31u, bit = 1u << b;
+        const uint32_t old = atomicOr(bm + (idx >> 5), bit);
+        if (!(old & bit)) return idx;
+        const uint32_t fr = ~old & (0xFFFFFFFEu << b);  // free cells above b in the word
+        idx = fr ? ((idx & ~31) | __builtin_ctz(fr)) : (((idx | 31) + 1) & mask);
     }
     return -1;
 }
 
 // Algorithm R deletion of the entry at cell c (homes from the tokens row, or
-// from the per-slot token hashes in the compact form).
+// from the per-slot token hashes in the compact form); the cell left empty is
+// cleared in the occupancy bitmap fin.
 template <bool kC>
-__device__ void rdel_at(uint16_t *ht, const void *tokv, int32_t ntok, int32_t c, int32_t mask, Guard &g)
+__device__ void rdel_at(uint16_t *ht, uint32_t *fin, const void *tokv, int32_t ntok, int32_t c, int32_t mask,
+                        Guard &g)
 {
     int32_t j = c, i = c;
     for (int32_t n = 0;; ++n) {
@@ -283,6 +290,7 @@ __device__ void rdel_at(uint16_t *ht, const void *tokv, int32_t ntok, int32_t c,
         }
     }
     ht[j] = 0;
+    atomicAnd(fin + (j >> 5), ~(1u << (j & 31)));
 }
 
 // Copy n bytes (multiple of 16) with the workgroup, four 16-byte chunks in
@@ -413,6 +421,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *ber = reinterpret_cast<uint32_t *>(smem + lay.ber);   // cells of evicted tokens
     uint32_t *occ = reinterpret_cast<uint32_t *>(smem + lay.occ);   // occupied cells of the pre-step table
     uint8_t *occ8 = smem + lay.occ;
+    uint32_t *fin = reinterpret_cast<uint32_t *>(smem + lay.fin);   // occupied cells as erase and claims change them
+    uint8_t *fin8 = smem + lay.fin;
+    uint32_t *nkb = reinterpret_cast<uint32_t *>(smem + lay.nkb);   // cells claimed by new keys
     uint64_t *cmask = reinterpret_cast<uint64_t *>(smem + lay.cmask);  // first occurrences of candidates
     uint64_t *emask = reinterpret_cast<uint64_t *>(smem + lay.emask);  // conversion positions
     uint64_t *smask = reinterpret_cast<uint64_t *>(smem + lay.smask);  // evicted SM slots
@@ -539,10 +550,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     auto table_update = [&](int32_t Nev, bool setVset) {
         const int32_t Pn = (Nev + NT - 1) / NT;
         Guard g;
+        uint32_t ecR = 0;  // ecell of the lane's first event, carried across the phases
         for (int32_t q = 0; q < Pn; ++q) {
             const int32_t r = tid + q * NT;
             if (r >= Nev) break;
             const uint32_t ec = ecell[r];
+            if (q == 0) ecR = ec;
             const uint32_t s = ec >> 16;
             if (setVset) atomicOr(vset + (s >> 5), 1u << (s & 31u));
             const uint32_t c = ec & 0xFFFFu;
@@ -568,7 +581,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             // snapshot finds the next marked cell and the cluster's start
             int32_t y = static_cast<int32_t>(c);
             for (int32_t n = 0; n <= H; ++n) {
-                rdel_at<kC>(ht, smem + lay.tok, padded, y, mask, g);
+                rdel_at<kC>(ht, fin, smem + lay.tok, padded, y, mask, g);
                 int32_t nx = -1;
                 int32_t x2 = (y - 1) & mask;  // scan words leftward from x2
                 for (int32_t m = 0; m <= (H >> 5); ++m) {
@@ -595,7 +608,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         for (int32_t q = 0; q < Pn; ++q) {
             const int32_t r = tid + q * NT;
             if (r >= Nev) break;
-            const uint32_t s = ecell[r] >> 16;
+            const uint32_t s = ((q == 0) ? ecR : ecell[r]) >> 16;
             const int32_t t = ntokv[r];
             if constexpr (kC) {
                 hv[s] = static_cast<uint16_t>(ht_hash(t) & static_cast<uint32_t>(mask));
@@ -603,34 +616,88 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             } else {
                 tok[s] = t;
             }
-            const int32_t c = lds_claim16(ht32, static_cast<int32_t>(ht_hash(t)) & mask, mask,
-                                          static_cast<uint16_t>(padded + 1 + r));
-            if (c < 0) g.code = kOverflowProbe;
-            else ecell[r] = static_cast<uint32_t>(c) | (s << 16);
+            const int32_t c = lds_claim_bit(fin, static_cast<int32_t>(ht_hash(t)) & mask, mask);
+            if (c < 0) {
+                g.code = kOverflowProbe;
+                continue;
+            }
+            ht[c] = static_cast<uint16_t>(padded + 1 + r);
+            atomicOr(nkb + (c >> 5), 1u << (c & 31));
+            ecell[r] = static_cast<uint32_t>(c) | (s << 16);
+            if (q == 0) ecR = static_cast<uint32_t>(c) | (s << 16);
         }
         __syncthreads();
         STAMP(8);
-        // ---- final cluster of each new key: alone in it, the key takes its
-        // cell; with others, the earliest event redoes the cluster
+        // ---- final cluster of each new key, from the bitmaps: the leftmost
+        // new key of a cluster leads it; alone, the key takes its cell, with
+        // others the leader queues the cluster's start for the redo
+        const int32_t wmask = (H >> 5) - 1;
         for (int32_t q = 0; q < Pn; ++q) {
             const int32_t r = tid + q * NT;
             if (r >= Nev) break;
-            const uint32_t ec = ecell[r];
-            const int32_t c = static_cast<int32_t>(ec & 0xFFFFu);
-            int32_t st = c;
-            for (int32_t n = 0; n < H && ht[(st - 1) & mask] != 0; ++n) st = (st - 1) & mask;
-            uint32_t m = 0, mn = 0xFFFFFFFFu;
-            int32_t x = st;
-            for (int32_t n = 0; n < H && ht[x] != 0; ++n, x = (x + 1) & mask) {
-                const uint32_t e = ht[x];
-                if (e > static_cast<uint32_t>(padded)) {
-                    ++m;
-                    mn = min(mn, e);
+            const uint32_t ec = (q == 0) ? ecR : ecell[r];
+            const int32_t c = static_cast<int32_t>(ec & 0xFFFFu) & mask;  // in range even after a failed claim
+            // the bitmap words either side of c, read together
+            const int32_t wl = ((c - 1) & mask) >> 5, wr = ((c + 1) & mask) >> 5;
+            const uint32_t fL = fin[wl], nL = nkb[wl], fR = fin[wr], nR = nkb[wr];
+            asm volatile("" : : "v"(fL), "v"(nL), "v"(fR), "v"(nR));
+            // leftwards from c - 1 to the cluster's start: a new key on the
+            // way leads instead
+            int32_t st = -1;
+            bool leads = true;
+            {
+                int32_t w = wl;
+                uint32_t keep = (2u << ((c - 1) & 31)) - 1u, fw = fL, nw0 = nL;  // bits 0..(c-1)&31
+                for (int32_t n = 0; n <= wmask; ++n) {
+                    if (n > 0) {
+                        fw = fin[w];
+                        nw0 = nkb[w];
+                    }
+                    const uint32_t empt = ~fw & keep, nw = nw0 & keep;
+                    const int32_t hiE = empt ? 31 - __builtin_clz(empt) : -1;
+                    const uint32_t after = (hiE >= 0) ? (nw & ~((2u << hiE) - 1u)) : nw;
+                    if (after) {
+                        leads = false;
+                        break;
+                    }
+                    if (hiE >= 0) {
+                        st = ((w << 5) + hiE + 1) & mask;
+                        break;
+                    }
+                    w = (w - 1) & wmask;
+                    keep = 0xFFFFFFFFu;
                 }
             }
-            if (m == 1u) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
-            else if (mn == static_cast<uint32_t>(padded + 1 + r)) lead[atomicAdd(&ms.nLead, 1)] = static_cast<uint16_t>(st);
+            if (!leads) continue;
+            if (st < 0) {
+                g.code = kOverflowProbe;
+                continue;
+            }
+            // rightwards from c + 1 to the cluster's end: another new key
+            bool alone = true;
+            {
+                int32_t w = wr;
+                uint32_t sel = 0xFFFFFFFFu << ((c + 1) & 31), fw = fR, nw = nR;
+                for (int32_t n = 0; n <= wmask; ++n) {
+                    if (n > 0) {
+                        fw = fin[w];
+                        nw = nkb[w];
+                    }
+                    const uint32_t empt = ~fw & sel;
+                    const uint32_t before = empt ? ((1u << __builtin_ctz(empt)) - 1u) : 0xFFFFFFFFu;
+                    if (nw & sel & before) {
+                        alone = false;
+                        break;
+                    }
+                    if (empt) break;
+                    w = (w + 1) & wmask;
+                    sel = 0xFFFFFFFFu;
+                }
+            }
+            if (alone) ht[c] = static_cast<uint16_t>((ec >> 16) + 1u);
+            else lead[atomicAdd(&ms.nLead, 1)] = static_cast<uint16_t>(st);
         }
+        if (g.code) atomicOr(&ms.late, 1);
         __syncthreads();
         STAMP(9);
         // ---- redo: insert the cluster's new keys in event order.  The cells
@@ -639,14 +706,47 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         // and swaps in; the key it displaces keeps its event number.  One
         // wave per cluster, a lane per cell (longer clusters: one lane).
         const int32_t nLead = ms.nLead;
+        const int32_t st0 = lead[wave];  // read with nLead; used only when wave < nLead
+        DBGVAL(0, nLead);
+        DBGVAL(1, Nev);
+        SUBSTAMP(2);
+        if (nLead == 0) return;
         for (int32_t li = wave; li < nLead; li += NWAVES) {
-            const int32_t st = lead[li];
+            const int32_t st = (li == wave) ? st0 : lead[li];
             const int32_t x = (st + static_cast<int32_t>(lane)) & mask;
             uint32_t e = ht[x];
             const uint64_t empt = __ballot(e == 0u);
+            if (li == 0) SUBSTAMP(4);
             if (empt != 0ull) {
                 const int32_t Lc = __builtin_ctzll(empt);  // cluster length
                 bool un = static_cast<int32_t>(lane) < Lc && e > static_cast<uint32_t>(padded);
+                // each unprocessed key's home (offset from st) and final
+                // entry, read once; they move with the key when it is displaced
+                int32_t hoff = 0;
+                uint32_t fe = 0;
+                if (un) {
+                    const uint32_t rr = e - static_cast<uint32_t>(padded) - 1u;
+                    hoff = ((static_cast<int32_t>(ht_hash(ntokv[rr])) & mask) - st) & mask;
+                    fe = (ecell[rr] >> 16) + 1u;
+                }
+                if (li == 0) SUBSTAMP(5);
+                const uint64_t um0 = __ballot(un);
+                if (__popcll(um0) == 2) {
+                    // two keys at a < b: the earlier event's key takes the
+                    // first of them at or after its home, the other the rest
+                    const int32_t a = __builtin_ctzll(um0), b = 63 - __builtin_clzll(um0);
+                    const uint32_t ea = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), a));
+                    const uint32_t eb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), b));
+                    const uint32_t fa = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(fe), a));
+                    const uint32_t fb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(fe), b));
+                    const int32_t x0 = (ea < eb) ? a : b;
+                    const int32_t hX = __builtin_amdgcn_readlane(hoff, x0);
+                    const int32_t f = (hX <= a) ? a : (hX <= b) ? b : x0;
+                    const uint32_t fX = (x0 == a) ? fa : fb, fY = (x0 == a) ? fb : fa;
+                    if (static_cast<int32_t>(lane) == a) e = (f == a) ? fX : fY;
+                    if (static_cast<int32_t>(lane) == b) e = (f == b) ? fX : fY;
+                    un = false;
+                }
                 for (int32_t it = 0; it < 64; ++it) {
                     uint64_t um = __ballot(un);
                     if (um == 0ull) break;
@@ -660,18 +760,24 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                             cm = l;
                         }
                     }
-                    const uint32_t rr = best - static_cast<uint32_t>(padded) - 1u;
-                    const int32_t hl = ((static_cast<int32_t>(ht_hash(ntokv[rr])) & mask) - st) & mask;
-                    const uint32_t fin = (ecell[rr] >> 16) + 1u;
+                    const int32_t hl = __builtin_amdgcn_readlane(hoff, cm);
+                    const uint32_t fv = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(fe), cm));
                     const uint64_t fm = __ballot(un && static_cast<int32_t>(lane) >= hl);
                     const int32_t f = fm ? __builtin_ctzll(fm) : cm;  // the home lies in the cluster
                     const uint32_t ef = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), f));
-                    if (static_cast<int32_t>(lane) == cm) e = ef;
+                    const int32_t hf = __builtin_amdgcn_readlane(hoff, f);
+                    const uint32_t ff = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(fe), f));
+                    if (static_cast<int32_t>(lane) == cm) {
+                        e = ef;
+                        hoff = hf;
+                        fe = ff;
+                    }
                     if (static_cast<int32_t>(lane) == f) {
-                        e = fin;
+                        e = fv;
                         un = false;
                     }
                 }
+                if (li == 0) SUBSTAMP(6);
                 if (static_cast<int32_t>(lane) < Lc) ht[x] = static_cast<uint16_t>(e);
             } else if (lane == 0) {
                 for (int32_t it = 0; it < H; ++it) {
@@ -694,6 +800,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
             }
         }
+        SUBSTAMP(3);
         if (g.code) atomicOr(&ms.late, 1);
         __syncthreads();
     };
@@ -783,6 +890,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     const uint32_t xo = m4[0] | (m4[1] << 2) | (m4[2] << 4) | (m4[3] << 6);
                     const uint32_t ob = (xo | (xo >> 15)) & 0xFFu;
                     occ8[c] = static_cast<uint8_t>(ob);
+                    fin8[c] = static_cast<uint8_t>(ob);
                     nEnt += static_cast<uint32_t>(__popc(ob));
                 }
             }
@@ -802,7 +910,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         for (int32_t i = tid; i < vsetWords; i += NT) vset[i] = 0u;
-        for (int32_t i = tid; i < (H >> 5); i += NT) ber[i] = 0u;
+        for (int32_t i = tid; i < (H >> 5); i += NT) {
+            ber[i] = 0u;
+            nkb[i] = 0u;
+        }
         for (int32_t i = tid; i < 2 * P * NWAVES; i += NT) emask[i] = 0ull;  // emask, smask (adjacent)
         const int32_t dw = static_cast<int32_t>(wave_sum(nTok)) - static_cast<int32_t>(wave_sum(nEnt));
         if (lane == 0 && dw != 0) atomicAdd(&ms.diff, dw);
@@ -972,8 +1083,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         old = prev;
                     }
                 }
-                pinf[k] = inf[b];
                 if constexpr (kFixed) iR[b] = inf[b];
+                else pinf[k] = inf[b];
             }
         }
         __syncthreads();
@@ -1037,8 +1148,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     inf = CLS_INV << 30;
                 }
             }
-            pinf[k] = inf;
             if constexpr (kFixed) iR[q] = inf;
+            else pinf[k] = inf;
         }
         if (g.code) atomicOr(&ms.ovf, 1);
         __syncthreads();
@@ -1053,8 +1164,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if ((inf >> 30) != CLS_CAND) continue;
                 const uint32_t e = ht[pcell[k]];
                 const uint32_t ni = (CLS_CAND << 30) | (e - static_cast<uint32_t>(padded) - 1u);
-                pinf[k] = ni;
                 if constexpr (kFixed) iR[q] = ni;
+                else pinf[k] = ni;
             }
             __syncthreads();
         }
@@ -1080,8 +1191,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     if (direct) {
                         const int32_t t = kFixed ? tR[kFixed ? q : 0] : ptok[k];
                         k1 = static_cast<uint32_t>(inv[t]) - static_cast<uint32_t>(padded) - 1u;
-                        pinf[k] = (CLS_CAND << 30) | k1;
                         if constexpr (kFixed) iR[q] = (CLS_CAND << 30) | k1;
+                        else pinf[k] = (CLS_CAND << 30) | k1;
                     } else {
                         k1 = inf & 0xFFFFu;
                     }
