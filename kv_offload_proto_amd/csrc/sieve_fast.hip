@@ -89,7 +89,10 @@ constexpr uint32_t NOCELL = 0xFFFFu;   // evicted slot without a table entry
 constexpr int32_t kCanonFlag = 0x4B565843;
 
 // Phase timestamps for profiling builds (-DKVX_SIEVE_PHASE_STAMPS): thread 0
-// of each workgroup records clock64() at phase boundaries into kvx_dbg_stamps.
+// of each workgroup records clock64() at phase boundaries into kvx_dbg_stamps,
+// and into kvx_dbg_sub the constant-rate clock at entry [12] and exit [13],
+// clock64() at entry [14] and the wave's HW_ID [10] and XCC_ID [11] (the
+// shader clocks of different XCDs are not aligned; the constant-rate one is).
 #ifdef KVX_SIEVE_PHASE_STAMPS
 __device__ unsigned long long kvx_dbg_stamps[1024][16];
 #define STAMP(i)                                                        \
@@ -97,10 +100,6 @@ __device__ unsigned long long kvx_dbg_stamps[1024][16];
         if (tid == 0 && bid < 1024) kvx_dbg_stamps[bid][i] = clock64(); \
     } while (0)
 __device__ unsigned long long kvx_dbg_sub[1024][16];
-#define SUBSTAMP(i)                                                   \
-    do {                                                              \
-        if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = clock64();  \
-    } while (0)
 #define DBGVAL(i, v)                                                  \
     do {                                                              \
         if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = (v);        \
@@ -108,9 +107,6 @@ __device__ unsigned long long kvx_dbg_sub[1024][16];
 #else
 #define STAMP(i) \
     do {         \
-    } while (0)
-#define SUBSTAMP(i) \
-    do {            \
     } while (0)
 #define DBGVAL(i, v) \
     do {             \
@@ -342,6 +338,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const int32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    DBGVAL(12, __builtin_amdgcn_s_memrealtime());
+    DBGVAL(14, clock64());
+    DBGVAL(10, __builtin_amdgcn_s_getreg((31 << 11) | 4));   // HW_ID
+    DBGVAL(11, __builtin_amdgcn_s_getreg((15 << 11) | 20));  // XCC_ID
     // (the grid is exactly maxNumReqs workgroups.)  The pointers are loaded
     // from the arguments in one batch, ahead of the first branch: fetched on
     // demand they would each cost a round trip.
@@ -707,16 +707,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         // wave per cluster, a lane per cell (longer clusters: one lane).
         const int32_t nLead = ms.nLead;
         const int32_t st0 = lead[wave];  // read with nLead; used only when wave < nLead
-        DBGVAL(0, nLead);
-        DBGVAL(1, Nev);
-        SUBSTAMP(2);
         if (nLead == 0) return;
         for (int32_t li = wave; li < nLead; li += NWAVES) {
             const int32_t st = (li == wave) ? st0 : lead[li];
             const int32_t x = (st + static_cast<int32_t>(lane)) & mask;
             uint32_t e = ht[x];
             const uint64_t empt = __ballot(e == 0u);
-            if (li == 0) SUBSTAMP(4);
             if (empt != 0ull) {
                 const int32_t Lc = __builtin_ctzll(empt);  // cluster length
                 bool un = static_cast<int32_t>(lane) < Lc && e > static_cast<uint32_t>(padded);
@@ -729,7 +725,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     hoff = ((static_cast<int32_t>(ht_hash(ntokv[rr])) & mask) - st) & mask;
                     fe = (ecell[rr] >> 16) + 1u;
                 }
-                if (li == 0) SUBSTAMP(5);
                 const uint64_t um0 = __ballot(un);
                 if (__popcll(um0) == 2) {
                     // two keys at a < b: the earlier event's key takes the
@@ -777,7 +772,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         un = false;
                     }
                 }
-                if (li == 0) SUBSTAMP(6);
                 if (static_cast<int32_t>(lane) < Lc) ht[x] = static_cast<uint16_t>(e);
             } else if (lane == 0) {
                 for (int32_t it = 0; it < H; ++it) {
@@ -800,7 +794,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
             }
         }
-        SUBSTAMP(3);
         if (g.code) atomicOr(&ms.late, 1);
         __syncthreads();
     };
@@ -1661,6 +1654,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if (hintw != 0) gHand[2] = 0;
             }
             STAMP(11);
+            DBGVAL(13, __builtin_amdgcn_s_memrealtime());
             return;
         }
         if constexpr (kC) {
