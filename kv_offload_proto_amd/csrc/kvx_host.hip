@@ -37,7 +37,6 @@ struct State {
     kvx::RowScratch scratch{};
     int32_t *shadow = nullptr;      // wave-wide SIEVE variant: table shadow
     uint64_t shadowCells = 0;
-    uint32_t epoch = 0;
     int lastSieveVariant = -1;
     int forcedSieveVariant = -1;
 };
@@ -118,8 +117,7 @@ void EnsureWinScratch(uint64_t entries)
     hipCheck(hipMalloc(&p, cap * sizeof(unsigned long long)), "hipMalloc(gather scratch)");
     hipCheck(hipMemset(p, 0, cap * sizeof(unsigned long long)), "hipMemset(gather scratch)");
     g.scratch.win = static_cast<unsigned long long *>(p);
-    g.scratch.winEntries = cap;
-    g.epoch = 0;
+    g.scratch.winEntries = cap;  // a zeroed table is valid under any epoch
 }
 
 // Grow-only shadow table (one int32 per hash-table cell per batch row) of the
@@ -156,16 +154,6 @@ void EnsureListScratch(uint64_t entries)
     g.scratch.listSrc = static_cast<uint64_t *>(p);
     g.scratch.listDst = g.scratch.listSrc + cap;
     g.scratch.listCap = cap;
-}
-
-uint32_t NextEpoch(hipStream_t stream)
-{
-    if (++g.epoch == 0) {  // tags of 2^32 calls ago could alias: clear and restart
-        hipCheck(hipMemsetAsync(g.scratch.win, 0, g.scratch.winEntries * sizeof(unsigned long long), stream),
-                 "hipMemsetAsync(gather scratch)");
-        g.epoch = 1;
-    }
-    return g.epoch;
 }
 
 struct GatherCall {
@@ -228,7 +216,6 @@ void DoGather(const GatherCall &c)
     EnsureWinScratch(need);
     EnsureListScratch(positions);
     hipStream_t st = AsStream(c.stream);
-    plan.epoch = NextEpoch(st);
     if (c.fused) {
         for (uint32_t s = 0; s < c.nodeNum; ++s) ClearStatusWords(c.status, s, bd);
     } else {
@@ -269,6 +256,7 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         g.scratch.errs = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + kTable);
         g.scratch.tickets = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + 2 * kTable);
         g.scratch.listCount = g.scratch.tickets + 8;
+        g.scratch.epoch = g.scratch.tickets + 9;
         g.inited = true;
     });
 }
@@ -604,7 +592,6 @@ int kvx_close(void)
             for (const Alloc &a : g.status) (void)hipHostFree(reinterpret_cast<void *>(a.addr));
             g.status.clear();
         }
-        g.epoch = 0;
         g.inited = false;
     });
 }

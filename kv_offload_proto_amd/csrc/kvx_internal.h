@@ -45,6 +45,7 @@ struct RowScratch {
     uint32_t *counters;        // [64 nodes][8 status words] queued counts
     uint32_t *errs;            // [64 nodes][8 status words] first error code
     uint32_t *tickets;         // [4] last-block tickets (gather, export)
+    uint32_t *epoch;           // gather winner-tag epoch, advanced on the device by each call
     uint64_t *listSrc;         // gather row list: source byte addresses
     uint64_t *listDst;         // gather row list: destination byte addresses
     uint64_t listCap;          // capacity of the row list
@@ -196,7 +197,6 @@ struct GatherPlan {
     KvcGatherArgs a;               // args of the first (or only) segment
     const uint64_t *segBases;      // device-visible bases of all segments (fused) or null
     uint32_t fused;                // 1: copy for every node; 0: only a.myNode
-    uint32_t epoch;                // winner tag epoch of this call
     uint32_t spanRows;             // bid stride used for the winner index
     uint32_t statusWords;          // words per node slot (block_dim)
 };

@@ -36,8 +36,8 @@ struct GatherExtra {
     uint32_t *counters;
     uint32_t *errs;
     uint32_t *tickets;
+    uint32_t *epoch;       // winner-tag epoch of the current call (device counter)
     uint32_t fused;
-    uint32_t epoch;
     uint32_t spanRows;
     uint32_t statusWords;
 };
@@ -116,8 +116,10 @@ __device__ __forceinline__ uint64_t win_index(int64_t bid, int32_t slot, uint32_
 }
 
 // Pass 1: per destination row, the last valid miss position (tagged with the
-// call's epoch so the scratch never needs clearing).  Block 0 also zeroes the
-// queued counters and the status words of the nodes this call reports.
+// call's epoch so the scratch never needs clearing; the epoch lives in device
+// memory and the last copy workgroup advances it, so a captured graph replays
+// correctly).  Block 0 also zeroes the queued counters and the status words
+// of the nodes this call reports.
 __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
 {
     const KvcGatherArgs &a = P.l.a;
@@ -143,7 +145,7 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
     const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
     const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
     const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
-    const unsigned long long tagHi = static_cast<unsigned long long>(x.epoch) << 32;
+    const unsigned long long tagHi = static_cast<unsigned long long>(*x.epoch) << 32;
     for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < total;
          p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         if (miss[p] == 0) continue;
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(256) void kvx_gather_list(GatherParams P)
     const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
     const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
     const int64_t *hostBase = reinterpret_cast<const int64_t *>(a.reqHostBase);
-    const unsigned long long tagHi = static_cast<unsigned long long>(x.epoch) << 32;
+    const unsigned long long tagHi = static_cast<unsigned long long>(*x.epoch) << 32;
     const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
     for (uint32_t i = threadIdx.x; i < 64u * 8u; i += blockDim.x) sCnt[i] = 0u;
     __syncthreads();
@@ -269,7 +271,17 @@ __global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
         sLast = (ticket == gridDim.x - 1u) ? 1 : 0;
     }
     __syncthreads();
-    if (!sLast || a.status == 0) return;
+    if (!sLast) return;
+    // the next call's epoch; at the wrap to 0 the tags of 2^32 calls ago
+    // could alias, so the table is cleared (once in 2^32 calls)
+    __shared__ uint32_t sEpoch;
+    if (threadIdx.x == 0) sEpoch = *x.epoch + 1u;
+    __syncthreads();
+    if (sEpoch == 0u) {
+        for (uint64_t i = threadIdx.x; i < x.winEntries; i += blockDim.x) x.win[i] = 0ull;
+    }
+    if (threadIdx.x == 0) *x.epoch = sEpoch;
+    if (a.status == 0) return;
     __threadfence();
     const uint32_t n0 = x.fused ? 0u : a.myNode;
     const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
@@ -380,7 +392,7 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     P.x.errs = scr.errs;
     P.x.tickets = scr.tickets;
     P.x.fused = plan.fused;
-    P.x.epoch = plan.epoch;
+    P.x.epoch = scr.epoch;
     P.x.spanRows = plan.spanRows;
     P.x.statusWords = plan.statusWords;
     const uint64_t positions = static_cast<uint64_t>(plan.a.maxNumReqs) * plan.a.topK;
