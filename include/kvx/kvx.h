@@ -81,6 +81,25 @@ int kvx_export_seg_alllayer(uint64_t channel, uint64_t seg_base, uint32_t per_la
                             uint32_t node_num, uint32_t my_node, uint64_t status, uint64_t stream,
                             uint32_t block_dim);
 
+/* Decode-incremental single-layer export, the reference design's
+ * kvops.export_rows / kvc_scatter_rows (doc/kv_offload_design.md:322-327,
+ * 353-354, 394-396; design only, no implementation in the reference): entry
+ * i < *num_real (int32 on the device, clamped to max_rows) names host row
+ * indices_host[i] (int64 on the device); if that row maps to my_node, the
+ * row_bytes at src_layer_base + i*row_bytes (HBM) are written to segment row
+ * layer_id*per_layer_seg_rows + segRow(row).  Negative rows are skipped;
+ * entries naming one segment row leave the last one's bytes (sequential
+ * order).  Status word b (< block_dim <= 8) of node my_node covers entries
+ * [b*ppc, (b+1)*ppc), ppc = ceil(max_rows/block_dim): (owned << 40) |
+ * (1 << 32) | err, err = 0x200 + (i & 0xFF) + (1 << 16) for the lowest entry
+ * i whose segment row lies outside the layer region (nothing written for
+ * it), as the import reports (kvc_gather_rows.cpp:78-81).  channel and
+ * indices_dst_unused are accepted and ignored, as in the design. */
+int kvx_export_rows(uint64_t channel, uint64_t seg_base, uint32_t layer_id, uint32_t per_layer_seg_rows,
+                    uint32_t row_bytes, uint64_t src_layer_base, uint64_t indices_host, uint64_t indices_dst_unused,
+                    uint64_t num_real, uint32_t max_rows, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node,
+                    uint64_t status, uint64_t stream, uint32_t block_dim);
+
 /* kvops_ext.cpp:281-336 kv_sieve_update.  Same validation messages; the hash
  * table size is derived identically; block_dim is accepted and only feeds the
  * informational reqsPerCore field (the grid is one workgroup per batch row).

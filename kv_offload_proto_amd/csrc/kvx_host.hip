@@ -434,6 +434,43 @@ int kvx_export_seg_alllayer(uint64_t channel, uint64_t seg_base, uint32_t per_la
     });
 }
 
+int kvx_export_rows(uint64_t channel, uint64_t seg_base, uint32_t layer_id, uint32_t per_layer_seg_rows,
+                    uint32_t row_bytes, uint64_t src_layer_base, uint64_t indices_host, uint64_t indices_dst_unused,
+                    uint64_t num_real, uint32_t max_rows, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node,
+                    uint64_t status, uint64_t stream, uint32_t block_dim)
+{
+    (void)channel;
+    (void)indices_dst_unused;
+    return Guarded([&] {
+        EnsureInited();
+        if (block_dim > 8) throw Error("export blockDim must be <= 8 (status slot layout)");
+        if (row_bytes == 0 || row_bytes % 16 != 0) throw Error("export_rows: row_bytes must be a positive multiple of 16");
+        if (node_num == 0 || node_num > 64) throw Error("export_rows: node_num must be in [1, 64]");
+        if (my_node >= node_num) throw Error("export_rows: my_node must be < node_num");
+        CheckAligned16(seg_base, "export_rows: seg_base");
+        CheckAligned16(src_layer_base, "export_rows: src_layer_base");
+        if (max_rows == 0) return;
+        if (indices_host == 0 || num_real == 0) throw Error("export_rows: indices_host and num_real must be device addresses");
+        kvx::ExportRowsArgs a{};
+        a.segBase = seg_base;
+        a.srcLayerBase = src_layer_base;
+        a.indicesHost = indices_host;
+        a.numReal = num_real;
+        a.status = status;
+        a.layerId = layer_id;
+        a.perLayerSegRows = per_layer_seg_rows;
+        a.rowBytes = row_bytes;
+        a.maxRows = max_rows;
+        a.stripeRows = stripe_rows;
+        a.nodeNum = node_num;
+        a.myNode = my_node;
+        a.statusWords = block_dim == 0 ? 1u : block_dim;
+        EnsureWinScratch(std::max<uint64_t>(per_layer_seg_rows, 1));
+        ClearStatusWords(status, my_node, a.statusWords);
+        hipCheck(kvx::launch_export_rows(a, g.scratch, AsStream(stream)), "export_rows launch");
+    });
+}
+
 int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t seq_lens, uint64_t prefill_lens,
                      uint64_t device_buffer_tokens, uint64_t device_buffer_visited, uint64_t device_buffer_ht,
                      uint64_t sieve_hand, uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real,

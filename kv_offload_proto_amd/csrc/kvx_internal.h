@@ -203,6 +203,18 @@ struct GatherPlan {
 hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t overflowSlot,
                          hipStream_t stream);
 hipError_t launch_stream_copy(uint64_t dst, uint64_t src, uint64_t bytes, hipStream_t stream);
+// Arguments of the decode-incremental single-layer export (the reference
+// design's export_rows, doc/kv_offload_design.md:322-327; no args struct of
+// the reference exists for it).
+struct ExportRowsArgs {
+    uint64_t segBase;         // host base of segment myNode
+    uint64_t srcLayerBase;    // HBM rows: entry i at srcLayerBase + i*rowBytes
+    uint64_t indicesHost;     // int64 host logical rows, one per entry
+    uint64_t numReal;         // device int32: entries in use
+    uint64_t status;          // status slot base (node myNode at +64*myNode)
+    uint32_t layerId, perLayerSegRows, rowBytes, maxRows, stripeRows, nodeNum, myNode, statusWords;
+};
+hipError_t launch_export_rows(const ExportRowsArgs &a, const RowScratch &scr, hipStream_t stream);
 hipError_t launch_export(const KvcScatterAllArgs &a, const RowScratch &scr, uint64_t overflowSlot,
                          hipStream_t stream);
 

@@ -347,6 +347,125 @@ __global__ __launch_bounds__(256) void kvx_export_alllayer(ExportParams P)
     }
 }
 
+// Decode-incremental export of one layer (the reference design's
+// export_rows / kvc_scatter_rows, doc/kv_offload_design.md:322-327,394-396:
+// the import's shape with the direction reversed).  Entry i < num_real names
+// host row indices[i]; the row owned by myNode is copied from
+// srcLayerBase + i*rowBytes to its segment row of layer layerId.  Entries
+// naming one segment row resolve as a sequential walk would: the last wins.
+struct ExportRowsParams {
+    ExportRowsArgs a;
+    unsigned long long *win;
+    uint64_t winEntries;
+    uint32_t *counters;
+    uint32_t *errs;
+    uint32_t *tickets;
+    uint32_t *epoch;
+};
+
+__device__ __forceinline__ bool export_row_target(const ExportRowsArgs &a, int64_t row, uint32_t &segRow)
+{
+    if (row < 0) return false;
+    const uint32_t r = static_cast<uint32_t>(row);  // the mapping is u32 math (kvc_common.h:81-89)
+    if (kvx_node_of(r, a.stripeRows, a.nodeNum) != a.myNode) return false;
+    segRow = kvx_seg_row_of(r, a.stripeRows, a.nodeNum);
+    return true;
+}
+
+// Pass 1: the last entry per segment row (winner tags, as in the import);
+// block 0 resets this node's counters and status words.
+__global__ __launch_bounds__(256) void kvx_export_rows_prep(ExportRowsParams P)
+{
+    const ExportRowsArgs &a = P.a;
+    const int32_t n = clamp_num_real(a.numReal, a.maxRows);
+    if (blockIdx.x == 0) {
+        for (uint32_t b = threadIdx.x; b < a.statusWords; b += blockDim.x) {
+            P.counters[a.myNode * 8u + b] = 0u;
+            P.errs[a.myNode * 8u + b] = 0xFFFFFFFFu;  // lowest failing entry, min-reduced
+            if (a.status != 0) store_status(a.status + a.myNode * 64ull + b * 8ull, 0ull);
+        }
+    }
+    const int64_t *idx = reinterpret_cast<const int64_t *>(a.indicesHost);
+    const unsigned long long tagHi = static_cast<unsigned long long>(*P.epoch) << 32;
+    for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        uint32_t segRow;
+        if (!export_row_target(a, idx[i], segRow) || segRow >= a.perLayerSegRows) continue;
+        if (segRow < P.winEntries) atomicMax(&P.win[segRow], tagHi | static_cast<unsigned long long>(i));
+    }
+}
+
+// Pass 2: each wave takes 64 entries, counts the owned ones per status word,
+// records out-of-segment rows and copies its winners; the last workgroup
+// advances the epoch and writes the status words.
+__global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
+{
+    __shared__ uint64_t sSrc[kWaves][64];
+    __shared__ uint64_t sDst[kWaves][64];
+    __shared__ int sLast;
+    __shared__ uint32_t sEpoch;
+    const ExportRowsArgs &a = P.a;
+    const int wave = threadIdx.x / 64;
+    const uint32_t lane = static_cast<uint32_t>(lane_id());
+    const int32_t n = clamp_num_real(a.numReal, a.maxRows);
+    const int64_t *idx = reinterpret_cast<const int64_t *>(a.indicesHost);
+    const unsigned long long tagHi = static_cast<unsigned long long>(*P.epoch) << 32;
+    const uint32_t cpr = a.rowBytes / 16u;
+    const uint32_t words = a.statusWords;
+    const uint32_t ppc = (a.maxRows + words - 1u) / words;  // entries per status word
+    for (int32_t base = (blockIdx.x * kWaves + wave) * 64; base < n; base += gridDim.x * kWaves * 64) {
+        const int32_t i = base + static_cast<int32_t>(lane);
+        bool copy = false;
+        uint64_t src = 0, dst = 0;
+        uint32_t segRow;
+        if (i < n && export_row_target(a, idx[i], segRow)) {
+            const uint32_t key = a.myNode * 8u + static_cast<uint32_t>(i) / ppc;
+            atomicAdd(&P.counters[key], 1u);
+            if (segRow >= a.perLayerSegRows) {  // outside the segment's layer region: report, do not write
+                atomicMin(&P.errs[key], static_cast<uint32_t>(i));
+            } else {
+                copy = segRow >= P.winEntries || P.win[segRow] == (tagHi | static_cast<unsigned long long>(i));
+                src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
+                dst = a.segBase + (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;
+            }
+        }
+        const uint64_t cm = __ballot(copy);
+        if (copy) {
+            const uint32_t at = static_cast<uint32_t>(__popcll(cm & ((1ull << lane) - 1ull)));
+            sSrc[wave][at] = src;
+            sDst[wave][at] = dst;
+        }
+        wave_sync_lds();
+        wave_copy_rows(sSrc[wave], sDst[wave], static_cast<uint32_t>(__popcll(cm)), cpr);
+        wave_sync_lds();
+    }
+
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int ticket = atomicInc(&P.tickets[2], gridDim.x - 1u);
+        sLast = (ticket == gridDim.x - 1u) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sLast) return;
+    if (threadIdx.x == 0) sEpoch = *P.epoch + 1u;
+    __syncthreads();
+    if (sEpoch == 0u) {
+        for (uint64_t k = threadIdx.x; k < P.winEntries; k += blockDim.x) P.win[k] = 0ull;
+    }
+    if (threadIdx.x == 0) *P.epoch = sEpoch;
+    if (a.status == 0) return;
+    __threadfence_system();
+    for (uint32_t b = threadIdx.x; b < words; b += blockDim.x) {
+        uint64_t word = 1ull << 32;
+        if (static_cast<int64_t>(b) * ppc < n) {
+            const uint32_t q = __hip_atomic_load(&P.counters[a.myNode * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t e = __hip_atomic_load(&P.errs[a.myNode * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            word |= (static_cast<uint64_t>(q) << 40) | (e == 0xFFFFFFFFu ? 0u : row_error_code(e));
+        }
+        store_status(a.status + a.myNode * 64ull + b * 8ull, word);
+    }
+}
+
 // Plain streaming copy, 16 B per lane, kUnroll chunks in flight per lane.
 __global__ __launch_bounds__(256) void kvx_stream_copy(u32x4 *dst, const u32x4 *src, uint64_t n16)
 {
@@ -435,6 +554,27 @@ hipError_t launch_export(const KvcScatterAllArgs &a, const RowScratch &scr, uint
     if (blocks < 1) blocks = 1;
     if (blocks > 2048) blocks = 2048;
     hipLaunchKernelGGL(kvx_export_alllayer, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, P);
+    return hipGetLastError();
+}
+
+hipError_t launch_export_rows(const ExportRowsArgs &a, const RowScratch &scr, hipStream_t stream)
+{
+    ExportRowsParams P{};
+    P.a = a;
+    P.win = scr.win;
+    P.winEntries = scr.winEntries;
+    P.counters = scr.counters;
+    P.errs = scr.errs;
+    P.tickets = scr.tickets;
+    P.epoch = scr.epoch;
+    uint64_t prep = (static_cast<uint64_t>(a.maxRows) + 255ull) / 256ull;
+    prep = prep < 1 ? 1 : (prep > 1024 ? 1024 : prep);
+    hipLaunchKernelGGL(kvx_export_rows_prep, dim3(static_cast<uint32_t>(prep)), dim3(256), 0, stream, P);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    uint64_t copy = (static_cast<uint64_t>(a.maxRows) + 64ull * kWaves - 1ull) / (64ull * kWaves);
+    copy = copy < 1 ? 1 : (copy > 256 ? 256 : copy);
+    hipLaunchKernelGGL(kvx_export_rows_copy, dim3(static_cast<uint32_t>(copy)), dim3(256), 0, stream, P);
     return hipGetLastError();
 }
 

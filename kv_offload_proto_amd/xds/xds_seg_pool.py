@@ -248,6 +248,23 @@ class HostSegPool:
                                        self.stripe_rows, self.node_num, s, status, stream, block_dim)
         return status
 
+    # ---- decode-incremental export of one layer (the reference design's
+    # MemPoolHost.batch_export_rows, doc/kv_offload_design.md:353-354) ----
+    def batch_export_rows(self, layer_id: int, src_layer_base, indices_host, num_real, max_rows: int,
+                          stream: int = 0, block_dim: int = 1) -> int:
+        """Entry i < num_real writes the row at src_layer_base + i*row_bytes to
+        host row indices_host[i] (int64) of layer layer_id, one export per
+        segment sharing a status slot like batch_read."""
+        if self.pool is None:
+            raise RuntimeError("pool not created")
+        status = self.next_status()
+        for s in range(self.node_num):
+            seg = self.pool.segments[s]
+            _kvops.export_rows(self.channels[s], seg.seg_base, layer_id, self.per_layer_seg_rows, self.row_bytes,
+                               _ptr(src_layer_base), _ptr(indices_host), 0, _ptr(num_real), max_rows,
+                               self.stripe_rows, self.node_num, s, status, stream, block_dim)
+        return status
+
     # ---- completion (xds_ems_pool.py:233-241) ----
     def wait(self, status: int, timeout_us: int = 60_000_000, block_dim: int = 1) -> None:
         for s in range(self.node_num):

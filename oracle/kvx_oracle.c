@@ -25,6 +25,12 @@
  *                       (tests/test_oracle_rows.py); parity with the reference
  *                       hardware path is unpinned (HCOMM ReadNbi is not vendored).
  *   orc_export_alllayer same as gather.
+ *   orc_export_rows     the reference has only a design for it
+ *                       (doc/kv_offload_design.md:322-327,394-396); checked in
+ *                       tests/test_oracle_rows.py against orc_export_alllayer
+ *                       (a contiguous index list must give the same segment
+ *                       bytes) and brute-force last-entry-wins; parity with a
+ *                       reference implementation is unpinned (none exists).
  */
 #include <stdint.h>
 #include <stdlib.h>
@@ -369,4 +375,53 @@ int64_t orc_export_alllayer(uint8_t *seg, const uint8_t *src0, uint64_t srcLayer
         }
     }
     return queued;
+}
+
+/* Decode-incremental single-layer export (the reference design's export_rows /
+ * kvc_scatter_rows, doc/kv_offload_design.md:322-327,353-354,394-396: the
+ * import's arguments with the direction reversed).  For entries i in
+ * [0, min(numReal, maxRows)) in increasing order: row = idx[i]; negative rows
+ * are skipped; rows owned by myNode (kvc_common.h:81-89 mapping on the low 32
+ * bits, as the import) are copied from src + i*rowBytes to
+ * seg + (layerId*plsr + segRow)*rowBytes, so the last entry naming a segment
+ * row wins.  A segment row >= plsr is not written; the status word of its
+ * entry block records the lowest such entry (error code band of
+ * kvc_gather_rows.cpp:78-81).  statusWords[b], b < blockDim:
+ * (owned << 40) | (1 << 32) | err over entries [b*ppc, (b+1)*ppc),
+ * ppc = ceil(maxRows/blockDim); an empty range gives 1 << 32.
+ * Returns the number of entries written. */
+int64_t orc_export_rows(uint8_t *seg, const uint8_t *src, const int64_t *idx, int32_t numRealIn, uint32_t maxRows,
+                        uint32_t layerId, uint32_t plsr, uint32_t rowBytes, uint32_t S, uint32_t N, uint32_t myNode,
+                        uint32_t blockDim, uint64_t *statusWords)
+{
+    int32_t n = numRealIn;
+    if (n > (int32_t)maxRows) n = (int32_t)maxRows;
+    if (n < 0) n = 0;
+    if (blockDim == 0) blockDim = 1;
+    const int64_t ppc = ((int64_t)maxRows + blockDim - 1) / blockDim;
+    uint64_t owned[8] = {0};
+    int64_t firstErr[8];
+    for (uint32_t b = 0; b < 8; ++b) firstErr[b] = -1;
+    int64_t written = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        if (idx[i] < 0) continue;
+        const uint32_t row = (uint32_t)idx[i];
+        if (orc_node_of(row, S, N) != myNode) continue;
+        const int64_t b = i / ppc;
+        if (b < 8) owned[b] += 1;
+        const uint64_t segRow = orc_seg_row_of(row, S, N);
+        if (segRow >= plsr) {
+            if (b < 8 && firstErr[b] < 0) firstErr[b] = i;
+            continue;
+        }
+        memcpy(seg + ((uint64_t)layerId * plsr + segRow) * rowBytes, src + (uint64_t)i * rowBytes, rowBytes);
+        ++written;
+    }
+    for (uint32_t b = 0; b < blockDim; ++b) {
+        if ((int64_t)b * ppc >= n) { statusWords[b] = 1ull << 32; continue; }
+        uint64_t err = 0;
+        if (firstErr[b] >= 0) err = 0x200u + ((uint64_t)firstErr[b] & 0xFFu) + (1u << 16);
+        statusWords[b] = (owned[b] << 40) | (1ull << 32) | err;
+    }
+    return written;
 }

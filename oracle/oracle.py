@@ -81,6 +81,8 @@ def lib():
         L.orc_export_alllayer.argtypes = [_u8p, _u8p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
                                           ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                           ctypes.c_uint32, ctypes.c_uint32]
+        L.orc_export_rows.restype = ctypes.c_int64
+        L.orc_export_rows.argtypes = [_u8p, _u8p, _i64p, ctypes.c_int32] + [ctypes.c_uint32] * 8 + [_u64p]
         _LIB = L
     return _LIB
 
@@ -230,6 +232,17 @@ def gather_rows(segs, hot, layer_offset_rows, row_bytes, topk, req_pool, req_hos
                               _p(np.ascontiguousarray(is_miss, dtype=np.int8), _i8p), int(num_real), top_k,
                               max_num_reqs, stripe_rows, node_num, my_node, hot_req_stride_rows, max(block_dim, 1),
                               _p(words, _u64p))
+    return int(n), words
+
+
+def export_rows(seg, src, indices, num_real, max_rows, layer_id, plsr, row_bytes, stripe_rows, node_num, my_node,
+                block_dim=1):
+    """Oracle decode-incremental export into one segment (uint8 array) from src
+    (uint8 array of max_rows rows).  Returns (entries written, status words)."""
+    words = np.zeros(max(block_dim, 1), dtype=np.uint64)
+    n = lib().orc_export_rows(_p(seg, _u8p), _p(src, _u8p), _p(np.ascontiguousarray(indices, dtype=np.int64), _i64p),
+                              int(num_real), max_rows, layer_id, plsr, row_bytes, stripe_rows, node_num, my_node,
+                              max(block_dim, 1), _p(words, _u64p))
     return int(n), words
 
 

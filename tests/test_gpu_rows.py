@@ -14,6 +14,7 @@ from oracle import oracle as orc
 pytestmark = pytest.mark.gpu
 
 DONE = 1 << 32
+ROW = 1152
 
 
 def _src(layers, rows, row_bytes, seed):
@@ -123,3 +124,44 @@ def test_status_poll_and_timeout(kvops):
     assert kvops.poll_status(st, 2000) == -0x2000
     # not a status address
     assert kvops.poll_status(12345, 10) == -0x1000
+
+
+@pytest.mark.parametrize("S,N,block_dim,max_rows,num_real", [(1, 2, 1, 64, 64), (1, 3, 3, 500, 377), (64, 4, 2, 256, 256),
+                                                             (4, 2, 8, 1000, 999), (1, 1, 1, 40, 0)])
+def test_export_rows_parity(kvops, S, N, block_dim, max_rows, num_real):
+    """Decode-incremental export of one layer into every segment against the
+    oracle: host rows with duplicates (last entry wins), negative rows and rows
+    outside the layer region (reported, not written), num_real below the
+    capacity; all segment bytes and every node's status words."""
+    print("export_rows case", S, N, block_dim, max_rows, num_real, flush=True)
+    L, layer_rows = 3, 4096
+    pool = HostSegPool(0, L, layer_rows, ROW, stripe_rows=S, node_num=N)
+    pool.create_pool()
+    try:
+        plsr = pool.per_layer_seg_rows
+        views = pool.segment_views()
+        rng = np.random.default_rng(S * 1000 + N * 10 + block_dim)
+        # non-zero starting content so untouched rows are checked too
+        for v in views:
+            v[...] = rng.integers(0, 256, size=v.shape, dtype=np.uint8)
+        expect = [v.copy().reshape(-1) for v in views]
+        idx = rng.integers(0, layer_rows, size=max_rows).astype(np.int64)
+        dup = rng.integers(0, max_rows, size=max_rows // 4)
+        idx[dup] = idx[rng.integers(0, max_rows, size=dup.size)]
+        idx[rng.integers(0, max_rows, size=max_rows // 16)] = -1
+        idx[rng.integers(0, max_rows, size=max_rows // 32)] = layer_rows * S * N + 7  # beyond the layer region
+        src = rng.integers(0, 256, size=(max_rows, ROW), dtype=np.uint8)
+        src_d = torch.from_numpy(src).cuda()
+        idx_d = to_dev(idx)
+        nr_d = to_dev(np.array([num_real], dtype=np.int32))
+        layer = 1
+        status = pool.batch_export_rows(layer, src_d, idx_d, nr_d, max_rows, block_dim=block_dim)
+        torch.cuda.synchronize()  # (the status words carry error codes here, so no pool.wait)
+        for s in range(N):
+            _, words = orc.export_rows(expect[s], src.reshape(-1), idx, num_real, max_rows, layer, plsr, ROW, S, N, s,
+                                       block_dim)
+            got = _read_words(status + s * 64, block_dim)
+            assert got == [int(w) for w in words], (s, got, [int(w) for w in words])
+            np.testing.assert_array_equal(views[s].reshape(-1), expect[s], err_msg="segment {}".format(s))
+    finally:
+        pool.destroy(close_ext=False)

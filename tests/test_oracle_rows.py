@@ -176,3 +176,53 @@ def test_export_round_trip(S, N, lo, cnt):
                 if (node, seg_row) not in last:
                     off = (l * plsr + seg_row) * ROW_BYTES
                     assert not segs[node][off:off + ROW_BYTES].any()
+
+
+# ---- decode-incremental export (the design's export_rows) ----
+
+@pytest.mark.parametrize("S,N,row_lo,row_cnt,block_dim", [(1, 2, 0, 300, 1), (1, 3, 17, 250, 3), (64, 4, 0, 1024, 2),
+                                                           (5, 2, 3, 97, 1)])
+def test_export_rows_contiguous_equals_alllayer(S, N, row_lo, row_cnt, block_dim):
+    """A contiguous index list [row_lo, row_lo+row_cnt) with entry i sourced
+    from row row_lo+i leaves every segment exactly as the all-layer export of
+    that range does for one layer (both resolve a stripe's shared segment row
+    to its highest row), and the owned counts agree with its queued count."""
+    rng = np.random.default_rng(S * 100 + N)
+    layer_rows = row_lo + row_cnt + 64
+    plsr = -(-layer_rows // N) if S == 1 else -(-layer_rows // (S * N)) + 1
+    src = rng.integers(0, 256, size=layer_rows * ROW_BYTES, dtype=np.uint8)
+    idx = np.arange(row_lo, row_lo + row_cnt, dtype=np.int64)
+    for my in range(N):
+        seg_a = np.zeros(plsr * ROW_BYTES, dtype=np.uint8)
+        seg_b = np.zeros(plsr * ROW_BYTES, dtype=np.uint8)
+        queued = orc.export_alllayer(seg_a, src, layer_rows * ROW_BYTES, plsr, ROW_BYTES, row_lo, row_cnt, 1, S, N, my)
+        n, words = orc.export_rows(seg_b, np.ascontiguousarray(src[row_lo * ROW_BYTES:]), idx, row_cnt, row_cnt, 0,
+                                   plsr, ROW_BYTES, S, N, my, block_dim)
+        np.testing.assert_array_equal(seg_a, seg_b)
+        assert sum(int(w) >> 40 for w in words) == queued
+        assert all((int(w) >> 32) & 0xFF == 1 and int(w) & 0xFFFFFFFF == 0 for w in words)
+
+
+def test_export_rows_last_entry_wins_and_errors():
+    """Entries naming one host row leave the last one's bytes; negative rows,
+    rows of other nodes and entries past num_real write nothing; a row whose
+    segment row is outside the layer region is reported with the import's
+    error code for the lowest such entry of its status block."""
+    S, N, plsr, layers = 1, 2, 40, 3
+    src = np.repeat(np.arange(1, 11, dtype=np.uint8), ROW_BYTES)  # entry i's row is all (i+1)
+    idx = np.array([4, 6, 4, -1, 5, 200, 4, 9, 202, 6], dtype=np.int64)
+    seg = np.zeros(layers * plsr * ROW_BYTES, dtype=np.uint8)
+    n, words = orc.export_rows(seg, src, idx, 9, 10, 1, plsr, ROW_BYTES, S, N, 0, 2)
+    rows = seg.reshape(layers, plsr, ROW_BYTES)
+    # node 0 owns even rows: 4 -> segment row 2 (entries 0, 2, 6: last is 6), 6 -> row 3 (entry 1; entry 9 is
+    # past num_real), 200 -> row 100 >= plsr (entry 5, error), 202 -> row 101 (entry 8, error)
+    assert (rows[1, 2] == 7).all() and (rows[1, 3] == 2).all()
+    assert n == 4
+    written = {2, 3}
+    for r in range(plsr):
+        if r not in written:
+            assert (rows[1, r] == 0).all(), r
+    assert (rows[0] == 0).all() and (rows[2] == 0).all()
+    # status blocks of 5 entries: [0,5) owns entries 0,1,2 ; [5,9) owns 5,6,8 with the first error at 5
+    assert int(words[0]) == (3 << 40) | (1 << 32)
+    assert int(words[1]) == (3 << 40) | (1 << 32) | (0x200 + 5 + (1 << 16))
