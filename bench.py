@@ -212,6 +212,48 @@ def graph_pass(runner, snap, warm, timed, fused, eager_ms, log):
     return res
 
 
+def export_rows_pass(runner, log, reps=3):
+    """Decode-incremental export: one row per request per layer (the row a
+    decode step would append; here the last prefill row, rewritten with the
+    bytes it already holds), timed per layer with HIP events, then checked in
+    the host segments."""
+    import numpy as np
+    import torch
+
+    cfg, pool = runner.cfg, runner.pool
+    R = cfg.req_num
+    rows = [cfg.host_base(r) + cfg.prefill - 1 for r in range(R)]
+    rows_d = torch.tensor(rows, dtype=torch.int64, device=runner.dev)
+    nr = torch.tensor([R], dtype=torch.int32, device=runner.dev)
+    srcs = [runner.src[l].index_select(0, rows_d).contiguous() for l in range(cfg.layers)]
+    stream = torch.cuda.current_stream()
+    us = []
+    st = None
+    for _ in range(reps):
+        for l in range(cfg.layers):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            st = pool.batch_export_rows(l, srcs[l], rows_d, nr, R, stream=stream.cuda_stream)
+            e1.record(stream)
+            us.append((e0, e1))
+        pool.wait(st)
+    torch.cuda.synchronize()
+    us = [a.elapsed_time(b) * 1e3 for a, b in us]
+    views = pool.segment_views()
+    S, N = max(cfg.stripe_rows, 1), cfg.node_num
+    ok = True
+    for l in (0, cfg.layers // 2, cfg.layers - 1):
+        want = srcs[l].cpu().numpy()
+        for r, row in enumerate(rows):
+            node, seg_row = (row // S) % N, (row // S) // N
+            ok = ok and bool(np.array_equal(views[node][l, seg_row], want[r]))
+    med = pct(us, 50)
+    log("[bench] export_rows: {} rows x {} segments per layer, {:.1f} us/layer median; segments hold the rows: {}".format(
+        R, N, med, ok))
+    return {"rows_per_layer": R, "segments": N, "us_per_layer_median": med, "us_per_layer_p99": pct(us, 99),
+            "GBps": R * cfg.row_bytes / (med * 1e-6) / 1e9, "match": ok}
+
+
 def cpu_baseline(runner, plan, n_warm, budget_s, log):
     """The C oracle (oracle/liboracle.so) replaying the same batches from the
     same initial state on one host core: the warmup layer-steps untimed
@@ -436,6 +478,7 @@ def main():
         "verify": ok,
     }
     out["graph"] = None if args.no_graph else graph_pass(runner, snap, warm, timed, fused, total_ms, log)
+    out["export_rows"] = export_rows_pass(runner, log)
     if not args.no_cpu:
         runner.restore(snap)
         out["cpu_baseline"] = cpu_baseline(runner, plan, len(warm), args.cpu_sample_s, log)

@@ -103,6 +103,24 @@ void ClearStatusWords(uint64_t status, uint32_t node, uint32_t words)
     }
 }
 
+// A status block whose base lies inside a kvx_alloc_status allocation must
+// end inside it: the kernels write node n's words at status + 64n + 8b.
+void CheckStatusBlock(uint64_t status, uint32_t firstNode, uint32_t nodes, uint32_t words, const char *what)
+{
+    if (status == 0 || nodes == 0) return;
+    const uint64_t lo = status;
+    const uint64_t hi = status + (static_cast<uint64_t>(firstNode) + nodes - 1ull) * 64ull + words * 8ull;
+    std::lock_guard<std::mutex> lk(g_statusMu);
+    for (const Alloc &a : g.status) {
+        if (lo >= a.addr && lo < a.addr + a.bytes) {
+            if (hi > a.addr + a.bytes) {
+                throw Error(std::string(what) + ": status slots of this call run past the end of their alloc_status block");
+            }
+            return;
+        }
+    }
+}
+
 void EnsureWinScratch(uint64_t entries)
 {
     if (g.scratch.winEntries >= entries) return;
@@ -217,8 +235,10 @@ void DoGather(const GatherCall &c)
     EnsureListScratch(positions);
     hipStream_t st = AsStream(c.stream);
     if (c.fused) {
+        CheckStatusBlock(c.status, 0, c.nodeNum, bd, "import_all");
         for (uint32_t s = 0; s < c.nodeNum; ++s) ClearStatusWords(c.status, s, bd);
     } else {
+        CheckStatusBlock(c.status, c.myNode, 1, bd, "import_seg");
         ClearStatusWords(c.status, c.myNode, bd);
     }
     hipCheck(kvx::launch_gather(plan, g.scratch, reinterpret_cast<uint64_t>(g.overflow), st), "kvc_gather_rows launch");
@@ -428,6 +448,7 @@ int kvx_export_seg_alllayer(uint64_t channel, uint64_t seg_base, uint32_t per_la
         if (geo.nStripes != 0 && geo.maxSegRow >= per_layer_seg_rows) {
             throw Error("export_seg_alllayer: rows [row_lo, row_lo+row_cnt) exceed per_layer_seg_rows of the segment");
         }
+        CheckStatusBlock(status, my_node, 1, a.blockDim, "export_seg_alllayer");
         ClearStatusWords(status, my_node, a.blockDim);
         hipCheck(kvx::launch_export(a, g.scratch, reinterpret_cast<uint64_t>(g.overflow), AsStream(stream)),
                  "kvc_scatter_rows_alllayer launch");
@@ -466,6 +487,7 @@ int kvx_export_rows(uint64_t channel, uint64_t seg_base, uint32_t layer_id, uint
         a.myNode = my_node;
         a.statusWords = block_dim == 0 ? 1u : block_dim;
         EnsureWinScratch(std::max<uint64_t>(per_layer_seg_rows, 1));
+        CheckStatusBlock(status, my_node, 1, a.statusWords, "export_rows");
         ClearStatusWords(status, my_node, a.statusWords);
         hipCheck(kvx::launch_export_rows(a, g.scratch, AsStream(stream)), "export_rows launch");
     });

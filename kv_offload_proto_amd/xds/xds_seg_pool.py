@@ -182,8 +182,12 @@ class HostSegPool:
         self._status_cursor = 0
 
     def next_status(self) -> int:
+        """Base of the next status block: node s of a call writes slot base +
+        s*64, so the cursor steps by node_num slots (the reference steps by one,
+        xds_ems_pool.py:182-185, so consecutive calls share slots and the last
+        blocks of its ring run past the allocation)."""
         addr = self._status_base + self._status_cursor * 64
-        self._status_cursor = (self._status_cursor + 1) % self._status_count
+        self._status_cursor = (self._status_cursor + self.node_num) % self._status_count
         return addr
 
     def destroy(self, close_ext: bool = True) -> None:

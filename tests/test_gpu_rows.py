@@ -165,3 +165,31 @@ def test_export_rows_parity(kvops, S, N, block_dim, max_rows, num_real):
             np.testing.assert_array_equal(views[s].reshape(-1), expect[s], err_msg="segment {}".format(s))
     finally:
         pool.destroy(close_ext=False)
+
+
+def test_status_ring_blocks(kvops):
+    """next_status hands out disjoint blocks of node_num slots inside the ring;
+    a call whose status block would run past its alloc_status block is
+    rejected before anything is launched."""
+    N = 3
+    pool = HostSegPool(0, 1, 64, ROW, stripe_rows=1, node_num=N)
+    pool.create_pool()
+    try:
+        base, count = pool._status_base, pool._status_count
+        blocks = [pool.next_status() for _ in range(30)]
+        for addr in blocks:
+            assert base <= addr and addr + N * 64 <= base + count * 64
+        assert len(set(blocks[:count // N])) == count // N
+        idx = to_dev(np.array([-1], dtype=np.int64))
+        nr = to_dev(np.array([1], dtype=np.int32))
+        src = torch.zeros((1, ROW), dtype=torch.uint8, device="cuda")
+        seg = pool.pool.segments[N - 1].seg_base
+        with pytest.raises(RuntimeError, match="past the end"):
+            kvops.export_rows(0, seg, 0, pool.per_layer_seg_rows, ROW, src.data_ptr(), idx.data_ptr(), 0,
+                              nr.data_ptr(), 1, 1, N, N - 1, base + (count - 1) * 64, 0, 1)
+        kvops.export_rows(0, seg, 0, pool.per_layer_seg_rows, ROW, src.data_ptr(), idx.data_ptr(), 0, nr.data_ptr(),
+                          1, 1, N, N - 1, base, 0, 1)
+        torch.cuda.synchronize()
+        assert _read_words(base + (N - 1) * 64, 1) == [DONE]
+    finally:
+        pool.destroy(close_ext=False)
