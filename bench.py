@@ -227,18 +227,20 @@ def export_rows_pass(runner, log, reps=3):
     nr = torch.tensor([R], dtype=torch.int32, device=runner.dev)
     srcs = [runner.src[l].index_select(0, rows_d).contiguous() for l in range(cfg.layers)]
     stream = torch.cuda.current_stream()
-    us = []
-    st = None
-    for _ in range(reps):
-        for l in range(cfg.layers):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            st = pool.batch_export_rows(l, srcs[l], rows_d, nr, R, stream=stream.cuda_stream)
-            e1.record(stream)
-            us.append((e0, e1))
-        pool.wait(st)
-    torch.cuda.synchronize()
-    us = [a.elapsed_time(b) * 1e3 for a, b in us]
+    timing = {}
+    for name, export in (("per_segment", pool.batch_export_rows), ("fused", pool.batch_export_rows_fused)):
+        us = []
+        st = None
+        for _ in range(reps):
+            for l in range(cfg.layers):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                st = export(l, srcs[l], rows_d, nr, R, stream=stream.cuda_stream)
+                e1.record(stream)
+                us.append((e0, e1))
+            pool.wait(st)
+        torch.cuda.synchronize()
+        timing[name] = [a.elapsed_time(b) * 1e3 for a, b in us]
     views = pool.segment_views()
     S, N = max(cfg.stripe_rows, 1), cfg.node_num
     ok = True
@@ -247,11 +249,11 @@ def export_rows_pass(runner, log, reps=3):
         for r, row in enumerate(rows):
             node, seg_row = (row // S) % N, (row // S) // N
             ok = ok and bool(np.array_equal(views[node][l, seg_row], want[r]))
-    med = pct(us, 50)
-    log("[bench] export_rows: {} rows x {} segments per layer, {:.1f} us/layer median; segments hold the rows: {}".format(
-        R, N, med, ok))
-    return {"rows_per_layer": R, "segments": N, "us_per_layer_median": med, "us_per_layer_p99": pct(us, 99),
-            "GBps": R * cfg.row_bytes / (med * 1e-6) / 1e9, "match": ok}
+    med, med_seg = pct(timing["fused"], 50), pct(timing["per_segment"], 50)
+    log("[bench] export_rows: {} rows per layer over {} segments, {:.1f} us/layer median fused ({:.1f} per segment); "
+        "segments hold the rows: {}".format(R, N, med, med_seg, ok))
+    return {"rows_per_layer": R, "segments": N, "us_per_layer_median": med, "us_per_layer_p99": pct(timing["fused"], 99),
+            "per_segment_us_per_layer_median": med_seg, "GBps": R * cfg.row_bytes / (med * 1e-6) / 1e9, "match": ok}
 
 
 def cpu_baseline(runner, plan, n_warm, budget_s, log):

@@ -100,6 +100,15 @@ int kvx_export_rows(uint64_t channel, uint64_t seg_base, uint32_t layer_id, uint
                     uint64_t num_real, uint32_t max_rows, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node,
                     uint64_t status, uint64_t stream, uint32_t block_dim);
 
+/* All N segments of kvx_export_rows in one launch pair (the design issues one
+ * export per segment, doc/kv_offload_design.md:353-354; this is the fused
+ * form, like kvx_import_all): seg_bases points to node_num host integers;
+ * status words are written for every node. */
+int kvx_export_rows_all(const uint64_t *seg_bases, uint32_t layer_id, uint32_t per_layer_seg_rows, uint32_t row_bytes,
+                        uint64_t src_layer_base, uint64_t indices_host, uint64_t indices_dst_unused, uint64_t num_real,
+                        uint32_t max_rows, uint32_t stripe_rows, uint32_t node_num, uint64_t status, uint64_t stream,
+                        uint32_t block_dim);
+
 /* kvops_ext.cpp:281-336 kv_sieve_update.  Same validation messages; the hash
  * table size is derived identically; block_dim is accepted and only feeds the
  * informational reqsPerCore field (the grid is one workgroup per batch row).

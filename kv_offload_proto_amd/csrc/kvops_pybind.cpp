@@ -119,6 +119,21 @@ PYBIND11_MODULE(_kvops, m)
         py::arg("status"), py::arg("stream") = 0, py::arg("block_dim") = 1);
 
     m.def(
+        "export_rows_all",
+        [](const std::vector<uint64_t> &seg_bases, uint32_t layer_id, uint32_t per_layer_seg_rows, uint32_t row_bytes,
+           uint64_t src_layer_base, uint64_t indices_host, uint64_t indices_dst_unused, uint64_t num_real,
+           uint32_t max_rows, uint32_t stripe_rows, uint64_t status, uint64_t stream, uint32_t block_dim) {
+            if (seg_bases.empty()) throw std::runtime_error("export_rows_all: seg_bases is empty");
+            Check(kvx_export_rows_all(seg_bases.data(), layer_id, per_layer_seg_rows, row_bytes, src_layer_base,
+                                      indices_host, indices_dst_unused, num_real, max_rows, stripe_rows,
+                                      static_cast<uint32_t>(seg_bases.size()), status, stream, block_dim));
+        },
+        py::arg("seg_bases"), py::arg("layer_id"), py::arg("per_layer_seg_rows"), py::arg("row_bytes"),
+        py::arg("src_layer_base"), py::arg("indices_host"), py::arg("indices_dst_unused"), py::arg("num_real"),
+        py::arg("max_rows"), py::arg("stripe_rows"), py::arg("status"), py::arg("stream") = 0,
+        py::arg("block_dim") = 1);
+
+    m.def(
         "sieve_update",
         [](uint64_t topk_indices, uint64_t req_pool_indices, uint64_t seq_lens, uint64_t prefill_lens,
            uint64_t device_buffer_tokens, uint64_t device_buffer_visited, uint64_t device_buffer_ht,

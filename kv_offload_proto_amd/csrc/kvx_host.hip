@@ -244,6 +244,47 @@ void DoGather(const GatherCall &c)
     hipCheck(kvx::launch_gather(plan, g.scratch, reinterpret_cast<uint64_t>(g.overflow), st), "kvc_gather_rows launch");
 }
 
+void DoExportRows(const uint64_t *segBases, bool fused, uint32_t layer_id, uint32_t per_layer_seg_rows,
+                  uint32_t row_bytes, uint64_t src_layer_base, uint64_t indices_host, uint64_t num_real,
+                  uint32_t max_rows, uint32_t stripe_rows, uint32_t node_num, uint32_t my_node, uint64_t status,
+                  uint64_t stream, uint32_t block_dim)
+{
+    EnsureInited();
+    if (block_dim > 8) throw Error("export blockDim must be <= 8 (status slot layout)");
+    if (row_bytes == 0 || row_bytes % 16 != 0) throw Error("export_rows: row_bytes must be a positive multiple of 16");
+    if (node_num == 0 || node_num > 64) throw Error("export_rows: node_num must be in [1, 64]");
+    if (my_node >= node_num) throw Error("export_rows: my_node must be < node_num");
+    const uint32_t nSeg = fused ? node_num : 1u;
+    for (uint32_t s = 0; s < nSeg; ++s) CheckAligned16(segBases[s], "export_rows: seg_base");
+    CheckAligned16(src_layer_base, "export_rows: src_layer_base");
+    if (max_rows == 0) return;
+    if (indices_host == 0 || num_real == 0) throw Error("export_rows: indices_host and num_real must be device addresses");
+    kvx::ExportRowsArgs a{};
+    a.segBase = segBases[0];
+    a.srcLayerBase = src_layer_base;
+    a.indicesHost = indices_host;
+    a.numReal = num_real;
+    a.status = status;
+    a.layerId = layer_id;
+    a.perLayerSegRows = per_layer_seg_rows;
+    a.rowBytes = row_bytes;
+    a.maxRows = max_rows;
+    a.stripeRows = stripe_rows;
+    a.nodeNum = node_num;
+    a.myNode = fused ? 0u : my_node;
+    a.statusWords = block_dim == 0 ? 1u : block_dim;
+    a.fused = fused ? 1u : 0u;
+    EnsureWinScratch(std::max<uint64_t>(static_cast<uint64_t>(per_layer_seg_rows) * (fused ? node_num : 1u), 1));
+    if (fused) {
+        CheckStatusBlock(status, 0, node_num, a.statusWords, "export_rows_all");
+        for (uint32_t s = 0; s < node_num; ++s) ClearStatusWords(status, s, a.statusWords);
+    } else {
+        CheckStatusBlock(status, my_node, 1, a.statusWords, "export_rows");
+        ClearStatusWords(status, my_node, a.statusWords);
+    }
+    hipCheck(kvx::launch_export_rows(a, segBases, g.scratch, AsStream(stream)), "export_rows launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -463,33 +504,21 @@ int kvx_export_rows(uint64_t channel, uint64_t seg_base, uint32_t layer_id, uint
     (void)channel;
     (void)indices_dst_unused;
     return Guarded([&] {
-        EnsureInited();
-        if (block_dim > 8) throw Error("export blockDim must be <= 8 (status slot layout)");
-        if (row_bytes == 0 || row_bytes % 16 != 0) throw Error("export_rows: row_bytes must be a positive multiple of 16");
-        if (node_num == 0 || node_num > 64) throw Error("export_rows: node_num must be in [1, 64]");
-        if (my_node >= node_num) throw Error("export_rows: my_node must be < node_num");
-        CheckAligned16(seg_base, "export_rows: seg_base");
-        CheckAligned16(src_layer_base, "export_rows: src_layer_base");
-        if (max_rows == 0) return;
-        if (indices_host == 0 || num_real == 0) throw Error("export_rows: indices_host and num_real must be device addresses");
-        kvx::ExportRowsArgs a{};
-        a.segBase = seg_base;
-        a.srcLayerBase = src_layer_base;
-        a.indicesHost = indices_host;
-        a.numReal = num_real;
-        a.status = status;
-        a.layerId = layer_id;
-        a.perLayerSegRows = per_layer_seg_rows;
-        a.rowBytes = row_bytes;
-        a.maxRows = max_rows;
-        a.stripeRows = stripe_rows;
-        a.nodeNum = node_num;
-        a.myNode = my_node;
-        a.statusWords = block_dim == 0 ? 1u : block_dim;
-        EnsureWinScratch(std::max<uint64_t>(per_layer_seg_rows, 1));
-        CheckStatusBlock(status, my_node, 1, a.statusWords, "export_rows");
-        ClearStatusWords(status, my_node, a.statusWords);
-        hipCheck(kvx::launch_export_rows(a, g.scratch, AsStream(stream)), "export_rows launch");
+        DoExportRows(&seg_base, false, layer_id, per_layer_seg_rows, row_bytes, src_layer_base, indices_host, num_real,
+                     max_rows, stripe_rows, node_num, my_node, status, stream, block_dim);
+    });
+}
+
+int kvx_export_rows_all(const uint64_t *seg_bases, uint32_t layer_id, uint32_t per_layer_seg_rows, uint32_t row_bytes,
+                        uint64_t src_layer_base, uint64_t indices_host, uint64_t indices_dst_unused, uint64_t num_real,
+                        uint32_t max_rows, uint32_t stripe_rows, uint32_t node_num, uint64_t status, uint64_t stream,
+                        uint32_t block_dim)
+{
+    (void)indices_dst_unused;
+    return Guarded([&] {
+        if (seg_bases == nullptr) throw Error("export_rows_all: seg_bases is null");
+        DoExportRows(seg_bases, true, layer_id, per_layer_seg_rows, row_bytes, src_layer_base, indices_host, num_real,
+                     max_rows, stripe_rows, node_num, 0, status, stream, block_dim);
     });
 }
 

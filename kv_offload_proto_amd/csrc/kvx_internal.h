@@ -213,8 +213,10 @@ struct ExportRowsArgs {
     uint64_t numReal;         // device int32: entries in use
     uint64_t status;          // status slot base (node myNode at +64*myNode)
     uint32_t layerId, perLayerSegRows, rowBytes, maxRows, stripeRows, nodeNum, myNode, statusWords;
+    uint32_t fused;           // 1: every node's rows (segBases), status words of every node
 };
-hipError_t launch_export_rows(const ExportRowsArgs &a, const RowScratch &scr, hipStream_t stream);
+hipError_t launch_export_rows(const ExportRowsArgs &a, const uint64_t *segBases, const RowScratch &scr,
+                              hipStream_t stream);
 hipError_t launch_export(const KvcScatterAllArgs &a, const RowScratch &scr, uint64_t overflowSlot,
                          hipStream_t stream);
 

@@ -355,6 +355,7 @@ __global__ __launch_bounds__(256) void kvx_export_alllayer(ExportParams P)
 // naming one segment row resolve as a sequential walk would: the last wins.
 struct ExportRowsParams {
     ExportRowsArgs a;
+    uint64_t segBases[64];   // fused form: every node's segment base
     unsigned long long *win;
     uint64_t winEntries;
     uint32_t *counters;
@@ -363,11 +364,13 @@ struct ExportRowsParams {
     uint32_t *epoch;
 };
 
-__device__ __forceinline__ bool export_row_target(const ExportRowsArgs &a, int64_t row, uint32_t &segRow)
+__device__ __forceinline__ bool export_row_target(const ExportRowsArgs &a, int64_t row, uint32_t &node,
+                                                  uint32_t &segRow)
 {
     if (row < 0) return false;
     const uint32_t r = static_cast<uint32_t>(row);  // the mapping is u32 math (kvc_common.h:81-89)
-    if (kvx_node_of(r, a.stripeRows, a.nodeNum) != a.myNode) return false;
+    node = kvx_node_of(r, a.stripeRows, a.nodeNum);
+    if (a.fused ? node >= a.nodeNum : node != a.myNode) return false;
     segRow = kvx_seg_row_of(r, a.stripeRows, a.nodeNum);
     return true;
 }
@@ -378,19 +381,22 @@ __global__ __launch_bounds__(256) void kvx_export_rows_prep(ExportRowsParams P)
 {
     const ExportRowsArgs &a = P.a;
     const int32_t n = clamp_num_real(a.numReal, a.maxRows);
+    const uint32_t n0 = a.fused ? 0u : a.myNode, n1 = a.fused ? a.nodeNum : a.myNode + 1u;
     if (blockIdx.x == 0) {
-        for (uint32_t b = threadIdx.x; b < a.statusWords; b += blockDim.x) {
-            P.counters[a.myNode * 8u + b] = 0u;
-            P.errs[a.myNode * 8u + b] = 0xFFFFFFFFu;  // lowest failing entry, min-reduced
-            if (a.status != 0) store_status(a.status + a.myNode * 64ull + b * 8ull, 0ull);
+        for (uint32_t k = threadIdx.x; k < (n1 - n0) * a.statusWords; k += blockDim.x) {
+            const uint32_t node = n0 + k / a.statusWords, b = k % a.statusWords;
+            P.counters[node * 8u + b] = 0u;
+            P.errs[node * 8u + b] = 0xFFFFFFFFu;  // lowest failing entry, min-reduced
+            if (a.status != 0) store_status(a.status + node * 64ull + b * 8ull, 0ull);
         }
     }
     const int64_t *idx = reinterpret_cast<const int64_t *>(a.indicesHost);
     const unsigned long long tagHi = static_cast<unsigned long long>(*P.epoch) << 32;
     for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        uint32_t segRow;
-        if (!export_row_target(a, idx[i], segRow) || segRow >= a.perLayerSegRows) continue;
-        if (segRow < P.winEntries) atomicMax(&P.win[segRow], tagHi | static_cast<unsigned long long>(i));
+        uint32_t node, segRow;
+        if (!export_row_target(a, idx[i], node, segRow) || segRow >= a.perLayerSegRows) continue;
+        const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
+        if (w < P.winEntries) atomicMax(&P.win[w], tagHi | static_cast<unsigned long long>(i));
     }
 }
 
@@ -416,16 +422,18 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
         const int32_t i = base + static_cast<int32_t>(lane);
         bool copy = false;
         uint64_t src = 0, dst = 0;
-        uint32_t segRow;
-        if (i < n && export_row_target(a, idx[i], segRow)) {
-            const uint32_t key = a.myNode * 8u + static_cast<uint32_t>(i) / ppc;
+        uint32_t node, segRow;
+        if (i < n && export_row_target(a, idx[i], node, segRow)) {
+            const uint32_t key = node * 8u + static_cast<uint32_t>(i) / ppc;
             atomicAdd(&P.counters[key], 1u);
             if (segRow >= a.perLayerSegRows) {  // outside the segment's layer region: report, do not write
                 atomicMin(&P.errs[key], static_cast<uint32_t>(i));
             } else {
-                copy = segRow >= P.winEntries || P.win[segRow] == (tagHi | static_cast<unsigned long long>(i));
+                const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
+                copy = w >= P.winEntries || P.win[w] == (tagHi | static_cast<unsigned long long>(i));
                 src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
-                dst = a.segBase + (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;
+                dst = (a.fused ? P.segBases[node] : a.segBase) +
+                      (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;
             }
         }
         const uint64_t cm = __ballot(copy);
@@ -455,14 +463,16 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
     if (threadIdx.x == 0) *P.epoch = sEpoch;
     if (a.status == 0) return;
     __threadfence_system();
-    for (uint32_t b = threadIdx.x; b < words; b += blockDim.x) {
+    const uint32_t n0 = a.fused ? 0u : a.myNode, n1 = a.fused ? a.nodeNum : a.myNode + 1u;
+    for (uint32_t k = threadIdx.x; k < (n1 - n0) * words; k += blockDim.x) {
+        const uint32_t node = n0 + k / words, b = k % words;
         uint64_t word = 1ull << 32;
         if (static_cast<int64_t>(b) * ppc < n) {
-            const uint32_t q = __hip_atomic_load(&P.counters[a.myNode * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint32_t e = __hip_atomic_load(&P.errs[a.myNode * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t q = __hip_atomic_load(&P.counters[node * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t e = __hip_atomic_load(&P.errs[node * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             word |= (static_cast<uint64_t>(q) << 40) | (e == 0xFFFFFFFFu ? 0u : row_error_code(e));
         }
-        store_status(a.status + a.myNode * 64ull + b * 8ull, word);
+        store_status(a.status + node * 64ull + b * 8ull, word);
     }
 }
 
@@ -557,10 +567,14 @@ hipError_t launch_export(const KvcScatterAllArgs &a, const RowScratch &scr, uint
     return hipGetLastError();
 }
 
-hipError_t launch_export_rows(const ExportRowsArgs &a, const RowScratch &scr, hipStream_t stream)
+hipError_t launch_export_rows(const ExportRowsArgs &a, const uint64_t *segBases, const RowScratch &scr,
+                              hipStream_t stream)
 {
     ExportRowsParams P{};
     P.a = a;
+    if (a.fused) {
+        for (uint32_t s = 0; s < a.nodeNum && s < 64u; ++s) P.segBases[s] = segBases[s];
+    }
     P.win = scr.win;
     P.winEntries = scr.winEntries;
     P.counters = scr.counters;

@@ -269,6 +269,18 @@ class HostSegPool:
                                self.stripe_rows, self.node_num, s, status, stream, block_dim)
         return status
 
+    def batch_export_rows_fused(self, layer_id: int, src_layer_base, indices_host, num_real, max_rows: int,
+                                stream: int = 0, block_dim: int = 1) -> int:
+        """All N segments in one launch pair; same result and status words as
+        batch_export_rows."""
+        if self.pool is None:
+            raise RuntimeError("pool not created")
+        status = self.next_status()
+        _kvops.export_rows_all([sg.seg_base for sg in self.pool.segments], layer_id, self.per_layer_seg_rows,
+                               self.row_bytes, _ptr(src_layer_base), _ptr(indices_host), 0, _ptr(num_real), max_rows,
+                               self.stripe_rows, status, stream, block_dim)
+        return status
+
     # ---- completion (xds_ems_pool.py:233-241) ----
     def wait(self, status: int, timeout_us: int = 60_000_000, block_dim: int = 1) -> None:
         for s in range(self.node_num):

@@ -126,14 +126,15 @@ def test_status_poll_and_timeout(kvops):
     assert kvops.poll_status(12345, 10) == -0x1000
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("S,N,block_dim,max_rows,num_real", [(1, 2, 1, 64, 64), (1, 3, 3, 500, 377), (64, 4, 2, 256, 256),
                                                              (4, 2, 8, 1000, 999), (1, 1, 1, 40, 0)])
-def test_export_rows_parity(kvops, S, N, block_dim, max_rows, num_real):
+def test_export_rows_parity(kvops, S, N, block_dim, max_rows, num_real, fused):
     """Decode-incremental export of one layer into every segment against the
     oracle: host rows with duplicates (last entry wins), negative rows and rows
     outside the layer region (reported, not written), num_real below the
     capacity; all segment bytes and every node's status words."""
-    print("export_rows case", S, N, block_dim, max_rows, num_real, flush=True)
+    print("export_rows case", S, N, block_dim, max_rows, num_real, fused, flush=True)
     L, layer_rows = 3, 4096
     pool = HostSegPool(0, L, layer_rows, ROW, stripe_rows=S, node_num=N)
     pool.create_pool()
@@ -155,7 +156,8 @@ def test_export_rows_parity(kvops, S, N, block_dim, max_rows, num_real):
         idx_d = to_dev(idx)
         nr_d = to_dev(np.array([num_real], dtype=np.int32))
         layer = 1
-        status = pool.batch_export_rows(layer, src_d, idx_d, nr_d, max_rows, block_dim=block_dim)
+        export = pool.batch_export_rows_fused if fused else pool.batch_export_rows
+        status = export(layer, src_d, idx_d, nr_d, max_rows, block_dim=block_dim)
         torch.cuda.synchronize()  # (the status words carry error codes here, so no pool.wait)
         for s in range(N):
             _, words = orc.export_rows(expect[s], src.reshape(-1), idx, num_real, max_rows, layer, plsr, ROW, S, N, s,
