@@ -347,9 +347,16 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // demand they would each cost a round trip.
     asm volatile("" : : "s"(a.topkIndices), "s"(a.reqPoolIndices), "s"(a.seqLens), "s"(a.prefillLens),
                  "s"(a.deviceBufferTokens), "s"(a.deviceBufferVisited), "s"(a.deviceBufferHt), "s"(a.sieveHand),
-                 "s"(a.topKDeviceSlots), "s"(a.isMiss), "s"(a.numReal));
+                 "s"(a.topKDeviceSlots), "s"(a.isMiss), "s"(a.numReal), "s"(a.topK), "s"(a.maxNumReqs),
+                 "s"(a.htSize), "s"(a.poolSize), "s"(a.reserved));
 
+    // num_real and the batch row's request and length in one round trip (the
+    // row's entries exist for every bid < maxNumReqs, so they are read before
+    // num_real is known; the asm use keeps them ahead of the branch)
     int32_t numReal = *(KVX_C const int32_t *)(a.numReal);
+    const int64_t reqRaw = ((KVX_C const int64_t *)(a.reqPoolIndices))[bid];
+    const int32_t seqLen = ((KVX_C const int32_t *)(a.seqLens))[bid];
+    asm volatile("" : : "s"(reqRaw), "s"(seqLen));
     if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
     KVX_G int32_t *rs = (KVX_G int32_t *)(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
     KVX_G int8_t *rm = (KVX_G int8_t *)(a.isMiss) + static_cast<int64_t>(bid) * K;
@@ -357,12 +364,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
-    // the batch row's request, length and topK row in one round trip.  An
-    // invalid request index is acted on after staging (row 0, which exists,
-    // is staged meanwhile): an early exit here would let the compiler sink
-    // the loads below it, each then waited for on its own.
-    const int64_t reqRaw = ((KVX_C const int64_t *)(a.reqPoolIndices))[bid];
-    const int32_t seqLen = ((KVX_C const int32_t *)(a.seqLens))[bid];
+    // the topK row.  An invalid request index is acted on after staging (row
+    // 0, which exists, is staged meanwhile): an early exit here would let the
+    // compiler sink the loads below it, each then waited for on its own.
     KVX_G const int32_t *rt = (KVX_G const int32_t *)(a.topkIndices) + static_cast<int64_t>(bid) * K;
     // unconditional (clamped, K >= 1 here) loads: a load under a branch makes
     // the compiler wait for it at the branch's end
