@@ -538,10 +538,9 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     // grid-stride row tasks; 512 waves keep enough 16-byte reads in flight
-    // for the host link, and few workgroups keep the completion ticket cheap
-    uint64_t copyBlocks = (positions + 63ull) / 64ull;
-    if (copyBlocks < 1) copyBlocks = 1;
-    if (copyBlocks > 128) copyBlocks = 128;
+    // for the host link (and give a short list one row per wave: one host
+    // round trip), few workgroups keep the completion ticket cheap
+    const uint64_t copyBlocks = 128;
     hipLaunchKernelGGL(kvx_gather_copy, dim3(static_cast<uint32_t>(copyBlocks)), dim3(256), 0, stream, P);
     return hipGetLastError();
 }
