@@ -400,9 +400,12 @@ __global__ __launch_bounds__(256) void kvx_export_rows_prep(ExportRowsParams P)
     }
 }
 
-// Pass 2: each wave takes 64 entries, counts the owned ones per status word,
-// records out-of-segment rows and copies its winners; the last workgroup
-// advances the epoch and writes the status words.
+// Pass 2: each wave takes kExportRowsPerWave entries (a decode step exports
+// a few rows per layer: spread over many waves they move in one round trip),
+// counts the owned ones per status word, records out-of-segment rows and
+// copies its winners; the last workgroup advances the epoch and writes the
+// status words.
+constexpr int kExportRowsPerWave = 8;
 __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
 {
     __shared__ uint64_t sSrc[kWaves][64];
@@ -418,12 +421,13 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
     const uint32_t cpr = a.rowBytes / 16u;
     const uint32_t words = a.statusWords;
     const uint32_t ppc = (a.maxRows + words - 1u) / words;  // entries per status word
-    for (int32_t base = (blockIdx.x * kWaves + wave) * 64; base < n; base += gridDim.x * kWaves * 64) {
+    constexpr int32_t R = kExportRowsPerWave;
+    for (int32_t base = (blockIdx.x * kWaves + wave) * R; base < n; base += gridDim.x * kWaves * R) {
         const int32_t i = base + static_cast<int32_t>(lane);
         bool copy = false;
         uint64_t src = 0, dst = 0;
         uint32_t node, segRow;
-        if (i < n && export_row_target(a, idx[i], node, segRow)) {
+        if (static_cast<int32_t>(lane) < R && i < n && export_row_target(a, idx[i], node, segRow)) {
             const uint32_t key = node * 8u + static_cast<uint32_t>(i) / ppc;
             atomicAdd(&P.counters[key], 1u);
             if (segRow >= a.perLayerSegRows) {  // outside the segment's layer region: report, do not write
@@ -585,7 +589,7 @@ hipError_t launch_export_rows(const ExportRowsArgs &a, const uint64_t *segBases,
     hipLaunchKernelGGL(kvx_export_rows_prep, dim3(static_cast<uint32_t>(prep)), dim3(256), 0, stream, P);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    uint64_t copy = (static_cast<uint64_t>(a.maxRows) + 64ull * kWaves - 1ull) / (64ull * kWaves);
+    uint64_t copy = (static_cast<uint64_t>(a.maxRows) + kExportRowsPerWave * kWaves - 1ull) / (kExportRowsPerWave * kWaves);
     copy = copy < 1 ? 1 : (copy > 256 ? 256 : copy);
     hipLaunchKernelGGL(kvx_export_rows_copy, dim3(static_cast<uint32_t>(copy)), dim3(256), 0, stream, P);
     return hipGetLastError();
