@@ -19,7 +19,8 @@ Rules for the caller:
   topK buffers, the coordinator's ``_req_pool_indices`` / ``_seq_lens``,
   ``num_real`` through :meth:`set_num_real`) -- never rebind them;
 * :meth:`capture` first runs the step once with ``num_real = 0`` (no state
-  changes) so the library sizes its scratch buffers outside the capture;
+  or hot-row changes; the slot/miss output buffers get padding rows) so the
+  library sizes its scratch buffers outside the capture;
 * :meth:`replay` clears the host-visible status words before launching, and
   :meth:`wait` polls them like ``EmsPool.wait``; replays go on one stream
   (the import's scratch is shared by every call on the device).
