@@ -212,6 +212,34 @@ def graph_pass(runner, snap, warm, timed, fused, eager_ms, log):
     return res
 
 
+def sieve_pipelined(runner, snap, warm, timed, log):
+    """SIEVE alone over the timed layer-steps, launched back to back from the
+    same starting state with HIP events only around the whole sequence: the
+    per-layer cost in a stream of launches, without an event pair per launch.
+    The final state must equal the eager run's."""
+    import torch
+
+    c = runner.coord
+    names = ("device_buffer_tokens", "device_buffer_visited", "device_buffer_ht", "sieve_hand")
+    ref = [getattr(c, n).clone() for n in names]
+    runner.restore(snap)
+    for _, layer, topk_d, _, _ in warm:
+        runner.sieve(layer, topk_d)
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _, layer, topk_d, _, _ in timed:
+        runner.sieve(layer, topk_d)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / len(timed)
+    ok = all(torch.equal(a, getattr(c, n)) for a, n in zip(ref, names))
+    log("[bench] SIEVE back to back: {:.2f} us/layer over {} launches; state equal to the eager run: {}".format(
+        us, len(timed), ok))
+    return {"us_per_layer": us, "launches": len(timed), "state_match": ok}
+
+
 def export_rows_pass(runner, log, reps=3):
     """Decode-incremental export: one row per request per layer (the row a
     decode step would append; here the last prefill row, rewritten with the
@@ -479,6 +507,7 @@ def main():
         "roofline_other": other,
         "verify": ok,
     }
+    out["sieve_back_to_back"] = sieve_pipelined(runner, snap, warm, timed, log)
     out["graph"] = None if args.no_graph else graph_pass(runner, snap, warm, timed, fused, total_ms, log)
     out["export_rows"] = export_rows_pass(runner, log)
     if not args.no_cpu:
