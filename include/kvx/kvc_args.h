@@ -23,7 +23,7 @@
  * myNode is copied from segment row (layerOffsetRows + segRow) into hot row
  * slot (+ bid * hotReqStrideRows). */
 struct KvcGatherArgs {
-    uint64_t channel;          /* segment index on this build (HCOMM channel in the reference) */
+    uint64_t channel;          /* segment index in kvx (HCOMM channel in the reference) */
     uint64_t segBase;          /* device-visible address of the segment's first byte */
     uint64_t topkIndices;      /* int32 [maxNumReqs, topK] */
     uint64_t reqPoolIndices;   /* int64 [maxNumReqs] */

@@ -167,7 +167,7 @@ PYBIND11_MODULE(_kvops, m)
 
     m.def("close", []() { Check(kvx_close()); });
 
-    // ---- additions of this build (no counterpart in the reference) ----
+    // ---- additions of kvx (no counterpart in the reference) ----
     m.def(
         "host_alloc",
         [](uint64_t nbytes, bool coherent) {

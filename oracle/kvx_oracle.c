@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the decode-time KV data plane.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker: it is built into
+ * TEST INFRASTRUCTURE ONLY.  This file is a test oracle: it is built into
  * oracle/liboracle.so and loaded by tests/, by __graft_entry__.smoke() and by
  * bench.py's cpu_baseline leg.  Nothing in the product path links or calls it.
  *

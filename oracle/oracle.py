@@ -1,6 +1,6 @@
 """numpy/ctypes front end of the C oracle (oracle/kvx_oracle.c).
 
-TEST INFRASTRUCTURE ONLY (the checker): loaded by tests/, by
+TEST INFRASTRUCTURE ONLY: loaded by tests/, by
 __graft_entry__.smoke() and by bench.py's cpu_baseline leg.
 
 Functions mirror the reference's algorithms on numpy arrays:

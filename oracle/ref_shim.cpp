@@ -1,7 +1,7 @@
 // C entry points over two of the reference's own headers, compiled where the
 // reference is mounted (see Makefile target `ref`).  TEST INFRASTRUCTURE ONLY:
 // tests load oracle/_ref/libkvref.so to check the layout mapping and the
-// launch-argument byte layout of this build against the reference's code.
+// launch-argument byte layout of kvx against the reference's code.
 //
 //   kv_layout.h  (common/kv_layout.h:26-57)   -> kvref_node/seg_row/offset/validate
 //   kvc_args.h   (kvops/kernel/kvc_args.h)    -> kvref_args_layout (sizeof/offsetof)

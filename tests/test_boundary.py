@@ -44,7 +44,7 @@ REFERENCE_SURFACE = {
     "close": [],
 }
 
-# Arguments this build appends after the reference's (keyword, with defaults).
+# Arguments kvx appends after the reference's (keyword, with defaults).
 EXTENSIONS = {"import_seg": [("hot_req_stride_rows", "0")]}
 
 

@@ -1,6 +1,6 @@
 """Row-ownership mapping (common/kv_layout.h:26-57, kvc_common.h:81-89).
 
-Three implementations must agree: the oracle's C restatement, this build's
+Three implementations must agree: the oracle's C restatement, kvx's
 header include/kvx/kv_layout.h (compiled here with g++), and -- where the
 reference is mounted -- the reference's own kv_layout.h compiled into
 oracle/_ref/libkvref.so.  The known answers are the literals of the
