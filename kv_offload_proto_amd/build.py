@@ -5,7 +5,8 @@
 * ``kvops_ext/_kvops*.so`` -- the pybind11 module with the reference's
   ``kvops_ext._kvops`` surface, linked against libkvx.so (rpath $ORIGIN).
 
-Run ``python -m kv_offload_proto_amd.build`` (or call :func:`build`).
+Run ``python kv_offload_proto_amd/build.py`` (as a script: importing the package
+needs what this builds), or call :func:`build`.
 """
 import os
 import subprocess

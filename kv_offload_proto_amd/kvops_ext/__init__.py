@@ -18,7 +18,7 @@ try:
     from . import _kvops  # noqa: F401
 except ImportError as exc:  # pragma: no cover - exercised only on a broken install
     raise ImportError(
-        "kvops_ext native module is not built ({}); run `python -m kv_offload_proto_amd.build`".format(exc)
+        "kvops_ext native module is not built ({}); run `python kv_offload_proto_amd/build.py`".format(exc)
     ) from exc
 
 
