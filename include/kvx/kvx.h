@@ -16,6 +16,17 @@
  *     err (bits 0..31) | doneSeq=1 (bits 32..39) | queued (bits 40..63)
  * once every row of that launch has landed.  kvx_poll_status() masks the
  * doneSeq byte, so EmsPool-style waits that poll st + s*64 + b*8 work as-is.
+ *
+ * Streams and scratch: the row movers (import, export_rows, the prefill
+ * export) and the HBM-resident SIEVE variant keep device scratch (winner
+ * tags, a row list, counters, a table shadow).  The library holds one scratch
+ * set per stream: launches on one stream run in order and share it, launches
+ * on different streams (from any threads) never share it.  A stream's set is
+ * created by its first launch (the null stream's by kvx_init) and grows when
+ * a launch needs more; creation and growth allocate device memory and queue a
+ * clear on that stream, and are refused during stream capture, so a stream
+ * that will be captured is sized first with kvx_reserve_scratch.  Buffers are
+ * never freed before kvx_close (a captured graph may hold their addresses).
  */
 #ifndef KVX_KVX_H
 #define KVX_KVX_H
@@ -131,9 +142,24 @@ int kvx_sieve_ht_init(uint64_t device_buffer_tokens, uint64_t device_buffer_ht, 
                       uint32_t device_buffer_size, uint32_t padded_buffer_size, uint32_t ht_size,
                       uint64_t stream, uint32_t block_dim);
 
-/* kvops_ext.cpp:360-371 kv_close.  Frees the tail-slot word, the status
- * allocations and the library scratch; idempotent. */
+/* kvops_ext.cpp:360-371 kv_close.  Waits for the device, then frees the
+ * tail-slot word, the status allocations and every stream's scratch;
+ * idempotent. */
 int kvx_close(void);
+
+/* No counterpart in the reference (its launches keep no device scratch):
+ * size the scratch of `stream` so that later launches on it allocate
+ * nothing -- imports of up to max_num_reqs x top_k positions with
+ * hot_req_stride_rows, decode-incremental exports into segments of
+ * per_layer_seg_rows rows (node_num segments fused; 0 = none), and SIEVE
+ * updates of max_num_reqs rows of device_buffer_size slots with top_k
+ * positions (0 = none; only the HBM-resident variant keeps scratch).  Must be
+ * called before capturing launches on `stream`. */
+int kvx_reserve_scratch(uint64_t stream, uint32_t max_num_reqs, uint32_t top_k, uint32_t hot_req_stride_rows,
+                        uint32_t per_layer_seg_rows, uint32_t node_num, uint32_t device_buffer_size);
+
+/* Device bytes held by the scratch of `stream` (0 if it has none). */
+int kvx_scratch_bytes(uint64_t stream, uint64_t *out_bytes);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *kvx_last_error(void);

@@ -183,6 +183,23 @@ PYBIND11_MODULE(_kvops, m)
         return v;
     });
     m.def("clear_overflow", []() { Check(kvx_clear_overflow()); });
+    m.def(
+        "reserve_scratch",
+        [](uint64_t stream, uint32_t max_num_reqs, uint32_t top_k, uint32_t hot_req_stride_rows,
+           uint32_t per_layer_seg_rows, uint32_t node_num, uint32_t device_buffer_size) {
+            Check(kvx_reserve_scratch(stream, max_num_reqs, top_k, hot_req_stride_rows, per_layer_seg_rows, node_num,
+                                      device_buffer_size));
+        },
+        py::arg("stream"), py::arg("max_num_reqs"), py::arg("top_k"), py::arg("hot_req_stride_rows") = 0,
+        py::arg("per_layer_seg_rows") = 0, py::arg("node_num") = 0, py::arg("device_buffer_size") = 0);
+    m.def(
+        "scratch_bytes",
+        [](uint64_t stream) {
+            uint64_t b = 0;
+            Check(kvx_scratch_bytes(stream, &b));
+            return b;
+        },
+        py::arg("stream") = 0);
     m.def("last_sieve_variant", []() { return kvx_last_sieve_variant(); });
     m.def("sieve_force_variant", [](int variant) { Check(kvx_sieve_force_variant(variant)); }, py::arg("variant"));
     m.def(

@@ -28,15 +28,25 @@ struct Alloc {
     uint64_t bytes;
 };
 
+// Scratch of the launches on one stream.  Launches on one stream run in
+// order, so they share it; launches on different streams never do.  Buffers
+// only grow, and a replaced buffer is kept until kvx_close: a captured graph
+// or a launch still in flight may hold its address.
+struct StreamScratch {
+    uint64_t stream = 0;
+    kvx::RowScratch rows{};
+    int32_t *shadow = nullptr;      // HBM-resident SIEVE variant: per-cell token shadow
+    uint64_t shadowCells = 0;
+};
+
 struct State {
     bool inited = false;
     int device = 0;
     uint64_t *overflow = nullptr;   // the 8-byte tail-slot word
     size_t ldsLimit = 0;            // dynamic LDS per workgroup usable by SIEVE
     std::vector<Alloc> status;      // kvx_alloc_status allocations
-    kvx::RowScratch scratch{};
-    int32_t *shadow = nullptr;      // wave-wide SIEVE variant: table shadow
-    uint64_t shadowCells = 0;
+    std::vector<StreamScratch *> scratch;  // one per stream that launched or reserved
+    std::vector<void *> retired;    // replaced scratch buffers, freed by kvx_close
     int lastSieveVariant = -1;
     int forcedSieveVariant = -1;
 };
@@ -45,6 +55,7 @@ State g;
 std::mutex g_hostMu;
 std::map<uint64_t, uint64_t> g_hostAllocs;  // kvx_host_alloc: addr -> bytes
 std::mutex g_statusMu;
+std::mutex g_scratchMu;
 
 struct Error : std::runtime_error {
     using std::runtime_error::runtime_error;
@@ -121,57 +132,132 @@ void CheckStatusBlock(uint64_t status, uint32_t firstNode, uint32_t nodes, uint3
     }
 }
 
-void EnsureWinScratch(uint64_t entries)
+// Scratch needs of one launch (entries of each buffer; 0 = not used).
+struct ScratchNeed {
+    uint64_t win = 0, list = 0, shadow = 0;
+};
+
+bool Capturing(hipStream_t s)
 {
-    if (g.scratch.winEntries >= entries) return;
-    uint64_t cap = std::max<uint64_t>(entries, 65536);
-    if (g.scratch.win != nullptr) {
-        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
-        hipCheck(hipFree(g.scratch.win), "hipFree");
-        g.scratch.win = nullptr;
-        g.scratch.winEntries = 0;
-    }
-    void *p = nullptr;
-    hipCheck(hipMalloc(&p, cap * sizeof(unsigned long long)), "hipMalloc(gather scratch)");
-    hipCheck(hipMemset(p, 0, cap * sizeof(unsigned long long)), "hipMemset(gather scratch)");
-    g.scratch.win = static_cast<unsigned long long *>(p);
-    g.scratch.winEntries = cap;  // a zeroed table is valid under any epoch
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
 
-// Grow-only shadow table (one int32 per hash-table cell per batch row) of the
-// wave-wide HBM SIEVE variant.
-int32_t *EnsureShadow(uint64_t cells)
+// Device buffer of `bytes` zeroed in order on `stream` (no host sync).
+void *ScratchAlloc(uint64_t bytes, hipStream_t stream, const char *what)
 {
-    if (g.shadowCells >= cells) return g.shadow;
-    if (g.shadow != nullptr) {
-        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
-        hipCheck(hipFree(g.shadow), "hipFree");
-        g.shadow = nullptr;
-        g.shadowCells = 0;
-    }
     void *p = nullptr;
-    hipCheck(hipMalloc(&p, cells * sizeof(int32_t)), "hipMalloc(sieve shadow)");
-    g.shadow = static_cast<int32_t *>(p);
-    g.shadowCells = cells;
-    return g.shadow;
+    hipCheck(hipMalloc(&p, bytes), (std::string("hipMalloc(") + what + ")").c_str());
+    const hipError_t e = hipMemsetAsync(p, 0, bytes, stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        hipCheck(e, "hipMemsetAsync(scratch)");
+    }
+    return p;
 }
 
-// Grow-only gather row list (source and destination addresses per row).
-void EnsureListScratch(uint64_t entries)
+// The scratch of `stream`, created or grown to `need`.  Creation and growth
+// allocate and queue a clear on the stream; both are refused while the stream
+// is being captured (kvx_reserve_scratch sizes a stream beforehand).  The
+// caller holds g_scratchMu.
+StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *what)
 {
-    if (g.scratch.listCap >= entries) return;
-    const uint64_t cap = std::max<uint64_t>(entries, 65536);
-    if (g.scratch.listSrc != nullptr) {
-        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
-        hipCheck(hipFree(g.scratch.listSrc), "hipFree");
-        g.scratch.listSrc = g.scratch.listDst = nullptr;
-        g.scratch.listCap = 0;
+    StreamScratch *sc = nullptr;
+    for (StreamScratch *s : g.scratch) {
+        if (s->stream == stream) sc = s;
     }
-    void *p = nullptr;
-    hipCheck(hipMalloc(&p, 2 * cap * sizeof(uint64_t)), "hipMalloc(gather list)");
-    g.scratch.listSrc = static_cast<uint64_t *>(p);
-    g.scratch.listDst = g.scratch.listSrc + cap;
-    g.scratch.listCap = cap;
+    const bool create = sc == nullptr;
+    const bool grow = create || sc->rows.winEntries < need.win || sc->rows.listCap < need.list ||
+                      sc->shadowCells < need.shadow;
+    if (!grow) return *sc;
+    hipStream_t st = AsStream(stream);
+    if (Capturing(st)) {
+        throw Error(std::string(what) + ": the scratch of this stream is too small for the call and cannot grow "
+                    "during stream capture; call reserve_scratch for the stream before capturing");
+    }
+    if (create) {
+        auto *s = new StreamScratch();
+        s->stream = stream;
+        uint32_t *c = static_cast<uint32_t *>(ScratchAlloc(kvx::kControlWords * sizeof(uint32_t), st, "scratch control"));
+        s->rows.counters = c;
+        s->rows.errs = c + 64 * 8;
+        s->rows.tickets = c + 2 * 64 * 8;
+        s->rows.listCount = s->rows.tickets + 8;
+        s->rows.epoch = s->rows.tickets + 9;
+        g.scratch.push_back(s);
+        sc = s;
+    }
+    kvx::RowScratch &r = sc->rows;
+    if (r.winEntries < need.win) {
+        // a zeroed table is valid under any epoch
+        const uint64_t cap = std::max<uint64_t>(need.win, std::max<uint64_t>(2 * r.winEntries, 65536));
+        void *p = ScratchAlloc(cap * sizeof(unsigned long long), st, "winner table");
+        if (r.win != nullptr) g.retired.push_back(r.win);
+        r.win = static_cast<unsigned long long *>(p);
+        r.winEntries = cap;
+    }
+    if (r.listCap < need.list) {
+        const uint64_t cap = std::max<uint64_t>(need.list, std::max<uint64_t>(2 * r.listCap, 65536));
+        void *p = ScratchAlloc(2 * cap * sizeof(uint64_t), st, "row list");
+        if (r.listSrc != nullptr) g.retired.push_back(r.listSrc);
+        r.listSrc = static_cast<uint64_t *>(p);
+        r.listDst = r.listSrc + cap;
+        r.listCap = cap;
+    }
+    if (sc->shadowCells < need.shadow) {
+        void *p = ScratchAlloc(need.shadow * sizeof(int32_t), st, "sieve shadow");
+        if (sc->shadow != nullptr) g.retired.push_back(sc->shadow);
+        sc->shadow = static_cast<int32_t *>(p);
+        sc->shadowCells = need.shadow;
+    }
+    return *sc;
+}
+
+// The SIEVE kernel a row shape launches: 2 = parallel LDS kernel, 4 = the same
+// with the compact LDS layout (token hashes in LDS, tokens in HBM), 0 =
+// sequential LDS kernel, 3 = sequential HBM-resident kernel with wave-wide
+// probes (1 = the single-lane HBM kernel, only when forced).
+struct SievePlan {
+    int variant = 0;
+    size_t ldsLaunch = 0;   // dynamic LDS of the launch
+    uint32_t invCap = 0;    // entries of the parallel kernel's token -> slot map
+};
+
+SievePlan PlanSieve(uint32_t top_k, uint32_t dbs, uint32_t padded, uint32_t visStrideB, uint32_t poolSize,
+                    uint32_t htSize)
+{
+    SievePlan p;
+    const size_t lds = static_cast<size_t>(padded) * 4 + static_cast<size_t>(htSize) * 2 + visStrideB;
+    const bool fastShape = top_k >= 1 && poolSize >= 1 && top_k < 0x3FFF &&
+                           static_cast<uint64_t>(padded) + 1 + top_k <= 65535 && dbs <= 32u * kvx::kFastThreads &&
+                           htSize <= 32768;
+    const size_t ldsFast = kvx::fast_layout_for(padded, htSize, top_k, dbs, visStrideB, false).total;
+    const size_t ldsCompact = kvx::fast_layout_for(padded, htSize, top_k, dbs, visStrideB, true).total;
+    const bool fastOk = fastShape && ldsFast <= g.ldsLimit;
+    const bool compactOk = fastShape && ldsCompact <= g.ldsLimit && lds <= g.ldsLimit;
+    int v = fastOk ? 2 : (compactOk ? 4 : (lds <= g.ldsLimit ? 0 : 3));
+    const int f = g.forcedSieveVariant;
+    if (f == 0 && lds <= g.ldsLimit) v = 0;
+    if (f == 1) v = 1;
+    if (f == 2 && fastOk) v = 2;
+    if (f == 3) v = 3;
+    if (f == 4 && compactOk) v = 4;
+    p.variant = v;
+    p.ldsLaunch = v == 2 ? ldsFast : (v == 4 ? std::max(ldsCompact, lds) : (v == 0 ? lds : 0));
+    // the parallel kernel's direct token -> slot map takes the LDS left over
+    // (rows whose prefill exceeds it probe the table instead)
+    if (v == 2 && g.ldsLimit > ldsFast) {
+        p.invCap = static_cast<uint32_t>(std::min<size_t>((g.ldsLimit - ldsFast) / 2, 65536)) & ~15u;
+        p.ldsLaunch = ldsFast + static_cast<size_t>(p.invCap) * 2;
+    }
+    return p;
+}
+
+ScratchNeed SieveScratchNeed(const SievePlan &p, uint32_t maxNumReqs, uint32_t htSize)
+{
+    ScratchNeed n;
+    if (p.variant == 3) n.shadow = static_cast<uint64_t>(maxNumReqs) * htSize;
+    return n;
 }
 
 struct GatherCall {
@@ -230,18 +316,23 @@ void DoGather(const GatherCall &c)
     plan.spanRows = c.stride == 0 ? 0u : std::min<uint32_t>(c.stride, 65536u);
     plan.statusWords = bd;
 
-    const uint64_t need = static_cast<uint64_t>(c.maxNumReqs - 1) * plan.spanRows + 65536ull;
-    EnsureWinScratch(need);
-    EnsureListScratch(positions);
+    ScratchNeed need;
+    need.win = kvx::gather_win_entries(c.maxNumReqs, c.stride);
+    need.list = positions;
     hipStream_t st = AsStream(c.stream);
     if (c.fused) {
         CheckStatusBlock(c.status, 0, c.nodeNum, bd, "import_all");
-        for (uint32_t s = 0; s < c.nodeNum; ++s) ClearStatusWords(c.status, s, bd);
     } else {
         CheckStatusBlock(c.status, c.myNode, 1, bd, "import_seg");
+    }
+    std::lock_guard<std::mutex> lk(g_scratchMu);
+    const kvx::RowScratch scr = ScratchFor(c.stream, need, c.fused ? "import_all" : "import_seg").rows;
+    if (c.fused) {
+        for (uint32_t s = 0; s < c.nodeNum; ++s) ClearStatusWords(c.status, s, bd);
+    } else {
         ClearStatusWords(c.status, c.myNode, bd);
     }
-    hipCheck(kvx::launch_gather(plan, g.scratch, reinterpret_cast<uint64_t>(g.overflow), st), "kvc_gather_rows launch");
+    hipCheck(kvx::launch_gather(plan, scr, reinterpret_cast<uint64_t>(g.overflow), st), "kvc_gather_rows launch");
 }
 
 void DoExportRows(const uint64_t *segBases, bool fused, uint32_t layer_id, uint32_t per_layer_seg_rows,
@@ -274,15 +365,21 @@ void DoExportRows(const uint64_t *segBases, bool fused, uint32_t layer_id, uint3
     a.myNode = fused ? 0u : my_node;
     a.statusWords = block_dim == 0 ? 1u : block_dim;
     a.fused = fused ? 1u : 0u;
-    EnsureWinScratch(std::max<uint64_t>(static_cast<uint64_t>(per_layer_seg_rows) * (fused ? node_num : 1u), 1));
+    ScratchNeed need;
+    need.win = kvx::export_rows_win_entries(per_layer_seg_rows, fused ? node_num : 1u);
     if (fused) {
         CheckStatusBlock(status, 0, node_num, a.statusWords, "export_rows_all");
-        for (uint32_t s = 0; s < node_num; ++s) ClearStatusWords(status, s, a.statusWords);
     } else {
         CheckStatusBlock(status, my_node, 1, a.statusWords, "export_rows");
+    }
+    std::lock_guard<std::mutex> lk(g_scratchMu);
+    const kvx::RowScratch scr = ScratchFor(stream, need, fused ? "export_rows_all" : "export_rows").rows;
+    if (fused) {
+        for (uint32_t s = 0; s < node_num; ++s) ClearStatusWords(status, s, a.statusWords);
+    } else {
         ClearStatusWords(status, my_node, a.statusWords);
     }
-    hipCheck(kvx::launch_export_rows(a, segBases, g.scratch, AsStream(stream)), "export_rows launch");
+    hipCheck(kvx::launch_export_rows(a, segBases, scr, AsStream(stream)), "export_rows launch");
 }
 
 }  // namespace
@@ -309,16 +406,58 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         g.ldsLimit = static_cast<size_t>(lds) - 1024;  // room for the kernels' static LDS (under 1 KiB)
         hipCheck(kvx::sieve_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS)");
         hipCheck(kvx::sieve_fast_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS fast)");
-        void *c = nullptr;
-        constexpr size_t kTable = 64 * 8 * sizeof(uint32_t);
-        hipCheck(hipMalloc(&c, 2 * kTable + 64), "hipMalloc(counters)");
-        hipCheck(hipMemset(c, 0, 2 * kTable + 64), "hipMemset(counters)");
-        g.scratch.counters = static_cast<uint32_t *>(c);
-        g.scratch.errs = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + kTable);
-        g.scratch.tickets = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(c) + 2 * kTable);
-        g.scratch.listCount = g.scratch.tickets + 8;
-        g.scratch.epoch = g.scratch.tickets + 9;
+        {
+            // the null stream's scratch at a default size, so that callers on
+            // the null stream start without an allocation on the launch path
+            std::lock_guard<std::mutex> lk(g_scratchMu);
+            ScratchNeed need;
+            need.win = 65536;
+            need.list = 65536;
+            (void)ScratchFor(0, need, "init");
+        }
+        hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
         g.inited = true;
+    });
+}
+
+int kvx_reserve_scratch(uint64_t stream, uint32_t max_num_reqs, uint32_t top_k, uint32_t hot_req_stride_rows,
+                        uint32_t per_layer_seg_rows, uint32_t node_num, uint32_t device_buffer_size)
+{
+    return Guarded([&] {
+        EnsureInited();
+        if (node_num > 64) throw Error("reserve_scratch: node_num must be in [0, 64]");
+        ScratchNeed need;
+        need.list = static_cast<uint64_t>(max_num_reqs) * top_k;
+        need.win = std::max(kvx::gather_win_entries(max_num_reqs, hot_req_stride_rows),
+                            kvx::export_rows_win_entries(per_layer_seg_rows, std::max<uint32_t>(node_num, 1u)));
+        if (device_buffer_size > 0 && max_num_reqs > 0) {
+            // the shape rules of the coordinator and kvops_ext.cpp:288-300
+            const uint32_t padded = (device_buffer_size + 15u) & ~15u;
+            const uint32_t vis = ((padded + 7u) / 8u + 63u) & ~63u;
+            uint64_t ht = 1024;
+            while (ht < 2ull * (static_cast<uint64_t>(padded) + top_k)) ht <<= 1;
+            if (padded <= 65534 && ht <= (1ull << 31)) {
+                const SievePlan p = PlanSieve(top_k, device_buffer_size, padded, vis, 1, static_cast<uint32_t>(ht));
+                need.shadow = SieveScratchNeed(p, max_num_reqs, static_cast<uint32_t>(ht)).shadow;
+            }
+        }
+        std::lock_guard<std::mutex> lk(g_scratchMu);
+        (void)ScratchFor(stream, need, "reserve_scratch");
+    });
+}
+
+int kvx_scratch_bytes(uint64_t stream, uint64_t *out_bytes)
+{
+    return Guarded([&] {
+        EnsureInited();
+        std::lock_guard<std::mutex> lk(g_scratchMu);
+        uint64_t b = 0;
+        for (const StreamScratch *s : g.scratch) {
+            if (s->stream != stream) continue;
+            b = kvx::kControlWords * sizeof(uint32_t) + s->rows.winEntries * sizeof(unsigned long long) +
+                s->rows.listCap * 2 * sizeof(uint64_t) + s->shadowCells * sizeof(int32_t);
+        }
+        *out_bytes = b;
     });
 }
 
@@ -490,8 +629,10 @@ int kvx_export_seg_alllayer(uint64_t channel, uint64_t seg_base, uint32_t per_la
             throw Error("export_seg_alllayer: rows [row_lo, row_lo+row_cnt) exceed per_layer_seg_rows of the segment");
         }
         CheckStatusBlock(status, my_node, 1, a.blockDim, "export_seg_alllayer");
+        std::lock_guard<std::mutex> lk(g_scratchMu);
+        const kvx::RowScratch scr = ScratchFor(stream, ScratchNeed{}, "export_seg_alllayer").rows;
         ClearStatusWords(status, my_node, a.blockDim);
-        hipCheck(kvx::launch_export(a, g.scratch, reinterpret_cast<uint64_t>(g.overflow), AsStream(stream)),
+        hipCheck(kvx::launch_export(a, scr, reinterpret_cast<uint64_t>(g.overflow), AsStream(stream)),
                  "kvc_scatter_rows_alllayer launch");
     });
 }
@@ -584,47 +725,24 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
         a.reqsPerCore = static_cast<uint32_t>(rpc);
         a.htSize = static_cast<uint32_t>(htSize);
         a.poolSize = pool_size;
-        // Variant: 2 = parallel LDS kernel, 4 = the same with the compact LDS layout (token
-        // hashes in LDS, tokens in HBM), 0 = sequential LDS kernel, 3 = sequential HBM-resident
-        // with wave-wide probes (1 = the single-lane HBM kernel, by request only).
-        const size_t lds = static_cast<size_t>(padded_buffer_size) * 4 + static_cast<size_t>(htSize) * 2 +
-                           visited_stride_b;
-        const bool fastShape = top_k >= 1 && pool_size >= 1 && top_k < 0x3FFF && static_cast<uint64_t>(padded_buffer_size) + 1 + top_k <= 65535 &&
-                               device_buffer_size <= 32u * kvx::kFastThreads && htSize <= 32768;
-        const size_t ldsFast = kvx::fast_layout_for(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
-                                                    device_buffer_size, visited_stride_b, false).total;
-        const size_t ldsCompact = kvx::fast_layout_for(padded_buffer_size, static_cast<uint32_t>(htSize), top_k,
-                                                       device_buffer_size, visited_stride_b, true).total;
-        const bool fastOk = fastShape && ldsFast <= g.ldsLimit;
-        const bool compactOk = fastShape && ldsCompact <= g.ldsLimit && lds <= g.ldsLimit;
-        int variant = fastOk ? 2 : (compactOk ? 4 : (lds <= g.ldsLimit ? 0 : 3));
-        if (g.forcedSieveVariant == 0 && lds <= g.ldsLimit) variant = 0;
-        if (g.forcedSieveVariant == 1) variant = 1;
-        if (g.forcedSieveVariant == 2 && fastOk) variant = 2;
-        if (g.forcedSieveVariant == 3) variant = 3;
-        if (g.forcedSieveVariant == 4 && compactOk) variant = 4;
-        // the parallel kernel's direct token -> slot map takes the LDS left over
-        // (rows whose prefill exceeds it probe the table instead)
-        uint32_t invCap = 0;
-        size_t ldsLaunch = variant == 2 ? ldsFast : std::max(ldsCompact, lds);
-        if (variant == 2 && g.ldsLimit > ldsFast) {
-            invCap = static_cast<uint32_t>(std::min<size_t>((g.ldsLimit - ldsFast) / 2, 65536)) & ~15u;
-            ldsLaunch = ldsFast + static_cast<size_t>(invCap) * 2;
-        }
-        a.reserved = static_cast<uint32_t>(variant) | (invCap << 8);
-        g.lastSieveVariant = variant;
+        const SievePlan plan = PlanSieve(top_k, device_buffer_size, padded_buffer_size, visited_stride_b, pool_size,
+                                         static_cast<uint32_t>(htSize));
+        a.reserved = static_cast<uint32_t>(plan.variant) | (plan.invCap << 8);
+        g.lastSieveVariant = plan.variant;
         if (max_num_reqs == 0) return;
-        if (variant == 2 || variant == 4) {
-            hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow), ldsLaunch, variant == 4,
-                                                   AsStream(stream)),
+        if (plan.variant == 2 || plan.variant == 4) {
+            hipCheck(kvx::launch_sieve_update_fast(a, reinterpret_cast<uint64_t>(g.overflow), plan.ldsLaunch,
+                                                   plan.variant == 4, AsStream(stream)),
                      "hisp_sieve_update launch");
-        } else if (variant == 3) {
-            int32_t *shadow = EnsureShadow(static_cast<uint64_t>(max_num_reqs) * static_cast<uint64_t>(htSize));
+        } else if (plan.variant == 3) {
+            std::lock_guard<std::mutex> lk(g_scratchMu);
+            int32_t *shadow = ScratchFor(stream, SieveScratchNeed(plan, max_num_reqs, static_cast<uint32_t>(htSize)),
+                                         "sieve_update").shadow;
             hipCheck(kvx::launch_sieve_update_wave(a, reinterpret_cast<uint64_t>(g.overflow), shadow, AsStream(stream)),
                      "hisp_sieve_update launch");
         } else {
-            hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), variant,
-                                              variant == 0 ? lds : 0, AsStream(stream)),
+            hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), plan.variant,
+                                              plan.variant == 0 ? plan.ldsLaunch : 0, AsStream(stream)),
                      "hisp_sieve_update launch");
         }
     });
@@ -666,15 +784,22 @@ int kvx_sieve_ht_init(uint64_t device_buffer_tokens, uint64_t device_buffer_ht, 
 int kvx_close(void)
 {
     return Guarded([&] {
+        if (g.inited) (void)hipDeviceSynchronize();  // nothing in flight may still use the scratch
         if (g.overflow != nullptr) (void)hipFree(g.overflow);
         g.overflow = nullptr;
-        if (g.scratch.win != nullptr) (void)hipFree(g.scratch.win);
-        if (g.scratch.listSrc != nullptr) (void)hipFree(g.scratch.listSrc);
-        if (g.shadow != nullptr) (void)hipFree(g.shadow);
-        g.shadow = nullptr;
-        g.shadowCells = 0;
-        if (g.scratch.counters != nullptr) (void)hipFree(g.scratch.counters);
-        g.scratch = kvx::RowScratch{};
+        {
+            std::lock_guard<std::mutex> lk(g_scratchMu);
+            for (StreamScratch *s : g.scratch) {
+                if (s->rows.win != nullptr) (void)hipFree(s->rows.win);
+                if (s->rows.listSrc != nullptr) (void)hipFree(s->rows.listSrc);
+                if (s->rows.counters != nullptr) (void)hipFree(s->rows.counters);
+                if (s->shadow != nullptr) (void)hipFree(s->shadow);
+                delete s;
+            }
+            g.scratch.clear();
+            for (void *p : g.retired) (void)hipFree(p);
+            g.retired.clear();
+        }
         {
             std::lock_guard<std::mutex> lk(g_statusMu);
             for (const Alloc &a : g.status) (void)hipHostFree(reinterpret_cast<void *>(a.addr));

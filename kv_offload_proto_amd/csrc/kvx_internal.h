@@ -37,20 +37,42 @@ __host__ __device__ __forceinline__ uint32_t row_error_code(uint64_t pos)
 constexpr int32_t kHandStride = 16;
 
 // ---------------------------------------------------------------------------
-// Scratch owned by the library (one per device), used by the row movers.
+// Scratch of the row movers.  The library keeps one set per stream (launches
+// on one stream run in order and may share it; launches on different streams
+// never do); the no-allocation entry point uses a fixed device array.
 // ---------------------------------------------------------------------------
 struct RowScratch {
     unsigned long long *win;   // winner tags, (epoch << 32) | position
     uint64_t winEntries;       // capacity of win[]
     uint32_t *counters;        // [64 nodes][8 status words] queued counts
     uint32_t *errs;            // [64 nodes][8 status words] first error code
-    uint32_t *tickets;         // [4] last-block tickets (gather, export)
+    uint32_t *tickets;         // [8] last-block tickets (gather, export, export_rows)
     uint32_t *epoch;           // gather winner-tag epoch, advanced on the device by each call
     uint64_t *listSrc;         // gather row list: source byte addresses
     uint64_t *listDst;         // gather row list: destination byte addresses
     uint64_t listCap;          // capacity of the row list
     uint32_t *listCount;       // rows listed by the current gather
 };
+
+// Control words of one scratch set: counters, error words, tickets, the list
+// count and the epoch, in this order (kControlWords uint32 words).
+constexpr uint32_t kControlWords = 64 * 8 * 2 + 8 + 8;
+
+// Winner-table entries an import needs: request b's destinations are
+// b*spanRows + slot with slot < 65536 (uint16 slot numbers).
+__host__ __device__ __forceinline__ uint64_t gather_win_entries(uint32_t maxNumReqs, uint32_t hotReqStrideRows)
+{
+    const uint64_t span = hotReqStrideRows == 0 ? 0ull : (hotReqStrideRows < 65536u ? hotReqStrideRows : 65536u);
+    return (maxNumReqs == 0 ? 0ull : static_cast<uint64_t>(maxNumReqs - 1u) * span) + 65536ull;
+}
+
+// Winner-table entries a decode-incremental export needs: one per segment row
+// of the layer, for one segment or (fused) every segment.
+__host__ __device__ __forceinline__ uint64_t export_rows_win_entries(uint32_t perLayerSegRows, uint32_t segments)
+{
+    const uint64_t n = static_cast<uint64_t>(perLayerSegRows) * segments;
+    return n == 0 ? 1ull : n;
+}
 
 // ---------------------------------------------------------------------------
 // LDS layout of the parallel SIEVE kernel (byte offsets, 16-byte aligned):

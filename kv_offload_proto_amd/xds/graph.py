@@ -18,15 +18,16 @@ Rules for the caller:
 * the captured tensors are fixed: write new inputs into them in place (the
   topK buffers, the coordinator's ``_req_pool_indices`` / ``_seq_lens``,
   ``num_real`` through :meth:`set_num_real`) -- never rebind them;
-* :meth:`capture` first runs the step once with ``num_real = 0`` (no state
-  or hot-row changes; the slot/miss output buffers get padding rows) so the
-  library sizes its scratch buffers outside the capture;
+* :meth:`capture` records on a stream of its own (or the one given), whose
+  library scratch it first sizes with ``reserve_scratch`` so that nothing is
+  allocated during the capture; the graph's launches keep that stream's
+  scratch, so replays of one graph must not overlap each other or eager
+  launches on the capture stream;
 * :meth:`replay` clears the host-visible status words before launching, and
-  :meth:`wait` polls them like ``EmsPool.wait``; replays go on one stream
-  (the import's scratch is shared by every call on the device).
+  :meth:`wait` polls them like ``EmsPool.wait``.
 """
 import ctypes
-from typing import List, Sequence
+from typing import List, Optional, Sequence
 
 import torch
 
@@ -39,7 +40,8 @@ def _ptr(x) -> int:
 
 class DecodeStepGraph:
     def __init__(self, coord, pool, layers: Sequence[int], topk: Sequence[torch.Tensor], hot: Sequence,
-                 hot_req_stride_rows: int = 0, block_dim: int = 1, sieve_block_dim: int = 8):
+                 hot_req_stride_rows: int = 0, block_dim: int = 1, sieve_block_dim: int = 8,
+                 capture_stream: Optional[torch.cuda.Stream] = None):
         if len(layers) != len(topk) or len(layers) != len(hot):
             raise ValueError("layers, topk and hot must have one entry per layer")
         if pool.pool is None:
@@ -56,6 +58,7 @@ class DecodeStepGraph:
         self.n_slots = pool.node_num * len(self.layers)
         self.status_base = _kvops.alloc_status(self.n_slots)
         self.graph = None
+        self.capture_stream = capture_stream
 
     def status_of(self, i: int) -> int:
         """Status address of the i-th captured layer (node s at +s*64)."""
@@ -76,14 +79,13 @@ class DecodeStepGraph:
         c = self.coord
         if c._req_pool_indices is None:
             raise RuntimeError("set_batch must be called before capture")
-        torch.cuda.synchronize()
-        saved = c.num_real.clone()
-        c.num_real.zero_()
-        self._run()  # sizes the library's scratch; num_real = 0 leaves the state untouched
-        c.num_real.copy_(saved)
+        if self.capture_stream is None:
+            self.capture_stream = torch.cuda.Stream(device=c.device)  # default priority
+        _kvops.reserve_scratch(self.capture_stream.cuda_stream, c.max_num_reqs, c.top_k, self.stride, 0, 0,
+                               c.device_buffer_size)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=self.capture_stream):
             self._run()
         torch.cuda.synchronize()
 

@@ -47,3 +47,10 @@ class DevSieve:
         np.testing.assert_array_equal(self.hand.cpu().numpy()[sl][..., 0], st.hand[sl][..., 0])
         if check_ht:
             np.testing.assert_array_equal(self.ht.cpu().numpy().view(np.uint16)[sl], st.ht[sl])
+
+
+def read_words(addr, n):
+    """n status words (uint64) at a host-visible status address."""
+    import ctypes
+
+    return [int(x) for x in (ctypes.c_uint64 * n).from_address(addr)]

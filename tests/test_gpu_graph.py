@@ -1,8 +1,8 @@
 """Decode-step graph capture (SIEVE update + fused import of every layer):
-each replay must leave the same state, outputs, hot rows and status words as
-the eager calls on the same inputs, for full batches and padded ones
-(num_real below the captured maximum), and 1000 replays must not grow device
-memory (doc/kv_offload_design.md:84,94)."""
+each replay must leave the state, outputs, hot rows and status words that the
+oracle computes for the same inputs, and the same as the eager calls, for
+full batches and padded ones (num_real below the captured maximum), and 1000
+replays must not grow device memory (doc/kv_offload_design.md:84,94,477)."""
 import ctypes
 
 import numpy as np
@@ -11,6 +11,7 @@ import torch
 
 from kv_offload_proto_amd.kvops_ext import _kvops
 from kv_offload_proto_amd.xds import DecodeStepGraph, HostSegPool, XdsOffloadCoordinator, streams
+from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -60,6 +61,14 @@ def test_graph_replay_matches_eager(kvops, L, req, prefill, top_k, dbs, N):
         for a, b in zip(_state(ce)[:4], _state(cg)[:4]):
             np.testing.assert_array_equal(a, b)
         st_e = _kvops.alloc_status(N)
+        # the oracle twin: same admission, same batches, same num_real
+        orc_st = orc.SieveState(L, req, dbs, top_k)
+        for r in range(req):
+            orc_st.admit(r, prefill)
+        hot_o = np.zeros((L, req * padded, ROW), dtype=np.uint8)
+        segs = [v.reshape(-1) for v in pool.segment_views()]
+        plsr = pool.per_layer_seg_rows
+        pool_idx, seq = np.arange(req, dtype=np.int64), np.full(req, prefill, dtype=np.int32)
         rng = np.random.default_rng(17)
         for step, nr in enumerate([req, req, req // 2 + 1, req, 1, 0, req]):
             batches = []
@@ -91,6 +100,21 @@ def test_graph_replay_matches_eager(kvops, L, req, prefill, top_k, dbs, N):
             for name, a, b in zip(["tokens", "visited", "ht", "hand", "slots", "is_miss"], _state(ce), _state(cg)):
                 np.testing.assert_array_equal(a, b, err_msg="step {} num_real {} {}".format(step, nr, name))
             assert torch.equal(hot_e, hot_g), (step, nr)
+            # the oracle, layer by layer in the captured order
+            for l in range(L):
+                o_slots, o_miss = orc_st.update(l, batches[l], pool_idx, seq, nr, max_num_reqs=req)
+                for s_ in range(N):
+                    _, w = orc.gather_rows(segs, hot_o[l].reshape(-1), l * plsr, ROW, batches[l], pool_idx,
+                                           pool_idx * prefill, o_slots, o_miss, nr, top_k, req, 1, N, s_,
+                                           hot_req_stride_rows=padded)
+                    assert _words(graph.status_of(l) + s_ * 64, 1) == [int(x) for x in w], (step, nr, l, s_)
+            gs = _state(cg)
+            for name, a, b in zip(["tokens", "visited", "ht", "hand"], gs[:4],
+                                  [orc_st.tokens, orc_st.vis, orc_st.ht.view(np.int16), orc_st.hand[..., 0]]):
+                np.testing.assert_array_equal(a, b, err_msg="oracle: step {} num_real {} {}".format(step, nr, name))
+            np.testing.assert_array_equal(gs[4], o_slots, err_msg="oracle slots, step {}".format(step))
+            np.testing.assert_array_equal(gs[5], o_miss, err_msg="oracle is_miss, step {}".format(step))
+            assert torch.equal(hot_g, torch.from_numpy(hot_o).cuda()), ("oracle hot rows", step, nr)
     finally:
         pool.destroy(close_ext=False)
 
