@@ -9,15 +9,20 @@ by running SIEVE over the same state and are resident in HBM; the state is
 restored before the timed replay, which therefore repeats the same work.
 
 Prints one JSON line.  ``value`` is miss rows imported per second through the
-whole path (SIEVE + import) over the timed steps.  SIEVE us/layer, import
-GB/s against the measured host-link peak, the prefill export rate, the
-roofline of the dominant kernel and the CPU oracle's rate are reported beside.
+whole path (SIEVE + import) over the timed steps.  Beside it: SIEVE us/layer,
+the import's rate against the measured host-link peak (its bound) and against
+HBM, the prefill export rate, the decode-step graph replay and its launch
+overhead, the CPU baseline (the oracle on 1 thread and on all cores, and the
+CPU serial pipeline for the import), and ``verify``: every layer's final
+SIEVE state and hot buffer compared with an independent oracle replay of all
+the layer-steps.
 """
 import argparse
 import json
 import os
 import sys
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 METRIC = "SIEVE µs/layer; miss-row gather GB/s (% of host-link peak); rows/sec"
 HBM_PEAK_GBPS = 8000.0
@@ -31,9 +36,10 @@ def parse_args():
     p.add_argument("--config", type=int, default=2, help="workload id (0-4), default 2 = DSA-decode scale")
     p.add_argument("--per-segment", action="store_true", help="N per-segment imports instead of the fused import")
     p.add_argument("--coherent", action="store_true", help="fine-grained (coherent) pinned segments")
-    p.add_argument("--cpu-sample-s", type=float, default=12.0, help="seconds of CPU oracle work for the baseline")
+    p.add_argument("--cpu-sample-s", type=float, default=12.0, help="seconds of CPU work for the baseline")
+    p.add_argument("--cpu-threads", type=int, default=16, help="threads of the all-cores CPU baseline")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--verify", action="store_true", help="check the last step's imported rows on the GPU")
+    p.add_argument("--no-verify", action="store_true", help="skip the oracle replay of the timed run")
     p.add_argument("--link-mib", type=int, default=256)
     p.add_argument("--no-graph", action="store_true",
                    help="skip the replay of the timed steps as captured HIP graphs")
@@ -48,6 +54,23 @@ def pct(xs, q):
     return float(np.percentile(np.asarray(xs), q)) if len(xs) else None
 
 
+def cpu_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        usable = os.cpu_count()
+    return {"model": model, "cpus_visible": os.cpu_count(), "cpus_usable": usable}
+
+
 def measure_link_peak(runner, mib, log):
     """Best of hipMemcpyAsync H2D from pinned memory and a zero-copy streaming
     read from a host segment (16 B loads), both of `mib` MiB."""
@@ -60,45 +83,32 @@ def measure_link_peak(runner, mib, log):
     pinned.fill_(1)
     stream = torch.cuda.current_stream()
     res = {}
-    best = 0.0
-    for _ in range(5):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        dst.copy_(pinned, non_blocking=True)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        best = max(best, n / (e0.elapsed_time(e1) * 1e-3) / 1e9)
-    res["memcpy_h2d_GBps"] = best
+
+    def best_of(fn, nbytes):
+        best = 0.0
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            best = max(best, nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+        return best
+
+    res["memcpy_h2d_GBps"] = best_of(lambda: dst.copy_(pinned, non_blocking=True), n)
     seg = runner.seg_bases[0]
-    seg_bytes = runner.pool.pool.segments[0].size_bytes
-    m = min(n, seg_bytes // 16 * 16)
-    best = 0.0
-    for _ in range(5):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        _kvops.stream_copy(dst.data_ptr(), seg, m, stream.cuda_stream)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        best = max(best, m / (e0.elapsed_time(e1) * 1e-3) / 1e9)
-    res["zero_copy_read_GBps"] = best
+    m = min(n, runner.pool.pool.segments[0].size_bytes // 16 * 16)
+    res["zero_copy_read_GBps"] = best_of(lambda: _kvops.stream_copy(dst.data_ptr(), seg, m, stream.cuda_stream), m)
     res["peak_GBps"] = max(res["memcpy_h2d_GBps"], res["zero_copy_read_GBps"])
-    # HBM -> HBM copy of the same size with the same streaming kernel: the
-    # known-size copy that calibrates FETCH_SIZE / WRITE_SIZE readings
+    # HBM -> HBM copy with the same streaming kernel: the known-size copy that
+    # calibrates FETCH_SIZE / WRITE_SIZE readings
     src = torch.empty(n, dtype=torch.uint8, device=runner.dev)
     src.fill_(3)
-    best = 0.0
-    for _ in range(5):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        _kvops.stream_copy(dst.data_ptr(), src.data_ptr(), n, stream.cuda_stream)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        best = max(best, 2 * n / (e0.elapsed_time(e1) * 1e-3) / 1e9)
-    res["hbm_copy_GBps"] = best
-    del src
+    res["hbm_copy_GBps"] = best_of(lambda: _kvops.stream_copy(dst.data_ptr(), src.data_ptr(), n, stream.cuda_stream),
+                                   2 * n)
+    del src, dst, pinned
     log("[bench] host link: memcpy H2D {:.1f} GB/s, zero-copy read {:.1f} GB/s; HBM copy {:.0f} GB/s (read+write)".format(
         res["memcpy_h2d_GBps"], res["zero_copy_read_GBps"], res["hbm_copy_GBps"]))
-    del dst, pinned
     return res
 
 
@@ -111,7 +121,7 @@ def sieve_bytes(cfg, padded, vis_stride, ht_size, dirty_reqs):
     return cfg.req_num * per_req + dirty_reqs * (padded * 4 + ht_size * 2)
 
 
-# Counter profiles committed for a workload: HBM bytes per dispatch, from
+# Counter profiles committed per workload: HBM bytes per dispatch, from
 # FETCH_SIZE and WRITE_SIZE runs scaled by a known-size copy.
 TRAFFIC_PROFILES = {"c2-dsa-decode": "profiles/pmc_traffic_dsa_decode.md"}
 
@@ -132,11 +142,210 @@ def load_traffic(workload):
     return out, rel
 
 
+# ---------------------------------------------------------------- oracle replays
+def _layer_state(runner, snap, layer):
+    """Oracle SieveState of one layer (a one-layer state) from the snapshot."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    cfg = runner.cfg
+    st = orc.SieveState(1, cfg.req_num, cfg.dbs, cfg.top_k)
+    st.tokens[0] = snap[0][layer].cpu().numpy()
+    st.vis[0] = snap[1][layer].cpu().numpy()
+    st.ht[0] = snap[2][layer].cpu().numpy().view(np.uint16)
+    st.hand[0] = snap[3][layer].cpu().numpy()
+    st.prefill_lens[:] = runner.coord.prefill_lens.cpu().numpy()
+    return st
+
+
+class _Batch:
+    """Host-side batch context of the workload for oracle calls."""
+
+    def __init__(self, runner):
+        import numpy as np
+
+        cfg = runner.cfg
+        self.R = cfg.req_num
+        self.req_pool = np.arange(cfg.req_num, dtype=np.int64)
+        self.seq = np.full(cfg.req_num, cfg.prefill, dtype=np.int32)
+        self.host_base = np.array([cfg.host_base(r) for r in range(cfg.req_num)], dtype=np.int64)
+        self.segs = [sg.view() for sg in runner.pool.pool.segments]
+        self.plsr = runner.pool.per_layer_seg_rows
+
+
+def verify_against_oracle(runner, snap, plan, threads, log):
+    """Replay every layer-step of `plan` (warmup and timed) on the oracle,
+    layer by layer from the snapshot, SIEVE then the import of every segment
+    into a zeroed hot buffer, and compare each layer's final SIEVE state
+    (tokens, visited, table, hand) and every byte of its hot buffer with the
+    GPU's after the timed run."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    cfg, c = runner.cfg, runner.coord
+    b = _Batch(runner)
+    final = [t.cpu().numpy() for t in (c.device_buffer_tokens, c.device_buffer_visited, c.device_buffer_ht,
+                                       c.sieve_hand)]
+    final[2] = final[2].view(np.uint16)
+    by_layer = {}
+    for ls in plan:
+        by_layer.setdefault(ls.layer, []).append(ls)
+    hot_bytes = runner.hot[0].numel()
+    workers = max(1, min(threads, int((24 << 30) // (2 * hot_bytes))))
+
+    def one(layer):
+        st = _layer_state(runner, snap, layer)
+        hot = np.zeros(hot_bytes, dtype=np.uint8)
+        for ls in by_layer[layer]:
+            slots, miss = st.update(0, ls.batch, b.req_pool, b.seq, b.R)
+            for s in range(cfg.node_num):
+                orc.gather_rows(b.segs, hot, layer * b.plsr, cfg.row_bytes, ls.batch, b.req_pool, b.host_base,
+                                slots, miss, b.R, cfg.top_k, b.R, cfg.stripe_rows, cfg.node_num, s,
+                                hot_req_stride_rows=runner.padded)
+        state_ok = (np.array_equal(st.tokens[0], final[0][layer]) and np.array_equal(st.vis[0], final[1][layer])
+                    and np.array_equal(st.ht[0], final[2][layer])
+                    and np.array_equal(st.hand[0][:, 0], final[3][layer][:, 0]))
+        hot_ok = bool(np.array_equal(hot, runner.hot[layer].cpu().numpy().reshape(-1)))
+        return layer, state_ok, hot_ok
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        res = list(ex.map(one, sorted(by_layer)))
+    bad_state = [l for l, s, _ in res if not s]
+    bad_hot = [l for l, _, h in res if not h]
+    ok = not bad_state and not bad_hot and orc.get_error() == 0
+    log("[bench] verify: {} layers x {} layer-steps replayed on the oracle ({} threads, {:.1f} s): state {} hot rows "
+        "{}".format(len(res), len(plan), workers, time.perf_counter() - t0, "equal" if not bad_state else bad_state,
+                    "equal" if not bad_hot else bad_hot))
+    return {"ok": ok, "layers": len(res), "layer_steps": len(plan), "state_mismatch_layers": bad_state,
+            "hot_mismatch_layers": bad_hot,
+            "what": "final SIEVE state and every hot-buffer byte of each layer vs the oracle's replay of all "
+                    "layer-steps (SIEVE + import of every segment)"}
+
+
+def cpu_baseline(runner, snap, plan, n_warm, budget_s, threads, log):
+    """The oracle on the box's host cores over the same stream.
+
+    * SIEVE: the layer-steps replayed in order on 1 thread, and layers spread
+      over `threads` threads (the layers' states are independent), from the
+      state the timed steps start from.
+    * Import, as the CPU serial pipeline the reference design replaces
+      (doc/kv_offload_design.md:21): the winning miss rows are copied on the
+      host into a pinned staging buffer (1 thread, then `threads` threads),
+      then one host-to-device copy and a device scatter into the hot buffer.
+    ``value`` is the pipeline's rows/s on `threads` threads:
+    misses / (SIEVE + staging + copy + scatter) per layer-step."""
+    import numpy as np
+    import torch
+    from oracle import oracle as orc
+
+    cfg = runner.cfg
+    b = _Batch(runner)
+    layers = sorted({ls.layer for ls in plan})
+    states = {l: _layer_state(runner, snap, l) for l in layers}
+    for ls in plan[:n_warm]:  # the state the timed steps start from (untimed)
+        states[ls.layer].update(0, ls.batch, b.req_pool, b.seq, b.R)
+    timed = plan[n_warm:]
+    start = {l: st.copy() for l, st in states.items()}
+
+    # SIEVE on one thread, in order, for about a third of the budget
+    outs = []
+    t_one = 0.0
+    for ls in timed:
+        t0 = time.perf_counter()
+        slots, miss = states[ls.layer].update(0, ls.batch, b.req_pool, b.seq, b.R)
+        t_one += time.perf_counter() - t0
+        outs.append((ls, slots, miss))
+        if t_one >= budget_s / 3:
+            break
+    n_one = len(outs)
+    sieve_us_1 = t_one / n_one * 1e6
+
+    # SIEVE on `threads` threads: layers spread over the threads, each layer's
+    # timed steps in order; as many layers as keep it near a third of the budget
+    per_layer = max(1, len(timed) // max(1, len(layers)))
+    fit = int(threads * (budget_s / 3) / (per_layer * sieve_us_1 * 1e-6)) if sieve_us_1 > 0 else len(layers)
+    use = layers[:max(1, min(len(layers), max(fit, threads)))]
+    steps_of = {l: [ls for ls in timed if ls.layer == l] for l in use}
+    work = {l: start[l].copy() for l in use}
+
+    def run_layer(l):
+        st = work[l]
+        for ls in steps_of[l]:
+            st.update(0, ls.batch, b.req_pool, b.seq, b.R)
+        return len(steps_of[l])
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        n_t = sum(ex.map(run_layer, use))
+    sieve_us_t = (time.perf_counter() - t0) / n_t * 1e6
+
+    # the serial pipeline over the layer-steps SIEVE'd on one thread
+    R, padded, rb = cfg.req_num, runner.padded, cfg.row_bytes
+    cap = R * cfg.top_k
+    staging = torch.empty((cap, rb), dtype=torch.uint8, pin_memory=True)
+    dst_rows = torch.empty(cap, dtype=torch.int64, pin_memory=True)
+    staging_np, dst_np = staging.numpy(), dst_rows.numpy()
+    staging_d = torch.empty((cap, rb), dtype=torch.uint8, device=runner.dev)
+    dst_d = torch.empty(cap, dtype=torch.int64, device=runner.dev)
+    hot = torch.zeros((R * padded, rb), dtype=torch.uint8, device=runner.dev)
+
+    def pipeline(nthreads, budget):
+        rows = 0
+        t = 0.0
+        done = 0
+        for ls, slots, miss in outs:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            n = orc.stage_rows(b.segs, staging_np, dst_np, ls.layer * b.plsr, rb, ls.batch, b.req_pool, b.host_base,
+                               slots, miss, R, cfg.top_k, R, cfg.stripe_rows, cfg.node_num, padded, nthreads)
+            if n > 0:
+                staging_d[:n].copy_(staging[:n], non_blocking=True)
+                dst_d[:n].copy_(dst_rows[:n], non_blocking=True)
+                hot.index_copy_(0, dst_d[:n], staging_d[:n])
+            torch.cuda.synchronize()
+            t += time.perf_counter() - t0
+            rows += n
+            done += 1
+            if t >= budget:
+                break
+        return t / done * 1e6, rows / t / 1e9 * rb if t > 0 else None, done
+
+    pipe_us_1, pipe_gbps_1, n_p1 = pipeline(1, budget_s / 6)
+    pipe_us_t, pipe_gbps_t, n_pt = pipeline(threads, budget_s / 6)
+    misses = float(np.mean([ls.misses for ls, _, _ in outs]))
+    rows_1 = misses / ((sieve_us_1 + pipe_us_1) * 1e-6)
+    rows_t = misses / ((sieve_us_t + pipe_us_t) * 1e-6)
+    info = cpu_info()
+    log("[bench] cpu baseline ({}): SIEVE {:.0f} us/layer on 1 thread, {:.0f} on {} threads; serial pipeline "
+        "{:.1f} GB/s on 1 thread, {:.1f} on {}; {:.0f} / {:.0f} rows/s".format(
+            info["model"], sieve_us_1, sieve_us_t, threads, pipe_gbps_1 or 0, pipe_gbps_t or 0, threads, rows_1,
+            rows_t))
+    return {
+        "value": rows_t,
+        "unit": "rows/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": "timed layer-steps of the benchmark stream from the state they start from: SIEVE on 1 thread "
+                  "over {} of them, on {} threads over {} ({} layers); the serial pipeline (host staging, one H2D, "
+                  "device scatter) over {} / {}".format(n_one, threads, n_t, len(use), n_p1, n_pt),
+        "single_thread": {"sieve_us_per_layer": sieve_us_1, "pipeline_us_per_layer": pipe_us_1,
+                          "gather_GBps": pipe_gbps_1, "rows_per_s": rows_1},
+        "all_cores": {"threads": threads, "sieve_us_per_layer": sieve_us_t, "pipeline_us_per_layer": pipe_us_t,
+                      "gather_GBps": pipe_gbps_t, "rows_per_s": rows_t},
+        "cpu": info,
+    }
+
+
+# ---------------------------------------------------------------- GPU passes
 def graph_pass(runner, snap, warm, timed, fused, eager_ms, log):
     """Replay the timed layer-steps again from the same starting state, each
     decode step as one captured HIP graph (SIEVE update + fused import of all
     its layers), and check that the final state and hot rows equal the eager
-    run's."""
+    run's.  Launch overhead, the reference design's graph-mode target
+    (doc/kv_offload_design.md:94: under 50% of per-call launches): the host
+    time to issue a step's launches, eager calls against one graph replay, and
+    the GPU time of the launches alone (num_real = 0)."""
     import torch
     from kv_offload_proto_amd.xds import DecodeStepGraph
 
@@ -150,18 +359,20 @@ def graph_pass(runner, snap, warm, timed, fused, eager_ms, log):
     ref_hot = runner.hot.clone() if torch.cuda.mem_get_info()[0] > 2 * hot_bytes + (8 << 30) else None
     runner.restore(snap)
     runner.hot.zero_()  # the eager run started from a zeroed hot buffer too
-    for _, layer, topk_d, _, _ in warm:
-        runner.sieve(layer, topk_d)
-        runner.gather(layer, topk_d, fused=True)
+    for ls in warm:
+        runner.sieve(ls.layer, ls.topk)
+        runner.gather(ls.layer, ls.topk, fused=True)
     steps = {}
-    for step, layer, topk_d, _, _ in timed:
-        steps.setdefault(step, []).append((layer, topk_d))
+    for ls in timed:
+        steps.setdefault(ls.step, []).append((ls.layer, ls.topk))
     t0 = time.perf_counter()
     graphs = []
+    cap_stream = torch.cuda.Stream(device=runner.dev)
     for step in sorted(steps):
         layers = [l for l, _ in steps[step]]
         g = DecodeStepGraph(c, runner.pool, layers, [t for _, t in steps[step]], [runner.hot[l] for l in layers],
-                            hot_req_stride_rows=runner.padded, block_dim=1, sieve_block_dim=runner.block_dim)
+                            hot_req_stride_rows=runner.padded, block_dim=1, sieve_block_dim=runner.block_dim,
+                            capture_stream=cap_stream)
         g.capture()
         graphs.append(g)
     capture_s = time.perf_counter() - t0
@@ -179,36 +390,46 @@ def graph_pass(runner, snap, warm, timed, fused, eager_ms, log):
     outs_ok = torch.equal(ref_outs[0], c.top_k_device_slots) and torch.equal(ref_outs[1], c.is_miss)
     hot_ok = None if ref_hot is None else torch.equal(ref_hot, runner.hot)
     del ref_hot, ref_state
-    # launch overhead alone: the same layer-steps with num_real = 0 (every
-    # kernel launched, no row does work), eager calls against graph replays
+    # launch overhead: the same layer-steps with num_real = 0 (every kernel
+    # launched, no row does work)
     saved = c.num_real.clone()
     c.num_real.zero_()
     torch.cuda.synchronize()
+    n = len(timed)
+    h0 = time.perf_counter()
     e0.record(stream)
-    for _, layer, topk_d, _, _ in timed:
-        runner.sieve(layer, topk_d)
-        runner.gather(layer, topk_d, fused=True)
+    for ls in timed:
+        runner.sieve(ls.layer, ls.topk)
+        runner.gather(ls.layer, ls.topk, fused=True)
     e1.record(stream)
+    host_eager = time.perf_counter() - h0
     torch.cuda.synchronize()
     idle_eager_ms = e0.elapsed_time(e1)
+    h0 = time.perf_counter()
     e0.record(stream)
     for g in graphs:
         g.replay(clear_status=False)
     e1.record(stream)
+    host_graph = time.perf_counter() - h0
     torch.cuda.synchronize()
     idle_graph_ms = e0.elapsed_time(e1)
     c.num_real.copy_(saved)
     torch.cuda.synchronize()
-    n = len(timed)
     res = {"steps": len(graphs), "layer_steps": n, "capture_s": capture_s,
            "us_per_layer": graph_ms * 1e3 / n, "eager_us_per_layer": eager_ms * 1e3 / n,
            "speedup": eager_ms / graph_ms, "state_match": state_ok, "outputs_match": outs_ok, "hot_match": hot_ok,
-           "launch_only_us_per_layer": {"eager": idle_eager_ms * 1e3 / n, "graph": idle_graph_ms * 1e3 / n,
-                                        "graph_over_eager": idle_graph_ms / idle_eager_ms}}
+           "launch_overhead": {
+               "host_issue_us_per_layer": {"eager": host_eager * 1e6 / n, "graph": host_graph * 1e6 / n,
+                                           "graph_over_eager": host_graph / host_eager},
+               "gpu_launch_only_us_per_layer": {"eager": idle_eager_ms * 1e3 / n, "graph": idle_graph_ms * 1e3 / n,
+                                                "graph_over_eager": idle_graph_ms / idle_eager_ms},
+               "target_graph_over_eager": 0.5}}
     log("[bench] graph replay: {:.2f} us/layer vs eager {:.2f} us/layer ({} step graphs, capture {:.1f} s); "
-        "state {} outputs {} hot rows {}; launches alone (num_real 0): graph {:.2f} vs eager {:.2f} us/layer".format(
+        "state {} outputs {} hot rows {}; launch overhead per layer: host {:.2f} vs {:.2f} us ({:.2f}x), "
+        "GPU (num_real 0) {:.2f} vs {:.2f} us".format(
             res["us_per_layer"], res["eager_us_per_layer"], len(graphs), capture_s, state_ok, outs_ok, hot_ok,
-            idle_graph_ms * 1e3 / n, idle_eager_ms * 1e3 / n))
+            host_graph * 1e6 / n, host_eager * 1e6 / n, host_graph / host_eager, idle_graph_ms * 1e3 / n,
+            idle_eager_ms * 1e3 / n))
     return res
 
 
@@ -223,14 +444,14 @@ def sieve_pipelined(runner, snap, warm, timed, log):
     names = ("device_buffer_tokens", "device_buffer_visited", "device_buffer_ht", "sieve_hand")
     ref = [getattr(c, n).clone() for n in names]
     runner.restore(snap)
-    for _, layer, topk_d, _, _ in warm:
-        runner.sieve(layer, topk_d)
+    for ls in warm:
+        runner.sieve(ls.layer, ls.topk)
     stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _, layer, topk_d, _, _ in timed:
-        runner.sieve(layer, topk_d)
+    for ls in timed:
+        runner.sieve(ls.layer, ls.topk)
     e1.record(stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / len(timed)
@@ -284,90 +505,6 @@ def export_rows_pass(runner, log, reps=3):
             "per_segment_us_per_layer_median": med_seg, "GBps": R * cfg.row_bytes / (med * 1e-6) / 1e9, "match": ok}
 
 
-def cpu_baseline(runner, plan, n_warm, budget_s, log):
-    """The C oracle (oracle/liboracle.so) replaying the same batches from the
-    same initial state on one host core: the warmup layer-steps untimed
-    (SIEVE only, to reach the state the timed steps start from), then SIEVE +
-    import over the timed layer-steps for about budget_s."""
-    import numpy as np
-    import torch
-    from oracle import oracle as orc
-
-    cfg = runner.cfg
-    st = orc.SieveState(cfg.layers, cfg.req_num, cfg.dbs, cfg.top_k)
-    c = runner.coord
-    st.tokens[:] = c.device_buffer_tokens.cpu().numpy()
-    st.vis[:] = c.device_buffer_visited.cpu().numpy()
-    st.ht[:] = c.device_buffer_ht.cpu().numpy().view(np.uint16)
-    st.hand[:] = c.sieve_hand.cpu().numpy()
-    st.prefill_lens[:] = c.prefill_lens.cpu().numpy()
-    segs = [sg.view() for sg in runner.pool.pool.segments]
-    hot = np.zeros(cfg.req_num * runner.padded * cfg.row_bytes, dtype=np.uint8)
-    req_pool = np.arange(cfg.req_num, dtype=np.int64)
-    seq = np.full(cfg.req_num, cfg.prefill, dtype=np.int32)
-    host_base = np.array([cfg.host_base(r) for r in range(cfg.req_num)], dtype=np.int64)
-    plsr = runner.pool.per_layer_seg_rows
-    t_sieve = t_gather = 0.0
-    rows = done = 0
-    sieve_mismatch = 0
-    for step, layer, _, batch, gpu_misses in plan[:n_warm]:
-        st.update(layer, batch, req_pool, seq, cfg.req_num)
-    # a short stream is replayed from the same state until the budget is
-    # spent (at most 1000 passes), so small workloads are timed over more
-    # than a few microseconds of work
-    start = [a.copy() for a in (st.tokens, st.vis, st.ht, st.hand)]
-    timed_plan = plan[n_warm:]
-    passes = 0
-    while passes < 1000 and (passes == 0 or t_sieve + t_gather < budget_s):
-        if passes > 0:
-            for dst, src in zip((st.tokens, st.vis, st.ht, st.hand), start):
-                np.copyto(dst, src)
-        passes += 1
-        for step, layer, _, batch, gpu_misses in timed_plan:
-            t0 = time.perf_counter()
-            slots, miss = st.update(layer, batch, req_pool, seq, cfg.req_num)
-            t1 = time.perf_counter()
-            for s in range(cfg.node_num):
-                orc.gather_rows(segs, hot, layer * plsr, cfg.row_bytes, batch, req_pool, host_base, slots, miss,
-                                cfg.req_num, cfg.top_k, cfg.req_num, cfg.stripe_rows, cfg.node_num, s,
-                                hot_req_stride_rows=runner.padded)
-            t2 = time.perf_counter()
-            t_sieve += t1 - t0
-            t_gather += t2 - t1
-            n = int(miss.sum())
-            sieve_mismatch += int(n != gpu_misses)
-            rows += n
-            done += 1
-            if t_sieve + t_gather >= budget_s:
-                break
-    total = t_sieve + t_gather
-    log("[bench] cpu oracle: {} layer-steps ({} passes) in {:.1f} s, {:.0f} rows/s, sieve {:.0f} us/layer".format(
-        done, passes, total, rows / total, t_sieve / done * 1e6))
-    return {
-        "value": rows / total,
-        "unit": "rows/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": "{} timed layer-steps of the benchmark stream ({} passes over its first {}; {} miss rows), oracle "
-                  "SIEVE + import, 1 thread".format(done, passes, min(done, len(timed_plan)), rows),
-        "sieve_us_per_layer": t_sieve / done * 1e6,
-        "gather_GBps": rows * cfg.row_bytes / t_gather / 1e9 if t_gather > 0 else None,
-        "miss_count_mismatches": sieve_mismatch,
-        "cpu": _cpu_model(),
-    }
-
-
-def _cpu_model():
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return None
-
-
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -375,7 +512,6 @@ def main():
               "(--gpus {} is not supported; run with --gpus 1)".format(args.gpus), file=sys.stderr)
         return 2
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    import numpy as np
     import torch
 
     import kv_offload_proto_amd  # noqa: F401  (loads the native module)
@@ -389,6 +525,7 @@ def main():
         log("[bench] no GPU visible")
         return 1
     cfg = CONFIGS[args.config]
+    threads = max(1, min(args.cpu_threads, cpu_info()["cpus_usable"] or 1))
     t_start = time.perf_counter()
     runner = DecodeRunner(cfg, coherent=args.coherent, log=log)
     if args.sieve_variant >= 0:
@@ -413,9 +550,9 @@ def main():
 
     fused = not args.per_segment
     stream = torch.cuda.current_stream()
-    for _, layer, topk_d, _, _ in warm:
-        runner.sieve(layer, topk_d)
-        runner.gather(layer, topk_d, fused=fused)
+    for ls in warm:
+        runner.sieve(ls.layer, ls.topk)
+        runner.gather(ls.layer, ls.topk, fused=fused)
     torch.cuda.synchronize()
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
@@ -423,29 +560,31 @@ def main():
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
-    for (a, b, c), (_, layer, topk_d, _, _) in zip(ev, timed):
+    for (a, b, c), ls in zip(ev, timed):
         a.record(stream)
-        runner.sieve(layer, topk_d)
+        runner.sieve(ls.layer, ls.topk)
         b.record(stream)
-        runner.gather(layer, topk_d, fused=fused)
+        runner.gather(ls.layer, ls.topk, fused=fused)
         c.record(stream)
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
     sieve_us = [a.elapsed_time(b) * 1e3 for a, b, _ in ev]
     gather_us = [b.elapsed_time(c) * 1e3 for _, b, c in ev]
-    rows = sum(m for *_, m in timed)
-    ok, checked = (None, 0)
-    if args.verify and timed:
-        ok, checked = runner.verify_last_gather(timed[-1][1], timed[-1][2])
-        log("[bench] verify last step: {} ({} rows)".format(ok, checked))
+    rows = sum(ls.misses for ls in timed)
+    moved = sum(ls.moved for ls in timed)
+    unique_src = sum(ls.unique_src for ls in timed)
 
-    # roofline of the dominant kernel
+    verify = None if args.no_verify else verify_against_oracle(runner, snap, plan, threads, log)
+
+    # rooflines: the import is bound by the host link, SIEVE by HBM
     c = runner.coord
     positions = cfg.req_num * cfg.top_k
-    gather_bytes = [m * cfg.row_bytes * 2 + positions * 9 for *_, m in timed]
-    gather_gbps_alg = sum(gather_bytes) / (sum(gather_us) * 1e-6) / 1e9
-    link_gbps = rows * cfg.row_bytes / (sum(gather_us) * 1e-6) / 1e9
+    t_gather = sum(gather_us) * 1e-6
+    link_gbps = moved * cfg.row_bytes / t_gather / 1e9
+    unique_gbps = unique_src * cfg.row_bytes / t_gather / 1e9
+    hbm_bytes = [ls.moved * cfg.row_bytes * 2 + positions * 9 for ls in timed]
+    hbm_gbps = sum(hbm_bytes) / t_gather / 1e9
     sb = sieve_bytes(cfg, c.padded_buffer_size, c.visited_stride_b, c.ht_size, cfg.req_num)
     sieve_gbps_alg = sb * len(timed) / (sum(sieve_us) * 1e-6) / 1e9
     traffic, traffic_src = load_traffic(cfg.name)
@@ -462,29 +601,30 @@ def main():
         return total
 
     gather_kernels = ("kvx_gather_prep", "kvx_gather_list", "kvx_gather_copy")
-    gather_roof = {"kernel": "+".join(gather_kernels), "bound": "hbm", "achieved": gather_gbps_alg,
-                   "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gather_gbps_alg / HBM_PEAK_GBPS,
+    gather_roof = {"kernel": "+".join(gather_kernels), "bound": "host-link", "achieved": link_gbps,
+                   "peak": link["peak_GBps"], "unit": "GB/s", "frac": link_gbps / link["peak_GBps"],
                    "traffic": traffic_of(*gather_kernels), "traffic_source": traffic_src,
-                   "bytes_per_launch": sum(gather_bytes) / len(timed),
+                   "bytes_per_launch": moved * cfg.row_bytes / len(timed),
+                   "bytes_rule": "rows moved (distinct destinations after the winner rule) x row_bytes, read over "
+                                 "the host link",
                    "avg_launch_us": sum(gather_us) / len(timed),
-                   "link": {"achieved": link_gbps, "peak": link["peak_GBps"], "unit": "GB/s",
-                            "frac": link_gbps / link["peak_GBps"]}}
+                   "hbm": {"achieved": hbm_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": hbm_gbps / HBM_PEAK_GBPS,
+                           "bytes_rule": "rows moved x row_bytes read + written, + 9 B per position of index scan"}}
     sieve_roof = {"kernel": "kvx_sieve_update", "bound": "hbm", "achieved": sieve_gbps_alg, "peak": HBM_PEAK_GBPS,
                   "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS,
                   "traffic": traffic_of("kvx_sieve_update_fast"), "traffic_source": traffic_src, "bytes_per_launch": sb,
                   "avg_launch_us": sum(sieve_us) / len(timed)}
     dominant, other = (gather_roof, sieve_roof) if sum(gather_us) >= sum(sieve_us) else (sieve_roof, gather_roof)
 
-    n_timed_steps = args.steps
     value = rows / (total_ms * 1e-3)
     out = {
         "metric": METRIC,
         "value": value,
         "unit": "rows/s",
         "n_gpus": 1,
-        "steps": n_timed_steps,
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": total_ms / n_timed_steps,
+        "ms_per_step": total_ms / args.steps,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -499,20 +639,22 @@ def main():
                                "mean": sum(sieve_us) / len(sieve_us)},
         "gather": {"us_per_layer_median": pct(gather_us, 50), "GBps": link_gbps,
                    "frac_of_link_peak": link_gbps / link["peak_GBps"], "frac_of_hbm_peak": link_gbps / HBM_PEAK_GBPS,
-                   "rows_per_s": rows / (sum(gather_us) * 1e-6), "rows": rows},
+                   "unique_host_GBps": unique_gbps, "unique_host_frac_of_link_peak": unique_gbps / link["peak_GBps"],
+                   "rows_moved_per_s": moved / t_gather, "miss_rows_per_s": rows / t_gather, "rows_moved": moved,
+                   "miss_rows": rows, "unique_host_rows": unique_src},
         "host_link": link,
         "export": {"row_bytes_total": runner.export_bytes, "bytes_moved": runner.export_moved_bytes,
                    "us": export_us, "GBps_moved": export_gbps},
         "roofline": dominant,
         "roofline_other": other,
-        "verify": ok,
+        "verify": None if verify is None else verify["ok"],
+        "verify_detail": verify,
     }
     out["sieve_back_to_back"] = sieve_pipelined(runner, snap, warm, timed, log)
     out["graph"] = None if args.no_graph else graph_pass(runner, snap, warm, timed, fused, total_ms, log)
     out["export_rows"] = export_rows_pass(runner, log)
     if not args.no_cpu:
-        runner.restore(snap)
-        out["cpu_baseline"] = cpu_baseline(runner, plan, len(warm), args.cpu_sample_s, log)
+        out["cpu_baseline"] = cpu_baseline(runner, snap, plan, len(warm), args.cpu_sample_s, threads, log)
     else:
         out["cpu_baseline"] = None
     out["wall_s"] = time.perf_counter() - t_start

@@ -8,6 +8,7 @@ step runs ``sieve_update`` then the miss import for one layer.  The hot buffer
 of layer l is ``hot[l]``, rows ``slot + bid*padded`` (one slice per request).
 """
 import time
+from collections import namedtuple
 
 import numpy as np
 import torch
@@ -16,6 +17,14 @@ from ..kvops_ext import _kvops
 from . import streams
 from .xds_offload import XdsOffloadCoordinator
 from .xds_seg_pool import HostSegPool
+
+
+# One layer-step of a generated stream: the topK batch (device and host
+# copies), the miss count (sum of is_miss), the rows the import moves
+# (distinct destination rows after the last-position-wins rule) and the
+# distinct host segment rows it reads (fewer when S > 1 aliases a stripe's
+# rows to one segment row, or when requests share host rows).
+LayerStep = namedtuple("LayerStep", "step layer topk batch misses moved unique_src")
 
 
 class DecodeRunner:
@@ -120,10 +129,29 @@ class DecodeRunner:
                                             miss_pool=pool)
             topk_d = torch.from_numpy(batch).to(self.dev)
             self.coord.sieve_update(layer, topk_d, block_dim=self.block_dim)
-            misses = int(self.coord.is_miss.sum().item())
-            plan.append((step, layer, topk_d, batch, misses))
+            misses, moved, unique_src = self.import_counts(topk_d)
+            plan.append(LayerStep(step, layer, topk_d, batch, misses, moved, unique_src))
         self.restore(snap)
         return plan, snap
+
+    def import_counts(self, topk_d):
+        """(misses, rows moved, distinct host segment rows) of the import of
+        the last SIEVE update's outputs."""
+        cfg, c = self.cfg, self.coord
+        miss = c.is_miss.bool()
+        misses = int(miss.sum().item())
+        valid = miss & (topk_d >= 0) & (c.top_k_device_slots >= 0)
+        pos = torch.nonzero(valid.reshape(-1)).reshape(-1)
+        if pos.numel() == 0:
+            return misses, 0, 0
+        bid = pos // cfg.top_k
+        dest = c.top_k_device_slots.reshape(-1)[pos].to(torch.int64) + bid * self.padded
+        moved = int(torch.unique(dest).numel())
+        row = (c.req_host_base[bid] + topk_d.reshape(-1)[pos].to(torch.int64)) & 0xFFFFFFFF
+        S, N = max(cfg.stripe_rows, 1), cfg.node_num
+        q = row // S
+        key = (q % N) * self.pool.per_layer_seg_rows + q // N
+        return misses, moved, int(torch.unique(key).numel())
 
     # ---- one decode layer-step ----
     def sieve(self, layer, topk_d):

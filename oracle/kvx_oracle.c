@@ -32,6 +32,7 @@
  *                       bytes) and brute-force last-entry-wins; parity with a
  *                       reference implementation is unpinned (none exists).
  */
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -351,6 +352,87 @@ int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffset
         statusWords[b] = (statusWords[b] << 40) | (1ull << 32);
     }
     return copied;
+}
+
+/* Host staging step of the CPU serial pipeline (the baseline the reference
+ * design replaces, doc/kv_offload_design.md:21: CPU miss list -> host copy
+ * into a staging buffer -> one H2D -> device scatter).  Lists the winning
+ * valid miss rows of every segment (the winner rule of orc_gather_rows), in
+ * position order, and copies them into the dense `staging` buffer with
+ * `threads` threads; dstRows[i] receives the hot row of staging row i.
+ * Returns the number of staged rows (or -1 if memory runs out).  Timing
+ * baseline only: the GPU path is checked against orc_gather_rows. */
+struct orc_stage_job {
+    uint8_t *staging;
+    const uint8_t *const *src;
+    int64_t lo, hi;
+    uint32_t rowBytes;
+};
+
+static void *orc_stage_copy(void *arg)
+{
+    const struct orc_stage_job *j = (const struct orc_stage_job *)arg;
+    for (int64_t i = j->lo; i < j->hi; ++i) memcpy(j->staging + (uint64_t)i * j->rowBytes, j->src[i], j->rowBytes);
+    return NULL;
+}
+
+int64_t orc_stage_rows(uint8_t *const *segs, uint8_t *staging, int64_t *dstRows, uint32_t layerOffsetRows,
+                       uint32_t rowBytes, const int32_t *topk, const int64_t *reqPool, const int64_t *reqHostBase,
+                       const int32_t *slots, const int8_t *isMiss, int32_t numRealIn, uint32_t topK,
+                       uint32_t maxNumReqs, uint32_t S, uint32_t N, uint32_t hotReqStrideRows, int32_t threads)
+{
+    int32_t numReal = numRealIn;
+    if (numReal > (int32_t)maxNumReqs) numReal = (int32_t)maxNumReqs;
+    if (numReal < 0) numReal = 0;
+    const int64_t total = (int64_t)numReal * topK;
+    uint64_t cap = 1024;
+    while (cap < 2 * (uint64_t)(total + 1)) cap <<= 1;
+    uint64_t *seen = (uint64_t *)calloc(cap, sizeof(uint64_t));
+    const uint8_t **src = (const uint8_t **)malloc(sizeof(uint8_t *) * (size_t)(total + 1));
+    if (seen == NULL || src == NULL) { free(seen); free(src); return -1; }
+    int64_t n = 0;
+    for (int64_t p = total - 1; p >= 0; --p) {  /* backwards: first seen = last position = winner */
+        if (isMiss[p] == 0) continue;
+        const int64_t bid = p / topK;
+        const int32_t tp = topk[p], slot = slots[p];
+        if (tp < 0 || slot < 0 || reqPool[bid] < 0) continue;
+        const uint32_t row = (uint32_t)(reqHostBase[bid] + tp);
+        const uint32_t node = orc_node_of(row, S, N);
+        if (node >= N) continue;
+        const uint64_t dst = (uint64_t)slot + (uint64_t)bid * hotReqStrideRows;
+        uint64_t i = (dst * 0x9E3779B97F4A7C15ull) & (cap - 1);
+        int winner = 1;
+        while (seen[i] != 0) {
+            if (seen[i] == dst + 1) { winner = 0; break; }
+            i = (i + 1) & (cap - 1);
+        }
+        if (!winner) continue;
+        seen[i] = dst + 1;
+        src[n] = segs[node] + ((uint64_t)layerOffsetRows + orc_seg_row_of(row, S, N)) * rowBytes;
+        dstRows[n] = (int64_t)dst;
+        ++n;
+    }
+    free(seen);
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t tid[64];
+    struct orc_stage_job job[64];
+    int started = 0;
+    for (int t = 0; t < threads; ++t) {
+        job[t].staging = staging;
+        job[t].src = src;
+        job[t].lo = n * t / threads;
+        job[t].hi = n * (t + 1) / threads;
+        job[t].rowBytes = rowBytes;
+        if (t == threads - 1 || pthread_create(&tid[t], NULL, orc_stage_copy, &job[t]) != 0) {
+            orc_stage_copy(&job[t]);
+        } else {
+            ++started;
+        }
+    }
+    for (int t = 0; t < started; ++t) pthread_join(tid[t], NULL);
+    free(src);
+    return n;
 }
 
 /* kvops/kernel/kvc_scatter_rows_alllayer.cpp:11-67 for segment `myNode`:

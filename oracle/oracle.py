@@ -7,6 +7,7 @@ Functions mirror the reference's algorithms on numpy arrays:
   sieve_update       kvops/kernel/hisp_sieve_update.cpp:17-176
   sieve_ht_init      kvops/kernel/hisp_sieve_ht_init.cpp:14-60
   gather_rows        kvops/kernel/kvc_gather_rows.cpp:12-96 (+ last-position-wins rule)
+  stage_rows         the host staging step of the CPU serial pipeline (bench baseline)
   export_alllayer    kvops/kernel/kvc_scatter_rows_alllayer.cpp:11-67
   layout helpers     common/kv_layout.h:26-57
   ht_size, reqs_per_core  kvops/kvops_ext/kvops_ext.cpp:297-312
@@ -81,6 +82,10 @@ def lib():
         L.orc_export_alllayer.argtypes = [_u8p, _u8p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
                                           ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                           ctypes.c_uint32, ctypes.c_uint32]
+        L.orc_stage_rows.restype = ctypes.c_int64
+        L.orc_stage_rows.argtypes = [ctypes.POINTER(_u8p), _u8p, _i64p, ctypes.c_uint32, ctypes.c_uint32, _i32p,
+                                     _i64p, _i64p, _i32p, _i8p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32,
+                                     ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int32]
         L.orc_export_rows.restype = ctypes.c_int64
         L.orc_export_rows.argtypes = [_u8p, _u8p, _i64p, ctypes.c_int32] + [ctypes.c_uint32] * 8 + [_u64p]
         _LIB = L
@@ -233,6 +238,22 @@ def gather_rows(segs, hot, layer_offset_rows, row_bytes, topk, req_pool, req_hos
                               max_num_reqs, stripe_rows, node_num, my_node, hot_req_stride_rows, max(block_dim, 1),
                               _p(words, _u64p))
     return int(n), words
+
+
+def stage_rows(segs, staging, dst_rows, layer_offset_rows, row_bytes, topk, req_pool, req_host_base, slots, is_miss,
+               num_real, top_k, max_num_reqs, stripe_rows, node_num, hot_req_stride_rows, threads):
+    """Host staging step of the CPU serial pipeline: the winning miss rows of
+    every segment copied into `staging` (uint8, rows x row_bytes) with
+    `threads` threads; dst_rows (int64) receives each staged row's hot row.
+    Returns the number of rows staged."""
+    arr = (_u8p * len(segs))(*[_p(s, _u8p) for s in segs])
+    return int(lib().orc_stage_rows(arr, _p(staging, _u8p), _p(dst_rows, _i64p), layer_offset_rows, row_bytes,
+                                    _p(np.ascontiguousarray(topk, dtype=np.int32), _i32p),
+                                    _p(np.ascontiguousarray(req_pool, dtype=np.int64), _i64p),
+                                    _p(np.ascontiguousarray(req_host_base, dtype=np.int64), _i64p),
+                                    _p(np.ascontiguousarray(slots, dtype=np.int32), _i32p),
+                                    _p(np.ascontiguousarray(is_miss, dtype=np.int8), _i8p), int(num_real), top_k,
+                                    max_num_reqs, stripe_rows, node_num, hot_req_stride_rows, int(threads)))
 
 
 def export_rows(seg, src, indices, num_real, max_rows, layer_id, plsr, row_bytes, stripe_rows, node_num, my_node,

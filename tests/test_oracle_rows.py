@@ -226,3 +226,28 @@ def test_export_rows_last_entry_wins_and_errors():
     # status blocks of 5 entries: [0,5) owns entries 0,1,2 ; [5,9) owns 5,6,8 with the first error at 5
     assert int(words[0]) == (3 << 40) | (1 << 32)
     assert int(words[1]) == (3 << 40) | (1 << 32) | (0x200 + 5 + (1 << 16))
+
+
+@pytest.mark.parametrize("threads", [1, 3, 16])
+@pytest.mark.parametrize("S,N,stride", [(1, 2, 0), (1, 4, 12), (64, 2, 12), (3, 3, 12)])
+def test_stage_rows_scatter_equals_gather(threads, S, N, stride):
+    """The CPU pipeline's staging step: scattering the staged rows to their
+    hot rows gives what orc_gather_rows gives over all segments (each
+    destination staged once, with its winning row)."""
+    rng = np.random.default_rng(77 + threads + S + N)
+    c = _gather_case(rng, S, N, stride, 1)
+    want = np.zeros(c["hot_rows"] * ROW_BYTES, dtype=np.uint8)
+    for my in range(N):
+        orc.gather_rows(c["segs"], want, c["layer"] * c["plsr"], ROW_BYTES, c["topk"], c["req_pool"], c["host_base"],
+                        c["slots"], c["is_miss"], c["num_real"], c["top_k"], c["max_num_reqs"], S, N, my,
+                        hot_req_stride_rows=stride)
+    cap = c["max_num_reqs"] * c["top_k"]
+    staging = np.zeros((cap, ROW_BYTES), dtype=np.uint8)
+    dst = np.full(cap, -1, dtype=np.int64)
+    n = orc.stage_rows(c["segs"], staging, dst, c["layer"] * c["plsr"], ROW_BYTES, c["topk"], c["req_pool"],
+                       c["host_base"], c["slots"], c["is_miss"], c["num_real"], c["top_k"], c["max_num_reqs"], S, N,
+                       stride, threads)
+    assert n == len(set(dst[:n].tolist()))
+    got = np.zeros_like(want).reshape(-1, ROW_BYTES)
+    got[dst[:n]] = staging[:n]
+    np.testing.assert_array_equal(got.reshape(-1), want)
