@@ -83,6 +83,23 @@ int kvx_import_all(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32
                    uint32_t stripe_rows, uint32_t node_num, uint64_t status, uint64_t stream,
                    uint32_t block_dim, uint32_t hot_req_stride_rows);
 
+/* No counterpart in the reference: kvx_import_all for callers that cannot
+ * allocate device memory (launches under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  Same arguments, results and
+ * status words as kvx_import_all; it allocates nothing and creates no
+ * per-stream scratch: its scratch is one fixed array per GPU (26.2 MB, held
+ * from library load to process exit) shared by every call of this entry
+ * point on that GPU, so calls that overlap on one GPU race (run them on one
+ * stream, or order them).  Limits: max_num_reqs * top_k <= 524288 and
+ * (max_num_reqs - 1) * min(hot_req_stride_rows, 65536) + 65536 <= 2228224;
+ * a larger call fails with an error before anything is queued. */
+int kvx_import_all_noalloc(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,
+                           uint32_t row_bytes, uint64_t topk_indices, uint64_t req_pool_indices,
+                           uint64_t req_host_base, uint64_t topk_device_slots, uint64_t is_miss,
+                           uint64_t num_real, uint64_t hot_row_base, uint32_t top_k, uint32_t max_num_reqs,
+                           uint32_t stripe_rows, uint32_t node_num, uint64_t status, uint64_t stream,
+                           uint32_t block_dim, uint32_t hot_req_stride_rows);
+
 /* kvops_ext.cpp:256-278 kv_export_seg_alllayer: copy rows [row_lo,
  * row_lo+row_cnt) of every layer owned by my_node from HBM to the segment.
  * block_dim only sets how many status words are written (<= 8). */

@@ -89,6 +89,26 @@ PYBIND11_MODULE(_kvops, m)
         py::arg("hot_req_stride_rows") = 0);
 
     m.def(
+        "import_all_noalloc",
+        [](const std::vector<uint64_t> &seg_bases, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,
+           uint32_t row_bytes, uint64_t topk_indices, uint64_t req_pool_indices, uint64_t req_host_base,
+           uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real, uint64_t hot_row_base, uint32_t top_k,
+           uint32_t max_num_reqs, uint32_t stripe_rows, uint64_t status, uint64_t stream, uint32_t block_dim,
+           uint32_t hot_req_stride_rows) {
+            if (seg_bases.empty()) throw std::runtime_error("import_all_noalloc: seg_bases is empty");
+            Check(kvx_import_all_noalloc(seg_bases.data(), layer_offset_rows, per_layer_seg_rows, row_bytes,
+                                         topk_indices, req_pool_indices, req_host_base, topk_device_slots, is_miss,
+                                         num_real, hot_row_base, top_k, max_num_reqs, stripe_rows,
+                                         static_cast<uint32_t>(seg_bases.size()), status, stream, block_dim,
+                                         hot_req_stride_rows));
+        },
+        py::arg("seg_bases"), py::arg("layer_offset_rows"), py::arg("per_layer_seg_rows"), py::arg("row_bytes"),
+        py::arg("topk_indices"), py::arg("req_pool_indices"), py::arg("req_host_base"), py::arg("topk_device_slots"),
+        py::arg("is_miss"), py::arg("num_real"), py::arg("hot_row_base"), py::arg("top_k"), py::arg("max_num_reqs"),
+        py::arg("stripe_rows"), py::arg("status"), py::arg("stream") = 0, py::arg("block_dim") = 1,
+        py::arg("hot_req_stride_rows") = 0);
+
+    m.def(
         "export_seg_alllayer",
         [](uint64_t channel, uint64_t seg_base, uint32_t per_layer_seg_rows, uint32_t row_bytes, uint32_t row_lo,
            uint32_t row_cnt, uint32_t layer_num, uint64_t src_layer0_base, uint64_t src_layer_stride,

@@ -39,6 +39,21 @@ struct StreamScratch {
     uint64_t shadowCells = 0;
 };
 
+// Scratch of kvx_import_all_noalloc: a fixed array in the library's code
+// object, so each GPU the library is loaded on holds its own copy from load
+// to process exit, and the entry point allocates nothing.  Layout: the
+// control words (counters, error words, tickets, list count, epoch), the
+// winner table, then the row list (sources, then destinations).  It starts
+// zeroed; the kernels clear the counters, error words and list count at the
+// start of every call, and the winner table is tagged with the epoch that
+// every call advances, so it is never cleared (except at the epoch's 2^32
+// wrap, by the last copy workgroup).
+constexpr uint64_t kNoAllocMaxPositions = 1ull << 19;       // max_num_reqs * top_k
+constexpr uint64_t kNoAllocMaxWinEntries = 34ull << 16;     // (max_num_reqs-1)*min(stride,65536) + 65536
+constexpr uint64_t kNoAllocControlBytes = (kvx::kControlWords * 4 + 255) / 256 * 256;
+constexpr uint64_t kNoAllocBytes = kNoAllocControlBytes + kNoAllocMaxWinEntries * 8 + kNoAllocMaxPositions * 16;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
 struct State {
     bool inited = false;
     int device = 0;
@@ -49,6 +64,7 @@ struct State {
     std::vector<void *> retired;    // replaced scratch buffers, freed by kvx_close
     int lastSieveVariant = -1;
     int forcedSieveVariant = -1;
+    void *noAllocScratch[64] = {};  // device address of `scratch`, per device (set at init)
 };
 
 State g;
@@ -272,7 +288,7 @@ struct GatherCall {
     uint32_t blockDim, stride;
 };
 
-void DoGather(const GatherCall &c)
+void DoGather(const GatherCall &c, const kvx::RowScratch *fixed = nullptr)
 {
     EnsureInited();
     if (c.blockDim > 8) throw Error("import blockDim must be <= 8 (status slot layout)");  // kvops_ext.cpp:228-230
@@ -324,6 +340,18 @@ void DoGather(const GatherCall &c)
         CheckStatusBlock(c.status, 0, c.nodeNum, bd, "import_all");
     } else {
         CheckStatusBlock(c.status, c.myNode, 1, bd, "import_seg");
+    }
+    if (fixed != nullptr) {
+        // the no-allocation form: the fixed scratch bounds the call
+        if (need.list > fixed->listCap || need.win > fixed->winEntries) {
+            throw Error("import_all_noalloc: max_num_reqs*top_k = " + std::to_string(need.list) + " (max " +
+                        std::to_string(fixed->listCap) + ") and winner rows (max_num_reqs-1)*min(stride,65536)+65536 = " +
+                        std::to_string(need.win) + " (max " + std::to_string(fixed->winEntries) +
+                        ") must fit the fixed scratch");
+        }
+        for (uint32_t s = 0; s < c.nodeNum; ++s) ClearStatusWords(c.status, s, bd);
+        hipCheck(kvx::launch_gather(plan, *fixed, reinterpret_cast<uint64_t>(g.overflow), st), "kvc_gather_rows launch");
+        return;
     }
     std::lock_guard<std::mutex> lk(g_scratchMu);
     const kvx::RowScratch scr = ScratchFor(c.stream, need, c.fused ? "import_all" : "import_seg").rows;
@@ -414,6 +442,15 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
             need.win = 65536;
             need.list = 65536;
             (void)ScratchFor(0, need, "init");
+        }
+        // the no-allocation entry point's scratch on this device: the
+        // symbol's device address (the host-side name is not one)
+        if (device_id < 0 || device_id >= 64) throw Error("kvx_init: device_id must be in [0, 64)");
+        if (g.noAllocScratch[device_id] == nullptr) {
+            void *p = nullptr;
+            hipCheck(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+            if (p == nullptr) throw Error("hipGetSymbolAddress(scratch) returned null");
+            g.noAllocScratch[device_id] = p;
         }
         hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
         g.inited = true;
@@ -591,6 +628,59 @@ int kvx_import_all(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32
         c.blockDim = block_dim;
         c.stride = hot_req_stride_rows;
         DoGather(c);
+    });
+}
+
+int kvx_import_all_noalloc(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,
+                           uint32_t row_bytes, uint64_t topk_indices, uint64_t req_pool_indices,
+                           uint64_t req_host_base, uint64_t topk_device_slots, uint64_t is_miss, uint64_t num_real,
+                           uint64_t hot_row_base, uint32_t top_k, uint32_t max_num_reqs, uint32_t stripe_rows,
+                           uint32_t node_num, uint64_t status, uint64_t stream, uint32_t block_dim,
+                           uint32_t hot_req_stride_rows)
+{
+    return Guarded([&] {
+        EnsureInited();
+        if (seg_bases == nullptr) throw Error("import_all_noalloc: seg_bases is null");
+        if (node_num == 0 || node_num > 64) throw Error("import_seg: node_num must be in [1, 64]");
+        void *base = g.noAllocScratch[g.device];
+        if (base == nullptr) throw Error("import_all_noalloc: scratch address not set up on this device");
+        unsigned char *b = static_cast<unsigned char *>(base);
+        kvx::RowScratch fixed{};
+        uint32_t *ctl = reinterpret_cast<uint32_t *>(b);
+        fixed.counters = ctl;
+        fixed.errs = ctl + 64 * 8;
+        fixed.tickets = ctl + 2 * 64 * 8;
+        fixed.listCount = fixed.tickets + 8;
+        fixed.epoch = fixed.tickets + 9;
+        fixed.win = reinterpret_cast<unsigned long long *>(b + kNoAllocControlBytes);
+        fixed.winEntries = kNoAllocMaxWinEntries;
+        fixed.listSrc = reinterpret_cast<uint64_t *>(b + kNoAllocControlBytes + kNoAllocMaxWinEntries * 8);
+        fixed.listDst = fixed.listSrc + kNoAllocMaxPositions;
+        fixed.listCap = kNoAllocMaxPositions;
+        GatherCall c{};
+        c.fused = true;
+        c.nSeg = node_num;
+        for (uint32_t s = 0; s < node_num; ++s) c.segBases[s] = seg_bases[s];
+        c.segBase = seg_bases[0];
+        c.layerOffsetRows = layer_offset_rows;
+        c.perLayerSegRows = per_layer_seg_rows;
+        c.rowBytes = row_bytes;
+        c.topk = topk_indices;
+        c.pool = req_pool_indices;
+        c.hostBase = req_host_base;
+        c.slots = topk_device_slots;
+        c.isMiss = is_miss;
+        c.numReal = num_real;
+        c.hotRowBase = hot_row_base;
+        c.topK = top_k;
+        c.maxNumReqs = max_num_reqs;
+        c.stripeRows = stripe_rows;
+        c.nodeNum = node_num;
+        c.status = status;
+        c.stream = stream;
+        c.blockDim = block_dim;
+        c.stride = hot_req_stride_rows;
+        DoGather(c, &fixed);
     });
 }
 

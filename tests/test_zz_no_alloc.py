@@ -1,0 +1,108 @@
+"""kvx_import_all_noalloc (the import with a fixed scratch array per GPU,
+for callers that cannot allocate) against kvx_import_all, both called
+through the C ABI: every hot-buffer byte and every status word equal, and
+equal to the oracle's, on two calls in a row with the second one smaller;
+a call beyond the fixed scratch's limits fails before anything runs."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import read_words
+from kv_offload_proto_amd.kvops_ext import lib_path
+from kv_offload_proto_amd.xds import HostSegPool, XdsOffloadCoordinator, streams
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+ROW = 1152
+_u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
+IMPORT_ARGS = [ctypes.POINTER(_u64), _u32, _u32, _u32, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _u32, _u32, _u32,
+               _u32, _u64, _u64, _u32, _u32]
+
+
+def _lib():
+    lib = ctypes.CDLL(lib_path())
+    for name in ("kvx_import_all", "kvx_import_all_noalloc"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = IMPORT_ARGS
+    lib.kvx_last_error.restype = ctypes.c_char_p
+    return lib
+
+
+def _call(lib, name, pool, layer, topk, coord, nr, hot, top_k, max_num_reqs, status, stride):
+    bases = (_u64 * pool.node_num)(*[sg.seg_base for sg in pool.pool.segments])
+    rc = getattr(lib, name)(bases, layer * pool.per_layer_seg_rows, pool.per_layer_seg_rows, ROW, topk.data_ptr(),
+                            coord._req_pool_indices.data_ptr(), coord.req_host_base.data_ptr(),
+                            coord.top_k_device_slots.data_ptr(), coord.is_miss.data_ptr(), nr.data_ptr(),
+                            hot.data_ptr(), top_k, max_num_reqs, pool.stripe_rows, pool.node_num, status,
+                            torch.cuda.current_stream().cuda_stream, 2, stride)
+    return rc
+
+
+def test_import_all_noalloc_matches_import_all(kvops):
+    L, R, prefill, dbs, top_k, N = 1, 16, 8192, 4096, 2048, 4
+    print("no-alloc import", R, prefill, dbs, top_k, N, flush=True)
+    lib = _lib()
+    rows = R * prefill
+    pool = HostSegPool(0, L, rows, ROW, stripe_rows=1, node_num=N)
+    pool.create_pool()
+    try:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(41)
+        src = torch.randint(0, 256, (L, rows, ROW), dtype=torch.uint8, device="cuda", generator=g)
+        pool.wait(pool.batch_write_alllayers(0, rows, src, rows * ROW))
+        coord = XdsOffloadCoordinator("cuda", L, R, dbs, top_k, R, prefill)
+        st = orc.SieveState(L, R, dbs, top_k)
+        for r in range(R):
+            coord.admit_request(r, r, prefill, r * prefill)
+            st.admit(r, prefill)
+        coord.set_batch(torch.arange(R, dtype=torch.int64, device="cuda"),
+                        torch.full((R,), prefill, dtype=torch.int32, device="cuda"))
+        padded = coord.padded_buffer_size
+        segs = [v.reshape(-1) for v in pool.segment_views()]
+        hot_a = torch.zeros((R * padded, ROW), dtype=torch.uint8, device="cuda")
+        hot_b = torch.zeros_like(hot_a)
+        hot_o = np.zeros((R * padded, ROW), dtype=np.uint8)
+        sa, sb = kvops.alloc_status(N), kvops.alloc_status(N)
+        rng = np.random.default_rng(12)
+        # call 1: every row of the batch; call 2: a smaller batch (5 rows
+        # allocated, 4 of them real) on the state the first call left
+        for call, (mnr, nreal) in enumerate([(R, R), (5, 4)]):
+            batch = streams.state_batch(rng, st.tokens[0, :, :dbs], prefill, top_k, 0.2, zipf_s=1.1)
+            batch[mnr:] = -1
+            topk_d = torch.from_numpy(batch).cuda()
+            nr = torch.tensor([nreal], dtype=torch.int32, device="cuda")
+            coord.num_real.fill_(nreal)
+            coord.sieve_update(0, topk_d)
+            e_slots, e_miss = st.update(0, batch, np.arange(R), np.full(R, prefill), nreal, max_num_reqs=R)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(coord.top_k_device_slots.cpu().numpy(), e_slots)
+            assert _call(lib, "kvx_import_all", pool, 0, topk_d, coord, nr, hot_a, top_k, mnr, sa, padded) == 0, \
+                lib.kvx_last_error()
+            assert _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_b, top_k, mnr, sb,
+                         padded) == 0, lib.kvx_last_error()
+            pool.wait(sa, block_dim=2)
+            pool.wait(sb, block_dim=2)
+            torch.cuda.synchronize()
+            for s in range(N):
+                _, w = orc.gather_rows(segs, hot_o.reshape(-1), 0, ROW, batch, np.arange(R), np.arange(R) * prefill,
+                                       e_slots, e_miss, nreal, top_k, mnr, 1, N, s, hot_req_stride_rows=padded,
+                                       block_dim=2)
+                want = [int(x) for x in w]
+                assert read_words(sa + s * 64, 2) == want, (call, s)
+                assert read_words(sb + s * 64, 2) == want, (call, s)
+            assert torch.equal(hot_a, hot_b), call
+            assert torch.equal(hot_b, torch.from_numpy(hot_o).cuda()), call
+        # beyond the fixed scratch: 300 x 2048 positions > 524288
+        before = hot_b.clone()
+        big = 300
+        rc = _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_b, top_k, big, sb, padded)
+        assert rc != 0 and b"must fit the fixed scratch" in lib.kvx_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(before, hot_b)
+    finally:
+        pool.destroy(close_ext=False)
