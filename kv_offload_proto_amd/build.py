@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "kvops_ext")
 INCLUDE = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["sieve.hip", "sieve_fast.hip", "sieve_wave.hip", "rows.hip", "kvx_host.hip"]
+HIP_SOURCES = ["sieve.hip", "sieve_fast.hip", "sieve_wave.hip", "sieve_batch.hip", "rows.hip", "kvx_host.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [

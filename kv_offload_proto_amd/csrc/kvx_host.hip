@@ -35,8 +35,10 @@ struct Alloc {
 struct StreamScratch {
     uint64_t stream = 0;
     kvx::RowScratch rows{};
-    int32_t *shadow = nullptr;      // HBM-resident SIEVE variant: per-cell token shadow
+    int32_t *shadow = nullptr;      // HBM-resident SIEVE variants: per-cell token shadow
     uint64_t shadowCells = 0;
+    uint32_t *aux = nullptr;        // batch HBM SIEVE variant: per-row map, first occurrences, homes
+    uint64_t auxWords = 0;
 };
 
 // Scratch of kvx_import_all_noalloc: a fixed array in the library's code
@@ -59,6 +61,7 @@ struct State {
     int device = 0;
     uint64_t *overflow = nullptr;   // the 8-byte tail-slot word
     size_t ldsLimit = 0;            // dynamic LDS per workgroup usable by SIEVE
+    size_t ldsBatch = 0;            // the same for the batch HBM kernel (more static LDS)
     std::vector<Alloc> status;      // kvx_alloc_status allocations
     std::vector<StreamScratch *> scratch;  // one per stream that launched or reserved
     std::vector<void *> retired;    // replaced scratch buffers, freed by kvx_close
@@ -150,7 +153,7 @@ void CheckStatusBlock(uint64_t status, uint32_t firstNode, uint32_t nodes, uint3
 
 // Scratch needs of one launch (entries of each buffer; 0 = not used).
 struct ScratchNeed {
-    uint64_t win = 0, list = 0, shadow = 0;
+    uint64_t win = 0, list = 0, shadow = 0, aux = 0;
 };
 
 bool Capturing(hipStream_t s)
@@ -184,7 +187,7 @@ StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *
     }
     const bool create = sc == nullptr;
     const bool grow = create || sc->rows.winEntries < need.win || sc->rows.listCap < need.list ||
-                      sc->shadowCells < need.shadow;
+                      sc->shadowCells < need.shadow || sc->auxWords < need.aux;
     if (!grow) return *sc;
     hipStream_t st = AsStream(stream);
     if (Capturing(st)) {
@@ -226,13 +229,21 @@ StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *
         sc->shadow = static_cast<int32_t *>(p);
         sc->shadowCells = need.shadow;
     }
+    if (sc->auxWords < need.aux) {
+        // zeroed: the batch kernel's maps must start empty (each launch leaves them empty)
+        void *p = ScratchAlloc(need.aux * sizeof(uint32_t), st, "sieve batch scratch");
+        if (sc->aux != nullptr) g.retired.push_back(sc->aux);
+        sc->aux = static_cast<uint32_t *>(p);
+        sc->auxWords = need.aux;
+    }
     return *sc;
 }
 
 // The SIEVE kernel a row shape launches: 2 = parallel LDS kernel, 4 = the same
 // with the compact LDS layout (token hashes in LDS, tokens in HBM), 0 =
-// sequential LDS kernel, 3 = sequential HBM-resident kernel with wave-wide
-// probes (1 = the single-lane HBM kernel, only when forced).
+// sequential LDS kernel, 5 = batch HBM-resident kernel (state in HBM,
+// decisions and bitmaps in LDS), 3 = sequential HBM-resident kernel with
+// wave-wide probes (1 = the single-lane HBM kernel, only when forced).
 struct SievePlan {
     int variant = 0;
     size_t ldsLaunch = 0;   // dynamic LDS of the launch
@@ -251,15 +262,19 @@ SievePlan PlanSieve(uint32_t top_k, uint32_t dbs, uint32_t padded, uint32_t visS
     const size_t ldsCompact = kvx::fast_layout_for(padded, htSize, top_k, dbs, visStrideB, true).total;
     const bool fastOk = fastShape && ldsFast <= g.ldsLimit;
     const bool compactOk = fastShape && ldsCompact <= g.ldsLimit && lds <= g.ldsLimit;
-    int v = fastOk ? 2 : (compactOk ? 4 : (lds <= g.ldsLimit ? 0 : 3));
+    const size_t ldsBatch = kvx::batch_layout(dbs, htSize, top_k).total;
+    const bool batchOk = top_k >= 1 && top_k < (1u << 24) && dbs <= 65535 && htSize >= 1024 && ldsBatch <= g.ldsBatch;
+    int v = fastOk ? 2 : (compactOk ? 4 : (lds <= g.ldsLimit ? 0 : (batchOk ? 5 : 3)));
     const int f = g.forcedSieveVariant;
     if (f == 0 && lds <= g.ldsLimit) v = 0;
     if (f == 1) v = 1;
     if (f == 2 && fastOk) v = 2;
     if (f == 3) v = 3;
     if (f == 4 && compactOk) v = 4;
+    if (f == 5 && batchOk) v = 5;
     p.variant = v;
-    p.ldsLaunch = v == 2 ? ldsFast : (v == 4 ? std::max(ldsCompact, lds) : (v == 0 ? lds : 0));
+    p.ldsLaunch = v == 2 ? ldsFast
+                         : (v == 4 ? std::max(ldsCompact, lds) : (v == 0 ? lds : (v == 5 ? ldsBatch : 0)));
     // the parallel kernel's direct token -> slot map takes the LDS left over
     // (rows whose prefill exceeds it probe the table instead)
     if (v == 2 && g.ldsLimit > ldsFast) {
@@ -272,7 +287,8 @@ SievePlan PlanSieve(uint32_t top_k, uint32_t dbs, uint32_t padded, uint32_t visS
 ScratchNeed SieveScratchNeed(const SievePlan &p, uint32_t maxNumReqs, uint32_t htSize)
 {
     ScratchNeed n;
-    if (p.variant == 3) n.shadow = static_cast<uint64_t>(maxNumReqs) * htSize;
+    if (p.variant == 3 || p.variant == 5) n.shadow = static_cast<uint64_t>(maxNumReqs) * htSize;
+    if (p.variant == 5) n.aux = static_cast<uint64_t>(maxNumReqs) * kvx::batch_aux_words(htSize);
     return n;
 }
 
@@ -434,6 +450,8 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         g.ldsLimit = static_cast<size_t>(lds) - 1024;  // room for the kernels' static LDS (under 1 KiB)
         hipCheck(kvx::sieve_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS)");
         hipCheck(kvx::sieve_fast_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS fast)");
+        g.ldsBatch = static_cast<size_t>(lds) - 6 * 1024;  // the batch kernel keeps ~4.2 KiB of static LDS
+        hipCheck(kvx::sieve_batch_set_lds_limit(g.ldsBatch), "hipFuncSetAttribute(LDS batch)");
         {
             // the null stream's scratch at a default size, so that callers on
             // the null stream start without an allocation on the launch path
@@ -475,7 +493,9 @@ int kvx_reserve_scratch(uint64_t stream, uint32_t max_num_reqs, uint32_t top_k, 
             while (ht < 2ull * (static_cast<uint64_t>(padded) + top_k)) ht <<= 1;
             if (padded <= 65534 && ht <= (1ull << 31)) {
                 const SievePlan p = PlanSieve(top_k, device_buffer_size, padded, vis, 1, static_cast<uint32_t>(ht));
-                need.shadow = SieveScratchNeed(p, max_num_reqs, static_cast<uint32_t>(ht)).shadow;
+                const ScratchNeed sn = SieveScratchNeed(p, max_num_reqs, static_cast<uint32_t>(ht));
+                need.shadow = sn.shadow;
+                need.aux = sn.aux;
             }
         }
         std::lock_guard<std::mutex> lk(g_scratchMu);
@@ -492,7 +512,8 @@ int kvx_scratch_bytes(uint64_t stream, uint64_t *out_bytes)
         for (const StreamScratch *s : g.scratch) {
             if (s->stream != stream) continue;
             b = kvx::kControlWords * sizeof(uint32_t) + s->rows.winEntries * sizeof(unsigned long long) +
-                s->rows.listCap * 2 * sizeof(uint64_t) + s->shadowCells * sizeof(int32_t);
+                s->rows.listCap * 2 * sizeof(uint64_t) + s->shadowCells * sizeof(int32_t) +
+                s->auxWords * sizeof(uint32_t);
         }
         *out_bytes = b;
     });
@@ -830,6 +851,13 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
                                          "sieve_update").shadow;
             hipCheck(kvx::launch_sieve_update_wave(a, reinterpret_cast<uint64_t>(g.overflow), shadow, AsStream(stream)),
                      "hisp_sieve_update launch");
+        } else if (plan.variant == 5) {
+            std::lock_guard<std::mutex> lk(g_scratchMu);
+            const StreamScratch &sc =
+                ScratchFor(stream, SieveScratchNeed(plan, max_num_reqs, static_cast<uint32_t>(htSize)), "sieve_update");
+            hipCheck(kvx::launch_sieve_update_batch(a, reinterpret_cast<uint64_t>(g.overflow), sc.shadow, sc.aux,
+                                                    AsStream(stream)),
+                     "hisp_sieve_update launch");
         } else {
             hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), plan.variant,
                                               plan.variant == 0 ? plan.ldsLaunch : 0, AsStream(stream)),
@@ -884,6 +912,7 @@ int kvx_close(void)
                 if (s->rows.listSrc != nullptr) (void)hipFree(s->rows.listSrc);
                 if (s->rows.counters != nullptr) (void)hipFree(s->rows.counters);
                 if (s->shadow != nullptr) (void)hipFree(s->shadow);
+                if (s->aux != nullptr) (void)hipFree(s->aux);
                 delete s;
             }
             g.scratch.clear();
@@ -953,7 +982,7 @@ int kvx_last_sieve_variant(void) { return g.lastSieveVariant; }
 int kvx_sieve_force_variant(int variant)
 {
     return Guarded([&] {
-        if (variant < -1 || variant > 4) throw Error("sieve_force_variant: variant must be -1 or 0..4");
+        if (variant < -1 || variant > 5) throw Error("sieve_force_variant: variant must be -1 or 0..5");
         g.forcedSieveVariant = variant;
     });
 }

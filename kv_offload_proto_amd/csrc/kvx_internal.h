@@ -203,6 +203,49 @@ __host__ __device__ __forceinline__ FastLayout fast_layout_for(uint32_t padded, 
     return fast_layout(padded, htSize, topK, visStrideB, compact);
 }
 
+// ---------------------------------------------------------------------------
+// The batch HBM SIEVE kernel (sieve_batch.hip): one workgroup of
+// kBatchThreads per batch row; LDS holds the row's visited and evicted
+// bitmaps, a bitmap over the table cells, per-position codes and slots, and
+// a stage of table cells; HBM scratch per row holds a token -> slot map and
+// first-occurrence table of kBatchMapCap tokens and a home per table cell.
+// ---------------------------------------------------------------------------
+constexpr int kBatchThreads = 1024;
+constexpr int kBatchWaves = kBatchThreads / 64;
+constexpr uint32_t kBatchStage = 4096;       // table cells staged per step of the deletion walk
+constexpr uint32_t kBatchMapCap = 1u << 18;  // tokens the map holds (rows with larger tokens run in order)
+
+struct BatchLayout {
+    uint32_t vis, ev, del, slot, uni, uniL1, uniL2, stage, total;
+};
+
+__host__ __device__ __forceinline__ BatchLayout batch_layout(uint32_t dbs, uint32_t htSize, uint32_t topK)
+{
+    BatchLayout l{};
+    const uint32_t nVisW = (dbs + 63u) / 64u, nCellW = htSize / 64u, nL1 = (nCellW + 63u) / 64u,
+                   nL2 = (nL1 + 63u) / 64u;
+    uint32_t o = 0;
+    l.vis = o;    o += nVisW * 8u;
+    l.ev = o;     o += nVisW * 8u;
+    l.del = o;    o += nCellW * 8u;
+    l.slot = o;   o += align16(topK * 4u);
+    l.uni = o;
+    l.uniL1 = o + nCellW * 8u;
+    l.uniL2 = l.uniL1 + nL1 * 8u;
+    const uint32_t bitBytes = (nCellW + nL1 + nL2) * 8u;
+    const uint32_t uniBytes = topK * 4u > bitBytes ? topK * 4u : bitBytes;
+    o += align16(uniBytes);
+    l.stage = o;  o += kBatchStage * 4u;
+    l.total = o;
+    return l;
+}
+
+// uint32 words of HBM scratch per row: map, first occurrences, homes (uint16).
+__host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t htSize)
+{
+    return 2ull * kBatchMapCap + htSize / 2u;
+}
+
 // Launchers (implemented next to their kernels).
 hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int variant,
                                size_t ldsBytes, hipStream_t stream);
@@ -214,6 +257,9 @@ hipError_t launch_sieve_update_wave(const HispSieveUpdateArgs &a, uint64_t overf
                                     hipStream_t stream);
 hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes,
                                     bool compact, hipStream_t stream);
+hipError_t launch_sieve_update_batch(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,
+                                     uint32_t *aux, hipStream_t stream);
+hipError_t sieve_batch_set_lds_limit(size_t bytes);
 
 struct GatherPlan {
     KvcGatherArgs a;               // args of the first (or only) segment

@@ -1,0 +1,790 @@
+// SIEVE update for rows whose state does not fit LDS, decided in one pass
+// and applied to the hash table in batch (variant 5).
+//
+// One 1024-lane workgroup per batch row; the state stays in HBM.  The result
+// equals the in-order recurrence of hisp_sieve_update.cpp:115-163 whenever
+// the row's table is canonical (every live token findable at its own slot)
+// and the step's hand does not pass a slot twice; otherwise the row runs that
+// recurrence (sieve_hbm.h) instead.  Phases:
+//
+//  1. check: a token -> slot map of the row (HBM scratch: every launch leaves
+//     the map, first-occurrence table and homes zeroed) finds duplicate tokens; a scan of the table checks that each
+//     occupied cell names a live slot, no slot twice, every live slot once,
+//     and that no empty cell lies between an entry's home and its cell (so a
+//     probe from the home reaches it); each cell's home is kept for step 4;
+//  2. decide, on one lane, from LDS only: each position's first occurrence in
+//     the batch and the initial slot of its token are found in parallel
+//     first; a later occurrence hits the first one's slot (without a wrap
+//     nothing placed or hit in this step leaves it), a first occurrence hits
+//     its initial slot unless the hand evicted that slot earlier in the step,
+//     and a miss sweeps the visited bitmap from the hand;
+//  3. outputs, tokens, visited bits and hand, in parallel;
+//  4. deletion of the evicted tokens' cells: Algorithm R leaves a table as if
+//     the deleted key had never been inserted, so all of the step's
+//     deletions give the same table in any order; one left-to-right pass per
+//     cluster that holds a deleted cell does them all: walking the cluster
+//     from its first deleted cell, each entry moves into the leftmost hole at
+//     or after its home, if any (its cell then becomes a hole).  The pass
+//     runs 64 cells at a time on one wave: which entries move depends only
+//     on the rightmost hole (an entry moves iff it is at or after its home),
+//     found with ballots to a fixpoint, and the moves then take their holes
+//     in order from a three-level hole bitmap;
+//  5. the step's new tokens go in in position order, each into the first
+//     empty cell at or after its home (a three-level bitmap of empty cells):
+//     with step 4 this is the table the in-order recurrence leaves, which
+//     equals inserting the live tokens in the order they were inserted.
+#include "kvx_internal.h"
+#include "sieve_hbm.h"
+
+namespace kvx {
+namespace {
+
+using namespace sieve_hbm;
+
+constexpr int BT = kBatchThreads;
+constexpr uint32_t kInvalid = 0xFFFFFFFFu;   // position: outside [0, seqLen)
+constexpr uint32_t kExt = 0xFFFFFFFEu;       // position: at or past prefill
+constexpr uint32_t kNotRes = 0xFFFFFFFDu;    // position: first occurrence, token not resident
+constexpr uint32_t kDup = 0x80000000u;       // position: later occurrence of the position in the low bits
+constexpr uint32_t kMissBit = 0x80000000u;   // slotOut: the position was a miss
+constexpr int kCheckUnroll = 8;              // 64-cell loads in flight per lane in the check
+
+struct BatchParams {
+    KvxLaunch<HispSieveUpdateArgs> L;
+    int32_t *shadow;   // [maxNumReqs][H] table shadow for the in-order fallback
+    uint32_t *aux;     // [maxNumReqs][auxWords]: map [mapCap], first [mapCap], homes [H] u16
+    uint64_t auxWords;
+    uint32_t mapCap;
+    BatchLayout lay;
+};
+
+__device__ __forceinline__ int bit_get(const uint64_t *b, uint32_t i) { return (b[i >> 6] >> (i & 63)) & 1; }
+
+// A three-level bitmap over n bits (n a multiple of 64): l1 bit w is set iff
+// l0 word w is nonzero, l2 bit v iff l1 word v is nonzero.  Searches read at
+// most one word per level going up and one going down (plus the l2 words,
+// 64 bits per 2^18 cells).  Uniform in the wave: every lane reads the same
+// words; one lane writes (the wave's LDS operations complete in order, so
+// its later reads see the writes).
+struct Bits3 {
+    uint64_t *l0, *l1, *l2;
+    uint32_t n;
+};
+
+__device__ __forceinline__ uint64_t from_bit(uint32_t b) { return ~0ull << (b & 63u); }
+
+// First set bit at or after i, or -1.
+__device__ __forceinline__ int64_t next_set(const Bits3 &m, uint32_t i)
+{
+    if (i >= m.n) return -1;
+    const uint32_t w = i >> 6;
+    const uint64_t x0 = m.l0[w] & from_bit(i);
+    if (x0) return (static_cast<int64_t>(w) << 6) + __builtin_ctzll(x0);
+    const uint32_t nw = m.n >> 6, n1 = (nw + 63u) >> 6;
+    const uint32_t s1 = w + 1u;  // l0 words after w
+    if (s1 < nw && (s1 & 63u)) {
+        const uint64_t x1 = m.l1[s1 >> 6] & from_bit(s1);
+        if (x1) {
+            const uint32_t w0 = ((s1 >> 6) << 6) + static_cast<uint32_t>(__builtin_ctzll(x1));
+            return (static_cast<int64_t>(w0) << 6) + __builtin_ctzll(m.l0[w0]);
+        }
+    }
+    uint32_t s2 = (s1 + 63u) >> 6;  // l1 words after the one searched
+    while (s2 < n1) {
+        const uint64_t x2 = m.l2[s2 >> 6] & from_bit(s2);
+        if (x2) {
+            const uint32_t w1 = ((s2 >> 6) << 6) + static_cast<uint32_t>(__builtin_ctzll(x2));
+            const uint32_t w0 = (w1 << 6) + static_cast<uint32_t>(__builtin_ctzll(m.l1[w1]));
+            return (static_cast<int64_t>(w0) << 6) + __builtin_ctzll(m.l0[w0]);
+        }
+        s2 = ((s2 >> 6) + 1u) << 6;
+    }
+    return -1;
+}
+
+__device__ __forceinline__ void set_bit3(const Bits3 &m, uint32_t i, bool writer)
+{
+    const uint32_t w = i >> 6, v = w >> 6;
+    const uint64_t x0 = m.l0[w] | (1ull << (i & 63u));
+    const uint64_t x1 = m.l1[v] | (1ull << (w & 63u));
+    const uint64_t x2 = m.l2[v >> 6] | (1ull << (v & 63u));
+    if (writer) {
+        m.l0[w] = x0;
+        m.l1[v] = x1;
+        m.l2[v >> 6] = x2;
+    }
+}
+
+__device__ __forceinline__ void clr_bit3(const Bits3 &m, uint32_t i, bool writer)
+{
+    const uint32_t w = i >> 6, v = w >> 6;
+    const uint64_t x0 = m.l0[w] & ~(1ull << (i & 63u));
+    if (writer) m.l0[w] = x0;
+    if (x0) return;
+    const uint64_t x1 = m.l1[v] & ~(1ull << (w & 63u));
+    if (writer) m.l1[v] = x1;
+    if (x1) return;
+    const uint64_t x2 = m.l2[v >> 6] & ~(1ull << (v & 63u));
+    if (writer) m.l2[v >> 6] = x2;
+}
+
+__global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
+{
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int32_t sScan[BT];
+    __shared__ int32_t sBad, sWrap, sLive, sOcc, sNamed, sNdel, sHand, sE0;
+
+    const HispSieveUpdateArgs &a = P.L.a;
+    const int32_t K = static_cast<int32_t>(a.topK);
+    const int32_t dbs = static_cast<int32_t>(a.deviceBufferSize);
+    const int32_t padded = static_cast<int32_t>(a.paddedBufferSize);
+    const int32_t visStrideB = static_cast<int32_t>(a.visitedStrideB);
+    const int32_t maxNumReqs = static_cast<int32_t>(a.maxNumReqs);
+    const int32_t H = static_cast<int32_t>(a.htSize);
+    const uint32_t mask = static_cast<uint32_t>(H) - 1u;
+    const int32_t poolSize = static_cast<int32_t>(a.poolSize);
+    const int32_t bid = blockIdx.x;
+    const int tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    if (bid >= maxNumReqs) return;
+
+    int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
+    if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
+    int32_t *rs = reinterpret_cast<int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
+    int8_t *rm = reinterpret_cast<int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
+    if (bid >= numReal) {
+        write_dummy_row(rs, rm, K);
+        return;
+    }
+    const int64_t reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
+    if (reqIdx < 0 || reqIdx >= poolSize) {
+        write_dummy_row(rs, rm, K);
+        return;
+    }
+    const int32_t seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
+    const int32_t prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
+    const int32_t *rt = reinterpret_cast<const int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    Row r;
+    r.tok = reinterpret_cast<int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
+    r.vis32 = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(a.deviceBufferVisited) + reqIdx * visStrideB);
+    r.ht = reinterpret_cast<uint16_t *>(a.deviceBufferHt) + reqIdx * H;
+    r.ct = P.shadow + static_cast<int64_t>(bid) * H;
+    r.mask = H - 1;
+    r.dbs = dbs;
+    r.padded = padded;
+    int32_t *gHand = reinterpret_cast<int32_t *>(a.sieveHand) + reqIdx * kHandStride;
+    uint64_t *vis64 = reinterpret_cast<uint64_t *>(r.vis32);
+    uint32_t *map = P.aux + static_cast<uint64_t>(bid) * P.auxWords;
+    uint32_t *first = map + P.mapCap;
+    uint16_t *homes = reinterpret_cast<uint16_t *>(first + P.mapCap);
+    const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
+
+    const BatchLayout &y = P.lay;
+    uint64_t *visB = reinterpret_cast<uint64_t *>(lds + y.vis);
+    uint64_t *evB = reinterpret_cast<uint64_t *>(lds + y.ev);
+    uint64_t *delB = reinterpret_cast<uint64_t *>(lds + y.del);       // also the named-slot bits of phase 1
+    uint32_t *slotOut = reinterpret_cast<uint32_t *>(lds + y.slot);
+    uint32_t *code = reinterpret_cast<uint32_t *>(lds + y.uni);       // phase 2 ...
+    uint64_t *bitL0 = reinterpret_cast<uint64_t *>(lds + y.uni);      // ... then holes (4), empty cells (5)
+    uint64_t *bitL1 = reinterpret_cast<uint64_t *>(lds + y.uniL1);
+    uint64_t *bitL2 = reinterpret_cast<uint64_t *>(lds + y.uniL2);
+    const Bits3 bits{bitL0, bitL1, bitL2, static_cast<uint32_t>(H)};
+    uint32_t *stage = reinterpret_cast<uint32_t *>(lds + y.stage);
+    const uint32_t nVisW = (static_cast<uint32_t>(dbs) + 63u) / 64u;
+    const uint32_t nCellW = static_cast<uint32_t>(H) / 64u;
+    const uint32_t nL1 = (nCellW + 63u) / 64u;
+    const uint32_t nL2 = (nL1 + 63u) / 64u;
+
+    // ---- 1. check ------------------------------------------------------
+    if (tid == 0) {
+        sBad = 0;
+        sWrap = 0;
+        sLive = 0;
+        sOcc = 0;
+        sNamed = 0;
+        sNdel = 0;
+    }
+    for (uint32_t w = tid; w < nVisW; w += BT) {
+        visB[w] = vis64[w];
+        evB[w] = 0ull;
+    }
+    for (uint32_t w = tid; w < nCellW; w += BT) delB[w] = 0ull;
+    __syncthreads();
+    {
+        // the map by plain stores; a token held by two slots is found when
+        // the map is read back below (one of them reads the other's slot)
+        int32_t live = 0, bad = 0;
+        for (int32_t s = tid; s < dbs; s += BT) {
+            const int32_t t = r.tok[s];
+            if (t < 0) continue;
+            ++live;
+            if (t >= mapLim) {
+                bad = 1;
+            } else {
+                map[t] = static_cast<uint32_t>(s + 1);
+            }
+        }
+        if (live) atomicAdd(&sLive, live);
+        if (bad) sBad = 1;
+    }
+    __syncthreads();
+    {
+        int32_t bad = 0;
+        for (int32_t s = tid; s < dbs; s += BT) {
+            const int32_t t = r.tok[s];
+            if (t >= 0 && t < mapLim && map[t] != static_cast<uint32_t>(s + 1)) bad = 1;
+        }
+        if (bad) sBad = 1;
+    }
+    // The table in one segment per wave, read 64 cells per load, four loads
+    // in flight: first the last empty cell of each segment; then, with the
+    // last empty cell before each segment (cyclic), every occupied cell.
+    const uint32_t wave = static_cast<uint32_t>(tid) >> 6;
+    const uint32_t segCells = static_cast<uint32_t>(H) / kBatchWaves;  // a multiple of 64
+    const uint32_t seg0 = wave * segCells;
+    {
+        int32_t last = -1;
+        for (uint32_t base = seg0; base < seg0 + segCells; base += 64u * kCheckUnroll) {
+            uint16_t e[kCheckUnroll];
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                const uint32_t c = base + 64u * q + lane;
+                e[q] = c < seg0 + segCells ? r.ht[c] : static_cast<uint16_t>(1);
+            }
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                const uint64_t em = __ballot(e[q] == 0);
+                if (em) last = static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(em));
+            }
+        }
+        if (lane == 0) sScan[wave] = last;
+    }
+    __syncthreads();
+    {
+        int32_t lastAll = -1, carry = -1;
+        for (uint32_t w = 0; w < kBatchWaves; ++w) {
+            const int32_t v = sScan[w];
+            if (v >= 0) {
+                lastAll = v;
+                if (w < wave) carry = v;
+            }
+        }
+        if (tid == 0) {
+            sE0 = lastAll;
+            if (lastAll < 0) sBad = 1;  // no empty cell: probes never stop
+        }
+        if (carry < 0) carry = lastAll;  // the probe runs wrap around the table end
+        int32_t occ = 0, bad = 0;
+        uint32_t *named = reinterpret_cast<uint32_t *>(delB);
+        for (uint32_t base = seg0; base < seg0 + segCells; base += 64u * kCheckUnroll) {
+            uint16_t e[kCheckUnroll];
+            int32_t t[kCheckUnroll];
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                const uint32_t c = base + 64u * q + lane;
+                e[q] = c < seg0 + segCells ? r.ht[c] : static_cast<uint16_t>(0);
+            }
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                const int32_t sl = static_cast<int32_t>(e[q]) - 1;
+                t[q] = (e[q] != 0 && sl < dbs) ? r.tok[sl] : -1;
+            }
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                const uint32_t c = base + 64u * q + lane;
+                const uint64_t em = __ballot(e[q] == 0 && c < seg0 + segCells);
+                // the last empty cell at or before this lane's cell
+                const uint64_t upTo = em & (lane == 63 ? ~0ull : ((2ull << lane) - 1ull));
+                const int32_t lastE = upTo ? static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(upTo)) : carry;
+                if (em) carry = static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(em));
+                if (e[q] == 0 || c >= seg0 + segCells) continue;
+                ++occ;
+                const int32_t sl = static_cast<int32_t>(e[q]) - 1;
+                if (sl >= dbs || t[q] < 0) {
+                    bad = 1;  // an entry naming a slot past the buffer or an empty slot
+                    continue;
+                }
+                atomicOr(named + (sl >> 5), 1u << (sl & 31));  // a slot named twice shows in the count below
+                const uint32_t home = ht_hash(t[q]) & mask;
+                homes[c] = static_cast<uint16_t>(home);
+                // no empty cell in [home, c): the last empty cell before c is
+                // further from c than the home is
+                if (((c - static_cast<uint32_t>(lastE)) & mask) <= ((c - home) & mask)) bad = 1;
+            }
+        }
+        if (occ) atomicAdd(&sOcc, occ);
+        if (bad) sBad = 1;
+    }
+    __syncthreads();
+    {
+        // every occupied cell names a distinct live slot iff the named slots
+        // number as many as the occupied cells (and as the live slots)
+        const uint32_t *named = reinterpret_cast<const uint32_t *>(delB);
+        int32_t cnt = 0;
+        for (int32_t w = tid; w < (dbs + 31) / 32; w += BT) cnt += __builtin_popcount(named[w]);
+        if (cnt) atomicAdd(&sNamed, cnt);
+    }
+    __syncthreads();
+    const bool canonical = sBad == 0 && sOcc == sLive && sNamed == sOcc;
+
+    // ---- 2. decide -----------------------------------------------------
+    if (canonical) {
+        for (int32_t k = tid; k < K; k += BT) {
+            const int32_t t = rt[k];
+            uint32_t c = kInvalid;
+            if (t >= 0 && t < seqLen) {
+                c = kExt;
+                if (t < prefill) {
+                    c = kNotRes;
+                    if (t < mapLim) atomicMax(first + t, static_cast<uint32_t>(K - k));
+                }
+            }
+            code[k] = c;
+            slotOut[k] = 0u;  // positions that change nothing read as hits of slot 0 without the miss bit
+        }
+        __syncthreads();
+        for (int32_t k = tid; k < K; k += BT) {
+            if (code[k] != kNotRes) continue;
+            const int32_t t = rt[k];
+            if (t >= mapLim) {
+                sBad = 1;  // a token the map cannot hold: decided in order instead
+                continue;
+            }
+            const int32_t f = K - static_cast<int32_t>(first[t]);
+            if (f < k) {
+                code[k] = kDup | static_cast<uint32_t>(f);
+            } else {
+                const uint32_t s0 = map[t];
+                if (s0 != 0u) code[k] = s0 - 1u;
+            }
+        }
+        __syncthreads();
+    }
+    if (canonical && sBad == 0 && tid < 64) {
+        // One wave, 64 positions per round: up to the round's first miss
+        // every position is a hit (a resident first occurrence whose slot the
+        // hand has not evicted, or a later occurrence) and is applied at
+        // once; the miss then sweeps.  The wave's LDS operations complete in
+        // order, so a sweep sees the visited bits set before it.
+        int32_t hand = gHand[0];
+        if (hand < 0 || hand >= dbs) hand = 0;  // hisp_sieve_update.cpp:108-111
+        int32_t passed = 0;
+        bool wrapped = false;
+        const uint32_t lastW = nVisW - 1u;
+        const uint64_t lastMask = (dbs & 63) ? ((1ull << (dbs & 63)) - 1ull) : ~0ull;
+        for (int32_t k0 = 0; k0 < K && !wrapped; k0 += 64) {
+            const int32_t k = k0 + static_cast<int32_t>(lane);
+            const uint32_t c = k < K ? code[k] : kInvalid;
+            const bool rel = c != kInvalid && c != kExt;
+            const bool res = rel && c != kNotRes && !(c & kDup);  // resident first occurrence: c is its slot
+            const bool dup = rel && c != kNotRes && (c & kDup);
+            const uint32_t cs = res ? c : 0u;  // an in-range slot for every lane
+            uint64_t pend = __ballot(rel);
+            while (pend) {
+                const bool mine = (pend >> lane) & 1ull;
+                const bool missNow = mine && (c == kNotRes || (res && bit_get(evB, cs)));
+                const uint64_t mm = __ballot(missNow);
+                const int j = mm ? __builtin_ctzll(mm) : 64;
+                const uint64_t seg = pend & (j < 64 ? ((1ull << j) - 1ull) : ~0ull);
+                if (((seg >> lane) & 1ull) && res) {
+                    slotOut[k] = c;
+                    atomicOr(reinterpret_cast<unsigned long long *>(visB + (c >> 6)), 1ull << (c & 63));
+                }
+                if (((seg >> lane) & 1ull) && dup) {
+                    // the first occurrence came earlier (an earlier round or
+                    // the slots just written): a hit on its slot, visited again
+                    const uint32_t sd = slotOut[c & ~kDup] & 0xFFFFu;
+                    slotOut[k] = sd;
+                    atomicOr(reinterpret_cast<unsigned long long *>(visB + (sd >> 6)), 1ull << (sd & 63));
+                }
+                pend &= ~seg;
+                if (j == 64) break;
+                // the miss: the hand passes visited slots, clearing them, and
+                // stops at the first unvisited one
+                int32_t h = -1;
+                while (h < 0) {
+                    const uint32_t wi = static_cast<uint32_t>(hand) >> 6;
+                    const uint32_t b = static_cast<uint32_t>(hand) & 63u;
+                    const uint64_t inRing = wi == lastW ? lastMask : ~0ull;
+                    const uint64_t word = visB[wi];
+                    const uint64_t unv = ~word & inRing & (~0ull << b);
+                    if (unv) {
+                        const uint32_t f = static_cast<uint32_t>(__builtin_ctzll(unv));
+                        const uint64_t cleared = ((1ull << f) - 1ull) & (~0ull << b);  // visited bits passed
+                        passed += static_cast<int32_t>(f - b) + 1;
+                        h = static_cast<int32_t>((wi << 6) + f);
+                        if (lane == 0) visB[wi] = (word & ~cleared) | (1ull << f);
+                    } else {
+                        const uint64_t cleared = inRing & (~0ull << b);
+                        passed += static_cast<int32_t>(__builtin_popcountll(cleared));
+                        if (lane == 0) visB[wi] = word & ~cleared;
+                        hand = wi == lastW ? 0 : static_cast<int32_t>((wi + 1u) << 6);
+                    }
+                    if (passed > dbs) {
+                        wrapped = true;
+                        break;
+                    }
+                }
+                if (wrapped) break;
+                if (lane == 0) {
+                    evB[h >> 6] |= 1ull << (h & 63);
+                    slotOut[k0 + j] = static_cast<uint32_t>(h) | kMissBit;
+                }
+                hand = h + 1 == dbs ? 0 : h + 1;
+                pend &= ~(1ull << j);
+            }
+        }
+        if (lane == 0) {
+            sHand = hand;
+            sWrap = wrapped ? 1 : 0;
+        }
+    }
+    __syncthreads();
+    const bool fast = canonical && sBad == 0 && sWrap == 0;
+
+    // the map and first-occurrence scratch are left zeroed (tokens still the
+    // initial ones here)
+    for (int32_t s = tid; s < dbs; s += BT) {
+        const int32_t t = r.tok[s];
+        if (t >= 0 && t < mapLim) map[t] = 0u;
+    }
+    for (int32_t k = tid; k < K; k += BT) {
+        const int32_t t = rt[k];
+        if (t >= 0 && t < seqLen && t < prefill && t < mapLim) first[t] = 0u;
+    }
+    __syncthreads();  // the cleanup read the initial tokens; phase 3 replaces some
+    if (!fast) {
+        // the homes too: the whole per-row scratch is zero between launches
+        // (a later launch may lay it out for another table size)
+        uint32_t *h32 = reinterpret_cast<uint32_t *>(homes);
+        for (int32_t w = tid; w < H / 2; w += BT) h32[w] = 0u;
+        // the in-order recurrence on the untouched row
+        build_shadow(r);
+        __threadfence_block();
+        __syncthreads();
+        if (tid < 64) recurrence(r, rt, rs, rm, K, seqLen, prefill, gHand, P.L.overflowSlot);
+        return;
+    }
+
+    // ---- 3. outputs, visited bits, hand; cells of the evicted slots -------
+    for (int32_t k = tid; k < K; k += BT) {
+        const uint32_t c = code[k];
+        int32_t slot = -1;
+        int8_t miss = 0;
+        if (c == kExt) {
+            slot = padded + (rt[k] - prefill);
+        } else if (c != kInvalid) {
+            const uint32_t s = slotOut[k];
+            slot = static_cast<int32_t>(s & 0xFFFFu);
+            miss = (s & kMissBit) ? 1 : 0;
+        }
+        rs[k] = slot;
+        rm[k] = miss;
+    }
+    for (uint32_t w = tid; w < nVisW; w += BT) vis64[w] = visB[w];
+    if (tid == 0) gHand[0] = sHand;
+    for (uint32_t w = tid; w < nCellW; w += BT) delB[w] = 0ull;
+    __syncthreads();  // code[] is dead from here on (its LDS becomes the bitmaps)
+    {
+        int32_t nd = 0;
+        for (uint32_t c = tid; c < static_cast<uint32_t>(H); c += BT) {
+            const uint16_t e = r.ht[c];
+            if (e != 0 && bit_get(evB, static_cast<uint32_t>(e) - 1u)) {
+                atomicOr(reinterpret_cast<unsigned long long *>(delB + (c >> 6)), 1ull << (c & 63));
+                ++nd;
+            }
+        }
+        if (nd) atomicAdd(&sNdel, nd);
+    }
+    // the new tokens (each evicted slot gets one: no wrap)
+    for (int32_t k = tid; k < K; k += BT) {
+        const uint32_t s = slotOut[k];
+        if (s & kMissBit) r.tok[s & 0xFFFFu] = rt[k];
+    }
+    for (uint32_t w = tid; w < nCellW; w += BT) bitL0[w] = 0ull;  // holes, in offsets from sE0
+    for (uint32_t w = tid; w < nL1; w += BT) bitL1[w] = 0ull;
+    for (uint32_t w = tid; w < nL2; w += BT) bitL2[w] = 0ull;
+    __syncthreads();
+
+    // ---- 4. the deletions, one pass per cluster with a deleted cell ------
+    // Offsets count cells from the empty cell sE0, so no cluster crosses 0.
+    // The walk's state lives in LDS and only wave 0 changes it; every wave
+    // stages the next chunk of cells.
+    __shared__ uint32_t sCur, sClusterLo;
+    __shared__ int32_t sLeft, sR;
+    const uint32_t e0 = static_cast<uint32_t>(sE0);
+    if (tid == 0) {
+        sCur = 1;
+        sLeft = sNdel;
+        sR = -1;
+        sClusterLo = 0;
+    }
+    for (;;) {
+        // every wave reads the walk state before wave 0 changes it again
+        __syncthreads();
+        const bool go = sLeft > 0 || sR >= 0;
+        const bool between = sR < 0;
+        __syncthreads();
+        if (!go) break;
+        if (between && tid < 64) {
+            // between clusters: skip to the next deleted cell (offset order)
+            uint32_t off = sCur;
+            uint32_t found = 0xFFFFFFFFu;
+            while (off < static_cast<uint32_t>(H)) {
+                const uint32_t cell = (e0 + off) & mask;
+                uint64_t m = delB[cell >> 6] & (~0ull << (cell & 63));
+                uint32_t span = 64u - (cell & 63);
+                const uint32_t toEnd = static_cast<uint32_t>(H) - off;
+                if (span > toEnd) {
+                    m &= (1ull << ((cell & 63) + toEnd)) - 1ull;
+                    span = toEnd;
+                }
+                if (m) {
+                    found = off + static_cast<uint32_t>(__builtin_ctzll(m)) - (cell & 63);
+                    break;
+                }
+                off += span;
+            }
+            if (lane == 0) {
+                if (found == 0xFFFFFFFFu) {
+                    sLeft = 0;  // cannot happen while deletions are left
+                } else {
+                    sCur = found;
+                    sClusterLo = found;
+                }
+            }
+        }
+        __syncthreads();
+        // wave 0 changes the state only after the staging barrier below
+        if (sLeft <= 0 && sR < 0) break;
+        // stage cells [chunk, chunk + kBatchStage) of the walk: entry | home << 16
+        const uint32_t chunk = sCur;
+        const uint32_t chunkEnd = chunk + kBatchStage < static_cast<uint32_t>(H) ? chunk + kBatchStage
+                                                                                : static_cast<uint32_t>(H);
+        for (uint32_t i = tid; i < kBatchStage; i += BT) {
+            const uint32_t off = chunk + i;
+            uint32_t v = 0u;
+            if (off < chunkEnd) {
+                const uint32_t cell = (e0 + off) & mask;
+                const uint16_t e = r.ht[cell];
+                v = e ? (static_cast<uint32_t>(e) | (static_cast<uint32_t>(homes[cell]) << 16)) : 0u;
+            }
+            stage[i] = v;
+        }
+        __syncthreads();
+        if (tid < 64) {
+            const bool wr = lane == 0;
+            bool bad = false;
+            int32_t R = sR;
+            uint32_t clusterLo = sClusterLo;
+            int32_t left = sLeft;
+            uint32_t w0 = chunk;
+            while ((left > 0 || R >= 0) && w0 < chunkEnd && !bad) {
+                if (R < 0) {
+                    // between clusters: the next deleted cell inside the chunk
+                    uint32_t off = w0;
+                    uint32_t found = 0xFFFFFFFFu;
+                    while (off < chunkEnd) {
+                        const uint32_t cell = (e0 + off) & mask;
+                        uint64_t m = delB[cell >> 6] & (~0ull << (cell & 63));
+                        uint32_t span = 64u - (cell & 63);
+                        if (span > chunkEnd - off) {
+                            m &= (1ull << ((cell & 63) + (chunkEnd - off))) - 1ull;
+                            span = chunkEnd - off;
+                        }
+                        if (m) {
+                            found = off + static_cast<uint32_t>(__builtin_ctzll(m)) - (cell & 63);
+                            break;
+                        }
+                        off += span;
+                    }
+                    if (found == 0xFFFFFFFFu) {
+                        w0 = chunkEnd;
+                        break;
+                    }
+                    w0 = found;
+                    clusterLo = found;
+                }
+                // one window of up to 64 cells from w0 (not past the chunk)
+                const uint32_t off = w0 + lane;
+                const bool inChunk = off < chunkEnd;
+                const uint32_t v = inChunk ? stage[off - chunk] : 0u;
+                const uint32_t cell = (e0 + off) & mask;
+                const uint32_t e = v & 0xFFFFu;
+                const bool occ = inChunk && e != 0u;
+                const bool del = occ && bit_get(delB, cell);
+                const uint32_t homeOff = ((v >> 16) - e0) & mask;
+                const uint64_t inMask = __ballot(inChunk);
+                // offset H is the empty cell e0 again: every cluster ends by then
+                const uint64_t emptyM = __ballot((inChunk && !occ) || off >= static_cast<uint32_t>(H));
+                const int f = emptyM ? __builtin_ctzll(emptyM) : 64;  // the cluster ends inside the window
+                const uint64_t active = (f < 64 ? ((1ull << f) - 1ull) : ~0ull) & inMask;
+                const uint64_t D = __ballot(del) & active;
+                // movers: an entry moves iff the rightmost hole before it (the
+                // last event so far) is at or after its home.  An entry right
+                // after an event moves iff it is displaced (home before its
+                // cell), so an event runs on through the displaced entries
+                // after it: each iteration extends the events through those
+                // runs (a segmented OR-scan by doubling) and then adds the
+                // entries whose home reaches back to the last event before them.
+                const uint64_t X = __ballot(occ && !del && homeOff < off) & active;  // displaced entries
+                uint64_t E = D;
+                for (int it = 0; it < 65; ++it) {
+                    uint64_t F = X & ((E << 1) | (R >= 0 && ((X & 1ull) != 0ull) &&
+                                                  static_cast<uint32_t>(R) == w0 - 1u ? 1ull : 0ull));
+                    uint64_t T = X;
+                    for (int d = 1; d < 64; d <<= 1) {
+                        F |= (F << d) & T;
+                        T &= T << d;
+                    }
+                    const uint64_t E1 = E | F;
+                    const uint64_t below = E1 & ((1ull << lane) - 1ull);
+                    const int32_t rcur = below ? static_cast<int32_t>(w0 + 63u - __builtin_clzll(below)) : R;
+                    const bool mv = occ && !del && ((active >> lane) & 1ull) && rcur >= 0 &&
+                                    static_cast<uint32_t>(rcur) >= homeOff;
+                    const uint64_t E2 = E1 | __ballot(mv);
+                    if (E2 == E) break;
+                    E = E2;
+                }
+                // the events in order: a deletion makes a hole; a mover takes
+                // the leftmost hole at or after its home and leaves a hole
+                uint64_t evs = E;
+                while (evs) {
+                    const int i = __builtin_ctzll(evs);
+                    evs &= evs - 1ull;
+                    const uint32_t offI = w0 + static_cast<uint32_t>(i);
+                    const uint32_t cellI = (e0 + offI) & mask;
+                    if ((D >> i) & 1ull) {
+                        if (wr) r.ht[cellI] = 0;
+                        --left;
+                    } else {
+                        const uint32_t hOff = static_cast<uint32_t>(lane_value(static_cast<int32_t>(homeOff), i));
+                        const uint32_t eI = static_cast<uint32_t>(lane_value(static_cast<int32_t>(e), i));
+                        const int64_t hole = next_set(bits, hOff);  // < offI
+                        if (hole < 0 || hole >= static_cast<int64_t>(offI)) {
+                            bad = true;  // not reachable by the move rule; reported, nothing written
+                        } else {
+                            clr_bit3(bits, static_cast<uint32_t>(hole), wr);
+                            if (wr) {
+                                r.ht[(e0 + static_cast<uint32_t>(hole)) & mask] = static_cast<uint16_t>(eI);
+                                r.ht[cellI] = 0;
+                            }
+                        }
+                    }
+                    set_bit3(bits, offI, wr);
+                }
+                if (E) R = static_cast<int32_t>(w0 + 63u - __builtin_clzll(E));
+                if (f < 64) {
+                    // the cluster ends at w0 + f: its remaining holes stay empty
+                    const uint32_t hi = w0 + static_cast<uint32_t>(f);
+                    const uint32_t top = hi < static_cast<uint32_t>(H) ? hi : static_cast<uint32_t>(H) - 1u;
+                    for (uint32_t w = (clusterLo >> 6) + lane; w <= (top >> 6); w += 64) bitL0[w] = 0ull;
+                    for (uint32_t w = (clusterLo >> 12) + lane; w <= (top >> 12); w += 64) bitL1[w] = 0ull;
+                    for (uint32_t w = (clusterLo >> 18) + lane; w <= (top >> 18); w += 64) bitL2[w] = 0ull;
+                    R = -1;
+                    w0 = hi + 1u;
+                } else {
+                    w0 = w0 + 64u < chunkEnd ? w0 + 64u : chunkEnd;  // the next window starts inside the stage
+                }
+            }
+            if (bad) {
+                // a broken invariant: stop the walk (the row's table is left
+                // partly updated) and report it in the tail slot
+                R = -1;
+                left = 0;
+                if (wr) report_overflow(P.L.overflowSlot, kOverflowProbe);
+            }
+            if (wr) {
+                sCur = w0;
+                sR = R;
+                sClusterLo = clusterLo;
+                sLeft = left;
+            }
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+
+    // ---- 5. the new tokens, in position order ----------------------------
+    {
+        uint32_t *h32 = reinterpret_cast<uint32_t *>(homes);  // scratch left zero (see above)
+        for (int32_t w = tid; w < H / 2; w += BT) h32[w] = 0u;
+    }
+    for (uint32_t w = tid; w < nCellW; w += BT) {
+        uint64_t m = 0ull;
+        const uint32_t *h32 = reinterpret_cast<const uint32_t *>(r.ht + (w << 6));
+        for (int q = 0; q < 32; ++q) {
+            const uint32_t pair = h32[q];
+            if ((pair & 0xFFFFu) == 0u) m |= 1ull << (2 * q);
+            if ((pair >> 16) == 0u) m |= 1ull << (2 * q + 1);
+        }
+        bitL0[w] = m;
+    }
+    __syncthreads();
+    for (uint32_t w = tid; w < nL1; w += BT) {
+        uint64_t sm = 0ull;
+        for (uint32_t q = 0; q < 64 && (w << 6) + q < nCellW; ++q) {
+            if (bitL0[(w << 6) + q]) sm |= 1ull << q;
+        }
+        bitL1[w] = sm;
+    }
+    __syncthreads();
+    for (uint32_t w = tid; w < nL2; w += BT) {
+        uint64_t sm = 0ull;
+        for (uint32_t q = 0; q < 64 && (w << 6) + q < nL1; ++q) {
+            if (bitL1[(w << 6) + q]) sm |= 1ull << q;
+        }
+        bitL2[w] = sm;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const bool wr = lane == 0;
+        for (int32_t k0 = 0; k0 < K; k0 += 64) {
+            const int32_t k = k0 + static_cast<int32_t>(lane);
+            const bool in = k < K;
+            const uint32_t s = in ? slotOut[k] : 0u;
+            const bool miss = (s & kMissBit) != 0u;
+            const int32_t t = miss ? rt[k] : 0;
+            uint64_t mm = __ballot(miss);
+            while (mm) {
+                const int i = __builtin_ctzll(mm);
+                mm &= mm - 1ull;
+                const int32_t ti = lane_value(t, i);
+                const uint32_t si = static_cast<uint32_t>(lane_value(static_cast<int32_t>(s), i)) & 0xFFFFu;
+                const uint32_t home = ht_hash(ti) & mask;
+                int64_t x = next_set(bits, home);
+                if (x < 0) x = next_set(bits, 0u);
+                if (x < 0) {
+                    if (wr) report_overflow(P.L.overflowSlot, kOverflowProbe);  // a full table: not reachable
+                    continue;
+                }
+                clr_bit3(bits, static_cast<uint32_t>(x), wr);
+                if (wr) r.ht[x] = static_cast<uint16_t>(si + 1u);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t sieve_batch_set_lds_limit(size_t bytes)
+{
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update_batch),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
+hipError_t launch_sieve_update_batch(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,
+                                     uint32_t *aux, hipStream_t stream)
+{
+    BatchParams P{};
+    P.L = KvxLaunch<HispSieveUpdateArgs>{a, overflowSlot};
+    P.shadow = shadow;
+    P.aux = aux;
+    P.mapCap = kBatchMapCap;
+    P.auxWords = batch_aux_words(a.htSize);
+    P.lay = batch_layout(a.deviceBufferSize, a.htSize, a.topK);
+    hipLaunchKernelGGL(kvx_sieve_update_batch, dim3(a.maxNumReqs), dim3(BT), P.lay.total, stream, P);
+    return hipGetLastError();
+}
+
+}  // namespace kvx

@@ -78,12 +78,13 @@ def test_sieve_state_stream_parity_all_layers(kvops):
     dev.assert_state_equal()
 
 
-@pytest.mark.parametrize("variant", [-1, 3])
+@pytest.mark.parametrize("variant", [-1, 3, 5])
 @pytest.mark.parametrize("seed", range(6))
 def test_sieve_defensive_cases_parity(kvops, seed, variant):
     """Padding rows, out-of-range pool rows, num_real > max, dirty hands,
     invalid and decode-extension positions, duplicates, tiny buffers (wrap);
-    automatic variant and the wave-wide HBM kernel."""
+    automatic variant, the wave-wide HBM kernel and the batch HBM kernel
+    (whose wrapping rows take its in-order path)."""
     rng = np.random.default_rng(500 + seed)
     dbs = int(rng.integers(1, 70))
     top_k = int(rng.integers(1, 90))
@@ -248,11 +249,11 @@ def test_sieve_parallel_kernel_shapes(kvops, K, dbs, force):
     assert kvops.read_overflow() == 0
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
 def test_sieve_variants_agree(kvops, variant):
-    """Sequential LDS (0), single-lane HBM (1), parallel (2), wave-wide HBM (3)
-    and parallel compact-layout (4) kernels give the oracle's results on the
-    same inputs."""
+    """Sequential LDS (0), single-lane HBM (1), parallel (2), wave-wide HBM (3),
+    parallel compact-layout (4) and batch HBM (5) kernels give the oracle's
+    results on the same inputs."""
     rng = np.random.default_rng(77)
     dbs, K, prefill, req = 700, 300, 3000, 4
     st = orc.SieveState(1, req, dbs, K)
@@ -301,7 +302,7 @@ def test_sieve_config4_parity(kvops):
     """The slot-limit stress shapes (4 requests, 65518 slots, topK 8192, a
     262144-entry table kept in HBM) with adversarial keys whose Knuth hashes
     share 4096 home buckets: the first step (thousands of evictions inside
-    one long probe run) and the next, full state after each."""
+    one long probe run) and the next ones, full state after each."""
     cfg = CONFIGS[4]
     st = orc.SieveState(1, cfg.req_num, cfg.dbs, cfg.top_k)
     for r in range(cfg.req_num):
@@ -311,12 +312,12 @@ def test_sieve_config4_parity(kvops):
     pool = streams.adversarial_pool(cfg.prefill, 4096)
     req_pool = np.arange(cfg.req_num)
     seq = np.full(cfg.req_num, cfg.prefill)
-    for step in range(2):
+    for step in range(4):
         batch = streams.state_batch(rng, st.tokens[0, :, :cfg.dbs], cfg.prefill, cfg.top_k, cfg.miss_ratio,
                                     miss_pool=pool)
         e_slots, e_miss = st.update(0, batch, req_pool, seq, cfg.req_num)
         g_slots, g_miss, _ = dev.update(kvops, 0, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
-        assert kvops.last_sieve_variant() == 3
+        assert kvops.last_sieve_variant() == 5
         np.testing.assert_array_equal(g_miss, e_miss)
         np.testing.assert_array_equal(g_slots, e_slots)
         dev.assert_state_equal()
@@ -411,4 +412,97 @@ def test_sieve_small_rows_inorder_paths(kvops, dbs, K, prefill):
         np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
         np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
         dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
+
+
+@pytest.mark.parametrize("variant", [5, 3])
+def test_sieve_hbm_noncanonical_table(kvops, variant):
+    """A table that is not canonical (two entries swapped so that probe
+    paths break, and an entry naming an empty slot): the batch kernel takes
+    its in-order path, and both HBM kernels give what the oracle gives on the
+    same table (the reference's probe semantics, whatever the table holds)."""
+    rng = np.random.default_rng(19)
+    dbs, K, prefill, req = 900, 256, 4000, 3
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    # row 0: swap two occupied cells of one cluster; row 1: an entry naming an
+    # empty slot; row 2 stays canonical
+    occ = np.nonzero(st.ht[0, 0])[0]
+    a, b = int(occ[10]), int(occ[11])
+    st.ht[0, 0, a], st.ht[0, 0, b] = st.ht[0, 0, b], st.ht[0, 0, a]
+    st.tokens[0, 1, 5] = -1
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(variant)
+    try:
+        for step in range(3):
+            batch = _random_state_stream(rng, st, K, prefill)
+            seq = np.full(req, prefill)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == variant
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_sieve_batch_kernel_wraps_and_dups(kvops, seed):
+    """The batch HBM kernel on rows whose steps sometimes wrap the hand
+    (more misses than slots: the in-order path) and sometimes do not,
+    with duplicate positions, invalid and decode-extension positions."""
+    rng = np.random.default_rng(900 + seed)
+    dbs = int(rng.integers(60, 400))
+    K = int(rng.integers(50, 600))
+    prefill = int(rng.integers(dbs + 10, 6 * dbs))
+    req = 4
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(5)
+    try:
+        for step in range(6):
+            seq = np.full(req, prefill + 5)
+            hi = prefill + 9 if step % 2 else dbs + 50
+            batch = rng.integers(-2, hi, size=(req, K)).astype(np.int32)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == 5
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg="seed {} step {}".format(seed, step))
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg="seed {} step {}".format(seed, step))
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
+def test_sieve_batch_scratch_across_shapes(kvops):
+    """The batch HBM kernel's per-row scratch is laid out by table size and
+    shared by every launch on the stream: launches on one shape, then on a
+    larger one with more rows, then the first again, all match the oracle
+    (each launch leaves the scratch zeroed)."""
+    shapes = [(7, 40, 64, 300), (4, 3000, 1000, 20000), (7, 40, 64, 300)]
+    rng = np.random.default_rng(4)
+    kvops.sieve_force_variant(5)
+    try:
+        for i, (req, dbs, K, prefill) in enumerate(shapes):
+            st = orc.SieveState(1, req, dbs, K)
+            for r in range(req):
+                st.admit(r, prefill)
+            dev = DevSieve(st)
+            for step in range(3):
+                batch = _random_state_stream(rng, st, K, prefill)
+                seq = np.full(req, prefill + 4)
+                e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+                g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+                assert kvops.last_sieve_variant() == 5
+                np.testing.assert_array_equal(g_miss, e_miss, err_msg="shape {} step {}".format(i, step))
+                np.testing.assert_array_equal(g_slots, e_slots, err_msg="shape {} step {}".format(i, step))
+                dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
     assert kvops.read_overflow() == 0
