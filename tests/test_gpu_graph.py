@@ -39,6 +39,7 @@ def _state(c):
 @pytest.mark.parametrize("L,req,prefill,top_k,dbs,N", [
     (3, 8, 1024, 256, 512, 2),       # generic parallel kernel
     (2, 4, 8192, 2048, 4096, 4),     # DSA-decode row shape (fixed-count kernel)
+    (1, 2, 40000, 2048, 20000, 2),   # a 65536-cell table kept in HBM (batch kernel, reserved scratch)
 ])
 def test_graph_replay_matches_eager(kvops, L, req, prefill, top_k, dbs, N):
     print("graph replay case", L, req, prefill, top_k, dbs, N, flush=True)
