@@ -95,16 +95,23 @@ constexpr int32_t kCanonFlag = 0x4B565843;
 // shader clocks of different XCDs are not aligned; the constant-rate one is).
 #ifdef KVX_SIEVE_PHASE_STAMPS
 __device__ unsigned long long kvx_dbg_stamps[1024][16];
+__device__ unsigned long long kvx_dbg_sub[1024][16];
+// the arrays' addresses are taken once, at entry: a stamp is then a clock
+// read and a store, with no address load queued ahead of the clock read
+#define DBG_SETUP()                                           \
+    unsigned long long *dbgSt = &kvx_dbg_stamps[0][0];        \
+    unsigned long long *dbgSub = &kvx_dbg_sub[0][0];          \
+    asm volatile("" : "+s"(dbgSt), "+s"(dbgSub))
 #define STAMP(i)                                                        \
     do {                                                                \
-        if (tid == 0 && bid < 1024) kvx_dbg_stamps[bid][i] = clock64(); \
+        if (tid == 0 && bid < 1024) dbgSt[bid * 16 + (i)] = clock64();  \
     } while (0)
-__device__ unsigned long long kvx_dbg_sub[1024][16];
 #define DBGVAL(i, v)                                                  \
     do {                                                              \
-        if (tid == 0 && bid < 1024) kvx_dbg_sub[bid][i] = (v);        \
+        if (tid == 0 && bid < 1024) dbgSub[bid * 16 + (i)] = (v);     \
     } while (0)
 #else
+#define DBG_SETUP()
 #define STAMP(i) \
     do {         \
     } while (0)
@@ -338,6 +345,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const int32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    DBG_SETUP();
     DBGVAL(12, __builtin_amdgcn_s_memrealtime());
     DBGVAL(14, clock64());
     DBGVAL(10, __builtin_amdgcn_s_getreg((31 << 11) | 4));   // HW_ID

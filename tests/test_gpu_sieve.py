@@ -190,6 +190,40 @@ def test_sieve_fast_kernel_parity_mid(kvops, seed):
     assert kvops.read_overflow() == 0
 
 
+@pytest.mark.parametrize("dbs", [4096, 8192])
+def test_sieve_fast_kernel_shuffled_batch(kvops, dbs):
+    """The fixed-count kernels (topK 2048; rings of 4096 slots in the full LDS
+    form, 8192 in the compact one) on
+    batches whose rows are not their pool rows: 32 of 40 requests in a new
+    random order each step, about a quarter of them at their own index, each
+    with its own prefill length, plus rows past num_real."""
+    top_k, pool, batch_n, max_reqs = 2048, 40, 32, 36
+    st = orc.SieveState(1, pool, dbs, top_k)
+    rng = np.random.default_rng(dbs + 5)
+    prefills = [int(rng.integers(dbs // 2, 3 * dbs)) for _ in range(pool)]
+    for r in range(pool):
+        st.admit(r, prefills[r])
+    dev = DevSieve(st)
+    for step in range(4):
+        perm = [int(x) for x in rng.permutation(pool)[:batch_n]]
+        for i in range(batch_n):
+            if rng.random() < 0.25 and i in perm:
+                j = perm.index(i)
+                perm[i], perm[j] = perm[j], perm[i]
+        assert perm != list(range(batch_n))
+        req_pool = perm + [int(x) for x in rng.integers(0, pool, size=max_reqs - batch_n)]
+        seq = [prefills[p] + step for p in req_pool]
+        batch = np.stack([streams.state_batch(rng, st.tokens[0, p:p + 1, :dbs], prefills[p], top_k, 0.2)[0]
+                          for p in req_pool]).astype(np.int32)
+        e_slots, e_miss = st.update(0, batch, req_pool, seq, batch_n, max_num_reqs=max_reqs)
+        g_slots, g_miss, _ = dev.update(kvops, 0, batch, req_pool, seq, batch_n, max_reqs, top_k)
+        assert kvops.last_sieve_variant() == (2 if dbs == 4096 else 4)  # 8192 slots: the compact LDS form
+        np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+        np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+        dev.assert_state_equal()
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_fast_kernel_parity_dsa_scale(kvops):
     """DSA-decode shapes (64 requests, topK 2048, 4096 slots, Zipf recency
     hits, 20% misses) over two layers and three steps."""
