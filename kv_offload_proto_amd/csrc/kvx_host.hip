@@ -892,9 +892,13 @@ int kvx_sieve_ht_init(uint64_t device_buffer_tokens, uint64_t device_buffer_ht, 
         a.paddedBufferSize = padded_buffer_size;
         a.htSize = ht_size;
         if (static_cast<uint64_t>(num_reqs) * layer_num == 0) return;
-        const size_t lds = static_cast<size_t>(ht_size) * 2;
-        hipCheck(kvx::launch_sieve_ht_init(a, reinterpret_cast<uint64_t>(g.overflow), lds <= g.ldsLimit ? lds : 0,
-                                           AsStream(stream)),
+        // the parallel build when its LDS form fits, else one lane per table
+        // on the table in LDS or in HBM
+        const size_t ldsPar = kvx::sieve_ht_init_par_lds(ht_size, device_buffer_size);
+        const bool parallel = ldsPar != 0 && ldsPar <= g.ldsLimit;
+        const size_t lds = parallel ? ldsPar : static_cast<size_t>(ht_size) * 2;
+        hipCheck(kvx::launch_sieve_ht_init(a, reinterpret_cast<uint64_t>(g.overflow),
+                                           parallel || lds <= g.ldsLimit ? lds : 0, AsStream(stream), parallel),
                  "hisp_sieve_ht_init launch");
     });
 }

@@ -147,6 +147,190 @@ __global__ __launch_bounds__(256) void kvx_sieve_ht_init(KvxLaunch<HispSieveHtIn
     }
 }
 
+// Parallel form of the same build for tables that fit LDS, one 256-lane
+// workgroup per (layer, pool row).  Linear probing fills the same set of
+// cells whatever the insertion order: with n(c) keys homed at cell c, the
+// backlog b(c) = max(0, b(c-1) + n(c) - 1) counts the keys homed at or before
+// c still waiting for a cell, and c is in use iff b(c-1) + n(c) >= 1.  A key
+// never leaves the cluster (maximal run of used cells) holding its home, so
+// inserting each cluster's keys alone, in slot order, gives the sequential
+// layout.  A later slot with a token already inserted meets the earlier entry
+// on its probe path and is skipped (hisp_kernel_common.h:97-112); both share
+// a home, so it is dropped from its home's list instead.
+//
+// LDS: table (2H B), per-home list ends (2H B, 16-bit, paired for atomics),
+// the slots bucketed by home (2 B each), the used-cell bitmap (H/8 B), the
+// scans' lane values (2 KiB); nothing static.
+constexpr int32_t kInitThreads = 256;
+
+__global__ __launch_bounds__(kInitThreads) void kvx_sieve_ht_init_par(KvxLaunch<HispSieveHtInitArgs> L)
+{
+    extern __shared__ __align__(16) uint8_t smem[];
+    const HispSieveHtInitArgs &a = L.a;
+    const int32_t numReqs = static_cast<int32_t>(a.numReqs);
+    const int32_t layerNum = static_cast<int32_t>(a.layerNum);
+    const int32_t poolSize = static_cast<int32_t>(a.poolSize);
+    const int32_t dbs = static_cast<int32_t>(a.deviceBufferSize);
+    const int32_t padded = static_cast<int32_t>(a.paddedBufferSize);
+    const int32_t H = static_cast<int32_t>(a.htSize);
+    const int32_t mask = H - 1;
+    const int32_t b = blockIdx.x;
+    if (b >= layerNum * numReqs) return;
+    const int32_t layer = b / numReqs;
+    const int64_t reqIdx = static_cast<int64_t>(a.reqStart) + b % numReqs;
+    if (reqIdx < 0 || reqIdx >= poolSize) return;
+    const int32_t *tok = reinterpret_cast<const int32_t *>(a.deviceBufferTokens) +
+                         (static_cast<int64_t>(layer) * poolSize + reqIdx) * padded;
+    uint16_t *gHt = reinterpret_cast<uint16_t *>(a.deviceBufferHt) +
+                    (static_cast<int64_t>(layer) * poolSize + reqIdx) * H;
+
+    const int32_t tid = threadIdx.x;
+    const int32_t per = H / kInitThreads;  // cells (homes) per lane, >= 4 (H >= 1024)
+    const int32_t c0 = tid * per;
+    uint16_t *ht = reinterpret_cast<uint16_t *>(smem);
+    uint16_t *ends = ht + H;  // per home: inclusive prefix of the counts, then (after the scatter) the list start
+    uint32_t *ends32 = reinterpret_cast<uint32_t *>(ends);
+    uint16_t *keys = ends + H;
+    uint32_t *used = reinterpret_cast<uint32_t *>(keys + ((dbs + 7) & ~7));
+    int32_t *sP = reinterpret_cast<int32_t *>(used + H / 32);  // the scans' lane values
+    int32_t *sQ = sP + kInitThreads;
+    int32_t &sTotal = sQ[kInitThreads];
+    constexpr uint16_t kGone = 0xFFFF;  // a dropped duplicate or an inserted slot
+    auto is_used = [&](int32_t c) { return (used[c >> 5] >> (c & 31)) & 1u; };
+
+    // clear the table, the counts and the bitmap
+    for (int32_t i = tid; i < H / 4; i += kInitThreads) reinterpret_cast<uint4 *>(smem)[i] = make_uint4(0, 0, 0, 0);  // 4H bytes
+    for (int32_t i = tid; i < H / 32; i += kInitThreads) used[i] = 0u;
+    __syncthreads();
+    // keys per home (two 16-bit counts per word; a count stays below 2^16)
+    for (int32_t s = tid; s < dbs; s += kInitThreads) {
+        const int32_t t = tok[s];
+        if (t >= 0) {
+            const int32_t h = static_cast<int32_t>(ht_hash(t)) & mask;
+            atomicAdd(ends32 + (h >> 1), 1u << ((h & 1) * 16));
+        }
+    }
+    __syncthreads();
+    // inclusive prefix over the homes: lane sums, a scan of the lane sums, then the lane's run
+    int32_t sum = 0;
+    for (int32_t i = 0; i < per; ++i) sum += ends[c0 + i];
+    sP[tid] = sum;
+    __syncthreads();
+    for (int32_t o = 1; o < kInitThreads; o <<= 1) {
+        const int32_t v = tid >= o ? sP[tid - o] : 0;
+        __syncthreads();
+        sP[tid] += v;
+        __syncthreads();
+    }
+    int32_t run = sP[tid] - sum;
+    for (int32_t i = 0; i < per; ++i) {
+        run += ends[c0 + i];
+        ends[c0 + i] = static_cast<uint16_t>(run);
+    }
+    if (tid == kInitThreads - 1) sTotal = sP[kInitThreads - 1];
+    __syncthreads();
+    // bucket the slots by home: each key takes the next position down from
+    // its home's end, so the entry ends as the home's list start
+    for (int32_t s = tid; s < dbs; s += kInitThreads) {
+        const int32_t t = tok[s];
+        if (t >= 0) {
+            const int32_t h = static_cast<int32_t>(ht_hash(t)) & mask;
+            const uint32_t sh = static_cast<uint32_t>(h & 1) * 16u;
+            const uint32_t old = atomicSub(ends32 + (h >> 1), 1u << sh);
+            keys[((old >> sh) & 0xFFFFu) - 1u] = static_cast<uint16_t>(s);
+        }
+    }
+    __syncthreads();
+    const int32_t total = sTotal;
+    auto list_end = [&](int32_t h) { return h + 1 < H ? static_cast<int32_t>(ends[h + 1]) : total; };
+    // per home: slot order, duplicates dropped, the count kept in the (still
+    // empty) table cell; the lane's segment as a backlog map x -> max(P, x + Q)
+    int32_t P = 0, Q = 0;
+    for (int32_t i = 0; i < per; ++i) {
+        const int32_t h = c0 + i;
+        const int32_t st = ends[h], en = list_end(h);
+        for (int32_t j = st + 1; j < en; ++j) {
+            const uint16_t v = keys[j];
+            int32_t k = j;
+            for (; k > st && keys[k - 1] > v; --k) keys[k] = keys[k - 1];
+            keys[k] = v;
+        }
+        int32_t n = 0;
+        for (int32_t j = st; j < en; ++j) {
+            bool dup = false;
+            if (j > st) {
+                const int32_t tj = tok[keys[j]];
+                for (int32_t k = st; k < j && !dup; ++k) dup = keys[k] != kGone && tok[keys[k]] == tj;
+            }
+            if (dup) keys[j] = kGone;
+            else ++n;
+        }
+        ht[h] = static_cast<uint16_t>(n);
+        P = max(0, P + n - 1);
+        Q += n - 1;
+    }
+    sP[tid] = P;
+    sQ[tid] = Q;
+    __syncthreads();
+    // compose the segment maps in cell order (inclusive scan); the ring's map
+    // has Q < 0 (fewer keys than cells), so its fixed point -- the backlog
+    // entering cell 0 -- is its P
+    for (int32_t o = 1; o < kInitThreads; o <<= 1) {
+        const bool has = tid >= o;
+        const int32_t pe = has ? sP[tid - o] : 0, qe = has ? sQ[tid - o] : 0;
+        __syncthreads();
+        if (has) {
+            const int32_t pc = sP[tid], qc = sQ[tid];
+            sP[tid] = max(pc, pe + qc);
+            sQ[tid] = qe + qc;
+        }
+        __syncthreads();
+    }
+    const int32_t x0 = sP[kInitThreads - 1];
+    int32_t x = tid == 0 ? x0 : max(sP[tid - 1], x0 + sQ[tid - 1]);
+    for (int32_t i = 0; i < per; ++i) {
+        const int32_t h = c0 + i;
+        const int32_t n = ht[h];
+        if (x + n >= 1) atomicOr(used + (h >> 5), 1u << (h & 31));
+        x = max(0, x + n - 1);
+        ht[h] = 0;
+    }
+    __syncthreads();
+    // each cluster, by the lane holding its first cell: its keys in slot
+    // order, each to the first free cell from its home (a cluster of L cells
+    // costs O(L^2) LDS reads: short at these load factors, at most H/2 keys)
+    for (int32_t i = 0; i < per; ++i) {
+        const int32_t c = c0 + i;
+        if (!is_used(c) || is_used((c - 1) & mask)) continue;
+        int32_t len = 0;
+        while (len < H && is_used((c + len) & mask)) ++len;
+        for (;;) {
+            int32_t best = 0x10000, bj = -1, bh = 0;
+            for (int32_t u = 0; u < len; ++u) {
+                const int32_t h = (c + u) & mask;
+                const int32_t en = list_end(h);
+                for (int32_t j = ends[h]; j < en; ++j) {
+                    const int32_t v = keys[j];
+                    if (v == kGone) continue;
+                    if (v < best) {
+                        best = v;
+                        bj = j;
+                        bh = h;
+                    }
+                    break;  // the home's list is in slot order
+                }
+            }
+            if (bj < 0) break;
+            keys[bj] = kGone;
+            int32_t y = bh;
+            for (int32_t n = 0; n < len && ht[y] != 0; ++n) y = (y + 1) & mask;
+            ht[y] = static_cast<uint16_t>(best + 1);
+        }
+    }
+    __syncthreads();
+    block_copy16(gHt, ht, static_cast<uint32_t>(H) * 2u);
+}
+
 }  // namespace
 
 hipError_t sieve_set_lds_limit(size_t bytes)
@@ -154,7 +338,10 @@ hipError_t sieve_set_lds_limit(size_t bytes)
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_update<true>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     if (e != hipSuccess) return e;
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_ht_init<true>),
+    e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_ht_init<true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(&kvx_sieve_ht_init_par),
                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
 }
 
@@ -171,12 +358,21 @@ hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSl
     return hipGetLastError();
 }
 
+size_t sieve_ht_init_par_lds(uint32_t htSize, uint32_t dbs)
+{
+    if (htSize < 1024u || dbs >= htSize) return 0;  // 4+ cells per lane; fewer keys than cells
+    return static_cast<size_t>(htSize) * 4u + static_cast<size_t>((dbs + 7u) & ~7u) * 2u + htSize / 8u +
+           (2u * kInitThreads + 4u) * 4u;
+}
+
 hipError_t launch_sieve_ht_init(const HispSieveHtInitArgs &a, uint64_t overflowSlot, size_t ldsBytes,
-                                hipStream_t stream)
+                                hipStream_t stream, bool parallel)
 {
     KvxLaunch<HispSieveHtInitArgs> L{a, overflowSlot};
     const dim3 grid(a.layerNum * a.numReqs), block(256);
-    if (ldsBytes != 0) {
+    if (parallel) {
+        hipLaunchKernelGGL(kvx_sieve_ht_init_par, grid, dim3(kInitThreads), ldsBytes, stream, L);
+    } else if (ldsBytes != 0) {
         hipLaunchKernelGGL(kvx_sieve_ht_init<true>, grid, block, ldsBytes, stream, L);
     } else {
         hipLaunchKernelGGL(kvx_sieve_ht_init<false>, grid, block, 0, stream, L);

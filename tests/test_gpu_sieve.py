@@ -37,6 +37,84 @@ def test_ht_init_parity(kvops):
     assert kvops.read_overflow() == 0
 
 
+def _home(t, ht_size):
+    return ((np.asarray(t, dtype=np.uint64) * 2654435761) & 0xFFFFFFFF) >> 16 & (ht_size - 1)
+
+
+def _ht_rows(rng, st, mode):
+    """Token rows for the admission build: 'unique', 'dups' (duplicates and
+    negatives), 'few_homes' (all keys on 8 home cells: long clusters) or
+    'wrap' (homes in the last 40 cells: clusters across the table's end)."""
+    L, R = st.tokens.shape[:2]
+    H = st.ht_size
+    st.tokens[:] = -1
+    cand = None
+    if mode in ("few_homes", "wrap"):
+        t = np.arange(0, 1 << 23, dtype=np.int64)
+        h = _home(t, H)
+        if mode == "few_homes":
+            homes = rng.choice(H, size=8, replace=False)
+            cand = t[np.isin(h, homes)]
+        else:
+            cand = t[h >= H - 40]
+    for l in range(L):
+        for r in range(R):
+            n = int(rng.integers(0, st.dbs + 1))
+            if mode == "unique":
+                vals = rng.choice(1 << 22, size=n, replace=False)
+            elif mode == "dups":
+                vals = rng.integers(-3, max(4, n // 3), size=n)
+            else:
+                n = min(n, len(cand), st.ht_size // 16)
+                vals = rng.choice(cand, size=n, replace=False)
+            slots = rng.choice(st.dbs, size=n, replace=False)
+            st.tokens[l, r, slots] = vals
+
+
+@pytest.mark.parametrize("mode", ["unique", "dups", "few_homes", "wrap"])
+@pytest.mark.parametrize("dbs,top_k", [(4096, 2048), (8192, 2048)])
+def test_ht_init_parallel_parity(kvops, dbs, top_k, mode):
+    """The admission build at the DSA-decode and large-batch table sizes
+    (16384 and 32768 cells, the parallel form): every table byte equals the
+    oracle's sequential inserts, rows outside [req_start, req_start+num_reqs)
+    untouched."""
+    import torch
+
+    rng = np.random.default_rng(dbs + len(mode))
+    layers, pool = 2, 3
+    st = orc.SieveState(layers, pool, dbs, top_k)
+    _ht_rows(rng, st, mode)
+    dev = DevSieve(st)
+    dev.ht.fill_(77)
+    st.ht[:] = 77
+    orc.sieve_ht_init(st.tokens, st.ht, 1, 2, layers, pool, dbs, st.padded, st.ht_size)
+    kvops.sieve_ht_init(dev.tokens.data_ptr(), dev.ht.data_ptr(), dev.prefill.data_ptr(), 1, 2, layers, pool,
+                        dbs, st.padded, st.ht_size, 0, 0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dev.ht.cpu().numpy().view(np.uint16), st.ht)
+    assert kvops.read_overflow() == 0
+
+
+def test_ht_init_small_table_parity(kvops):
+    """A 512-cell table (under the parallel form's 1024): the one-lane build."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    layers, pool, dbs = 2, 4, 200
+    st = orc.SieveState(layers, pool, dbs, 8)
+    _ht_rows(rng, st, "dups")
+    ht_size = 512
+    dev = DevSieve(st)
+    want = np.full((layers, pool, ht_size), 77, dtype=np.uint16)
+    got = torch.full((layers, pool, ht_size), 77, dtype=torch.int16, device="cuda")
+    orc.sieve_ht_init(st.tokens, want, 0, pool, layers, pool, dbs, st.padded, ht_size)
+    kvops.sieve_ht_init(dev.tokens.data_ptr(), got.data_ptr(), dev.prefill.data_ptr(), 0, pool, layers, pool,
+                        dbs, st.padded, ht_size, 0, 0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16), want)
+    assert kvops.read_overflow() == 0
+
+
 @pytest.mark.parametrize("cfg_id", [0, 1])
 def test_sieve_ref_stream_parity(kvops, cfg_id):
     """The reference driver's stream (xds_decode.py:211-225): one layer per step."""
