@@ -9,7 +9,8 @@
 // winners (the last miss position per destination row), a dense list of the
 // rows to move (with the reference's queued counts), and the copy, where
 // each wave moves 64 listed rows at a time as 16-byte chunks, 8 chunks in
-// flight per lane, so megabytes of host-link reads stay outstanding.
+// flight per lane, so megabytes of host-link reads stay outstanding.  A
+// small batch (up to 4096 positions) takes one launch instead (below).
 //
 // Completion: the last workgroup to finish (atomicInc ticket) stores the
 // status words with a system-scope release, after every workgroup fenced its
@@ -297,6 +298,122 @@ __global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
     }
 }
 
+// Small batches (max_num_reqs * top_k <= kSmallMaxPositions): the three
+// passes in one launch.  Every workgroup tags the winners of all positions
+// (the same atomicMax values, so the repeats are harmless) and counts the
+// queued rows and errors of all positions in its own LDS, then moves the
+// winners among its own kSmallSpan positions: the rows spread over
+// ceil(positions / kSmallSpan) CUs (one CU reads only a few GB/s from host
+// memory), with no counters shared between workgroups.  The last workgroup
+// (ticket) advances the epoch and stores the status words.
+constexpr uint32_t kSmallMaxPositions = 4096;
+constexpr uint32_t kSmallSpan = 32;
+
+__global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
+{
+    __shared__ uint32_t sCnt[64 * 8], sErr[64 * 8];
+    __shared__ uint64_t sSrc[kSmallSpan], sDst[kSmallSpan];
+    __shared__ uint32_t sN, sEpoch;
+    __shared__ int sLast;
+    const KvcGatherArgs &a = P.l.a;
+    const GatherExtra &x = P.x;
+    const uint32_t tid = threadIdx.x;
+    const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
+    const int64_t total = static_cast<int64_t>(numReal) * a.topK;  // <= kSmallMaxPositions (host)
+    const uint32_t n0 = x.fused ? 0u : a.myNode;
+    const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
+    const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
+    const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
+    const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
+    const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
+    const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
+    const int64_t *hostBase = reinterpret_cast<const int64_t *>(a.reqHostBase);
+    if (blockIdx.x == 0 && a.status != 0) {  // the call's status words read 0 until its rows have landed
+        for (uint32_t i = tid; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
+            const uint32_t node = n0 + i / x.statusWords, b = i % x.statusWords;
+            store_status(a.status + node * 64ull + b * 8ull, 0ull);
+        }
+    }
+    for (uint32_t i = tid; i < 64u * 8u; i += blockDim.x) sCnt[i] = sErr[i] = 0u;
+    if (tid == 0) {
+        sN = 0u;
+        sEpoch = *x.epoch;
+    }
+    __syncthreads();
+    const unsigned long long tagHi = static_cast<unsigned long long>(sEpoch) << 32;
+    for (int64_t p = tid; p < total; p += blockDim.x) {
+        if (miss[p] == 0) continue;
+        const int32_t t = topk[p], s = slots[p];
+        if (t < 0 || s < 0 || s >= 65536) continue;
+        const int64_t bid = p / a.topK;
+        if (pool[bid] < 0) continue;
+        const uint64_t d = win_index(bid, s, x.spanRows);
+        if (d < x.winEntries) atomicMax(&x.win[d], tagHi | static_cast<unsigned long long>(p));
+    }
+    __threadfence();
+    __syncthreads();
+    const int64_t lo = static_cast<int64_t>(blockIdx.x) * kSmallSpan, hi = lo + kSmallSpan;
+    for (int64_t p = tid; p < total; p += blockDim.x) {
+        if (miss[p] == 0) continue;
+        const int32_t t = topk[p], s = slots[p];
+        const int64_t bid = p / a.topK;
+        if (t < 0 || s < 0 || pool[bid] < 0) continue;
+        const uint32_t row = static_cast<uint32_t>(hostBase[bid] + t);  // kvc_gather_rows.cpp:69-73
+        const uint32_t node = kvx_node_of(row, a.stripeRows, a.nodeNum);
+        const bool owned = x.fused ? (node < a.nodeNum) : (node == a.myNode);
+        if (!owned) continue;
+        const uint32_t key = node * 8u + static_cast<uint32_t>(static_cast<uint64_t>(p) / ppc);
+        atomicAdd(&sCnt[key], 1u);
+        const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
+        if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
+            atomicCAS(&sErr[key], 0u, row_error_code(static_cast<uint64_t>(p)));
+            continue;
+        }
+        if (p < lo || p >= hi) continue;
+        if (s < 65536) {
+            const uint64_t d = win_index(bid, s, x.spanRows);
+            if (d < x.winEntries &&
+                __hip_atomic_load(&x.win[d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+                    (tagHi | static_cast<unsigned long long>(p))) {
+                continue;
+            }
+        }
+        const uint64_t segBase = x.fused ? x.segBases[node] : a.segBase;
+        const uint32_t at = atomicAdd(&sN, 1u);
+        sSrc[at] = segBase + (static_cast<uint64_t>(a.layerOffsetRows) + segRow) * a.rowBytes;
+        sDst[at] = a.hotRowBase + (static_cast<uint64_t>(s) + static_cast<uint64_t>(bid) * a.hotReqStrideRows) *
+                                      a.rowBytes;
+    }
+    __syncthreads();
+    {
+        // the rows, shared among the waves
+        const uint32_t n = sN, cpr = a.rowBytes / 16u, waves = blockDim.x / 64u, w = tid / 64u;
+        const uint32_t share = (n + waves - 1u) / waves, r0 = w * share;
+        if (r0 < n) wave_copy_rows(sSrc + r0, sDst + r0, (n - r0 < share) ? n - r0 : share, cpr);
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned int ticket = atomicInc(&x.tickets[3], gridDim.x - 1u);
+        sLast = (ticket == gridDim.x - 1u) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sLast) return;
+    // the next call's epoch (at the wrap to 0, once in 2^32 calls, the table is cleared)
+    if (sEpoch + 1u == 0u) {
+        for (uint64_t i = tid; i < x.winEntries; i += blockDim.x) x.win[i] = 0ull;
+    }
+    if (tid == 0) *x.epoch = sEpoch + 1u;
+    if (a.status == 0) return;
+    __threadfence();
+    for (uint32_t i = tid; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
+        const uint32_t node = n0 + i / x.statusWords, b = i % x.statusWords;
+        uint64_t word = 1ull << 32;  // kvc_gather_rows.cpp:29-33, :93
+        if (static_cast<int64_t>(b * ppc) < total) word |= (static_cast<uint64_t>(sCnt[node * 8u + b]) << 40) | sErr[node * 8u + b];
+        store_status(a.status + node * 64ull + b * 8ull, word);
+    }
+}
+
 // Prefill export: item (layer l, owned stripe i) copies the stripe's winning
 // row (its highest row inside the range) to segment row q/N of layer l.
 __global__ __launch_bounds__(256) void kvx_export_alllayer(ExportParams P)
@@ -529,6 +646,11 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     P.x.spanRows = plan.spanRows;
     P.x.statusWords = plan.statusWords;
     const uint64_t positions = static_cast<uint64_t>(plan.a.maxNumReqs) * plan.a.topK;
+    if (positions <= kSmallMaxPositions) {
+        const uint32_t blocks = static_cast<uint32_t>((positions + kSmallSpan - 1u) / kSmallSpan);
+        hipLaunchKernelGGL(kvx_gather_small, dim3(blocks), dim3(256), 0, stream, P);
+        return hipGetLastError();
+    }
     uint64_t prepBlocks = (positions + 255ull) / 256ull;
     if (prepBlocks < 1) prepBlocks = 1;
     if (prepBlocks > 2048) prepBlocks = 2048;
