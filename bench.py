@@ -169,7 +169,11 @@ def sieve_bytes(cfg, padded, vis_stride, ht_size, dirty_reqs):
 
 # Counter profiles committed per workload: HBM bytes per dispatch, from
 # FETCH_SIZE and WRITE_SIZE runs scaled by a known-size copy.
-TRAFFIC_PROFILES = {"c2-dsa-decode": "profiles/pmc_traffic_dsa_decode.md"}
+TRAFFIC_PROFILES = {"c2-dsa-decode": "profiles/pmc_traffic_dsa_decode.md",
+                    "c4-slot-limit-stress": "profiles/pmc_traffic_slot_limit_stress.md"}
+# SIEVE kernel of each variant (kvx_last_sieve_variant), as named in the profiles
+SIEVE_KERNELS = {0: "kvx_sieve_update", 1: "kvx_sieve_update", 2: "kvx_sieve_update_fast",
+                 3: "kvx_sieve_update_wave", 4: "kvx_sieve_update_fast", 5: "kvx_sieve_update_batch"}
 
 
 def load_traffic(workload):
@@ -214,7 +218,7 @@ class _Batch:
         self.R = cfg.req_num
         self.req_pool = np.arange(cfg.req_num, dtype=np.int64)
         self.seq = np.full(cfg.req_num, cfg.prefill, dtype=np.int32)
-        self.host_base = np.array([cfg.host_base(r) for r in range(cfg.req_num)], dtype=np.int64)
+        self.host_base = np.array(runner.host_bases, dtype=np.int64)
         self.segs = [sg.view() for sg in runner.pool.pool.segments]
         self.plsr = runner.pool.per_layer_seg_rows
 
@@ -545,7 +549,7 @@ def export_rows_pass(runner, log, reps=3):
 
     cfg, pool = runner.cfg, runner.pool
     R = cfg.req_num
-    rows = [cfg.host_base(r) + cfg.prefill - 1 for r in range(R)]
+    rows = [runner.host_bases[r] + cfg.prefill - 1 for r in range(R)]
     rows_d = torch.tensor(rows, dtype=torch.int64, device=runner.dev)
     nr = torch.tensor([R], dtype=torch.int32, device=runner.dev)
     srcs = [runner.src[l].index_select(0, rows_d).contiguous() for l in range(cfg.layers)]
@@ -685,9 +689,12 @@ def main():
                    "avg_launch_us": sum(gather_us) / len(timed),
                    "hbm": {"achieved": hbm_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": hbm_gbps / HBM_PEAK_GBPS,
                            "bytes_rule": "rows moved x row_bytes read + written, + 9 B per position of index scan"}}
-    sieve_roof = {"kernel": "kvx_sieve_update", "bound": "hbm", "achieved": sieve_gbps_alg, "peak": HBM_PEAK_GBPS,
+    from kv_offload_proto_amd.kvops_ext import _kvops
+
+    sieve_kernel = SIEVE_KERNELS.get(_kvops.last_sieve_variant(), "kvx_sieve_update")
+    sieve_roof = {"kernel": sieve_kernel, "bound": "hbm", "achieved": sieve_gbps_alg, "peak": HBM_PEAK_GBPS,
                   "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS,
-                  "traffic": traffic_of("kvx_sieve_update_fast"), "traffic_source": traffic_src, "bytes_per_launch": sb,
+                  "traffic": traffic_of(sieve_kernel), "traffic_source": traffic_src, "bytes_per_launch": sb,
                   "avg_launch_us": sum(sieve_us) / len(timed)}
     dominant, other = (gather_roof, sieve_roof) if sum(gather_us) >= sum(sieve_us) else (sieve_roof, gather_roof)
 

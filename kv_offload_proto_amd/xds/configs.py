@@ -41,11 +41,6 @@ class Workload:
         # (xds_decode.py:29-30,173); every workload sizes it to fit.
         return self.host_reqs * self.prefill
 
-    def host_base(self, r):
-        """First host row of decode request r (requests beyond the exported
-        set reuse an exported request's rows)."""
-        return (r % self.host_reqs) * self.prefill
-
     @property
     def padded(self):
         return -(-self.dbs // 16) * 16

@@ -27,6 +27,22 @@ from .xds_seg_pool import HostSegPool
 LayerStep = namedtuple("LayerStep", "step layer topk batch misses moved unique_src")
 
 
+def allocate_host_rows(pool, cfg):
+    """Host rows of the workload's requests from the pool's row allocator: one
+    run of `prefill` rows per exported request, which must be contiguous (the
+    import reads host row = host base + token; xds_decode.py:172-176).
+    Decode requests beyond the exported set reuse an exported request's run.
+    Returns the host base of every decode request."""
+    allocator = pool.make_allocator()
+    bases = []
+    for _ in range(cfg.host_reqs):
+        rows = allocator.alloc(cfg.prefill)
+        if rows != list(range(rows[0], rows[0] + cfg.prefill)):
+            raise RuntimeError("host rows of a request are not contiguous: the import reads host base + token")
+        bases.append(rows[0])
+    return [bases[r % cfg.host_reqs] for r in range(cfg.req_num)]
+
+
 class DecodeRunner:
     def __init__(self, cfg, device=0, fill="fp16", coherent=False, log=print, block_dim=8):
         self.cfg = cfg
@@ -60,6 +76,7 @@ class DecodeRunner:
         self.seq_lens = torch.full((cfg.req_num,), cfg.prefill, dtype=torch.int32, device=self.dev)
         self.seg_bases = [sg.seg_base for sg in self.pool.pool.segments]
         self.status = self.pool.next_status()
+        self.host_bases = allocate_host_rows(self.pool, cfg)
 
     # ---- prefill export (xds_decode.py:167-189) ----
     def export_prefill(self):
@@ -85,7 +102,7 @@ class DecodeRunner:
     def admit_all(self):
         cfg = self.cfg
         for r in range(cfg.req_num):
-            self.coord.admit_request(r, r, cfg.prefill, cfg.host_base(r))
+            self.coord.admit_request(r, r, cfg.prefill, self.host_bases[r])
         self.coord.set_batch(self.req_pool, self.seq_lens)
         torch.cuda.synchronize()
 

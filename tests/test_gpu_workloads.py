@@ -25,6 +25,7 @@ import torch
 from gpu_helpers import read_words
 from kv_offload_proto_amd.xds import HostSegPool, XdsOffloadCoordinator, streams
 from kv_offload_proto_amd.xds.configs import CONFIGS
+from kv_offload_proto_amd.xds.workload import allocate_host_rows
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -78,7 +79,7 @@ def _decode_parity(kvops, cfg, layers, steps, fused, seed_src, block_dim=2, miss
         R = cfg.req_num
         coord = XdsOffloadCoordinator("cuda", L, R, cfg.dbs, cfg.top_k, R, cfg.prefill)
         st = orc.SieveState(L, R, cfg.dbs, cfg.top_k)
-        host_base = np.array([cfg.host_base(r) for r in range(R)], dtype=np.int64)
+        host_base = np.array(allocate_host_rows(pool, cfg), dtype=np.int64)
         for r in range(R):
             coord.admit_request(r, r, cfg.prefill, int(host_base[r]))
             st.admit(r, cfg.prefill)
