@@ -1,0 +1,185 @@
+"""CPU checks of the two table algorithms the GPU kernels are built on.
+
+* Batch deletion (the HBM SIEVE kernel's phase 4, csrc/sieve_batch.hip): one
+  left-to-right pass per cluster, each surviving entry moving into the
+  leftmost hole at or after its home, leaves the same table as sequential
+  Algorithm R deletions (hisp_kernel_common.h:64-94) in any order, which is
+  also the table of inserting the survivors in their insertion order.
+* Parallel admission build (kvx_sieve_ht_init_par, csrc/sieve.hip): keys
+  bucketed by home with later duplicates dropped, the used cells from the
+  backlog recursion (the ring's fixed point entering cell 0), then each
+  cluster's keys in slot order; equal to the oracle's sequential inserts
+  (hisp_sieve_ht_init.cpp:14-60).
+
+These pin the algorithms (brute force over small tables); the kernels
+themselves are compared with the oracle in the GPU tests.
+"""
+import random
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+
+def _knuth_home(k, H):
+    return ((k * 2654435761) & 0xFFFFFFFF) >> 16 & (H - 1)
+
+
+def _insert(T, k, hf):
+    H = len(T)
+    i = hf(k)
+    while T[i] is not None:
+        if T[i] == k:
+            return
+        i = (i + 1) % H
+    T[i] = k
+
+
+def _erase(T, k, hf):
+    """Algorithm R: backward-shift deletion."""
+    H = len(T)
+    i = hf(k)
+    while T[i] != k:
+        assert T[i] is not None
+        i = (i + 1) % H
+    T[i] = None
+    j = i
+    while True:
+        j = (j + 1) % H
+        if T[j] is None:
+            return
+        h = hf(T[j])
+        inside = (i < h <= j) if i <= j else (h > i or h <= j)  # home cyclically in (i, j]
+        if not inside:
+            T[i], T[j] = T[j], None
+            i = j
+
+
+def _batch_delete(T, D, hf):
+    """One pass from an empty cell: deleted cells become holes; every other
+    entry moves into the leftmost hole at or after its home (its cell then
+    becomes a hole); an empty cell ends the cluster and its holes."""
+    H = len(T)
+    T = list(T)
+    start = next(c for c in range(H) if T[c] is None)
+    holes = []  # offsets from start, increasing
+    for off in range(1, H + 1):
+        c = (start + off) % H
+        if T[c] is None:
+            holes = []
+            continue
+        if T[c] in D:
+            T[c] = None
+            holes.append(off)
+            continue
+        hoff = (hf(T[c]) - start) % H
+        at = next((i for i, ho in enumerate(holes) if ho >= hoff), None)
+        if at is not None:
+            ho = holes.pop(at)
+            T[(start + ho) % H], T[c] = T[c], None
+            holes.append(off)
+    return T
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_batch_deletion_equals_algorithm_r(seed):
+    rng = random.Random(seed)
+    for trial in range(600):
+        H = rng.choice([16, 32, 64, 128])
+        n = rng.randint(1, H - 1)
+        skew = rng.choice([None, 3, 8])  # None: the Knuth hash; else a few homes (long clusters)
+        if skew is None:
+            def hf(k, H=H):
+                return _knuth_home(k, H)
+        else:
+            def hf(k, H=H, s=skew):
+                return (k * 7 % s + H - 2) % H  # homes next to the end: clusters wrap
+        keys = rng.sample(range(100000), n)
+        T = [None] * H
+        for k in keys:
+            _insert(T, k, hf)
+        D = set(rng.sample(keys, rng.randint(0, n)))
+        order = list(D)
+        rng.shuffle(order)
+        seq = list(T)
+        for k in order:
+            _erase(seq, k, hf)
+        fcfs = [None] * H
+        for k in keys:
+            if k not in D:
+                _insert(fcfs, k, hf)
+        assert seq == fcfs, (seed, trial)
+        assert _batch_delete(T, D, hf) == seq, (seed, trial, H, keys, sorted(D))
+
+
+def _parallel_build(tok, dbs, H, lanes=256):
+    mask = H - 1
+    lists = [[] for _ in range(H)]
+    for s in range(dbs):
+        t = int(tok[s])
+        if t >= 0:
+            lists[_knuth_home(t, H)].append(s)
+    for h in range(H):  # slot order, later duplicates of a token dropped
+        keep, seen = [], set()
+        for s in sorted(lists[h]):
+            if int(tok[s]) not in seen:
+                seen.add(int(tok[s]))
+                keep.append(s)
+        lists[h] = keep
+    n = [len(x) for x in lists]
+    per = H // lanes
+    maps = []
+    for k in range(lanes):  # each lane's segment as x -> max(P, x + Q)
+        P = Q = 0
+        for c in range(k * per, (k + 1) * per):
+            P, Q = max(0, P + n[c] - 1), Q + n[c] - 1
+        maps.append((P, Q))
+    P = Q = 0
+    for p, q in maps:  # composed in cell order
+        P, Q = max(p, P + q), Q + q
+    assert Q < 0
+    x = P  # the fixed point: the backlog entering cell 0
+    used = []
+    for c in range(H):
+        used.append(x + n[c] >= 1)
+        x = max(0, x + n[c] - 1)
+    assert x == P
+    ht = [0] * H
+    for c in range(H):
+        if used[c] and not used[(c - 1) & mask]:
+            homes, e = [], c
+            while used[e & mask]:
+                homes.append(e & mask)
+                e += 1
+            for s in sorted(s for h in homes for s in lists[h]):
+                y = _knuth_home(int(tok[s]), H)
+                while ht[y] != 0:
+                    y = (y + 1) & mask
+                ht[y] = s + 1
+    return np.array(ht, dtype=np.uint16)
+
+
+@pytest.mark.parametrize("mode", ["unique", "dups", "few_homes", "wrap"])
+def test_parallel_table_build_equals_sequential_inserts(mode):
+    rng = np.random.default_rng(len(mode))
+    for trial in range(6):
+        dbs = int(rng.choice([1, 64, 300, 1000]))
+        padded = (dbs + 15) // 16 * 16
+        top_k = int(rng.integers(1, 256))
+        H = orc.ht_size(padded, top_k)
+        tok = np.full(padded, -1, dtype=np.int32)
+        n = int(rng.integers(0, dbs + 1))
+        if mode == "unique":
+            vals = rng.choice(1 << 22, size=n, replace=False)
+        elif mode == "dups":
+            vals = rng.integers(-3, max(4, n // 3), size=n)
+        else:
+            t = np.arange(0, 1 << 21, dtype=np.int64)
+            h = ((t * 2654435761) & 0xFFFFFFFF) >> 16 & (H - 1)
+            cand = t[np.isin(h, rng.choice(H, size=4, replace=False))] if mode == "few_homes" else t[h >= H - 24]
+            vals = rng.choice(cand, size=min(n, len(cand)), replace=False)
+        tok[rng.choice(dbs, size=len(vals), replace=False)] = vals
+        want = np.zeros((1, 1, H), dtype=np.uint16)
+        orc.sieve_ht_init(tok.reshape(1, 1, padded).copy(), want, 0, 1, 1, 1, dbs, padded, H)
+        np.testing.assert_array_equal(_parallel_build(tok, dbs, H), want[0, 0], err_msg="{} {}".format(mode, trial))
