@@ -237,9 +237,12 @@ int64_t orc_ht_size(int64_t padded, int64_t topK)
 }
 
 /* :307-312 — requests per block, aligned so each block's output rows cover
- * whole 64-byte lines: align(ceil(maxNumReqs/blockDim), 64/gcd(topK,64)). */
+ * whole 64-byte lines: align(ceil(maxNumReqs/blockDim), 64/gcd(topK,64)).
+ * A block count below 1 reads as 1, as the launch layer maps block_dim 0
+ * (the reference divides by it). */
 int64_t orc_reqs_per_core(int64_t maxNumReqs, int64_t blockDim, int64_t topK)
 {
+    if (blockDim < 1) blockDim = 1;
     int64_t a = topK, b = 64;
     while (b != 0) { int64_t t = a % b; a = b; b = t; }
     const int64_t al = 64 / a;
