@@ -48,10 +48,12 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib);
  * receives that address. */
 int kvx_alloc_status(int count, uint64_t *out_addr);
 
-/* kvops_ext.cpp:198-218 kv_poll_status.  Reads the word at status_addr from
- * the host until its doneSeq byte is 1 and returns the err field; returns
- * -0x2000 after timeout_us microseconds (timeout_us < 0 waits forever) and
- * -0x1000 if status_addr is not inside a status allocation. */
+/* kvops_ext.cpp:198-218 kv_poll_status.  Reads the word at status_addr until
+ * its doneSeq byte is 1 and returns the err field; returns -0x2000 after
+ * timeout_us microseconds (timeout_us < 0 waits forever).  A word inside a
+ * kvx_alloc_status block is read directly from the host; any other address
+ * the runtime knows (device memory, pinned host memory) is read with an
+ * 8-byte copy per poll; an unknown address or a failed copy gives -0x1000. */
 int64_t kvx_poll_status(uint64_t status_addr, int64_t timeout_us);
 
 /* kvops_ext.cpp:221-254 kv_import_seg: copy this segment's miss rows into the

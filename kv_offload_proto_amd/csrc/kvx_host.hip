@@ -122,6 +122,38 @@ volatile uint64_t *StatusWord(uint64_t addr)
     return nullptr;
 }
 
+// A status word outside the kvx_alloc_status blocks (device memory, or host
+// memory HIP knows): read with an 8-byte copy per poll, as the reference polls
+// any status address (kvops_ext.cpp:198-218).  An address HIP does not know,
+// or a failed copy, gives -0x1000 (the reference's copy-failure code), a
+// timeout -0x2000; done is the doneSeq byte, as for the direct reads.
+int64_t PollCopiedWord(uint64_t addr, int64_t timeout_us)
+{
+    hipPointerAttribute_t attr{};
+    if (addr == 0 || (addr & 7u) != 0 ||
+        hipPointerGetAttributes(&attr, reinterpret_cast<const void *>(addr)) != hipSuccess ||
+        attr.type == hipMemoryTypeUnregistered) {
+        (void)hipGetLastError();
+        t_lastError = "poll_status: not a status address known to the runtime";
+        return -0x1000;
+    }
+    const auto t0 = std::chrono::steady_clock::now();
+    while (true) {
+        uint64_t v = 0;
+        if (hipMemcpy(&v, reinterpret_cast<const void *>(addr), 8, hipMemcpyDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            t_lastError = "poll_status: reading the status word failed";
+            return -0x1000;
+        }
+        if (((v >> 32) & 0xFFu) == 1u) return static_cast<int64_t>(v & 0xFFFFFFFFull);
+        if (timeout_us >= 0) {
+            const auto us = std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0);
+            if (us.count() >= timeout_us) return -0x2000;
+        }
+        std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+}
+
 // Clear `words` status words of node slot `node` from the host, before the
 // launch is queued (kvops_ext.cpp:252,276 clear synchronously too).
 void ClearStatusWords(uint64_t status, uint32_t node, uint32_t words)
@@ -550,7 +582,7 @@ int64_t kvx_poll_status(uint64_t status_addr, int64_t timeout_us)
         return -0x1000;
     }
     volatile uint64_t *w = StatusWord(status_addr);
-    if (w == nullptr) return -0x1000;
+    if (w == nullptr) return PollCopiedWord(status_addr, timeout_us);
     const auto t0 = std::chrono::steady_clock::now();
     uint32_t spins = 0;
     while (true) {

@@ -126,6 +126,21 @@ def test_status_poll_and_timeout(kvops):
     assert kvops.poll_status(12345, 10) == -0x1000
 
 
+def test_status_poll_device_memory(kvops):
+    """A status word in device memory (the reference polls any status
+    address, kvops_ext.cpp:198-218): pending times out, a done word returns
+    its err field, an unaligned address is refused."""
+    import torch
+
+    words = torch.zeros(16, dtype=torch.int64, device="cuda")
+    addr = words.data_ptr()
+    assert kvops.poll_status(addr, 2000) == -0x2000
+    words[1] = (1 << 32) | (5 << 40) | 0x203  # done, 5 rows queued, err 0x203
+    torch.cuda.synchronize()
+    assert kvops.poll_status(addr + 8, 1000) == 0x203
+    assert kvops.poll_status(addr + 4, 10) == -0x1000
+
+
 @pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("S,N,block_dim,max_rows,num_real", [(1, 2, 1, 64, 64), (1, 3, 3, 500, 377), (64, 4, 2, 256, 256),
                                                              (4, 2, 8, 1000, 999), (1, 1, 1, 40, 0)])
