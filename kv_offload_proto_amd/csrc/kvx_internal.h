@@ -46,7 +46,7 @@ struct RowScratch {
     uint64_t winEntries;       // capacity of win[]
     uint32_t *counters;        // [64 nodes][8 status words] queued counts
     uint32_t *errs;            // [64 nodes][8 status words] first error code
-    uint32_t *tickets;         // [8] last-block tickets (gather, export, export_rows, small gather)
+    uint32_t *tickets;         // [8] last-block tickets (gather, export, export_rows, small gather, small export_rows)
     uint32_t *epoch;           // gather winner-tag epoch, advanced on the device by each call
     uint64_t *listSrc;         // gather row list: source byte addresses
     uint64_t *listDst;         // gather row list: destination byte addresses

@@ -597,6 +597,108 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
     }
 }
 
+// Short exports (max_rows <= kExportSmallMax, the rows a decode step
+// appends): both passes in one launch.  Every workgroup tags the winners of
+// all entries (the same atomicMax values, so the repeats are harmless) and
+// counts the owned entries and the lowest out-of-region entry per status word
+// in its own LDS, then copies the winners among its own entries (8 per
+// wave); the last workgroup (ticket) advances the epoch and stores the
+// status words from its counts.
+constexpr uint32_t kExportSmallMax = 4096;
+
+__global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
+{
+    __shared__ uint64_t sSrc[kWaves][64];
+    __shared__ uint64_t sDst[kWaves][64];
+    __shared__ uint32_t sCnt[64 * 8], sErr[64 * 8];
+    __shared__ int sLast;
+    __shared__ uint32_t sEpoch;
+    const ExportRowsArgs &a = P.a;
+    const int wave = threadIdx.x / 64;
+    const uint32_t lane = static_cast<uint32_t>(lane_id());
+    const int32_t n = clamp_num_real(a.numReal, a.maxRows);  // <= kExportSmallMax (host)
+    const int64_t *idx = reinterpret_cast<const int64_t *>(a.indicesHost);
+    const uint32_t cpr = a.rowBytes / 16u;
+    const uint32_t words = a.statusWords;
+    const uint32_t ppc = (a.maxRows + words - 1u) / words;  // entries per status word
+    const uint32_t n0 = a.fused ? 0u : a.myNode, n1 = a.fused ? a.nodeNum : a.myNode + 1u;
+    if (blockIdx.x == 0 && a.status != 0) {  // the call's status words read 0 until its rows have landed
+        for (uint32_t k = threadIdx.x; k < (n1 - n0) * words; k += blockDim.x) {
+            store_status(a.status + (n0 + k / words) * 64ull + (k % words) * 8ull, 0ull);
+        }
+    }
+    for (uint32_t k = threadIdx.x; k < 64u * 8u; k += blockDim.x) {
+        sCnt[k] = 0u;
+        sErr[k] = 0xFFFFFFFFu;  // lowest failing entry, min-reduced
+    }
+    if (threadIdx.x == 0) sEpoch = *P.epoch;
+    __syncthreads();
+    const unsigned long long tagHi = static_cast<unsigned long long>(sEpoch) << 32;
+    for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        uint32_t node, segRow;
+        if (!export_row_target(a, idx[i], node, segRow) || segRow >= a.perLayerSegRows) continue;
+        const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
+        if (w < P.winEntries) atomicMax(&P.win[w], tagHi | static_cast<unsigned long long>(i));
+    }
+    __threadfence();
+    __syncthreads();
+    for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        uint32_t node, segRow;
+        if (!export_row_target(a, idx[i], node, segRow)) continue;
+        const uint32_t key = node * 8u + static_cast<uint32_t>(i) / ppc;
+        atomicAdd(&sCnt[key], 1u);
+        if (segRow >= a.perLayerSegRows) atomicMin(&sErr[key], static_cast<uint32_t>(i));
+    }
+    constexpr int32_t R = kExportRowsPerWave;
+    {
+        const int32_t i = (static_cast<int32_t>(blockIdx.x) * kWaves + wave) * R + static_cast<int32_t>(lane);
+        bool copy = false;
+        uint64_t src = 0, dst = 0;
+        uint32_t node, segRow;
+        if (static_cast<int32_t>(lane) < R && i < n && export_row_target(a, idx[i], node, segRow) &&
+            segRow < a.perLayerSegRows) {
+            const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
+            copy = w >= P.winEntries ||
+                   __hip_atomic_load(&P.win[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       (tagHi | static_cast<unsigned long long>(i));
+            src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
+            dst = (a.fused ? P.segBases[node] : a.segBase) +
+                  (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;
+        }
+        const uint64_t cm = __ballot(copy);
+        if (copy) {
+            const uint32_t at = static_cast<uint32_t>(__popcll(cm & ((1ull << lane) - 1ull)));
+            sSrc[wave][at] = src;
+            sDst[wave][at] = dst;
+        }
+        wave_sync_lds();
+        wave_copy_rows(sSrc[wave], sDst[wave], static_cast<uint32_t>(__popcll(cm)), cpr);
+    }
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int ticket = atomicInc(&P.tickets[4], gridDim.x - 1u);
+        sLast = (ticket == gridDim.x - 1u) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sLast) return;
+    if (sEpoch + 1u == 0u) {  // at the wrap (once in 2^32 calls) the tag table is cleared
+        for (uint64_t k = threadIdx.x; k < P.winEntries; k += blockDim.x) P.win[k] = 0ull;
+    }
+    if (threadIdx.x == 0) *P.epoch = sEpoch + 1u;
+    if (a.status == 0) return;
+    __threadfence_system();
+    for (uint32_t k = threadIdx.x; k < (n1 - n0) * words; k += blockDim.x) {
+        const uint32_t node = n0 + k / words, b = k % words;
+        uint64_t word = 1ull << 32;
+        if (static_cast<int64_t>(b) * ppc < n) {
+            const uint32_t e = sErr[node * 8u + b];
+            word |= (static_cast<uint64_t>(sCnt[node * 8u + b]) << 40) | (e == 0xFFFFFFFFu ? 0u : row_error_code(e));
+        }
+        store_status(a.status + node * 64ull + b * 8ull, word);
+    }
+}
+
 // Plain streaming copy, 16 B per lane, kUnroll chunks in flight per lane.
 __global__ __launch_bounds__(256) void kvx_stream_copy(u32x4 *dst, const u32x4 *src, uint64_t n16)
 {
@@ -706,6 +808,11 @@ hipError_t launch_export_rows(const ExportRowsArgs &a, const uint64_t *segBases,
     P.errs = scr.errs;
     P.tickets = scr.tickets;
     P.epoch = scr.epoch;
+    if (a.maxRows <= kExportSmallMax) {
+        const uint32_t blocks = (a.maxRows + kExportRowsPerWave * kWaves - 1u) / (kExportRowsPerWave * kWaves);
+        hipLaunchKernelGGL(kvx_export_rows_small, dim3(blocks), dim3(256), 0, stream, P);
+        return hipGetLastError();
+    }
     uint64_t prep = (static_cast<uint64_t>(a.maxRows) + 255ull) / 256ull;
     prep = prep < 1 ? 1 : (prep > 1024 ? 1024 : prep);
     hipLaunchKernelGGL(kvx_export_rows_prep, dim3(static_cast<uint32_t>(prep)), dim3(256), 0, stream, P);
