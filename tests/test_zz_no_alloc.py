@@ -70,8 +70,9 @@ def test_import_all_noalloc_matches_import_all(kvops):
         sa, sb = kvops.alloc_status(N), kvops.alloc_status(N)
         rng = np.random.default_rng(12)
         # call 1: every row of the batch; call 2: a smaller batch (5 rows
-        # allocated, 4 of them real) on the state the first call left
-        for call, (mnr, nreal) in enumerate([(R, R), (5, 4)]):
+        # allocated, 4 of them real) on the state the first call left; call
+        # 3: 2 rows x 2048 positions, the one-launch form of small batches
+        for call, (mnr, nreal) in enumerate([(R, R), (5, 4), (2, 2)]):
             batch = streams.state_batch(rng, st.tokens[0, :, :dbs], prefill, top_k, 0.2, zipf_s=1.1)
             batch[mnr:] = -1
             topk_d = torch.from_numpy(batch).cuda()
