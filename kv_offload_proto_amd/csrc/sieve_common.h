@@ -6,6 +6,11 @@
 
 #include "kvx_internal.h"
 
+// v_writelane_b32: x with lane l (the same in the whole wave) replaced by v,
+// whatever the exec mask.  The LLVM intrinsic, which this clang does not
+// expose as a builtin.
+extern "C" __device__ int32_t kvx_writelane_i32(int32_t v, int32_t l, int32_t x) __asm("llvm.amdgcn.writelane.i32");
+
 namespace kvx {
 namespace sieve {
 
@@ -20,6 +25,9 @@ constexpr int32_t kSmallTable = 4096;
 // Value of x in lane l, l the same in the whole wave (a register read, no
 // LDS round trip as a shuffle would take).
 __device__ __forceinline__ int32_t lane_value(int32_t x, int32_t l) { return __builtin_amdgcn_readlane(x, l); }
+
+// x with lane l set to v (a register write, no compare and select).
+__device__ __forceinline__ int32_t lane_set(int32_t x, int32_t l, int32_t v) { return kvx_writelane_i32(v, l, x); }
 
 // Token held by the slot an entry points at.  An entry past the tokens row
 // can only come from a corrupted table; it reads as the empty token (-1)
@@ -455,57 +463,54 @@ __device__ int32_t sieve_row_regs_decide(const int32_t *rt, int32_t *rs, int8_t 
 {
     const int32_t lane = static_cast<int32_t>(__lane_id());
     const bool mine = lane < dbs;
+    // slot s's token in lane s; -1 past dbs, so a valid token (>= 0) matches
+    // only a slot of the row
     int32_t tokR = mine ? tok[lane] : -1;
     const uint64_t all = dbs >= 64 ? ~0ull : ((1ull << dbs) - 1ull);
     uint64_t vm = __ballot(mine && ((vis[lane >> 3] >> (lane & 7)) & 1));
     int32_t hd = hand, ev = -1, nev = 0;
     for (int32_t k0 = 0; k0 < topK; k0 += 64) {
-        const int32_t kn = (topK - k0 < 64) ? topK - k0 : 64;
+        const int32_t kn = __builtin_amdgcn_readfirstlane((topK - k0 < 64) ? topK - k0 : 64);
         const int32_t myT = lane < kn ? rt[k0 + lane] : -1;
-        int32_t mySlot = -1, myMiss = 0;
-        for (int32_t kk = 0; kk < kn; ++kk) {
-            const int32_t tp = lane_value(myT, kk);
-            int32_t slot = -1, miss = 0;
-            if (tp < 0 || tp >= seqLen) {
-            } else if (tp >= prefill) {
-                slot = padded + (tp - prefill);
+        // invalid and decode-extension positions in parallel; the rest are
+        // looked up one after another (their outcomes change the row)
+        const bool valid = lane < kn && myT >= 0 && myT < seqLen;
+        int32_t mySlot = (valid && myT >= prefill) ? padded + (myT - prefill) : -1;
+        uint64_t missBits = 0;
+        for (uint64_t m = __ballot(valid && myT < prefill); m != 0ull; m &= m - 1ull) {
+            const int32_t kk = __builtin_ctzll(m);
+            const int32_t tp = __builtin_amdgcn_readlane(myT, kk);
+            const uint64_t hm = __ballot(tokR == tp);
+            int32_t slot;
+            if (hm != 0ull) {
+                slot = __builtin_ctzll(hm);
+                vm |= 1ull << slot;
             } else {
-                const uint64_t hm = __ballot(mine && tokR == tp);
-                if (hm != 0ull) {
-                    slot = __builtin_ctzll(hm);
-                    vm |= 1ull << slot;
-                } else {
-                    const uint64_t unv = ~vm & all, from = all & ~((1ull << hd) - 1ull);
-                    int32_t h;
-                    if (unv & from) {
-                        h = __builtin_ctzll(unv & from);
-                        vm &= ~(((1ull << h) - 1ull) & from);
-                    } else if (unv) {
-                        h = __builtin_ctzll(unv);
-                        vm &= ~(from | ((1ull << h) - 1ull));
-                    } else {  // every slot visited: a whole revolution clears them all
-                        h = hd;
-                        vm = 0ull;
-                    }
-                    if (lane == h) {
-                        tokR = tp;
-                        ev = nev;
-                    }
-                    ++nev;
-                    vm |= 1ull << h;
-                    hd = (h + 1 == dbs) ? 0 : h + 1;
-                    slot = h;
-                    miss = 1;
+                const uint64_t unv = ~vm & all, from = all & ~((1ull << hd) - 1ull);
+                int32_t h;
+                if (unv & from) {
+                    h = __builtin_ctzll(unv & from);
+                    vm &= ~(((1ull << h) - 1ull) & from);
+                } else if (unv) {
+                    h = __builtin_ctzll(unv);
+                    vm &= ~(from | ((1ull << h) - 1ull));
+                } else {  // every slot visited: a whole revolution clears them all
+                    h = hd;
+                    vm = 0ull;
                 }
+                tokR = lane_set(tokR, h, tp);
+                ev = lane_set(ev, h, nev);
+                ++nev;
+                vm |= 1ull << h;
+                hd = (h + 1 == dbs) ? 0 : h + 1;
+                slot = h;
+                missBits |= 1ull << kk;
             }
-            if (lane == kk) {
-                mySlot = slot;
-                myMiss = miss;
-            }
+            mySlot = lane_set(mySlot, kk, slot);
         }
         if (lane < kn) {
             rs[k0 + lane] = mySlot;
-            rm[k0 + lane] = static_cast<int8_t>(myMiss);
+            rm[k0 + lane] = static_cast<int8_t>((missBits >> lane) & 1ull);
         }
     }
     tokFinal = tokR;
