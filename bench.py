@@ -679,7 +679,8 @@ def main():
             total += sum(hits)
         return total
 
-    gather_kernels = ("kvx_gather_prep", "kvx_gather_list", "kvx_gather_copy")
+    # the library imports up to 4096 positions in one launch, larger batches in two
+    gather_kernels = ("kvx_gather_small",) if positions <= 4096 else ("kvx_gather_prep", "kvx_gather_span")
     gather_roof = {"kernel": "+".join(gather_kernels), "bound": "host-link", "achieved": link_gbps,
                    "peak": link["peak_GBps"], "unit": "GB/s", "frac": link_gbps / link["peak_GBps"],
                    "traffic": traffic_of(*gather_kernels), "traffic_source": traffic_src,

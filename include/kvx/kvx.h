@@ -19,7 +19,7 @@
  *
  * Streams and scratch: the row movers (import, export_rows, the prefill
  * export) and the HBM-resident SIEVE variant keep device scratch (winner
- * tags, a row list, counters, a table shadow).  The library holds one scratch
+ * tags, counters, a table shadow).  The library holds one scratch
  * set per stream: launches on one stream run in order and share it, launches
  * on different streams (from any threads) never share it.  A stream's set is
  * created by its first launch (the null stream's by kvx_init) and grows when
@@ -89,10 +89,10 @@ int kvx_import_all(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32
  * allocate device memory (launches under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation).  Same arguments, results and
  * status words as kvx_import_all; it allocates nothing and creates no
- * per-stream scratch: its scratch is one fixed array per GPU (26.2 MB, held
+ * per-stream scratch: its scratch is one fixed array per GPU (17.8 MB, held
  * from library load to process exit) shared by every call of this entry
  * point on that GPU, so calls that overlap on one GPU race (run them on one
- * stream, or order them).  Limits: max_num_reqs * top_k <= 524288 and
+ * stream, or order them).  Limit:
  * (max_num_reqs - 1) * min(hot_req_stride_rows, 65536) + 65536 <= 2228224;
  * a larger call fails with an error before anything is queued. */
 int kvx_import_all_noalloc(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,

@@ -44,16 +44,14 @@ struct StreamScratch {
 // Scratch of kvx_import_all_noalloc: a fixed array in the library's code
 // object, so each GPU the library is loaded on holds its own copy from load
 // to process exit, and the entry point allocates nothing.  Layout: the
-// control words (counters, error words, tickets, list count, epoch), the
-// winner table, then the row list (sources, then destinations).  It starts
-// zeroed; the kernels clear the counters, error words and list count at the
-// start of every call, and the winner table is tagged with the epoch that
-// every call advances, so it is never cleared (except at the epoch's 2^32
-// wrap, by the last copy workgroup).
-constexpr uint64_t kNoAllocMaxPositions = 1ull << 19;       // max_num_reqs * top_k
+// control words (counters, error words, tickets, chunk counter, epoch), then
+// the winner table.  It starts zeroed; the kernels clear the counters, error
+// words and chunk counter at the start of every call, and the winner table is
+// tagged with the epoch that every call advances, so it is never cleared
+// (except at the epoch's 2^32 wrap, by the last copy workgroup).
 constexpr uint64_t kNoAllocMaxWinEntries = 34ull << 16;     // (max_num_reqs-1)*min(stride,65536) + 65536
 constexpr uint64_t kNoAllocControlBytes = (kvx::kControlWords * 4 + 255) / 256 * 256;
-constexpr uint64_t kNoAllocBytes = kNoAllocControlBytes + kNoAllocMaxWinEntries * 8 + kNoAllocMaxPositions * 16;
+constexpr uint64_t kNoAllocBytes = kNoAllocControlBytes + kNoAllocMaxWinEntries * 8;
 static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 
 struct State {
@@ -185,7 +183,7 @@ void CheckStatusBlock(uint64_t status, uint32_t firstNode, uint32_t nodes, uint3
 
 // Scratch needs of one launch (entries of each buffer; 0 = not used).
 struct ScratchNeed {
-    uint64_t win = 0, list = 0, shadow = 0, aux = 0;
+    uint64_t win = 0, shadow = 0, aux = 0;
 };
 
 bool Capturing(hipStream_t s)
@@ -218,8 +216,8 @@ StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *
         if (s->stream == stream) sc = s;
     }
     const bool create = sc == nullptr;
-    const bool grow = create || sc->rows.winEntries < need.win || sc->rows.listCap < need.list ||
-                      sc->shadowCells < need.shadow || sc->auxWords < need.aux;
+    const bool grow = create || sc->rows.winEntries < need.win || sc->shadowCells < need.shadow ||
+                      sc->auxWords < need.aux;
     if (!grow) return *sc;
     hipStream_t st = AsStream(stream);
     if (Capturing(st)) {
@@ -233,7 +231,7 @@ StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *
         s->rows.counters = c;
         s->rows.errs = c + 64 * 8;
         s->rows.tickets = c + 2 * 64 * 8;
-        s->rows.listCount = s->rows.tickets + 8;
+        s->rows.chunkNext = s->rows.tickets + 8;
         s->rows.epoch = s->rows.tickets + 9;
         g.scratch.push_back(s);
         sc = s;
@@ -246,14 +244,6 @@ StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *
         if (r.win != nullptr) g.retired.push_back(r.win);
         r.win = static_cast<unsigned long long *>(p);
         r.winEntries = cap;
-    }
-    if (r.listCap < need.list) {
-        const uint64_t cap = std::max<uint64_t>(need.list, std::max<uint64_t>(2 * r.listCap, 65536));
-        void *p = ScratchAlloc(2 * cap * sizeof(uint64_t), st, "row list");
-        if (r.listSrc != nullptr) g.retired.push_back(r.listSrc);
-        r.listSrc = static_cast<uint64_t *>(p);
-        r.listDst = r.listSrc + cap;
-        r.listCap = cap;
     }
     if (sc->shadowCells < need.shadow) {
         void *p = ScratchAlloc(need.shadow * sizeof(int32_t), st, "sieve shadow");
@@ -382,7 +372,6 @@ void DoGather(const GatherCall &c, const kvx::RowScratch *fixed = nullptr)
 
     ScratchNeed need;
     need.win = kvx::gather_win_entries(c.maxNumReqs, c.stride);
-    need.list = positions;
     hipStream_t st = AsStream(c.stream);
     if (c.fused) {
         CheckStatusBlock(c.status, 0, c.nodeNum, bd, "import_all");
@@ -391,9 +380,8 @@ void DoGather(const GatherCall &c, const kvx::RowScratch *fixed = nullptr)
     }
     if (fixed != nullptr) {
         // the no-allocation form: the fixed scratch bounds the call
-        if (need.list > fixed->listCap || need.win > fixed->winEntries) {
-            throw Error("import_all_noalloc: max_num_reqs*top_k = " + std::to_string(need.list) + " (max " +
-                        std::to_string(fixed->listCap) + ") and winner rows (max_num_reqs-1)*min(stride,65536)+65536 = " +
+        if (need.win > fixed->winEntries) {
+            throw Error("import_all_noalloc: winner rows (max_num_reqs-1)*min(stride,65536)+65536 = " +
                         std::to_string(need.win) + " (max " + std::to_string(fixed->winEntries) +
                         ") must fit the fixed scratch");
         }
@@ -490,7 +478,6 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
             std::lock_guard<std::mutex> lk(g_scratchMu);
             ScratchNeed need;
             need.win = 65536;
-            need.list = 65536;
             (void)ScratchFor(0, need, "init");
         }
         // the no-allocation entry point's scratch on this device: the
@@ -514,7 +501,6 @@ int kvx_reserve_scratch(uint64_t stream, uint32_t max_num_reqs, uint32_t top_k, 
         EnsureInited();
         if (node_num > 64) throw Error("reserve_scratch: node_num must be in [0, 64]");
         ScratchNeed need;
-        need.list = static_cast<uint64_t>(max_num_reqs) * top_k;
         need.win = std::max(kvx::gather_win_entries(max_num_reqs, hot_req_stride_rows),
                             kvx::export_rows_win_entries(per_layer_seg_rows, std::max<uint32_t>(node_num, 1u)));
         if (device_buffer_size > 0 && max_num_reqs > 0) {
@@ -544,8 +530,7 @@ int kvx_scratch_bytes(uint64_t stream, uint64_t *out_bytes)
         for (const StreamScratch *s : g.scratch) {
             if (s->stream != stream) continue;
             b = kvx::kControlWords * sizeof(uint32_t) + s->rows.winEntries * sizeof(unsigned long long) +
-                s->rows.listCap * 2 * sizeof(uint64_t) + s->shadowCells * sizeof(int32_t) +
-                s->auxWords * sizeof(uint32_t);
+                s->shadowCells * sizeof(int32_t) + s->auxWords * sizeof(uint32_t);
         }
         *out_bytes = b;
     });
@@ -703,13 +688,10 @@ int kvx_import_all_noalloc(const uint64_t *seg_bases, uint32_t layer_offset_rows
         fixed.counters = ctl;
         fixed.errs = ctl + 64 * 8;
         fixed.tickets = ctl + 2 * 64 * 8;
-        fixed.listCount = fixed.tickets + 8;
+        fixed.chunkNext = fixed.tickets + 8;
         fixed.epoch = fixed.tickets + 9;
         fixed.win = reinterpret_cast<unsigned long long *>(b + kNoAllocControlBytes);
         fixed.winEntries = kNoAllocMaxWinEntries;
-        fixed.listSrc = reinterpret_cast<uint64_t *>(b + kNoAllocControlBytes + kNoAllocMaxWinEntries * 8);
-        fixed.listDst = fixed.listSrc + kNoAllocMaxPositions;
-        fixed.listCap = kNoAllocMaxPositions;
         GatherCall c{};
         c.fused = true;
         c.nSeg = node_num;
@@ -945,7 +927,6 @@ int kvx_close(void)
             std::lock_guard<std::mutex> lk(g_scratchMu);
             for (StreamScratch *s : g.scratch) {
                 if (s->rows.win != nullptr) (void)hipFree(s->rows.win);
-                if (s->rows.listSrc != nullptr) (void)hipFree(s->rows.listSrc);
                 if (s->rows.counters != nullptr) (void)hipFree(s->rows.counters);
                 if (s->shadow != nullptr) (void)hipFree(s->shadow);
                 if (s->aux != nullptr) (void)hipFree(s->aux);

@@ -48,14 +48,12 @@ struct RowScratch {
     uint32_t *errs;            // [64 nodes][8 status words] first error code
     uint32_t *tickets;         // [8] last-block tickets (gather, export, export_rows, small gather, small export_rows)
     uint32_t *epoch;           // gather winner-tag epoch, advanced on the device by each call
-    uint64_t *listSrc;         // gather row list: source byte addresses
-    uint64_t *listDst;         // gather row list: destination byte addresses
-    uint64_t listCap;          // capacity of the row list
-    uint32_t *listCount;       // rows listed by the current gather
+    uint32_t *chunkNext;       // next position chunk of the current gather
 };
 
-// Control words of one scratch set: counters, error words, tickets, the list
-// count and the epoch, in this order (kControlWords uint32 words).
+// Control words of one scratch set: counters, error words, tickets, the
+// import's chunk counter and the epoch, in this order (kControlWords uint32
+// words).
 constexpr uint32_t kControlWords = 64 * 8 * 2 + 8 + 8;
 
 // Winner-table entries an import needs: request b's destinations are

@@ -5,12 +5,12 @@
 // kvc_scatter_rows_alllayer.cpp:11-67 of the reference, with the row
 // ownership of kv_layout.h.  The reference moves each row with one HCOMM
 // ReadNbi/WriteNbi; here the host segments are pinned host memory mapped
-// into the device address space.  The import runs in three launches:
-// winners (the last miss position per destination row), a dense list of the
-// rows to move (with the reference's queued counts), and the copy, where
-// each wave moves 64 listed rows at a time as 16-byte chunks, 8 chunks in
-// flight per lane, so megabytes of host-link reads stay outstanding.  A
-// small batch (up to 4096 positions) takes one launch instead (below).
+// into the device address space.  The import runs in two launches: winners
+// (the last miss position per destination row), then the listing and the
+// copy, where 64 workgroups claim 256 positions at a time, list their rows in
+// LDS with the reference's queued counts, and move them as 16-byte chunks, 8
+// chunks in flight per lane.  A small batch (up to 4096 positions) takes one
+// launch instead (below).
 //
 // Completion: the last workgroup to finish (atomicInc ticket) stores the
 // status words with a system-scope release, after every workgroup fenced its
@@ -23,7 +23,6 @@ namespace {
 
 constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kUnroll = 8;         // 16-byte chunks in flight per lane
-constexpr int kGroup = 8;          // 64-position chunks a wave lists per row-list atomic
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -31,9 +30,7 @@ struct GatherExtra {
     uint64_t segBases[64];
     unsigned long long *win;
     uint64_t winEntries;
-    uint64_t *listSrc;     // rows to move: source and destination byte addresses
-    uint64_t *listDst;
-    uint32_t *listCount;
+    uint32_t *chunkNext;   // next position chunk of the current import
     uint32_t *counters;
     uint32_t *errs;
     uint32_t *tickets;
@@ -119,8 +116,8 @@ __device__ __forceinline__ uint64_t win_index(int64_t bid, int32_t slot, uint32_
 // Pass 1: per destination row, the last valid miss position (tagged with the
 // call's epoch so the scratch never needs clearing; the epoch lives in device
 // memory and the last copy workgroup advances it, so a captured graph replays
-// correctly).  Block 0 also zeroes the queued counters and the status words
-// of the nodes this call reports.
+// correctly).  Block 0 also zeroes the chunk counter, the queued counters
+// and the status words of the nodes this call reports.
 __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
 {
     const KvcGatherArgs &a = P.l.a;
@@ -130,7 +127,7 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
     if (blockIdx.x == 0) {
         const uint32_t n0 = x.fused ? 0u : a.myNode;
         const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
-        if (threadIdx.x == 0) *x.listCount = 0u;
+        if (threadIdx.x == 0) *x.chunkNext = 0u;
         for (uint32_t i = threadIdx.x; i < (n1 - n0) * 8u; i += blockDim.x) {
             x.counters[n0 * 8u + i] = 0u;
             x.errs[n0 * 8u + i] = 0u;
@@ -159,39 +156,55 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
     }
 }
 
-// Pass 2: list the winners owned by the node(s) of this call and count the
-// reference's queued rows per (node, status word).  Each wave takes kGroup
-// chunks of 64 positions at a time and appends their rows with one atomic;
-// counts are summed per workgroup in LDS and flushed once.
-__global__ __launch_bounds__(256) void kvx_gather_list(GatherParams P)
+// Pass 2: each workgroup claims kSpan consecutive positions at a time (a
+// counter the first pass zeroes), lists the winners owned by the node(s) of
+// this call in LDS while counting the queued rows per (node, status word),
+// and moves them with its four waves; no row list passes through HBM.
+// kSpanBlocks workgroups: fewer concurrent readers of host memory move more
+// bytes per second over the link than one workgroup per chunk, and claiming
+// chunks keeps them evenly loaded.  The last workgroup (ticket) advances the
+// epoch and stores the status words.
+constexpr uint32_t kSpan = 256;
+constexpr uint32_t kSpanBlocks = 64;
+
+__global__ __launch_bounds__(256) void kvx_gather_span(GatherParams P)
 {
     __shared__ uint32_t sCnt[64 * 8];
+    __shared__ uint64_t sSrc[kSpan], sDst[kSpan];
+    __shared__ uint32_t sN, sEpoch, sChunk;
+    __shared__ int sLast;
     const KvcGatherArgs &a = P.l.a;
     const GatherExtra &x = P.x;
-    const int wave = threadIdx.x / 64;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid / 64u;
     const uint32_t lane = static_cast<uint32_t>(lane_id());
+    const uint32_t cpr = a.rowBytes / 16u;
     const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
     const int64_t total = static_cast<int64_t>(numReal) * a.topK;
+    const int64_t chunks = (total + kSpan - 1) / kSpan;
+    const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
     const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
     const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
     const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
     const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
     const int64_t *hostBase = reinterpret_cast<const int64_t *>(a.reqHostBase);
-    const unsigned long long tagHi = static_cast<unsigned long long>(*x.epoch) << 32;
-    const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
-    for (uint32_t i = threadIdx.x; i < 64u * 8u; i += blockDim.x) sCnt[i] = 0u;
+    for (uint32_t i = tid; i < 64u * 8u; i += blockDim.x) sCnt[i] = 0u;
+    if (tid == 0) sEpoch = *x.epoch;
     __syncthreads();
-
-    const int64_t chunks = (total + 63) / 64;
-    const int64_t waves = static_cast<int64_t>(gridDim.x) * kWaves;
-    for (int64_t g0 = static_cast<int64_t>(blockIdx.x) * kWaves + wave; g0 < chunks; g0 += waves * kGroup) {
-        uint64_t src[kGroup], dst[kGroup], cm[kGroup];
-        uint32_t nAll = 0;
+    const unsigned long long tagHi = static_cast<unsigned long long>(sEpoch) << 32;
+    for (;;) {
+        if (tid == 0) {
+            sN = 0u;
+            sChunk = atomicAdd(x.chunkNext, 1u);
+        }
+        __syncthreads();
+        const int64_t chunk = sChunk;
+        if (chunk >= chunks) break;
 #pragma unroll
-        for (int j = 0; j < kGroup; ++j) {
-            const int64_t p = (g0 + j * waves) * 64 + lane;
+        for (uint32_t q = 0; q < kSpan / 256u; ++q) {
+            const int64_t p = chunk * kSpan + q * 256u + tid;
             bool copy = false;
-            src[j] = dst[j] = 0;
+            uint64_t src = 0, dst = 0;
             if (p < total && miss[p] != 0) {
                 const int32_t t = topk[p], s = slots[p];
                 const int64_t bid = p / a.topK;
@@ -207,67 +220,41 @@ __global__ __launch_bounds__(256) void kvx_gather_list(GatherParams P)
                             const uint64_t d = win_index(bid, s, x.spanRows);
                             if (d < x.winEntries) winner = (x.win[d] == (tagHi | static_cast<unsigned long long>(p)));
                         }
-                        const uint64_t segBase = x.fused ? x.segBases[node] : a.segBase;
                         const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
                         if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
                             atomicCAS(&x.errs[key], 0u, row_error_code(static_cast<uint64_t>(p)));
                             winner = false;
                         }
                         copy = winner;
-                        src[j] = segBase + (static_cast<uint64_t>(a.layerOffsetRows) + segRow) * a.rowBytes;
-                        dst[j] = a.hotRowBase + (static_cast<uint64_t>(s) +
-                                                 static_cast<uint64_t>(bid) * a.hotReqStrideRows) * a.rowBytes;
+                        const uint64_t segBase = x.fused ? x.segBases[node] : a.segBase;
+                        src = segBase + (static_cast<uint64_t>(a.layerOffsetRows) + segRow) * a.rowBytes;
+                        dst = a.hotRowBase +
+                              (static_cast<uint64_t>(s) + static_cast<uint64_t>(bid) * a.hotReqStrideRows) * a.rowBytes;
                     }
                 }
             }
-            cm[j] = __ballot(copy);
-            nAll += static_cast<uint32_t>(__popcll(cm[j]));
-        }
-        if (nAll == 0) continue;
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(x.listCount, nAll);
-        base = __shfl(base, 0);
-#pragma unroll
-        for (int j = 0; j < kGroup; ++j) {
-            if ((cm[j] >> lane) & 1ull) {
-                const uint32_t at = base + static_cast<uint32_t>(__popcll(cm[j] & ((1ull << lane) - 1ull)));
-                x.listSrc[at] = src[j];
-                x.listDst[at] = dst[j];
+            const uint64_t cm = __ballot(copy);
+            uint32_t base = 0;
+            if (lane == 0 && cm != 0ull) base = atomicAdd(&sN, static_cast<uint32_t>(__popcll(cm)));
+            base = static_cast<uint32_t>(__shfl(static_cast<int>(base), 0));
+            if (copy) {
+                const uint32_t at = base + static_cast<uint32_t>(__popcll(cm & ((1ull << lane) - 1ull)));
+                sSrc[at] = src;
+                sDst[at] = dst;
             }
-            base += static_cast<uint32_t>(__popcll(cm[j]));
         }
+        __syncthreads();
+        const uint32_t n = sN, share = (n + kWaves - 1u) / kWaves, r0 = wave * share;
+        if (r0 < n) wave_copy_rows(sSrc + r0, sDst + r0, (n - r0 < share) ? n - r0 : share, cpr);
+        __syncthreads();  // the list and the chunk are rewritten by the next round
     }
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < 64u * 8u; i += blockDim.x) {
+    for (uint32_t i = tid; i < 64u * 8u; i += blockDim.x) {
         if (sCnt[i] != 0u) atomicAdd(&x.counters[i], sCnt[i]);
-    }
-}
-
-// Pass 3: move the listed rows, 64 per wave task; the last workgroup reports.
-__global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
-{
-    __shared__ int sLast;
-    const KvcGatherArgs &a = P.l.a;
-    const GatherExtra &x = P.x;
-    const int wave = threadIdx.x / 64;
-    const uint32_t cpr = a.rowBytes / 16u;
-    const uint32_t n = *x.listCount;
-    const int32_t numReal = clamp_num_real(a.numReal, a.maxNumReqs);
-    const int64_t total = static_cast<int64_t>(numReal) * a.topK;
-    const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
-    // tasks of up to 64 rows, smaller when the list is short so that every
-    // wave of the grid has rows in flight
-    const uint32_t waves = gridDim.x * kWaves;
-    uint32_t task = (n + waves - 1u) / waves;
-    task = task < 1u ? 1u : (task > 64u ? 64u : task);
-    for (uint32_t r0 = (blockIdx.x * kWaves + wave) * task; r0 < n; r0 += waves * task) {
-        const uint32_t nr = (n - r0 < task) ? n - r0 : task;
-        wave_copy_rows(x.listSrc + r0, x.listDst + r0, nr, cpr);
     }
 
     __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         const unsigned int ticket = atomicInc(&x.tickets[0], gridDim.x - 1u);
         sLast = (ticket == gridDim.x - 1u) ? 1 : 0;
     }
@@ -275,18 +262,15 @@ __global__ __launch_bounds__(256) void kvx_gather_copy(GatherParams P)
     if (!sLast) return;
     // the next call's epoch; at the wrap to 0 the tags of 2^32 calls ago
     // could alias, so the table is cleared (once in 2^32 calls)
-    __shared__ uint32_t sEpoch;
-    if (threadIdx.x == 0) sEpoch = *x.epoch + 1u;
-    __syncthreads();
-    if (sEpoch == 0u) {
-        for (uint64_t i = threadIdx.x; i < x.winEntries; i += blockDim.x) x.win[i] = 0ull;
+    if (sEpoch + 1u == 0u) {
+        for (uint64_t i = tid; i < x.winEntries; i += blockDim.x) x.win[i] = 0ull;
     }
-    if (threadIdx.x == 0) *x.epoch = sEpoch;
+    if (tid == 0) *x.epoch = sEpoch + 1u;
     if (a.status == 0) return;
     __threadfence();
     const uint32_t n0 = x.fused ? 0u : a.myNode;
     const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
-    for (uint32_t i = threadIdx.x; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
+    for (uint32_t i = tid; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
         const uint32_t node = n0 + i / x.statusWords, b = i % x.statusWords;
         uint64_t word = 1ull << 32;  // kvc_gather_rows.cpp:29-33, :93
         if (static_cast<int64_t>(b * ppc) < total) {
@@ -737,9 +721,7 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     }
     P.x.win = scr.win;
     P.x.winEntries = scr.winEntries;
-    P.x.listSrc = scr.listSrc;
-    P.x.listDst = scr.listDst;
-    P.x.listCount = scr.listCount;
+    P.x.chunkNext = scr.chunkNext;
     P.x.counters = scr.counters;
     P.x.errs = scr.errs;
     P.x.tickets = scr.tickets;
@@ -759,17 +741,9 @@ hipError_t launch_gather(const GatherPlan &plan, const RowScratch &scr, uint64_t
     hipLaunchKernelGGL(kvx_gather_prep, dim3(static_cast<uint32_t>(prepBlocks)), dim3(256), 0, stream, P);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    uint64_t listBlocks = (positions + 64ull * kWaves * kGroup - 1ull) / (64ull * kWaves * kGroup);
-    if (listBlocks < 1) listBlocks = 1;
-    if (listBlocks > 1024) listBlocks = 1024;
-    hipLaunchKernelGGL(kvx_gather_list, dim3(static_cast<uint32_t>(listBlocks)), dim3(256), 0, stream, P);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    // grid-stride row tasks; 512 waves keep enough 16-byte reads in flight
-    // for the host link (and give a short list one row per wave: one host
-    // round trip), few workgroups keep the completion ticket cheap
-    const uint64_t copyBlocks = 128;
-    hipLaunchKernelGGL(kvx_gather_copy, dim3(static_cast<uint32_t>(copyBlocks)), dim3(256), 0, stream, P);
+    uint64_t spanBlocks = (positions + kSpan - 1ull) / kSpan;
+    if (spanBlocks > kSpanBlocks) spanBlocks = kSpanBlocks;
+    hipLaunchKernelGGL(kvx_gather_span, dim3(static_cast<uint32_t>(spanBlocks)), dim3(256), 0, stream, P);
     return hipGetLastError();
 }
 

@@ -98,9 +98,9 @@ def test_import_all_noalloc_matches_import_all(kvops):
                 assert read_words(sb + s * 64, 2) == want, (call, s)
             assert torch.equal(hot_a, hot_b), call
             assert torch.equal(hot_b, torch.from_numpy(hot_o).cuda()), call
-        # beyond the fixed scratch: 300 x 2048 positions > 524288
+        # beyond the fixed scratch: more winner rows than its 2228224 (checked before any launch)
         before = hot_b.clone()
-        big = 300
+        big = (2228224 - 65536) // min(padded, 65536) + 2
         rc = _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_b, top_k, big, sb, padded)
         assert rc != 0 and b"must fit the fixed scratch" in lib.kvx_last_error()
         torch.cuda.synchronize()
