@@ -118,6 +118,60 @@ def test_gather_parity_after_sieve(kvops, stride_mode, fused):
         pool.destroy(close_ext=False)
 
 
+@pytest.mark.parametrize("req,top_k,num_real,S,N,stride_mode,fused,block_dim", [
+    (3, 1500, 2, 1, 2, "padded", True, 3),    # 4500 positions: 18 chunks, the last one partial
+    (3, 1500, 3, 64, 4, "zero", False, 2),    # stride 0: requests collide on hot rows
+    (5, 4096, 5, 1, 3, "padded", True, 8),    # 80 chunks over the 64 workgroups
+    (2, 2049, 1, 1, 1, "zero", True, 1),      # 4098 positions: just past the one-launch form
+])
+def test_gather_large_batch_parity(kvops, req, top_k, num_real, S, N, stride_mode, fused, block_dim):
+    """The large-batch import (winner tags, then workgroups claiming chunks of
+    positions) against the oracle on constructed inputs: duplicate and
+    colliding destinations (the last valid miss wins), invalid tokens and
+    slots, a request without a pool row, num_real below max_num_reqs, partial
+    chunks; every hot byte and every node's status words."""
+    print("large import case", req, top_k, num_real, S, N, stride_mode, fused, block_dim, flush=True)
+    L, layer, prefill, dbs = 2, 1, 4096, 2048
+    padded = (dbs + 15) // 16 * 16
+    layer_rows = req * prefill
+    pool = HostSegPool(0, L, layer_rows, ROW, stripe_rows=S, node_num=N)
+    pool.create_pool()
+    try:
+        rng = np.random.default_rng(req * 100 + top_k + S + N)
+        views = pool.segment_views()
+        for v in views:
+            v[...] = rng.integers(0, 256, size=v.shape, dtype=np.uint8)
+        segs = [v.reshape(-1) for v in views]
+        topk = rng.integers(0, prefill, size=(req, top_k)).astype(np.int32)
+        topk[rng.random((req, top_k)) < 0.03] = -1
+        slots = rng.integers(0, dbs, size=(req, top_k)).astype(np.int32)
+        slots[rng.random((req, top_k)) < 0.02] = -1
+        miss = (rng.random((req, top_k)) < 0.5).astype(np.int8)
+        pool_idx = np.arange(req, dtype=np.int64)
+        if req >= 3:
+            pool_idx[1] = -1
+        host_base = np.arange(req, dtype=np.int64) * prefill
+        stride = padded if stride_mode == "padded" else 0
+        hot_rows = req * padded if stride else padded
+        hot_np = rng.integers(0, 256, size=(hot_rows, ROW), dtype=np.uint8)
+        hot = torch.from_numpy(hot_np.copy()).cuda()
+        args = (layer, to_dev(topk), to_dev(pool_idx), to_dev(host_base), to_dev(slots), to_dev(miss),
+                to_dev(np.array([num_real], dtype=np.int32)), hot, req, top_k)
+        read = pool.batch_read_fused if fused else pool.batch_read
+        status = read(*args, block_dim=block_dim, hot_req_stride_rows=stride)
+        pool.wait(status, block_dim=block_dim)
+        torch.cuda.synchronize()
+        plsr = pool.per_layer_seg_rows
+        for s in range(N):
+            _, words = orc.gather_rows(segs, hot_np.reshape(-1), layer * plsr, ROW, topk, pool_idx, host_base, slots,
+                                       miss, num_real, top_k, req, S, N, s, hot_req_stride_rows=stride,
+                                       block_dim=block_dim)
+            assert _read_words(status + s * 64, block_dim) == [int(w) for w in words], s
+        np.testing.assert_array_equal(hot.cpu().numpy(), hot_np)
+    finally:
+        pool.destroy(close_ext=False)
+
+
 def test_status_poll_and_timeout(kvops):
     st = kvops.alloc_status(4)
     # nothing launched: the slot stays pending and the poll times out
