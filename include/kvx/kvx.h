@@ -190,6 +190,18 @@ const char *kvx_last_error(void);
 int kvx_host_alloc(uint64_t bytes, uint32_t flags, uint64_t *out_addr);
 int kvx_host_free(uint64_t addr);
 
+/* Placement of host segments (the reference's daemon maps anonymous memory
+ * wherever the kernel puts it, ems/emsd/pool_mgr.cc:23-41).
+ * kvx_gpu_numa_node: the NUMA node of the GPU's PCI function as the
+ * platform reports it (sysfs), -1 when it reports none.
+ * kvx_host_alloc_node: kvx_host_alloc with the pages bound to `node` (the
+ * calling thread's memory policy is set to that node while the runtime
+ * allocates and pins them, then restored); node < 0 = no binding.
+ * *out_page_node (may be null) receives the node the first page landed on,
+ * -1 if the system cannot say.  Free with kvx_host_free. */
+int kvx_gpu_numa_node(int32_t device_id, int32_t *out_node);
+int kvx_host_alloc_node(uint64_t bytes, uint32_t flags, int32_t node, uint64_t *out_addr, int32_t *out_page_node);
+
 /* Value of the device tail-slot word (0 = no kernel hit a bound); reading it
  * synchronises the device.  kvx_clear_overflow() zeroes it. */
 int kvx_read_overflow(uint64_t *out_value);

@@ -197,6 +197,23 @@ PYBIND11_MODULE(_kvops, m)
         },
         py::arg("nbytes"), py::arg("coherent") = false);
     m.def("host_free", [](uint64_t addr) { Check(kvx_host_free(addr)); }, py::arg("addr"));
+    m.def(
+        "host_alloc_node",
+        [](uint64_t nbytes, bool coherent, int32_t node) {
+            uint64_t addr = 0;
+            int32_t pageNode = -1;
+            Check(kvx_host_alloc_node(nbytes, coherent ? 1u : 0u, node, &addr, &pageNode));
+            return py::make_tuple(addr, pageNode);
+        },
+        py::arg("nbytes"), py::arg("coherent") = false, py::arg("node") = -1);
+    m.def(
+        "gpu_numa_node",
+        [](int32_t device_id) {
+            int32_t node = -1;
+            Check(kvx_gpu_numa_node(device_id, &node));
+            return node;
+        },
+        py::arg("device_id") = 0);
     m.def("read_overflow", []() {
         uint64_t v = 0;
         Check(kvx_read_overflow(&v));

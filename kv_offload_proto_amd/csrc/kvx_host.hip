@@ -4,11 +4,18 @@
 // Ascend fatbin loading chain is replaced by kernels linked into this library.
 #include <hip/hip_runtime.h>
 
+#include <linux/mempolicy.h>
+#include <sys/syscall.h>
+#include <unistd.h>
+
 #include <algorithm>
 #include <atomic>
+#include <cerrno>
+#include <cctype>
 #include <chrono>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 #include <map>
 #include <mutex>
 #include <stdexcept>
@@ -445,6 +452,31 @@ void DoExportRows(const uint64_t *segBases, bool fused, uint32_t layer_id, uint3
     }
     hipCheck(kvx::launch_export_rows(a, segBases, scr, AsStream(stream)), "export_rows launch");
 }
+
+// Node masks for the memory-policy system calls: up to 1024 nodes (the
+// kernel's usual limit); maxnode counts one past the mask's bits, as the
+// kernel expects.
+constexpr unsigned long kMaskBits = 1024;
+constexpr unsigned long kMaskWords = kMaskBits / (8 * sizeof(unsigned long));
+
+long GetPolicy(int *mode, unsigned long *mask, void *addr, unsigned long flags)
+{
+    return syscall(SYS_get_mempolicy, mode, mask, mask == nullptr ? 0ul : kMaskBits + 1, addr, flags);
+}
+
+long SetPolicy(int mode, const unsigned long *mask)
+{
+    return syscall(SYS_set_mempolicy, mode, mask, mask == nullptr ? 0ul : kMaskBits + 1);
+}
+
+// Node holding the page at addr (-1 when the system cannot say).
+int32_t PageNode(const void *addr)
+{
+    int node = -1;
+    if (GetPolicy(&node, nullptr, const_cast<void *>(addr), MPOL_F_NODE | MPOL_F_ADDR) != 0) return -1;
+    return node;
+}
+
 
 }  // namespace
 
@@ -963,6 +995,69 @@ int kvx_host_alloc(uint64_t bytes, uint32_t flags, uint64_t *out_addr)
         std::lock_guard<std::mutex> lk(g_hostMu);
         g_hostAllocs[reinterpret_cast<uint64_t>(p)] = bytes;
         *out_addr = reinterpret_cast<uint64_t>(p);
+    });
+}
+
+int kvx_gpu_numa_node(int32_t device_id, int32_t *out_node)
+{
+    return Guarded([&] {
+        if (out_node == nullptr) throw Error("gpu_numa_node: out_node is null");
+        char bus[64] = {0};
+        hipCheck(hipDeviceGetPCIBusId(bus, sizeof(bus), device_id), "hipDeviceGetPCIBusId");
+        std::string id(bus);
+        for (char &c : id) c = static_cast<char>(std::tolower(static_cast<unsigned char>(c)));
+        std::ifstream f("/sys/bus/pci/devices/" + id + "/numa_node");
+        int n = -1;
+        if (!(f >> n)) n = -1;
+        *out_node = n < 0 ? -1 : n;
+    });
+}
+
+int kvx_host_alloc_node(uint64_t bytes, uint32_t flags, int32_t node, uint64_t *out_addr, int32_t *out_page_node)
+{
+    return Guarded([&] {
+        if (node < 0) {
+            const int rc = kvx_host_alloc(bytes, flags, out_addr);
+            if (rc != 0) throw Error(kvx_last_error());
+            if (out_page_node != nullptr) *out_page_node = PageNode(reinterpret_cast<void *>(*out_addr));
+            return;
+        }
+        if (bytes == 0) throw Error("host_alloc: bytes must be > 0");
+        if (static_cast<unsigned long>(node) >= kMaskBits) throw Error("host_alloc: node must be below 1024");
+        // bind this thread's allocations to the node while the runtime
+        // allocates and pins the pages, then restore its previous policy
+        int prevMode = MPOL_DEFAULT;
+        unsigned long prevMask[kMaskWords] = {0};
+        if (GetPolicy(&prevMode, prevMask, nullptr, 0) != 0) {
+            throw Error(std::string("host_alloc: get_mempolicy failed: ") + std::strerror(errno));
+        }
+        unsigned long mask[kMaskWords] = {0};
+        mask[node / (8 * sizeof(unsigned long))] = 1ul << (node % (8 * sizeof(unsigned long)));
+        if (SetPolicy(MPOL_BIND, mask) != 0) {
+            throw Error("host_alloc: node " + std::to_string(node) + " is not available (set_mempolicy: " +
+                        std::strerror(errno) + ")");
+        }
+        const unsigned f = hipHostMallocMapped | hipHostMallocNumaUser |
+                           (flags == 1 ? hipHostMallocCoherent : hipHostMallocNonCoherent);
+        void *p = nullptr;
+        const hipError_t e = hipHostMalloc(&p, bytes, f);
+        const bool restored = SetPolicy(prevMode, prevMode == MPOL_DEFAULT ? nullptr : prevMask) == 0;
+        if (e != hipSuccess || p == nullptr) {
+            throw Error("host_alloc: hipHostMalloc of " + std::to_string(bytes) + " bytes on node " +
+                        std::to_string(node) + " failed: " + hipGetErrorString(e));
+        }
+        void *d = nullptr;
+        if (!restored || hipHostGetDevicePointer(&d, p, 0) != hipSuccess || d != p) {
+            (void)hipHostFree(p);
+            throw Error(restored ? "host_alloc: device address differs from host address"
+                                 : "host_alloc: could not restore the thread's memory policy");
+        }
+        {
+            std::lock_guard<std::mutex> lk(g_hostMu);
+            g_hostAllocs[reinterpret_cast<uint64_t>(p)] = bytes;
+        }
+        *out_addr = reinterpret_cast<uint64_t>(p);
+        if (out_page_node != nullptr) *out_page_node = PageNode(p);
     });
 }
 

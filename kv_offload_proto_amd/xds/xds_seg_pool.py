@@ -126,22 +126,38 @@ class HostSegPool:
 
     ``coherent`` selects fine-grained (coherent) pinned memory; the default is
     coarse-grained, the faster mode for bulk GPU reads/writes over the link.
+
+    ``placement`` chooses the NUMA node of the segments' pages: ``"device"``
+    (default) binds them to the GPU's node when the platform reports one and
+    leaves them unbound otherwise, ``"none"`` never binds, an int binds to
+    that node.  The reference's daemon maps anonymous memory with no
+    placement (ems/emsd/pool_mgr.cc:23-41); a segment far from the GPU's
+    socket crosses the inter-socket link on every import.  After
+    ``create_pool``, ``placement_node`` is the node bound (-1: none) and
+    ``segment_nodes`` the node each segment's first page landed on (-1:
+    unknown).
     """
 
     def __init__(self, device_id: int, layer_num: int, layer_rows: int, row_bytes: int, stripe_rows: int = 1,
-                 node_num: int = 2, coherent: bool = False):
+                 node_num: int = 2, coherent: bool = False, placement="device"):
         if layer_num < 1 or layer_rows < 1 or row_bytes <= 0 or row_bytes % 128 != 0:
             raise ValueError("invalid pool dims: L={} rows={} rowBytes={}".format(layer_num, layer_rows, row_bytes))
         if node_num < 1 or node_num > 64:
             raise ValueError("node_num must be in [1, 64], got {}".format(node_num))
         if stripe_rows < 1:
             raise ValueError("stripe_rows must be >= 1")
+        if not (placement in ("device", "none") or (isinstance(placement, int) and not isinstance(placement, bool)
+                                                     and 0 <= placement < 1024)):
+            raise ValueError("placement must be 'device', 'none' or a node in [0, 1024), got {!r}".format(placement))
         self.device_id = device_id
         self.layer_num = layer_num
         self.layer_rows = layer_rows
         self.row_bytes = row_bytes
         self.stripe_rows = stripe_rows
         self.coherent = coherent
+        self.placement = placement
+        self.placement_node = -1
+        self.segment_nodes: List[int] = []
         self._node_num_cfg = node_num
         self.pool: Optional[PoolInfo] = None
         self.node_num = 0
@@ -162,15 +178,25 @@ class HostSegPool:
         seg_bytes = self.layer_num * self.per_layer_seg_rows * self.row_bytes
         if ems_size_bytes is not None and ems_size_bytes < self.layer_num * self.layer_rows * self.row_bytes:
             raise ValueError("ems_size_bytes smaller than layer_num*layer_rows*row_bytes")
-        segs = []
+        if self.placement == "none":
+            node = -1
+        elif self.placement == "device":
+            node = _kvops.gpu_numa_node(self.device_id)
+        else:
+            node = self.placement
+        segs, nodes = [], []
         try:
             for s in range(n):
-                segs.append(Segment(s, _kvops.host_alloc(seg_bytes, self.coherent), seg_bytes))
+                addr, page_node = _kvops.host_alloc_node(seg_bytes, self.coherent, node)
+                segs.append(Segment(s, addr, seg_bytes))
+                nodes.append(page_node)
         except Exception:
             for sg in segs:
                 _kvops.host_free(sg.seg_base)
             raise
         self.pool = PoolInfo(segs)
+        self.placement_node = node
+        self.segment_nodes = nodes
         self.channels = list(range(n))
         try:
             _kvops.init(self.device_id, fatbin_path)

@@ -81,7 +81,7 @@ def test_libkvx_exports_every_declared_symbol():
 
     lib = ctypes.CDLL(lib_path())
     syms = _declared_symbols()
-    assert len(syms) == 23, syms
+    assert len(syms) == 25, syms
     missing = [s for s in syms if not hasattr(lib, s)]
     assert missing == []
 

@@ -115,3 +115,15 @@ def test_adversarial_pool_collides():
     assert len(pool) > 0
     h = (pool.astype(np.uint64) * np.uint64(2654435761) % np.uint64(1 << 32)) >> np.uint64(16)
     assert (h < 4096).all()
+
+
+@pytest.mark.parametrize("bad", ["gpu", -1, 1024, 1.0, True, None])
+def test_pool_placement_argument(bad):
+    """placement is 'device', 'none' or a node number below 1024; anything
+    else is refused when the pool is configured, before any memory is taken."""
+    from kv_offload_proto_amd.xds.xds_seg_pool import HostSegPool
+
+    for ok in ("device", "none", 0, 3):
+        assert HostSegPool(0, 1, 64, 1152, placement=ok).placement == ok
+    with pytest.raises(ValueError, match="placement"):
+        HostSegPool(0, 1, 64, 1152, placement=bad)
