@@ -938,13 +938,23 @@ int kvx_sieve_ht_init(uint64_t device_buffer_tokens, uint64_t device_buffer_ht, 
         a.paddedBufferSize = padded_buffer_size;
         a.htSize = ht_size;
         if (static_cast<uint64_t>(num_reqs) * layer_num == 0) return;
-        // the parallel build when its LDS form fits, else one lane per table
-        // on the table in LDS or in HBM
+        // the parallel build when its LDS form fits, else the batched wave
+        // build (larger tables), else one lane per table on the table in LDS
+        // or in HBM
         const size_t ldsPar = kvx::sieve_ht_init_par_lds(ht_size, device_buffer_size);
-        const bool parallel = ldsPar != 0 && ldsPar <= g.ldsLimit;
-        const size_t lds = parallel ? ldsPar : static_cast<size_t>(ht_size) * 2;
-        hipCheck(kvx::launch_sieve_ht_init(a, reinterpret_cast<uint64_t>(g.overflow),
-                                           parallel || lds <= g.ldsLimit ? lds : 0, AsStream(stream), parallel),
+        const size_t ldsWave = kvx::sieve_ht_init_wave_lds(ht_size, device_buffer_size);
+        kvx::InitForm form = kvx::InitForm::kInOrder;
+        size_t lds = static_cast<size_t>(ht_size) * 2;
+        if (ldsPar != 0 && ldsPar <= g.ldsLimit) {
+            form = kvx::InitForm::kParallel;
+            lds = ldsPar;
+        } else if (ldsWave != 0 && ldsWave <= g.ldsLimit) {
+            form = kvx::InitForm::kWave;
+            lds = ldsWave;
+        } else if (lds > g.ldsLimit) {
+            lds = 0;
+        }
+        hipCheck(kvx::launch_sieve_ht_init(a, reinterpret_cast<uint64_t>(g.overflow), lds, AsStream(stream), form),
                  "hisp_sieve_ht_init launch");
     });
 }

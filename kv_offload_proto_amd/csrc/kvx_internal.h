@@ -247,11 +247,16 @@ __host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t htSize)
 // Launchers (implemented next to their kernels).
 hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int variant,
                                size_t ldsBytes, hipStream_t stream);
-// parallel: the one-workgroup-per-table parallel build, with ldsBytes =
-// sieve_ht_init_par_lds(htSize, dbs) (0: that form does not apply)
+// Forms of the admission build: kParallel (ldsBytes =
+// sieve_ht_init_par_lds(htSize, dbs)), kWave (ldsBytes =
+// sieve_ht_init_wave_lds(htSize, dbs)), kInOrder (one lane per table; the
+// table in LDS when ldsBytes = 2 htSize, in HBM when 0).  The size functions
+// return 0 where their form does not apply.
+enum class InitForm { kParallel, kWave, kInOrder };
 hipError_t launch_sieve_ht_init(const HispSieveHtInitArgs &a, uint64_t overflowSlot, size_t ldsBytes,
-                                hipStream_t stream, bool parallel);
+                                hipStream_t stream, InitForm form);
 size_t sieve_ht_init_par_lds(uint32_t htSize, uint32_t dbs);
+size_t sieve_ht_init_wave_lds(uint32_t htSize, uint32_t dbs);
 hipError_t sieve_set_lds_limit(size_t bytes);
 hipError_t sieve_fast_set_lds_limit(size_t bytes);
 hipError_t launch_sieve_update_wave(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,

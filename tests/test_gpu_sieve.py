@@ -95,6 +95,62 @@ def test_ht_init_parallel_parity(kvops, dbs, top_k, mode):
     assert kvops.read_overflow() == 0
 
 
+def _wave_rows(rng, st, mode):
+    """Token rows for tables past the parallel form's LDS budget: 'identity'
+    (slot s holds token s, the admission pattern), 'spread' (distinct tokens
+    below 2^20), 'dense' (distinct tokens homed in the lowest quarter: long
+    clusters), 'wrap' (homes in the last 64 cells: clusters across the end),
+    'dups' (repeated tokens) and 'big' (one token at 2^20 or above); the last
+    two take the one-lane inserts."""
+    L, R = st.tokens.shape[:2]
+    H, dbs = st.ht_size, st.dbs
+    st.tokens[:] = -1
+    t = np.arange(0, 1 << 20, dtype=np.int64)
+    h = _home(t, H)
+    cand = {"spread": t, "dense": t[h < H // 4], "wrap": t[h >= H - 64], "big": t, "dups": t}.get(mode)
+    for l in range(L):
+        for r in range(R):
+            n = int(rng.integers(dbs // 2, dbs + 1))
+            if mode == "identity":
+                st.tokens[l, r, :n] = np.arange(n)
+                continue
+            n = min(n, len(cand))
+            vals = rng.choice(cand, size=n, replace=False)
+            if mode == "dups" and n > 8:
+                vals[rng.integers(0, n, size=n // 8)] = vals[rng.integers(0, n, size=n // 8)]
+            if mode == "big" and n > 0:
+                vals[rng.integers(0, n)] = (1 << 20) + int(rng.integers(0, 1000))
+            st.tokens[l, r, rng.choice(dbs, size=n, replace=False)] = vals
+
+
+@pytest.mark.parametrize("mode", ["identity", "spread", "dense", "wrap", "dups", "big"])
+@pytest.mark.parametrize("dbs,top_k", [(16000, 2048), (32768, 2048), (65518, 8192)])
+def test_ht_init_wave_parity(kvops, dbs, top_k, mode):
+    """The admission build for tables past the parallel form's LDS budget
+    (65536, 131072 and 262144 cells: the batched wave build, or the one-lane
+    inserts for repeated or large tokens): every table byte equals the
+    oracle's sequential inserts, rows outside [req_start, req_start+num_reqs)
+    untouched."""
+    import torch
+
+    if mode == "wrap" and dbs != 16000:
+        pytest.skip("homes reach the table's end only in a 65536-cell table")
+    print("ht_init wave case", dbs, top_k, mode, flush=True)
+    rng = np.random.default_rng(dbs + 7 * len(mode))
+    layers, pool = 2, 3
+    st = orc.SieveState(layers, pool, dbs, top_k)
+    _wave_rows(rng, st, mode)
+    dev = DevSieve(st)
+    dev.ht.fill_(77)
+    st.ht[:] = 77
+    orc.sieve_ht_init(st.tokens, st.ht, 1, 2, layers, pool, dbs, st.padded, st.ht_size)
+    kvops.sieve_ht_init(dev.tokens.data_ptr(), dev.ht.data_ptr(), dev.prefill.data_ptr(), 1, 2, layers, pool,
+                        dbs, st.padded, st.ht_size, 0, 0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dev.ht.cpu().numpy().view(np.uint16), st.ht)
+    assert kvops.read_overflow() == 0
+
+
 def test_ht_init_small_table_parity(kvops):
     """A 512-cell table (under the parallel form's 1024): the one-lane build."""
     import torch

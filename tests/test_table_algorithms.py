@@ -11,6 +11,13 @@
   cluster's keys in slot order; equal to the oracle's sequential inserts
   (hisp_sieve_ht_init.cpp:14-60).
 
+* Batched admission build for tables larger than LDS (kvx_sieve_ht_init_wave,
+  csrc/sieve.hip): with distinct tokens, 64 keys at a time; keys whose
+  backlog is zero take their own first free cell at once, the rest sweep the
+  free cells in increasing order, earliest slot first; a batch whose probes
+  could wrap past the table's end inserts its keys one by one.  Equal to the
+  oracle's sequential inserts.
+
 These pin the algorithms (brute force over small tables); the kernels
 themselves are compared with the oracle in the GPU tests.
 """
@@ -183,3 +190,103 @@ def test_parallel_table_build_equals_sequential_inserts(mode):
         want = np.zeros((1, 1, H), dtype=np.uint16)
         orc.sieve_ht_init(tok.reshape(1, 1, padded).copy(), want, 0, 1, 1, 1, dbs, padded, H)
         np.testing.assert_array_equal(_parallel_build(tok, dbs, H), want[0, 0], err_msg="{} {}".format(mode, trial))
+
+
+def _batch_sweep_build(tok, dbs, H, batch=64, cap=4):
+    """Distinct tokens only (the kernel checks that first).  Per batch: each
+    key's first free cell t (table before the batch); with the keys in order
+    of t, the backlog b_k = max(0, b_{k-1} + 1 - D_k), D_k = free cells in
+    [t_{k-1}, t_k) counted up to cap (a smaller count only overstates b); keys
+    with b = 0 take their own t; the others sweep the free cells in
+    increasing order, each cell going to the earliest waiting key whose t is
+    at or before it (a jump goes to the first free cell at or after the next
+    key's t).  With at least as many free cells as keys at or after the last
+    t, nothing runs past the table's end; otherwise, or when a probe wraps,
+    the keys go in one by one."""
+    used = [False] * H
+    ht = [0] * H
+
+    def first_free(x):
+        for c in range(x, H):
+            if not used[c]:
+                return c
+        return -1
+
+    def place(c, s):
+        assert not used[c]
+        used[c], ht[c] = True, s + 1
+
+    for b0 in range(0, dbs, batch):
+        keys = [(s, _knuth_home(int(tok[s]), H)) for s in range(b0, min(b0 + batch, dbs)) if int(tok[s]) >= 0]
+        if not keys:
+            continue
+        targets = [first_free(h) for _, h in keys]
+        n = len(keys)
+        one_by_one = any(t < 0 for t in targets)
+        if not one_by_one:
+            one_by_one = sum(1 for c in range(max(targets), H) if not used[c]) < n
+        if one_by_one:
+            for s, h in keys:
+                c = first_free(h)
+                place(c if c >= 0 else first_free(0), s)
+            continue
+        order = sorted(range(n), key=lambda i: (targets[i], i))
+        st = [targets[i] for i in order]
+        backlog = [0]
+        for r in range(1, n):
+            d = 0
+            if st[r] > st[r - 1]:
+                d, x = 1, st[r - 1]
+                while d < cap:
+                    x = first_free(x + 1)
+                    if x < 0 or x >= st[r]:
+                        break
+                    d += 1
+            backlog.append(max(0, backlog[-1] + 1 - d))
+        for r in range(n):
+            if backlog[r] == 0:
+                place(st[r], keys[order[r]][0])
+        cong = [r for r in range(n) if backlog[r] > 0]
+        waiting, ready, nxt = {order[r] for r in cong}, set(), 0
+        c = first_free(st[cong[0]]) if cong else 0
+        while waiting:
+            while nxt < len(cong) and st[cong[nxt]] <= c:
+                ready.add(order[cong[nxt]])
+                nxt += 1
+            if not ready:
+                c = first_free(st[cong[nxt]])
+                continue
+            i = min(ready)  # the earliest slot
+            ready.discard(i)
+            waiting.discard(i)
+            place(c, keys[i][0])
+            if ready:
+                c = first_free(c + 1)
+    return np.array(ht, dtype=np.uint16)
+
+
+@pytest.mark.parametrize("mode", ["spread", "few_homes", "wrap", "dense"])
+def test_batched_sweep_build_equals_sequential_inserts(mode):
+    rng = np.random.default_rng(100 + len(mode))
+    for trial in range(8):
+        H = int(rng.choice([64, 256, 1024]))
+        dbs = int(rng.integers(1, H - 1))
+        tok = np.full(dbs, -1, dtype=np.int32)
+        n = int(rng.integers(0, dbs + 1))
+        t = np.arange(0, 1 << 20, dtype=np.int64)
+        h = ((t * 2654435761) & 0xFFFFFFFF) >> 16 & (H - 1)
+        if mode == "spread":
+            cand = t
+        elif mode == "few_homes":
+            cand = t[np.isin(h, rng.choice(H, size=3, replace=False))]
+        elif mode == "wrap":
+            cand = t[h >= H - max(4, H // 16)]
+        else:
+            cand = t[h < H // 4]
+        vals = rng.choice(cand, size=min(n, len(cand)), replace=False)
+        tok[rng.choice(dbs, size=len(vals), replace=False)] = vals
+        want = np.zeros((1, 1, H), dtype=np.uint16)
+        orc.sieve_ht_init(tok.reshape(1, 1, dbs).copy(), want, 0, 1, 1, 1, dbs, dbs, H)
+        for batch, cap in ((64, 4), (8, 1), (4, 4)):
+            np.testing.assert_array_equal(_batch_sweep_build(tok, dbs, H, batch, cap), want[0, 0],
+                                          err_msg="{} {} {} {}".format(mode, trial, batch, cap))
