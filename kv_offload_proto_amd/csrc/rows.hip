@@ -25,6 +25,10 @@ constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kUnroll = 8;         // 16-byte chunks in flight per lane
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// 16-byte chunk of device or host memory, addressed in the global address
+// space (global_* instructions: flat ones also count against the LDS wait
+// counter, and the copy loops read their row addresses from LDS)
+typedef __attribute__((address_space(1))) u32x4 GVec;
 
 struct GatherExtra {
     uint64_t segBases[64];
@@ -90,13 +94,13 @@ __device__ __forceinline__ void wave_copy_rows(const uint64_t *src, const uint64
             if (c < total) {
                 const uint32_t r = c / cpr;
                 const uint32_t o = (c - r * cpr) * 16u;
-                v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src[r] + o));
+                v[j] = __builtin_nontemporal_load(reinterpret_cast<const GVec *>(src[r] + o));
                 d[j] = dst[r] + o;
             }
         }
 #pragma unroll
         for (int j = 0; j < kUnroll; ++j) {
-            if (d[j] != 0) __builtin_nontemporal_store(v[j], reinterpret_cast<u32x4 *>(d[j]));
+            if (d[j] != 0) __builtin_nontemporal_store(v[j], reinterpret_cast<GVec *>(d[j]));
         }
     }
 }
