@@ -150,33 +150,33 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 
     int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
     if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
-    int32_t *rs = reinterpret_cast<int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
-    int8_t *rm = reinterpret_cast<int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
+    KVX_GM int32_t *rs = reinterpret_cast<KVX_GM int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
+    KVX_GM int8_t *rm = reinterpret_cast<KVX_GM int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
     if (bid >= numReal) {
-        write_dummy_row(rs, rm, K);
+        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
     const int64_t reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
     if (reqIdx < 0 || reqIdx >= poolSize) {
-        write_dummy_row(rs, rm, K);
+        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
     const int32_t seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
     const int32_t prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
-    const int32_t *rt = reinterpret_cast<const int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
     Row r;
-    r.tok = reinterpret_cast<int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
-    r.vis32 = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(a.deviceBufferVisited) + reqIdx * visStrideB);
-    r.ht = reinterpret_cast<uint16_t *>(a.deviceBufferHt) + reqIdx * H;
-    r.ct = P.shadow + static_cast<int64_t>(bid) * H;
+    r.tok = reinterpret_cast<KVX_GM int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
+    r.vis32 = reinterpret_cast<KVX_GM uint32_t *>(a.deviceBufferVisited + static_cast<uint64_t>(reqIdx) * visStrideB);
+    r.ht = reinterpret_cast<KVX_GM uint16_t *>(a.deviceBufferHt) + reqIdx * H;
+    r.ct = (KVX_GM int32_t *)P.shadow + static_cast<int64_t>(bid) * H;
     r.mask = H - 1;
     r.dbs = dbs;
     r.padded = padded;
-    int32_t *gHand = reinterpret_cast<int32_t *>(a.sieveHand) + reqIdx * kHandStride;
-    uint64_t *vis64 = reinterpret_cast<uint64_t *>(r.vis32);
-    uint32_t *map = P.aux + static_cast<uint64_t>(bid) * P.auxWords;
-    uint32_t *first = map + P.mapCap;
-    uint16_t *homes = reinterpret_cast<uint16_t *>(first + P.mapCap);
+    KVX_GM int32_t *gHand = reinterpret_cast<KVX_GM int32_t *>(a.sieveHand) + reqIdx * kHandStride;
+    KVX_GM uint64_t *vis64 = (KVX_GM uint64_t *)r.vis32;
+    KVX_GM uint32_t *map = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords;
+    KVX_GM uint32_t *first = map + P.mapCap;
+    KVX_GM uint16_t *homes = (KVX_GM uint16_t *)(first + P.mapCap);
     const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
 
     const BatchLayout &y = P.lay;
@@ -336,7 +336,10 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 c = kExt;
                 if (t < prefill) {
                     c = kNotRes;
-                    if (t < mapLim) atomicMax(first + t, static_cast<uint32_t>(K - k));
+                    if (t < mapLim) {
+                        __hip_atomic_fetch_max(first + t, static_cast<uint32_t>(K - k), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
             }
             code[k] = c;
@@ -456,7 +459,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     if (!fast) {
         // the homes too: the whole per-row scratch is zero between launches
         // (a later launch may lay it out for another table size)
-        uint32_t *h32 = reinterpret_cast<uint32_t *>(homes);
+        KVX_GM uint32_t *h32 = (KVX_GM uint32_t *)homes;
         for (int32_t w = tid; w < H / 2; w += BT) h32[w] = 0u;
         // the in-order recurrence on the untouched row
         build_shadow(r);
@@ -707,12 +710,12 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 
     // ---- 5. the new tokens, in position order ----------------------------
     {
-        uint32_t *h32 = reinterpret_cast<uint32_t *>(homes);  // scratch left zero (see above)
+        KVX_GM uint32_t *h32 = (KVX_GM uint32_t *)homes;  // scratch left zero (see above)
         for (int32_t w = tid; w < H / 2; w += BT) h32[w] = 0u;
     }
     for (uint32_t w = tid; w < nCellW; w += BT) {
         uint64_t m = 0ull;
-        const uint32_t *h32 = reinterpret_cast<const uint32_t *>(r.ht + (w << 6));
+        const KVX_GM uint32_t *h32 = (const KVX_GM uint32_t *)(r.ht + (w << 6));
         for (int q = 0; q < 32; ++q) {
             const uint32_t pair = h32[q];
             if ((pair & 0xFFFFu) == 0u) m |= 1ull << (2 * q);

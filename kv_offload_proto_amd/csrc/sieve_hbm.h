@@ -20,11 +20,16 @@ using namespace sieve;
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// HBM pointers carry the global address space, so accesses compile to
+// global_* instructions: flat ones also count against the LDS wait counter,
+// and these kernels interleave table accesses with LDS work.
+#define KVX_GM __attribute__((address_space(1)))
+
 struct Row {
-    uint16_t *ht;
-    int32_t *ct;  // shadow: token of the entry in each cell, -1 for empty
-    int32_t *tok;
-    uint32_t *vis32;
+    KVX_GM uint16_t *ht;
+    KVX_GM int32_t *ct;  // shadow: token of the entry in each cell, -1 for empty
+    KVX_GM int32_t *tok;
+    KVX_GM uint32_t *vis32;
     int32_t mask, dbs, padded;
 };
 
@@ -34,9 +39,23 @@ struct Row {
 // per move: a shift writes only cells behind the window it reads next.
 __device__ __forceinline__ void wave_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup"); }
 
-__device__ __forceinline__ uint16_t ld16(const uint16_t *p) { return *p; }
-__device__ __forceinline__ int32_t ld32(const int32_t *p) { return *p; }
-__device__ __forceinline__ uint32_t ldu32(const uint32_t *p) { return *p; }
+__device__ __forceinline__ uint16_t ld16(const KVX_GM uint16_t *p) { return *p; }
+__device__ __forceinline__ int32_t ld32(const KVX_GM int32_t *p) { return *p; }
+__device__ __forceinline__ uint32_t ldu32(const KVX_GM uint32_t *p) { return *p; }
+// relaxed device-scope atomics (atomicOr / atomicAnd) on global-space words
+__device__ __forceinline__ uint32_t g_or(KVX_GM uint32_t *p, uint32_t v)
+{
+    return __hip_atomic_fetch_or(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t g_and(KVX_GM uint32_t *p, uint32_t v)
+{
+    return __hip_atomic_fetch_and(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// token of the slot an entry names (-1 past the tokens row), as tok_at
+__device__ __forceinline__ int32_t g_tok_at(const KVX_GM int32_t *tok, uint32_t e, int32_t ntok)
+{
+    return (static_cast<int32_t>(e) - 1 < ntok) ? tok[static_cast<int32_t>(e) - 1] : -1;
+}
 
 constexpr int kBatch = 16;  // 64-cell windows loaded together (one memory round trip)
 
@@ -143,15 +162,16 @@ __device__ __forceinline__ void build_shadow(const Row &r)
 {
     for (int32_t c = threadIdx.x; c <= r.mask; c += blockDim.x) {
         const uint16_t e = r.ht[c];
-        r.ct[c] = (e != 0) ? tok_at(r.tok, e, r.padded) : -1;
+        r.ct[c] = (e != 0) ? g_tok_at(r.tok, e, r.padded) : -1;
     }
 }
 
 // The recurrence over every position of the row, run by one wave after the
 // shadow is built: outputs rs/rm, state updated in place, the hand stored in
 // gHand[0] and a bound violation reported to the tail slot.
-static __device__ void recurrence(const Row &r, const int32_t *rt, int32_t *rs, int8_t *rm, int32_t K, int32_t seqLen,
-                           int32_t prefill, int32_t *gHand, uint64_t overflowSlot)
+static __device__ void recurrence(const Row &r, const KVX_GM int32_t *rt, KVX_GM int32_t *rs, KVX_GM int8_t *rm,
+                                  int32_t K, int32_t seqLen, int32_t prefill, KVX_GM int32_t *gHand,
+                                  uint64_t overflowSlot)
 {
     const int32_t dbs = r.dbs;
     const int32_t padded = r.padded;
@@ -180,7 +200,7 @@ static __device__ void recurrence(const Row &r, const int32_t *rt, int32_t *rs, 
                 if (cell < 0) {
                 } else if (found) {
                     slot = static_cast<int32_t>(e) - 1;
-                    if (lane == 0) atomicOr(r.vis32 + (slot >> 5), 1u << (slot & 31));
+                    if (lane == 0) g_or(r.vis32 + (slot >> 5), 1u << (slot & 31));
                     wave_fence();
                 } else {
                     // the hand passes visited slots, clearing them, and stops at the first unvisited one
@@ -191,7 +211,7 @@ static __device__ void recurrence(const Row &r, const int32_t *rt, int32_t *rs, 
                         const bool v = on && ((ldu32(r.vis32 + (s >> 5)) >> (s & 31)) & 1u);
                         const uint64_t unv = __ballot(on && !v);
                         const int f = unv ? __builtin_ctzll(unv) : 64;
-                        if (static_cast<int>(lane) < f && v) atomicAnd(r.vis32 + (s >> 5), ~(1u << (s & 31)));
+                        if (static_cast<int>(lane) < f && v) g_and(r.vis32 + (s >> 5), ~(1u << (s & 31)));
                         // a later window of this sweep reads cleared bits only after a full turn
                         if (base + 2 * width > (base / dbs + 1) * dbs) wave_fence();
                         if (f < 64) h = lane_value(s, f);
@@ -219,7 +239,7 @@ static __device__ void recurrence(const Row &r, const int32_t *rt, int32_t *rs, 
                         }
                         if (lane == 0) {
                             r.tok[h] = tp;
-                            atomicOr(r.vis32 + (h >> 5), 1u << (h & 31));
+                            g_or(r.vis32 + (h >> 5), 1u << (h & 31));
                         }
                         wave_fence();
                         slot = h;

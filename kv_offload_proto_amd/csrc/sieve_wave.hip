@@ -36,29 +36,29 @@ __global__ __launch_bounds__(WT) void kvx_sieve_update_wave(KvxLaunch<HispSieveU
 
     int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
     if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
-    int32_t *rs = reinterpret_cast<int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
-    int8_t *rm = reinterpret_cast<int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
+    KVX_GM int32_t *rs = reinterpret_cast<KVX_GM int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
+    KVX_GM int8_t *rm = reinterpret_cast<KVX_GM int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
     if (bid >= numReal) {
-        write_dummy_row(rs, rm, K);
+        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
     const int64_t reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
     if (reqIdx < 0 || reqIdx >= poolSize) {
-        write_dummy_row(rs, rm, K);
+        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
     const int32_t seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
     const int32_t prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
-    const int32_t *rt = reinterpret_cast<const int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
     Row r;
-    r.tok = reinterpret_cast<int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
-    r.vis32 = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(a.deviceBufferVisited) + reqIdx * visStrideB);
-    r.ht = reinterpret_cast<uint16_t *>(a.deviceBufferHt) + reqIdx * H;
-    r.ct = shadow + static_cast<int64_t>(bid) * H;
+    r.tok = reinterpret_cast<KVX_GM int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
+    r.vis32 = reinterpret_cast<KVX_GM uint32_t *>(a.deviceBufferVisited + static_cast<uint64_t>(reqIdx) * visStrideB);
+    r.ht = reinterpret_cast<KVX_GM uint16_t *>(a.deviceBufferHt) + reqIdx * H;
+    r.ct = (KVX_GM int32_t *)shadow + static_cast<int64_t>(bid) * H;
     r.mask = H - 1;
     r.dbs = dbs;
     r.padded = padded;
-    int32_t *gHand = reinterpret_cast<int32_t *>(a.sieveHand) + reqIdx * kHandStride;
+    KVX_GM int32_t *gHand = reinterpret_cast<KVX_GM int32_t *>(a.sieveHand) + reqIdx * kHandStride;
     build_shadow(r);
     __threadfence_block();
     __syncthreads();
