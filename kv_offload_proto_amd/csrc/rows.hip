@@ -29,6 +29,18 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // space (global_* instructions: flat ones also count against the LDS wait
 // counter, and the copy loops read their row addresses from LDS)
 typedef __attribute__((address_space(1))) u32x4 GVec;
+// device and host memory read through global-space pointers, for the same reason
+#define KVX_G __attribute__((address_space(1)))
+
+// winner tags (the scratch table): relaxed device-scope max and load
+__device__ __forceinline__ void win_max(unsigned long long *p, unsigned long long v)
+{
+    __hip_atomic_fetch_max((KVX_G unsigned long long *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long win_load(const unsigned long long *p)
+{
+    return __hip_atomic_load((const KVX_G unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 struct GatherExtra {
     uint64_t segBases[64];
@@ -143,10 +155,10 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
             }
         }
     }
-    const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
-    const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
-    const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
-    const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
+    const KVX_G int32_t *topk = reinterpret_cast<const KVX_G int32_t *>(a.topkIndices);
+    const KVX_G int32_t *slots = reinterpret_cast<const KVX_G int32_t *>(a.topKDeviceSlots);
+    const KVX_G int8_t *miss = reinterpret_cast<const KVX_G int8_t *>(a.isMiss);
+    const KVX_G int64_t *pool = reinterpret_cast<const KVX_G int64_t *>(a.reqPoolIndices);
     const unsigned long long tagHi = static_cast<unsigned long long>(*x.epoch) << 32;
     for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < total;
          p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -156,7 +168,7 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
         const int64_t bid = p / a.topK;
         if (pool[bid] < 0) continue;
         const uint64_t d = win_index(bid, s, x.spanRows);
-        if (d < x.winEntries) atomicMax(&x.win[d], tagHi | static_cast<unsigned long long>(p));
+        if (d < x.winEntries) win_max(x.win + d, tagHi | static_cast<unsigned long long>(p));
     }
 }
 
@@ -187,11 +199,11 @@ __global__ __launch_bounds__(256) void kvx_gather_span(GatherParams P)
     const int64_t total = static_cast<int64_t>(numReal) * a.topK;
     const int64_t chunks = (total + kSpan - 1) / kSpan;
     const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
-    const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
-    const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
-    const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
-    const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
-    const int64_t *hostBase = reinterpret_cast<const int64_t *>(a.reqHostBase);
+    const KVX_G int32_t *topk = reinterpret_cast<const KVX_G int32_t *>(a.topkIndices);
+    const KVX_G int32_t *slots = reinterpret_cast<const KVX_G int32_t *>(a.topKDeviceSlots);
+    const KVX_G int8_t *miss = reinterpret_cast<const KVX_G int8_t *>(a.isMiss);
+    const KVX_G int64_t *pool = reinterpret_cast<const KVX_G int64_t *>(a.reqPoolIndices);
+    const KVX_G int64_t *hostBase = reinterpret_cast<const KVX_G int64_t *>(a.reqHostBase);
     for (uint32_t i = tid; i < 64u * 8u; i += blockDim.x) sCnt[i] = 0u;
     if (tid == 0) sEpoch = *x.epoch;
     __syncthreads();
@@ -222,7 +234,7 @@ __global__ __launch_bounds__(256) void kvx_gather_span(GatherParams P)
                         bool winner = true;
                         if (s < 65536) {
                             const uint64_t d = win_index(bid, s, x.spanRows);
-                            if (d < x.winEntries) winner = (x.win[d] == (tagHi | static_cast<unsigned long long>(p)));
+                            if (d < x.winEntries) winner = (win_load(x.win + d) == (tagHi | static_cast<unsigned long long>(p)));
                         }
                         const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
                         if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
@@ -311,11 +323,11 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
     const uint32_t n0 = x.fused ? 0u : a.myNode;
     const uint32_t n1 = x.fused ? a.nodeNum : a.myNode + 1u;
     const uint64_t ppc = a.positionsPerCore == 0 ? 1ull : a.positionsPerCore;
-    const int32_t *topk = reinterpret_cast<const int32_t *>(a.topkIndices);
-    const int32_t *slots = reinterpret_cast<const int32_t *>(a.topKDeviceSlots);
-    const int8_t *miss = reinterpret_cast<const int8_t *>(a.isMiss);
-    const int64_t *pool = reinterpret_cast<const int64_t *>(a.reqPoolIndices);
-    const int64_t *hostBase = reinterpret_cast<const int64_t *>(a.reqHostBase);
+    const KVX_G int32_t *topk = reinterpret_cast<const KVX_G int32_t *>(a.topkIndices);
+    const KVX_G int32_t *slots = reinterpret_cast<const KVX_G int32_t *>(a.topKDeviceSlots);
+    const KVX_G int8_t *miss = reinterpret_cast<const KVX_G int8_t *>(a.isMiss);
+    const KVX_G int64_t *pool = reinterpret_cast<const KVX_G int64_t *>(a.reqPoolIndices);
+    const KVX_G int64_t *hostBase = reinterpret_cast<const KVX_G int64_t *>(a.reqHostBase);
     if (blockIdx.x == 0 && a.status != 0) {  // the call's status words read 0 until its rows have landed
         for (uint32_t i = tid; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
             const uint32_t node = n0 + i / x.statusWords, b = i % x.statusWords;
@@ -336,7 +348,7 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
         const int64_t bid = p / a.topK;
         if (pool[bid] < 0) continue;
         const uint64_t d = win_index(bid, s, x.spanRows);
-        if (d < x.winEntries) atomicMax(&x.win[d], tagHi | static_cast<unsigned long long>(p));
+        if (d < x.winEntries) win_max(x.win + d, tagHi | static_cast<unsigned long long>(p));
     }
     __threadfence();
     __syncthreads();
@@ -361,7 +373,7 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
         if (s < 65536) {
             const uint64_t d = win_index(bid, s, x.spanRows);
             if (d < x.winEntries &&
-                __hip_atomic_load(&x.win[d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+                win_load(x.win + d) !=
                     (tagHi | static_cast<unsigned long long>(p))) {
                 continue;
             }
@@ -495,13 +507,13 @@ __global__ __launch_bounds__(256) void kvx_export_rows_prep(ExportRowsParams P)
             if (a.status != 0) store_status(a.status + node * 64ull + b * 8ull, 0ull);
         }
     }
-    const int64_t *idx = reinterpret_cast<const int64_t *>(a.indicesHost);
+    const KVX_G int64_t *idx = reinterpret_cast<const KVX_G int64_t *>(a.indicesHost);
     const unsigned long long tagHi = static_cast<unsigned long long>(*P.epoch) << 32;
     for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         uint32_t node, segRow;
         if (!export_row_target(a, idx[i], node, segRow) || segRow >= a.perLayerSegRows) continue;
         const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
-        if (w < P.winEntries) atomicMax(&P.win[w], tagHi | static_cast<unsigned long long>(i));
+        if (w < P.winEntries) win_max(P.win + w, tagHi | static_cast<unsigned long long>(i));
     }
 }
 
@@ -521,7 +533,7 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
     const int wave = threadIdx.x / 64;
     const uint32_t lane = static_cast<uint32_t>(lane_id());
     const int32_t n = clamp_num_real(a.numReal, a.maxRows);
-    const int64_t *idx = reinterpret_cast<const int64_t *>(a.indicesHost);
+    const KVX_G int64_t *idx = reinterpret_cast<const KVX_G int64_t *>(a.indicesHost);
     const unsigned long long tagHi = static_cast<unsigned long long>(*P.epoch) << 32;
     const uint32_t cpr = a.rowBytes / 16u;
     const uint32_t words = a.statusWords;
@@ -539,7 +551,7 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
                 atomicMin(&P.errs[key], static_cast<uint32_t>(i));
             } else {
                 const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
-                copy = w >= P.winEntries || P.win[w] == (tagHi | static_cast<unsigned long long>(i));
+                copy = w >= P.winEntries || win_load(P.win + w) == (tagHi | static_cast<unsigned long long>(i));
                 src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
                 dst = (a.fused ? P.segBases[node] : a.segBase) +
                       (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;
@@ -605,7 +617,7 @@ __global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
     const int wave = threadIdx.x / 64;
     const uint32_t lane = static_cast<uint32_t>(lane_id());
     const int32_t n = clamp_num_real(a.numReal, a.maxRows);  // <= kExportSmallMax (host)
-    const int64_t *idx = reinterpret_cast<const int64_t *>(a.indicesHost);
+    const KVX_G int64_t *idx = reinterpret_cast<const KVX_G int64_t *>(a.indicesHost);
     const uint32_t cpr = a.rowBytes / 16u;
     const uint32_t words = a.statusWords;
     const uint32_t ppc = (a.maxRows + words - 1u) / words;  // entries per status word
@@ -626,7 +638,7 @@ __global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
         uint32_t node, segRow;
         if (!export_row_target(a, idx[i], node, segRow) || segRow >= a.perLayerSegRows) continue;
         const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
-        if (w < P.winEntries) atomicMax(&P.win[w], tagHi | static_cast<unsigned long long>(i));
+        if (w < P.winEntries) win_max(P.win + w, tagHi | static_cast<unsigned long long>(i));
     }
     __threadfence();
     __syncthreads();
@@ -647,7 +659,7 @@ __global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
             segRow < a.perLayerSegRows) {
             const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
             copy = w >= P.winEntries ||
-                   __hip_atomic_load(&P.win[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   win_load(P.win + w) ==
                        (tagHi | static_cast<unsigned long long>(i));
             src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
             dst = (a.fused ? P.segBases[node] : a.segBase) +
