@@ -123,6 +123,7 @@ def test_gather_parity_after_sieve(kvops, stride_mode, fused):
     (3, 1500, 3, 64, 4, "zero", False, 2),    # stride 0: requests collide on hot rows
     (5, 4096, 5, 1, 3, "padded", True, 8),    # 80 chunks over the 64 workgroups
     (2, 2049, 1, 1, 1, "zero", True, 1),      # 4098 positions: just past the one-launch form
+    (3, 1500, 3, 1, 2, "wide", True, 2),      # stride 70000: winner rows spaced 65536 apart
 ])
 def test_gather_large_batch_parity(kvops, req, top_k, num_real, S, N, stride_mode, fused, block_dim):
     """The large-batch import (winner tags, then workgroups claiming chunks of
@@ -151,8 +152,8 @@ def test_gather_large_batch_parity(kvops, req, top_k, num_real, S, N, stride_mod
         if req >= 3:
             pool_idx[1] = -1
         host_base = np.arange(req, dtype=np.int64) * prefill
-        stride = padded if stride_mode == "padded" else 0
-        hot_rows = req * padded if stride else padded
+        stride = {"padded": padded, "zero": 0, "wide": 70000}[stride_mode]
+        hot_rows = (req - 1) * stride + padded  # the last request's slots end the buffer
         hot_np = rng.integers(0, 256, size=(hot_rows, ROW), dtype=np.uint8)
         hot = torch.from_numpy(hot_np.copy()).cuda()
         args = (layer, to_dev(topk), to_dev(pool_idx), to_dev(host_base), to_dev(slots), to_dev(miss),
