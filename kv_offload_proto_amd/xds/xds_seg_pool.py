@@ -326,7 +326,7 @@ class EmsPool(HostSegPool):
     def __init__(self, master_ip: str, master_port: int, device_id: int, layer_num: int, layer_rows: int,
                  row_bytes: int, stripe_rows: int = 1, acl_lib: str = "libascendcl.so", hcomm_lib: str = "libhcomm.so",
                  rootinfo_path: str = "/etc/hccl_rootinfo.json", timeout_sec: float = 120.0, node_num: int = 2,
-                 coherent: bool = False):
+                 coherent: bool = False, placement="device"):
         super().__init__(device_id, layer_num, layer_rows, row_bytes, stripe_rows=stripe_rows, node_num=node_num,
-                         coherent=coherent)
+                         coherent=coherent, placement=placement)
         self.master = (master_ip, master_port)
