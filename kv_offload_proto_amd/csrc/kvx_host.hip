@@ -502,7 +502,7 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         g.ldsLimit = static_cast<size_t>(lds) - 1024;  // room for the kernels' static LDS (under 1 KiB)
         hipCheck(kvx::sieve_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS)");
         hipCheck(kvx::sieve_fast_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS fast)");
-        g.ldsBatch = static_cast<size_t>(lds) - 6 * 1024;  // the batch kernel keeps ~4.2 KiB of static LDS
+        g.ldsBatch = static_cast<size_t>(lds) - 6 * 1024;  // the batch kernel keeps ~4.7 KiB of static LDS
         hipCheck(kvx::sieve_batch_set_lds_limit(g.ldsBatch), "hipFuncSetAttribute(LDS batch)");
         {
             // the null stream's scratch at a default size, so that callers on

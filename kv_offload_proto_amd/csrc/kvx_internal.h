@@ -35,6 +35,10 @@ __host__ __device__ __forceinline__ uint32_t row_error_code(uint64_t pos)
 
 // Stride of sieve_hand rows in int32 (64 bytes; hisp_kernel_common.h:20-21).
 constexpr int32_t kHandStride = 16;
+// sieve_hand[row][1]: set by the SIEVE kernels that left the row's table
+// consistent with its tokens (every live token findable at its own slot, one
+// entry per live slot); any other writer of the row clears it.
+constexpr int32_t kCanonFlag = 0x4B565843;
 
 // ---------------------------------------------------------------------------
 // Scratch of the row movers.  The library keeps one set per stream (launches
@@ -206,7 +210,7 @@ __host__ __device__ __forceinline__ FastLayout fast_layout_for(uint32_t padded, 
 // kBatchThreads per batch row; LDS holds the row's visited and evicted
 // bitmaps, a bitmap over the table cells, per-position codes and slots, and
 // a stage of table cells; HBM scratch per row holds a token -> slot map and
-// first-occurrence table of kBatchMapCap tokens and a home per table cell.
+// first-occurrence table of kBatchMapCap tokens.
 // ---------------------------------------------------------------------------
 constexpr int kBatchThreads = 1024;
 constexpr int kBatchWaves = kBatchThreads / 64;
@@ -238,10 +242,10 @@ __host__ __device__ __forceinline__ BatchLayout batch_layout(uint32_t dbs, uint3
     return l;
 }
 
-// uint32 words of HBM scratch per row: map, first occurrences, homes (uint16).
-__host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t htSize)
+// uint32 words of HBM scratch per row: map and first occurrences.
+__host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t)
 {
-    return 2ull * kBatchMapCap + htSize / 2u;
+    return 2ull * kBatchMapCap;
 }
 
 // Launchers (implemented next to their kernels).

@@ -8,10 +8,13 @@
 // recurrence (sieve_hbm.h) instead.  Phases:
 //
 //  1. check: a token -> slot map of the row (HBM scratch: every launch leaves
-//     the map, first-occurrence table and homes zeroed) finds duplicate tokens; a scan of the table checks that each
-//     occupied cell names a live slot, no slot twice, every live slot once,
-//     and that no empty cell lies between an entry's home and its cell (so a
-//     probe from the home reaches it); each cell's home is kept for step 4;
+//     the map and first-occurrence table zeroed) finds duplicate tokens; a
+//     scan of the table checks that each occupied cell names a live slot, no
+//     slot twice, every live slot once, and that no empty cell lies between
+//     an entry's home and its cell (so a probe from the home reaches it).  A
+//     row whose consistency flag (sieve_hand[row][1]) is set, which this
+//     kernel and the LDS kernel set when they leave the row consistent, only
+//     has its live tokens and entries counted;
 //  2. decide, on one lane, from LDS only: each position's first occurrence in
 //     the batch and the initial slot of its token are found in parallel
 //     first; a later occurrence hits the first one's slot (without a wrap
@@ -27,12 +30,16 @@
 //     or after its home, if any (its cell then becomes a hole).  The pass
 //     runs 64 cells at a time on one wave: which entries move depends only
 //     on the rightmost hole (an entry moves iff it is at or after its home),
-//     found with ballots to a fixpoint, and the moves then take their holes
-//     in order from a three-level hole bitmap;
+//     found one event at a time with one ballot each.  While the cluster
+//     holds at most 64 holes they sit in the wave's lanes (a mover's hole is
+//     one more ballot); beyond that, in a three-level hole bitmap for the
+//     rest of the cluster.  A window's moves are written after it, in
+//     parallel;
 //  5. the step's new tokens go in in position order, each into the first
 //     empty cell at or after its home (a three-level bitmap of empty cells):
 //     with step 4 this is the table the in-order recurrence leaves, which
-//     equals inserting the live tokens in the order they were inserted.
+//     equals inserting the live tokens in the order they were inserted.  The
+//     row's consistency flag is then set (cleared on the in-order path).
 #include "kvx_internal.h"
 #include "sieve_hbm.h"
 
@@ -48,11 +55,13 @@ constexpr uint32_t kNotRes = 0xFFFFFFFDu;    // position: first occurrence, toke
 constexpr uint32_t kDup = 0x80000000u;       // position: later occurrence of the position in the low bits
 constexpr uint32_t kMissBit = 0x80000000u;   // slotOut: the position was a miss
 constexpr int kCheckUnroll = 8;              // 64-cell loads in flight per lane in the check
+constexpr int kMapUnroll = 8;    // slots whose tokens a lane loads together in the check
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 bytes: eight table cells
 
 struct BatchParams {
     KvxLaunch<HispSieveUpdateArgs> L;
     int32_t *shadow;   // [maxNumReqs][H] table shadow for the in-order fallback
-    uint32_t *aux;     // [maxNumReqs][auxWords]: map [mapCap], first [mapCap], homes [H] u16
+    uint32_t *aux;     // [maxNumReqs][auxWords]: map [mapCap], first [mapCap]
     uint64_t auxWords;
     uint32_t mapCap;
     BatchLayout lay;
@@ -132,7 +141,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t sScan[BT];
-    __shared__ int32_t sBad, sWrap, sLive, sOcc, sNamed, sNdel, sHand, sE0;
+    __shared__ int32_t sBad, sWrap, sLive, sOcc, sNamed, sNdel, sHand, sE0, sTableBad;
 
     const HispSieveUpdateArgs &a = P.L.a;
     const int32_t K = static_cast<int32_t>(a.topK);
@@ -176,7 +185,9 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     KVX_GM uint64_t *vis64 = (KVX_GM uint64_t *)r.vis32;
     KVX_GM uint32_t *map = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords;
     KVX_GM uint32_t *first = map + P.mapCap;
-    KVX_GM uint16_t *homes = (KVX_GM uint16_t *)(first + P.mapCap);
+    // a row this kernel (or the LDS kernel) left consistent: the table scans
+    // of the check are skipped, its live tokens and entries still counted
+    const bool flagged = gHand[1] == kCanonFlag;
     const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
 
     const BatchLayout &y = P.lay;
@@ -203,6 +214,8 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         sOcc = 0;
         sNamed = 0;
         sNdel = 0;
+        sE0 = -1;
+        sTableBad = 0;
     }
     for (uint32_t w = tid; w < nVisW; w += BT) {
         visB[w] = vis64[w];
@@ -212,117 +225,177 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     __syncthreads();
     {
         // the map by plain stores; a token held by two slots is found when
-        // the map is read back below (one of them reads the other's slot)
+        // the map is read back below (one of them reads the other's slot).
+        // kMapUnroll slots' tokens are loaded before any is used (one memory
+        // round trip per group, not per slot).
         int32_t live = 0, bad = 0;
-        for (int32_t s = tid; s < dbs; s += BT) {
-            const int32_t t = r.tok[s];
-            if (t < 0) continue;
-            ++live;
-            if (t >= mapLim) {
-                bad = 1;
-            } else {
-                map[t] = static_cast<uint32_t>(s + 1);
+        for (int32_t s0 = tid; s0 < dbs; s0 += BT * kMapUnroll) {
+            int32_t tv[kMapUnroll];
+#pragma unroll
+            for (int q = 0; q < kMapUnroll; ++q) {
+                const int32_t s = s0 + q * BT;
+                tv[q] = s < dbs ? r.tok[s] : -1;
+            }
+#pragma unroll
+            for (int q = 0; q < kMapUnroll; ++q) {
+                const int32_t t = tv[q];
+                if (t < 0) continue;
+                ++live;
+                if (t >= mapLim) {
+                    bad = 1;
+                } else {
+                    map[t] = static_cast<uint32_t>(s0 + q * BT + 1);
+                }
             }
         }
         if (live) atomicAdd(&sLive, live);
         if (bad) sBad = 1;
     }
-    __syncthreads();
-    {
-        int32_t bad = 0;
-        for (int32_t s = tid; s < dbs; s += BT) {
-            const int32_t t = r.tok[s];
-            if (t >= 0 && t < mapLim && map[t] != static_cast<uint32_t>(s + 1)) bad = 1;
-        }
-        if (bad) sBad = 1;
-    }
-    // The table in one segment per wave, read 64 cells per load, four loads
-    // in flight: first the last empty cell of each segment; then, with the
-    // last empty cell before each segment (cyclic), every occupied cell.
-    const uint32_t wave = static_cast<uint32_t>(tid) >> 6;
-    const uint32_t segCells = static_cast<uint32_t>(H) / kBatchWaves;  // a multiple of 64
-    const uint32_t seg0 = wave * segCells;
-    {
-        int32_t last = -1;
-        for (uint32_t base = seg0; base < seg0 + segCells; base += 64u * kCheckUnroll) {
-            uint16_t e[kCheckUnroll];
-#pragma unroll
-            for (int q = 0; q < kCheckUnroll; ++q) {
-                const uint32_t c = base + 64u * q + lane;
-                e[q] = c < seg0 + segCells ? r.ht[c] : static_cast<uint16_t>(1);
-            }
-#pragma unroll
-            for (int q = 0; q < kCheckUnroll; ++q) {
-                const uint64_t em = __ballot(e[q] == 0);
-                if (em) last = static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(em));
-            }
-        }
-        if (lane == 0) sScan[wave] = last;
-    }
-    __syncthreads();
-    {
-        int32_t lastAll = -1, carry = -1;
-        for (uint32_t w = 0; w < kBatchWaves; ++w) {
-            const int32_t v = sScan[w];
-            if (v >= 0) {
-                lastAll = v;
-                if (w < wave) carry = v;
-            }
-        }
-        if (tid == 0) {
-            sE0 = lastAll;
-            if (lastAll < 0) sBad = 1;  // no empty cell: probes never stop
-        }
-        if (carry < 0) carry = lastAll;  // the probe runs wrap around the table end
-        int32_t occ = 0, bad = 0;
-        uint32_t *named = reinterpret_cast<uint32_t *>(delB);
-        for (uint32_t base = seg0; base < seg0 + segCells; base += 64u * kCheckUnroll) {
-            uint16_t e[kCheckUnroll];
-            int32_t t[kCheckUnroll];
-#pragma unroll
-            for (int q = 0; q < kCheckUnroll; ++q) {
-                const uint32_t c = base + 64u * q + lane;
-                e[q] = c < seg0 + segCells ? r.ht[c] : static_cast<uint16_t>(0);
-            }
-#pragma unroll
-            for (int q = 0; q < kCheckUnroll; ++q) {
-                const int32_t sl = static_cast<int32_t>(e[q]) - 1;
-                t[q] = (e[q] != 0 && sl < dbs) ? r.tok[sl] : -1;
-            }
-#pragma unroll
-            for (int q = 0; q < kCheckUnroll; ++q) {
-                const uint32_t c = base + 64u * q + lane;
-                const uint64_t em = __ballot(e[q] == 0 && c < seg0 + segCells);
-                // the last empty cell at or before this lane's cell
-                const uint64_t upTo = em & (lane == 63 ? ~0ull : ((2ull << lane) - 1ull));
-                const int32_t lastE = upTo ? static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(upTo)) : carry;
-                if (em) carry = static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(em));
-                if (e[q] == 0 || c >= seg0 + segCells) continue;
-                ++occ;
-                const int32_t sl = static_cast<int32_t>(e[q]) - 1;
-                if (sl >= dbs || t[q] < 0) {
-                    bad = 1;  // an entry naming a slot past the buffer or an empty slot
-                    continue;
+    if (!flagged) {
+        __syncthreads();
+        {
+            int32_t bad = 0;
+            for (int32_t s0 = tid; s0 < dbs; s0 += BT * kMapUnroll) {
+                int32_t tv[kMapUnroll];
+                uint32_t mv[kMapUnroll];
+    #pragma unroll
+                for (int q = 0; q < kMapUnroll; ++q) {
+                    const int32_t s = s0 + q * BT;
+                    tv[q] = s < dbs ? r.tok[s] : -1;
                 }
-                atomicOr(named + (sl >> 5), 1u << (sl & 31));  // a slot named twice shows in the count below
-                const uint32_t home = ht_hash(t[q]) & mask;
-                homes[c] = static_cast<uint16_t>(home);
-                // no empty cell in [home, c): the last empty cell before c is
-                // further from c than the home is
-                if (((c - static_cast<uint32_t>(lastE)) & mask) <= ((c - home) & mask)) bad = 1;
+    #pragma unroll
+                for (int q = 0; q < kMapUnroll; ++q) {
+                    const int32_t t = tv[q];
+                    mv[q] = (t >= 0 && t < mapLim) ? map[t] : 0u;
+                }
+    #pragma unroll
+                for (int q = 0; q < kMapUnroll; ++q) {
+                    const int32_t t = tv[q];
+                    if (t >= 0 && t < mapLim && mv[q] != static_cast<uint32_t>(s0 + q * BT + 1)) bad = 1;
+                }
+            }
+            if (bad) sBad = 1;
+        }
+        // The table in one segment per wave, read 64 cells per load, four loads
+        // in flight: first the last empty cell of each segment; then, with the
+        // last empty cell before each segment (cyclic), every occupied cell.
+        const uint32_t wave = static_cast<uint32_t>(tid) >> 6;
+        const uint32_t segCells = static_cast<uint32_t>(H) / kBatchWaves;  // a multiple of 64
+        const uint32_t seg0 = wave * segCells;
+        {
+            int32_t last = -1;
+            for (uint32_t base = seg0; base < seg0 + segCells; base += 64u * kCheckUnroll) {
+                uint16_t e[kCheckUnroll];
+    #pragma unroll
+                for (int q = 0; q < kCheckUnroll; ++q) {
+                    const uint32_t c = base + 64u * q + lane;
+                    e[q] = c < seg0 + segCells ? r.ht[c] : static_cast<uint16_t>(1);
+                }
+    #pragma unroll
+                for (int q = 0; q < kCheckUnroll; ++q) {
+                    const uint64_t em = __ballot(e[q] == 0);
+                    if (em) last = static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(em));
+                }
+            }
+            if (lane == 0) sScan[wave] = last;
+        }
+        __syncthreads();
+        {
+            int32_t lastAll = -1, carry = -1;
+            for (uint32_t w = 0; w < kBatchWaves; ++w) {
+                const int32_t v = sScan[w];
+                if (v >= 0) {
+                    lastAll = v;
+                    if (w < wave) carry = v;
+                }
+            }
+            if (tid == 0) {
+                sE0 = lastAll;
+                if (lastAll < 0) sBad = 1;  // no empty cell: probes never stop
+            }
+            if (carry < 0) carry = lastAll;  // the probe runs wrap around the table end
+            int32_t occ = 0, bad = 0;
+            uint32_t *named = reinterpret_cast<uint32_t *>(delB);
+            for (uint32_t base = seg0; base < seg0 + segCells; base += 64u * kCheckUnroll) {
+                uint16_t e[kCheckUnroll];
+                int32_t t[kCheckUnroll];
+    #pragma unroll
+                for (int q = 0; q < kCheckUnroll; ++q) {
+                    const uint32_t c = base + 64u * q + lane;
+                    e[q] = c < seg0 + segCells ? r.ht[c] : static_cast<uint16_t>(0);
+                }
+    #pragma unroll
+                for (int q = 0; q < kCheckUnroll; ++q) {
+                    const int32_t sl = static_cast<int32_t>(e[q]) - 1;
+                    t[q] = (e[q] != 0 && sl < dbs) ? r.tok[sl] : -1;
+                }
+    #pragma unroll
+                for (int q = 0; q < kCheckUnroll; ++q) {
+                    const uint32_t c = base + 64u * q + lane;
+                    const uint64_t em = __ballot(e[q] == 0 && c < seg0 + segCells);
+                    // the last empty cell at or before this lane's cell
+                    const uint64_t upTo = em & (lane == 63 ? ~0ull : ((2ull << lane) - 1ull));
+                    const int32_t lastE = upTo ? static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(upTo)) : carry;
+                    if (em) carry = static_cast<int32_t>(base + 64u * q + 63u - __builtin_clzll(em));
+                    if (e[q] == 0 || c >= seg0 + segCells) continue;
+                    ++occ;
+                    const int32_t sl = static_cast<int32_t>(e[q]) - 1;
+                    if (sl >= dbs || t[q] < 0) {
+                        bad = 1;  // an entry naming a slot past the buffer or an empty slot
+                        continue;
+                    }
+                    atomicOr(named + (sl >> 5), 1u << (sl & 31));  // a slot named twice shows in the count below
+                    const uint32_t home = ht_hash(t[q]) & mask;
+                    // no empty cell in [home, c): the last empty cell before c is
+                    // further from c than the home is
+                    if (((c - static_cast<uint32_t>(lastE)) & mask) <= ((c - home) & mask)) bad = 1;
+                }
+            }
+            if (occ) atomicAdd(&sOcc, occ);
+            if (bad) sBad = 1;
+        }
+        __syncthreads();
+        {
+            // every occupied cell names a distinct live slot iff the named slots
+            // number as many as the occupied cells (and as the live slots)
+            const uint32_t *named = reinterpret_cast<const uint32_t *>(delB);
+            int32_t cnt = 0;
+            for (int32_t w = tid; w < (dbs + 31) / 32; w += BT) cnt += __builtin_popcount(named[w]);
+            if (cnt) atomicAdd(&sNamed, cnt);
+        }
+    } else {
+        // the entries counted and the last empty cell found, 8 cells a load
+        int32_t occ = 0, last = -1;
+        const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
+        const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(r.ht);
+        for (uint32_t c0 = tid; c0 < nChunk; c0 += BT * kCheckUnroll) {
+            u32x4 v[kCheckUnroll];
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                const uint32_t c = c0 + static_cast<uint32_t>(q) * BT;
+                if (c < nChunk) v[q] = t16[c];
+            }
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                if (c0 + static_cast<uint32_t>(q) * BT >= nChunk) continue;
+                const uint32_t c = (c0 + static_cast<uint32_t>(q) * BT) * 8u;
+                const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const uint32_t lo = w[h] & 0xFFFFu, hi = w[h] >> 16;
+                    occ += (lo != 0u) + (hi != 0u);
+                    if (lo == 0u) last = static_cast<int32_t>(c + 2u * h);
+                    if (hi == 0u) last = static_cast<int32_t>(c + 2u * h + 1u);
+                }
             }
         }
         if (occ) atomicAdd(&sOcc, occ);
-        if (bad) sBad = 1;
-    }
-    __syncthreads();
-    {
-        // every occupied cell names a distinct live slot iff the named slots
-        // number as many as the occupied cells (and as the live slots)
-        const uint32_t *named = reinterpret_cast<const uint32_t *>(delB);
-        int32_t cnt = 0;
-        for (int32_t w = tid; w < (dbs + 31) / 32; w += BT) cnt += __builtin_popcount(named[w]);
-        if (cnt) atomicAdd(&sNamed, cnt);
+        if (last >= 0) atomicMax(&sE0, last);
+        __syncthreads();
+        if (tid == 0) {
+            sNamed = sOcc;
+            if (sE0 < 0) sBad = 1;  // no empty cell: probes never stop
+        }
     }
     __syncthreads();
     const bool canonical = sBad == 0 && sOcc == sLive && sNamed == sOcc;
@@ -457,11 +530,9 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     }
     __syncthreads();  // the cleanup read the initial tokens; phase 3 replaces some
     if (!fast) {
-        // the homes too: the whole per-row scratch is zero between launches
-        // (a later launch may lay it out for another table size)
-        KVX_GM uint32_t *h32 = (KVX_GM uint32_t *)homes;
-        for (int32_t w = tid; w < H / 2; w += BT) h32[w] = 0u;
-        // the in-order recurrence on the untouched row
+        // the in-order recurrence on the untouched row, which the next launch
+        // checks in full
+        if (tid == 0) gHand[1] = 0;
         build_shadow(r);
         __threadfence_block();
         __syncthreads();
@@ -515,6 +586,13 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     // stages the next chunk of cells.
     __shared__ uint32_t sCur, sClusterLo;
     __shared__ int32_t sLeft, sR;
+    // The cluster's holes while they number at most 64: offsets in wave 0's
+    // lanes, increasing with the lane (qmask: the lanes holding one; qend: the
+    // next lane to fill); sQ packs them when the lanes run out.
+    __shared__ uint32_t sQ[64];
+    uint32_t qv = 0u, qend = 0u;
+    uint64_t qmask = 0ull;
+    bool big = false;   // the cluster's holes are in the three-level bitmap instead
     const uint32_t e0 = static_cast<uint32_t>(sE0);
     if (tid == 0) {
         sCur = 1;
@@ -569,8 +647,12 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
             uint32_t v = 0u;
             if (off < chunkEnd) {
                 const uint32_t cell = (e0 + off) & mask;
-                const uint16_t e = r.ht[cell];
-                v = e ? (static_cast<uint32_t>(e) | (static_cast<uint32_t>(homes[cell]) << 16)) : 0u;
+                const uint32_t e = r.ht[cell];
+                // the entry's home from its token (a slot past the buffer only
+                // in a corrupted table: home 0)
+                const uint32_t sl = e - 1u;
+                const int32_t tk = (e != 0u && sl < static_cast<uint32_t>(dbs)) ? r.tok[sl] : 0;
+                v = e ? (e | ((ht_hash(tk) & mask) << 16)) : 0u;
             }
             stage[i] = v;
         }
@@ -582,6 +664,11 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
             uint32_t clusterLo = sClusterLo;
             int32_t left = sLeft;
             uint32_t w0 = chunk;
+            // wave 0's own state: uniform in the wave (the compiler cannot see
+            // that past the branch on the thread index)
+            qmask = uniform64(qmask);
+            qend = static_cast<uint32_t>(uniform32(static_cast<int32_t>(qend)));
+            big = uniform32(big ? 1 : 0) != 0;
             while ((left > 0 || R >= 0) && w0 < chunkEnd && !bad) {
                 if (R < 0) {
                     // between clusters: the next deleted cell inside the chunk
@@ -623,68 +710,100 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 const int f = emptyM ? __builtin_ctzll(emptyM) : 64;  // the cluster ends inside the window
                 const uint64_t active = (f < 64 ? ((1ull << f) - 1ull) : ~0ull) & inMask;
                 const uint64_t D = __ballot(del) & active;
-                // movers: an entry moves iff the rightmost hole before it (the
-                // last event so far) is at or after its home.  An entry right
-                // after an event moves iff it is displaced (home before its
-                // cell), so an event runs on through the displaced entries
-                // after it: each iteration extends the events through those
-                // runs (a segmented OR-scan by doubling) and then adds the
-                // entries whose home reaches back to the last event before them.
-                const uint64_t X = __ballot(occ && !del && homeOff < off) & active;  // displaced entries
-                uint64_t E = D;
-                for (int it = 0; it < 65; ++it) {
-                    uint64_t F = X & ((E << 1) | (R >= 0 && ((X & 1ull) != 0ull) &&
-                                                  static_cast<uint32_t>(R) == w0 - 1u ? 1ull : 0ull));
-                    uint64_t T = X;
-                    for (int d = 1; d < 64; d <<= 1) {
-                        F |= (F << d) & T;
-                        T &= T << d;
-                    }
-                    const uint64_t E1 = E | F;
-                    const uint64_t below = E1 & ((1ull << lane) - 1ull);
-                    const int32_t rcur = below ? static_cast<int32_t>(w0 + 63u - __builtin_clzll(below)) : R;
-                    const bool mv = occ && !del && ((active >> lane) & 1ull) && rcur >= 0 &&
-                                    static_cast<uint32_t>(rcur) >= homeOff;
-                    const uint64_t E2 = E1 | __ballot(mv);
-                    if (E2 == E) break;
-                    E = E2;
-                }
-                // the events in order: a deletion makes a hole; a mover takes
-                // the leftmost hole at or after its home and leaves a hole
-                uint64_t evs = E;
-                while (evs) {
-                    const int i = __builtin_ctzll(evs);
-                    evs &= evs - 1ull;
-                    const uint32_t offI = w0 + static_cast<uint32_t>(i);
-                    const uint32_t cellI = (e0 + offI) & mask;
-                    if ((D >> i) & 1ull) {
-                        if (wr) r.ht[cellI] = 0;
+                const uint64_t S = __ballot(occ && !del) & active;  // entries that stay unless they move
+                // The events in cell order: a deleted cell, or an entry whose
+                // home is at or before the rightmost hole (the last event).  A
+                // deletion makes a hole; a mover takes the leftmost hole at or
+                // after its home and leaves a hole.  Each event is found with one
+                // ballot; the moves are recorded per lane and written after the
+                // window.
+                const uint64_t below = (1ull << lane) - 1ull;
+                uint64_t rem = active, E = 0ull, Mv = 0ull, taken = 0ull;
+                uint32_t tgt = 0u;
+                for (;;) {
+                    R = uniform32(R);
+                    const uint64_t reach = R >= 0 ? __ballot(homeOff <= static_cast<uint32_t>(R)) & S : 0ull;
+                    const uint64_t cand = uniform64((D | reach) & rem);
+                    if (!cand) break;
+                    const int j = __builtin_ctzll(cand);
+                    rem &= ~((2ull << j) - 1ull);
+                    const uint32_t offJ = w0 + static_cast<uint32_t>(j);
+                    if ((D >> j) & 1ull) {
                         --left;
                     } else {
-                        const uint32_t hOff = static_cast<uint32_t>(lane_value(static_cast<int32_t>(homeOff), i));
-                        const uint32_t eI = static_cast<uint32_t>(lane_value(static_cast<int32_t>(e), i));
-                        const int64_t hole = next_set(bits, hOff);  // < offI
-                        if (hole < 0 || hole >= static_cast<int64_t>(offI)) {
-                            bad = true;  // not reachable by the move rule; reported, nothing written
+                        const uint32_t h = static_cast<uint32_t>(lane_value(static_cast<int32_t>(homeOff), j));
+                        uint32_t hole = 0xFFFFFFFFu;  // none
+                        if (__builtin_expect(!big, 1)) {
+                            const uint64_t m = __ballot(qv >= h) & qmask;
+                            if (m) {
+                                const int t = __builtin_ctzll(m);
+                                hole = static_cast<uint32_t>(lane_value(static_cast<int32_t>(qv), t));
+                                qmask &= ~(1ull << t);
+                            }
                         } else {
-                            clr_bit3(bits, static_cast<uint32_t>(hole), wr);
-                            if (wr) {
-                                r.ht[(e0 + static_cast<uint32_t>(hole)) & mask] = static_cast<uint16_t>(eI);
-                                r.ht[cellI] = 0;
+                            const int64_t x = next_set(bits, h);
+                            if (x >= 0 && x < static_cast<int64_t>(offJ)) {
+                                hole = static_cast<uint32_t>(x);
+                                clr_bit3(bits, hole, wr);
                             }
                         }
+                        if (hole >= offJ) {
+                            bad = true;  // not reachable by the move rule; reported, nothing written
+                            break;
+                        }
+                        tgt = static_cast<uint32_t>(lane_set(static_cast<int32_t>(tgt), j, static_cast<int32_t>(hole)));
+                        Mv |= 1ull << j;
+                        if (hole >= w0) taken |= 1ull << (hole - w0);
                     }
-                    set_bit3(bits, offI, wr);
+                    E |= 1ull << j;
+                    R = static_cast<int32_t>(offJ);
+                    // offJ is a hole now
+                    if (__builtin_expect(!big && qend < 64u, 1)) {
+                        qv = static_cast<uint32_t>(lane_set(static_cast<int32_t>(qv), static_cast<int32_t>(qend),
+                                                            static_cast<int32_t>(offJ)));
+                        qmask |= 1ull << qend;
+                        ++qend;
+                        continue;
+                    }
+                    if (!big) {
+                        // the queue's lanes are used up: pack the holes to the
+                        // front, or with 64 holes keep the rest of the cluster's
+                        // holes in the bitmap
+                        const uint32_t n = static_cast<uint32_t>(__builtin_popcountll(qmask));
+                        if (n < 64u) {
+                            if ((qmask >> lane) & 1ull) sQ[__builtin_popcountll(qmask & below)] = qv;
+                            qv = sQ[lane];
+                            qmask = n ? (~0ull >> (64u - n)) : 0ull;
+                            qv = static_cast<uint32_t>(lane_set(static_cast<int32_t>(qv), static_cast<int32_t>(n),
+                                                                static_cast<int32_t>(offJ)));
+                            qmask |= 1ull << n;
+                            qend = n + 1u;
+                            continue;
+                        }
+                        // every lane holds a hole (an offset below H)
+                        const uint32_t w = qv >> 6, v1 = w >> 6;
+                        atomicOr(reinterpret_cast<unsigned long long *>(bitL0 + w), 1ull << (qv & 63u));
+                        atomicOr(reinterpret_cast<unsigned long long *>(bitL1 + v1), 1ull << (w & 63u));
+                        atomicOr(reinterpret_cast<unsigned long long *>(bitL2 + (v1 >> 6)), 1ull << (v1 & 63u));
+                        big = true;
+                    }
+                    set_bit3(bits, offJ, wr);
                 }
-                if (E) R = static_cast<int32_t>(w0 + 63u - __builtin_clzll(E));
+                if ((Mv >> lane) & 1ull) r.ht[(e0 + tgt) & mask] = static_cast<uint16_t>(e);
+                if (((E & ~taken) >> lane) & 1ull) r.ht[cell] = 0;  // a hole no mover of the window took
                 if (f < 64) {
                     // the cluster ends at w0 + f: its remaining holes stay empty
                     const uint32_t hi = w0 + static_cast<uint32_t>(f);
                     const uint32_t top = hi < static_cast<uint32_t>(H) ? hi : static_cast<uint32_t>(H) - 1u;
-                    for (uint32_t w = (clusterLo >> 6) + lane; w <= (top >> 6); w += 64) bitL0[w] = 0ull;
-                    for (uint32_t w = (clusterLo >> 12) + lane; w <= (top >> 12); w += 64) bitL1[w] = 0ull;
-                    for (uint32_t w = (clusterLo >> 18) + lane; w <= (top >> 18); w += 64) bitL2[w] = 0ull;
+                    if (big) {
+                        for (uint32_t w = (clusterLo >> 6) + lane; w <= (top >> 6); w += 64) bitL0[w] = 0ull;
+                        for (uint32_t w = (clusterLo >> 12) + lane; w <= (top >> 12); w += 64) bitL1[w] = 0ull;
+                        for (uint32_t w = (clusterLo >> 18) + lane; w <= (top >> 18); w += 64) bitL2[w] = 0ull;
+                    }
                     R = -1;
+                    qmask = 0ull;
+                    qend = 0u;
+                    big = false;
                     w0 = hi + 1u;
                 } else {
                     w0 = w0 + 64u < chunkEnd ? w0 + 64u : chunkEnd;  // the next window starts inside the stage
@@ -696,6 +815,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 R = -1;
                 left = 0;
                 if (wr) report_overflow(P.L.overflowSlot, kOverflowProbe);
+                sTableBad = 1;
             }
             if (wr) {
                 sCur = w0;
@@ -709,17 +829,21 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     __syncthreads();
 
     // ---- 5. the new tokens, in position order ----------------------------
-    {
-        KVX_GM uint32_t *h32 = (KVX_GM uint32_t *)homes;  // scratch left zero (see above)
-        for (int32_t w = tid; w < H / 2; w += BT) h32[w] = 0u;
-    }
     for (uint32_t w = tid; w < nCellW; w += BT) {
+        // the empty cells of 64 cells, 8 cells a load
         uint64_t m = 0ull;
-        const KVX_GM uint32_t *h32 = (const KVX_GM uint32_t *)(r.ht + (w << 6));
-        for (int q = 0; q < 32; ++q) {
-            const uint32_t pair = h32[q];
-            if ((pair & 0xFFFFu) == 0u) m |= 1ull << (2 * q);
-            if ((pair >> 16) == 0u) m |= 1ull << (2 * q + 1);
+        const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(r.ht + (w << 6));
+        u32x4 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = t16[q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t x[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                if ((x[h] & 0xFFFFu) == 0u) m |= 1ull << (8 * q + 2 * h);
+                if ((x[h] >> 16) == 0u) m |= 1ull << (8 * q + 2 * h + 1);
+            }
         }
         bitL0[w] = m;
     }
@@ -759,12 +883,15 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 if (x < 0) x = next_set(bits, 0u);
                 if (x < 0) {
                     if (wr) report_overflow(P.L.overflowSlot, kOverflowProbe);  // a full table: not reachable
+                    sTableBad = 1;
                     continue;
                 }
                 clr_bit3(bits, static_cast<uint32_t>(x), wr);
                 if (wr) r.ht[x] = static_cast<uint16_t>(si + 1u);
             }
         }
+        // the row's table is consistent with its tokens unless a bound broke
+        if (wr) gHand[1] = sTableBad ? 0 : kCanonFlag;
     }
 }
 

@@ -26,6 +26,16 @@ constexpr int32_t kSmallTable = 4096;
 // LDS round trip as a shuffle would take).
 __device__ __forceinline__ int32_t lane_value(int32_t x, int32_t l) { return __builtin_amdgcn_readlane(x, l); }
 
+// x, the same in every lane, as a wave-uniform value: the compiler then keeps
+// it, and the loops and branches that depend on it, in scalar registers.
+__device__ __forceinline__ int32_t uniform32(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ uint64_t uniform64(uint64_t x)
+{
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(x)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(x >> 32)));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // x with lane l set to v (a register write, no compare and select).
 __device__ __forceinline__ int32_t lane_set(int32_t x, int32_t l, int32_t v) { return kvx_writelane_i32(v, l, x); }
 

@@ -85,8 +85,6 @@ constexpr uint32_t CLS_INV = 0u, CLS_EXT = 1u, CLS_HIT = 2u, CLS_CAND = 3u;
 constexpr uint16_t VT_NONE = 0xFFFF, VT_EVICTED = 0x8000, VT_PASSED = 0x4000, VT_NOCONV = 0x3FFF;
 constexpr uint16_t HV_EMPTY = 0xFFFF;  // compact form: slot without a token (hashes are masked below 2^15)
 constexpr uint32_t NOCELL = 0xFFFFu;   // evicted slot without a table entry
-// sieve_hand[row][1]: set when this kernel left the row's table consistent
-constexpr int32_t kCanonFlag = 0x4B565843;
 
 // Phase timestamps for profiling builds (-DKVX_SIEVE_PHASE_STAMPS): thread 0
 // of each workgroup records clock64() at phase boundaries into kvx_dbg_stamps,

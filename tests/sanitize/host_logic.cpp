@@ -82,7 +82,7 @@ int main()
             CHECK(b.stage + kvx::kBatchStage * 4u == b.total);
             CHECK(b.slot + K * 4u <= b.uni);
             CHECK(b.uniL2 <= b.stage);
-            CHECK(kvx::batch_aux_words(h) >= 2ull * kvx::kBatchMapCap + h / 2u);
+            CHECK(kvx::batch_aux_words(h) >= 2ull * kvx::kBatchMapCap);  // map, first occurrences
         }
     // winner tables: request b's destination b*min(stride, 65536) + slot, slot < 65536
     for (uint32_t reqs : {1u, 2u, 64u, 256u})

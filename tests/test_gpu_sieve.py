@@ -648,6 +648,70 @@ def test_sieve_batch_kernel_wraps_and_dups(kvops, seed):
     assert kvops.read_overflow() == 0
 
 
+CANON_FLAG = 0x4B565843  # sieve_hand[row][1] of a row a SIEVE kernel left consistent
+
+
+def test_sieve_batch_consistency_flag(kvops):
+    """The batch HBM kernel sets a row's consistency flag when it leaves the
+    row consistent, and then counts the row's live tokens and entries instead
+    of checking its table.  A row edited outside the kernel with the flag
+    cleared (an entry moved past an empty cell) is checked in full and takes
+    the in-order path, which clears the flag; a row left with one more live
+    token than entries with the flag set is caught by the counts.  Full state
+    against the oracle after every step."""
+    rng = np.random.default_rng(77)
+    dbs, K, prefill, req = 700, 200, 5000, 3
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    H = st.ht.shape[-1]
+    kvops.sieve_force_variant(5)
+    try:
+        for step in range(8):
+            if step == 3:
+                # row 1: the entry of an occupied cell moved to an empty cell
+                # past the end of its cluster (an empty cell between its home
+                # and its new cell), the flag cleared as the interface asks
+                ht = st.ht[0, 1]
+                c = int(np.nonzero(ht)[0][0])
+                x = c
+                while ht[x] != 0:
+                    x = (x + 1) % H
+                y = (x + 1) % H
+                while ht[y] != 0:
+                    y = (y + 1) % H
+                ht[y], ht[c] = ht[c], 0
+                dev.ht[0, 1, y] = int(ht[y])
+                dev.ht[0, 1, c] = 0
+                dev.hand[0, 1, 1] = 0
+            if step == 5:
+                # row 2: the entry at the end of a cluster removed (a live
+                # token without an entry), the flag left set
+                ht = st.ht[0, 2]
+                c = int(np.nonzero((ht != 0) & (np.roll(ht, -1) == 0))[0][0])
+                ht[c] = 0
+                dev.ht[0, 2, c] = 0
+            batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.3)
+            seq = np.full(req, prefill + 4)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == 5
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+            dev.assert_state_equal()
+            flags = dev.hand.cpu().numpy()[0, :, 1]
+            if step == 0:
+                assert list(flags) == [CANON_FLAG] * req
+            if step == 3:
+                assert flags[1] == 0 and flags[0] == CANON_FLAG and flags[2] == CANON_FLAG
+            if step == 5:
+                assert flags[2] == 0 and flags[0] == CANON_FLAG
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_batch_scratch_across_shapes(kvops):
     """The batch HBM kernel's per-row scratch is laid out by table size and
     shared by every launch on the stream: launches on one shape, then on a

@@ -4,7 +4,9 @@
   left-to-right pass per cluster, each surviving entry moving into the
   leftmost hole at or after its home, leaves the same table as sequential
   Algorithm R deletions (hisp_kernel_common.h:64-94) in any order, which is
-  also the table of inserting the survivors in their insertion order.
+  also the table of inserting the survivors in their insertion order; and so
+  does the kernel's windowed form of the pass (events found one at a time,
+  holes in a few queue lanes or a set, a window's writes after it).
 * Parallel admission build (kvx_sieve_ht_init_par, csrc/sieve.hip): keys
   bucketed by home with later duplicates dropped, the used cells from the
   backlog recursion (the ring's fixed point entering cell 0), then each
@@ -89,6 +91,73 @@ def _batch_delete(T, D, hf):
     return T
 
 
+def _batch_delete_windows(T, D, hf, rng, cap=64):
+    """The pass as the kernel runs it: windows of 1-64 cells; in each, the
+    events (a deleted cell, or an entry whose home is at or before the last
+    event) are found one at a time, each mover taking the leftmost hole at or
+    after its home, and the window's cells are written after it: each mover's
+    entry at its hole, each event cell no mover of the window took emptied.
+    The holes sit in `cap` queue lanes, filled in increasing order and packed
+    when the lanes run out; with `cap` holes the cluster's holes move to a
+    set for the rest of it.  Returns the table and the number of clusters
+    that needed the set."""
+    H = len(T)
+    T = list(T)
+    start = next(c for c in range(H) if T[c] is None)
+    lanes, big, R, spills = [None] * cap, None, -1, 0  # queue lanes (None: empty); big: the set
+    qend = 0
+    off = 1
+    while off <= H:
+        hi = min(off + rng.randint(1, 64), H + 1)
+        end, moves, events = None, [], []
+        for o in range(off, hi):
+            c = (start + o) % H
+            if o == H or T[c] is None:
+                end = o  # the cluster ends here
+                break
+            if T[c] in D:
+                pass
+            else:
+                hoff = (hf(T[c]) - start) % H
+                if not (R >= 0 and hoff <= R):
+                    continue
+                if big is None:
+                    at = next(i for i in range(qend) if lanes[i] is not None and lanes[i] >= hoff)
+                    hole, lanes[at] = lanes[at], None
+                else:
+                    hole = min(x for x in big if x >= hoff)
+                    big.remove(hole)
+                assert hole < o
+                moves.append((o, hole))
+            events.append(o)
+            R = o
+            if big is None and qend == cap:
+                held = [x for x in lanes if x is not None]
+                if len(held) < cap:
+                    lanes = held + [None] * (cap - len(held))
+                    qend = len(held)
+                else:
+                    big, spills = set(held), spills + 1
+            if big is None:
+                lanes[qend] = o
+                qend += 1
+            else:
+                big.add(o)
+        vals = {o: T[(start + o) % H] for o in events}
+        taken = {h for _, h in moves}
+        for o, h in moves:
+            T[(start + h) % H] = vals[o]
+        for o in events:
+            if o not in taken:
+                T[(start + o) % H] = None
+        if end is not None:
+            lanes, qend, big, R = [None] * cap, 0, None, -1
+            off = end + 1
+        else:
+            off = hi
+    return T, spills
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_batch_deletion_equals_algorithm_r(seed):
     rng = random.Random(seed)
@@ -118,6 +187,31 @@ def test_batch_deletion_equals_algorithm_r(seed):
                 _insert(fcfs, k, hf)
         assert seq == fcfs, (seed, trial)
         assert _batch_delete(T, D, hf) == seq, (seed, trial, H, keys, sorted(D))
+        for cap in (1, 2, 4, 64):
+            got, _ = _batch_delete_windows(T, D, hf, rng, cap)
+            assert got == seq, (seed, trial, H, cap, keys, sorted(D))
+
+
+def test_windowed_deletion_spills_and_packs_the_hole_lanes():
+    """Long clusters with many deletions: the hole lanes are packed and, once
+    full, spill to the set; the table still equals Algorithm R's."""
+    rng = random.Random(7)
+    H = 4096
+    def hf(k):
+        return (k * 7) % 2048
+    keys = rng.sample(range(1, 10 ** 6), 2000)
+    T = [None] * H
+    for k in keys:
+        _insert(T, k, hf)
+    for nd, cap in ((5, 4), (300, 8), (300, 64)):
+        D = set(rng.sample(keys, nd))
+        seq = list(T)
+        for k in D:
+            _erase(seq, k, hf)
+        got, spills = _batch_delete_windows(T, D, hf, rng, cap)
+        assert got == seq, (nd, cap)
+        if nd > 10 * cap:
+            assert spills > 0, (nd, cap)
 
 
 def _parallel_build(tok, dbs, H, lanes=256):
