@@ -141,7 +141,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t sScan[BT];
-    __shared__ int32_t sBad, sWrap, sLive, sOcc, sNamed, sNdel, sHand, sE0, sTableBad;
+    __shared__ int32_t sBad, sWrap, sLive, sOcc, sNamed, sNdel, sHand, sE0, sTableBad, sFirstMiss, sMisses;
 
     const HispSieveUpdateArgs &a = P.L.a;
     const int32_t K = static_cast<int32_t>(a.topK);
@@ -216,6 +216,8 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         sNdel = 0;
         sE0 = -1;
         sTableBad = 0;
+        sFirstMiss = K;
+        sMisses = 0;
     }
     for (uint32_t w = tid; w < nVisW; w += BT) {
         visB[w] = vis64[w];
@@ -431,8 +433,24 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 code[k] = kDup | static_cast<uint32_t>(f);
             } else {
                 const uint32_t s0 = map[t];
-                if (s0 != 0u) code[k] = s0 - 1u;
+                if (s0 != 0u) {
+                    code[k] = s0 - 1u;
+                } else {
+                    atomicMin(&sFirstMiss, k);  // a first occurrence not resident: a miss
+                }
             }
+        }
+        __syncthreads();
+        // Up to the first miss every position is a hit (no slot has been
+        // evicted yet): applied in parallel, a later occurrence taking its
+        // first occurrence's slot, which is a resident one before the miss.
+        const int32_t firstMiss = sFirstMiss;
+        for (int32_t k = tid; k < firstMiss; k += BT) {
+            const uint32_t c = code[k];
+            if (c == kInvalid || c == kExt) continue;
+            const uint32_t sl = (c & kDup) ? code[c & ~kDup] : c;
+            slotOut[k] = sl;
+            atomicOr(reinterpret_cast<unsigned long long *>(visB + (sl >> 6)), 1ull << (sl & 63));
         }
         __syncthreads();
     }
@@ -444,11 +462,13 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         // order, so a sweep sees the visited bits set before it.
         int32_t hand = gHand[0];
         if (hand < 0 || hand >= dbs) hand = 0;  // hisp_sieve_update.cpp:108-111
-        int32_t passed = 0;
+        int32_t passed = 0, nMiss = 0;
         bool wrapped = false;
         const uint32_t lastW = nVisW - 1u;
         const uint64_t lastMask = (dbs & 63) ? ((1ull << (dbs & 63)) - 1ull) : ~0ull;
-        for (int32_t k0 = 0; k0 < K && !wrapped; k0 += 64) {
+        // from the round of the first miss (the positions before it applied
+        // again change nothing)
+        for (int32_t k0 = sFirstMiss & ~63; k0 < K && !wrapped; k0 += 64) {
             const int32_t k = k0 + static_cast<int32_t>(lane);
             const uint32_t c = k < K ? code[k] : kInvalid;
             const bool rel = c != kInvalid && c != kExt;
@@ -506,6 +526,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                     evB[h >> 6] |= 1ull << (h & 63);
                     slotOut[k0 + j] = static_cast<uint32_t>(h) | kMissBit;
                 }
+                ++nMiss;
                 hand = h + 1 == dbs ? 0 : h + 1;
                 pend &= ~(1ull << j);
             }
@@ -513,6 +534,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         if (lane == 0) {
             sHand = hand;
             sWrap = wrapped ? 1 : 0;
+            sMisses = nMiss;
         }
     }
     __syncthreads();
@@ -520,9 +542,17 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 
     // the map and first-occurrence scratch are left zeroed (tokens still the
     // initial ones here)
-    for (int32_t s = tid; s < dbs; s += BT) {
-        const int32_t t = r.tok[s];
-        if (t >= 0 && t < mapLim) map[t] = 0u;
+    for (int32_t s0 = tid; s0 < dbs; s0 += BT * kMapUnroll) {
+        int32_t tv[kMapUnroll];
+#pragma unroll
+        for (int q = 0; q < kMapUnroll; ++q) {
+            const int32_t s = s0 + q * BT;
+            tv[q] = s < dbs ? r.tok[s] : -1;
+        }
+#pragma unroll
+        for (int q = 0; q < kMapUnroll; ++q) {
+            if (tv[q] >= 0 && tv[q] < mapLim) map[tv[q]] = 0u;
+        }
     }
     for (int32_t k = tid; k < K; k += BT) {
         const int32_t t = rt[k];
@@ -559,13 +589,34 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     if (tid == 0) gHand[0] = sHand;
     for (uint32_t w = tid; w < nCellW; w += BT) delB[w] = 0ull;
     __syncthreads();  // code[] is dead from here on (its LDS becomes the bitmaps)
-    {
+    if (sMisses > 0) {
+        // the cells whose entries name an evicted slot, 8 cells a load
         int32_t nd = 0;
-        for (uint32_t c = tid; c < static_cast<uint32_t>(H); c += BT) {
-            const uint16_t e = r.ht[c];
-            if (e != 0 && bit_get(evB, static_cast<uint32_t>(e) - 1u)) {
-                atomicOr(reinterpret_cast<unsigned long long *>(delB + (c >> 6)), 1ull << (c & 63));
-                ++nd;
+        const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
+        const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(r.ht);
+        for (uint32_t c0 = tid; c0 < nChunk; c0 += BT * kCheckUnroll) {
+            u32x4 v[kCheckUnroll];
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                const uint32_t c = c0 + static_cast<uint32_t>(q) * BT;
+                if (c < nChunk) v[q] = t16[c];
+            }
+#pragma unroll
+            for (int q = 0; q < kCheckUnroll; ++q) {
+                if (c0 + static_cast<uint32_t>(q) * BT >= nChunk) continue;
+                const uint32_t cb = (c0 + static_cast<uint32_t>(q) * BT) * 8u;
+                const uint32_t w[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+                uint32_t m = 0u;  // the load's deleted cells
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const uint32_t e = (w[h >> 1] >> (16 * (h & 1))) & 0xFFFFu;
+                    if (e != 0u && e - 1u < static_cast<uint32_t>(dbs) && bit_get(evB, e - 1u)) m |= 1u << h;
+                }
+                if (m) {
+                    atomicOr(reinterpret_cast<unsigned long long *>(delB + (cb >> 6)),
+                             static_cast<unsigned long long>(m) << (cb & 63u));
+                    nd += __builtin_popcount(m);
+                }
             }
         }
         if (nd) atomicAdd(&sNdel, nd);
@@ -829,6 +880,10 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     __syncthreads();
 
     // ---- 5. the new tokens, in position order ----------------------------
+    if (sMisses == 0) {
+        if (tid == 0) gHand[1] = sTableBad ? 0 : kCanonFlag;  // nothing to insert
+        return;
+    }
     for (uint32_t w = tid; w < nCellW; w += BT) {
         // the empty cells of 64 cells, 8 cells a load
         uint64_t m = 0ull;
