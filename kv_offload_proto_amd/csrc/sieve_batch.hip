@@ -57,6 +57,7 @@ constexpr uint32_t kMissBit = 0x80000000u;   // slotOut: the position was a miss
 constexpr int kCheckUnroll = 8;              // 64-cell loads in flight per lane in the check
 constexpr int kMapUnroll = 8;    // slots whose tokens a lane loads together in the check
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 bytes: eight table cells
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));   // 16 bytes: four slots' tokens
 
 struct BatchParams {
     KvxLaunch<HispSieveUpdateArgs> L;
@@ -185,10 +186,15 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     KVX_GM uint64_t *vis64 = (KVX_GM uint64_t *)r.vis32;
     KVX_GM uint32_t *map = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords;
     KVX_GM uint32_t *first = map + P.mapCap;
+    const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
     // a row this kernel (or the LDS kernel) left consistent: the table scans
     // of the check are skipped, its live tokens and entries still counted
     const bool flagged = gHand[1] == kCanonFlag;
-    const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
+    // such a row, with its tokens below the table size, needs no map: the
+    // step's tokens are marked in a bitmap over [0, mapLim) (the LDS of the
+    // deleted-cell bits, unused until the outputs), and one pass over the
+    // slots finds the resident ones
+    const bool useBits = flagged && mapLim <= H;
 
     const BatchLayout &y = P.lay;
     uint64_t *visB = reinterpret_cast<uint64_t *>(lds + y.vis);
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     }
     for (uint32_t w = tid; w < nCellW; w += BT) delB[w] = 0ull;
     __syncthreads();
-    {
+    if (!useBits) {
         // the map by plain stores; a token held by two slots is found when
         // the map is read back below (one of them reads the other's slot).
         // kMapUnroll slots' tokens are loaded before any is used (one memory
@@ -400,27 +406,86 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
     }
     __syncthreads();
-    const bool canonical = sBad == 0 && sOcc == sLive && sNamed == sOcc;
+    // with the bitmap, the live tokens are counted in the decide phase (and
+    // compared with the entries there)
+    const bool canonical = sBad == 0 && (useBits || (sOcc == sLive && sNamed == sOcc));
+    uint32_t *tokBits = reinterpret_cast<uint32_t *>(delB);
 
     // ---- 2. decide -----------------------------------------------------
     if (canonical) {
-        for (int32_t k = tid; k < K; k += BT) {
-            const int32_t t = rt[k];
-            uint32_t c = kInvalid;
-            if (t >= 0 && t < seqLen) {
-                c = kExt;
-                if (t < prefill) {
-                    c = kNotRes;
-                    if (t < mapLim) {
-                        __hip_atomic_fetch_max(first + t, static_cast<uint32_t>(K - k), __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
+        for (int32_t k0 = tid; k0 < K; k0 += BT * kMapUnroll) {
+            int32_t tv[kMapUnroll];  // loads in flight together
+#pragma unroll
+            for (int q = 0; q < kMapUnroll; ++q) tv[q] = k0 + q * BT < K ? rt[k0 + q * BT] : -1;
+#pragma unroll
+            for (int q = 0; q < kMapUnroll; ++q) {
+                const int32_t k = k0 + q * BT;
+                if (k >= K) continue;
+                const int32_t t = tv[q];
+                uint32_t c = kInvalid;
+                if (t >= 0 && t < seqLen) {
+                    c = kExt;
+                    if (t < prefill) {
+                        c = kNotRes;
+                        if (t < mapLim) {
+                            __hip_atomic_fetch_max(first + t, static_cast<uint32_t>(K - k), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                            if (useBits) atomicOr(tokBits + (t >> 5), 1u << (t & 31));
+                        }
                     }
                 }
+                code[k] = c;
+                slotOut[k] = 0u;  // positions that change nothing read as hits of slot 0 without the miss bit
             }
-            code[k] = c;
-            slotOut[k] = 0u;  // positions that change nothing read as hits of slot 0 without the miss bit
         }
         __syncthreads();
+        if (useBits) {
+            // the slots: live tokens counted; a slot holding a token of the
+            // step gives its first occurrence that slot
+            // (16 slots a lane per round: four 16-byte token loads, then the
+            // bit tests, then the first-occurrence loads of the hits, each
+            // group in flight together; the row holds padded >= dbs slots)
+            int32_t live = 0, bad = 0;
+            const KVX_GM i32x4 *t4 = reinterpret_cast<const KVX_GM i32x4 *>(r.tok);
+            const int32_t nQuad = (dbs + 3) / 4;
+            for (int32_t q0 = tid; q0 < nQuad; q0 += BT * 4) {
+                int32_t tv[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    i32x4 v = {-1, -1, -1, -1};
+                    if (q0 + q * BT < nQuad) v = t4[q0 + q * BT];
+                    tv[4 * q] = v.x;
+                    tv[4 * q + 1] = v.y;
+                    tv[4 * q + 2] = v.z;
+                    tv[4 * q + 3] = v.w;
+                }
+                bool hit[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int32_t sl = 4 * (q0 + (i >> 2) * BT) + (i & 3);
+                    const int32_t t = sl < dbs ? tv[i] : -1;
+                    hit[i] = false;
+                    if (t < 0) continue;
+                    ++live;
+                    if (t >= mapLim) {
+                        bad = 1;
+                    } else {
+                        hit[i] = (tokBits[t >> 5] >> (t & 31)) & 1u;
+                    }
+                }
+                uint32_t fv[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) fv[i] = hit[i] ? first[tv[i]] : 0u;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    if (hit[i]) code[K - static_cast<int32_t>(fv[i])] = static_cast<uint32_t>(4 * (q0 + (i >> 2) * BT) + (i & 3));
+                }
+            }
+            if (live) atomicAdd(&sLive, live);
+            if (bad) sBad = 1;
+            __syncthreads();
+            if (tid == 0 && sLive != sOcc) sBad = 1;  // a live token without an entry, or the reverse
+        }
         for (int32_t k = tid; k < K; k += BT) {
             if (code[k] != kNotRes) continue;
             const int32_t t = rt[k];
@@ -432,7 +497,9 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
             if (f < k) {
                 code[k] = kDup | static_cast<uint32_t>(f);
             } else {
-                const uint32_t s0 = map[t];
+                // a first occurrence still unresolved: with the bitmap, not
+                // resident; otherwise the map says
+                const uint32_t s0 = useBits ? 0u : map[t];
                 if (s0 != 0u) {
                     code[k] = s0 - 1u;
                 } else {
@@ -542,7 +609,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 
     // the map and first-occurrence scratch are left zeroed (tokens still the
     // initial ones here)
-    for (int32_t s0 = tid; s0 < dbs; s0 += BT * kMapUnroll) {
+    for (int32_t s0 = tid; s0 < dbs && !useBits; s0 += BT * kMapUnroll) {
         int32_t tv[kMapUnroll];
 #pragma unroll
         for (int q = 0; q < kMapUnroll; ++q) {

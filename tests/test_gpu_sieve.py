@@ -651,16 +651,19 @@ def test_sieve_batch_kernel_wraps_and_dups(kvops, seed):
 CANON_FLAG = 0x4B565843  # sieve_hand[row][1] of a row a SIEVE kernel left consistent
 
 
-def test_sieve_batch_consistency_flag(kvops):
+@pytest.mark.parametrize("prefill", [5000, 1500])
+def test_sieve_batch_consistency_flag(kvops, prefill):
     """The batch HBM kernel sets a row's consistency flag when it leaves the
     row consistent, and then counts the row's live tokens and entries instead
-    of checking its table.  A row edited outside the kernel with the flag
+    of checking its table (with tokens below the table size, 2048 cells here,
+    the step's tokens go in a bitmap instead of a token map).  A row edited
+    outside the kernel with the flag
     cleared (an entry moved past an empty cell) is checked in full and takes
     the in-order path, which clears the flag; a row left with one more live
     token than entries with the flag set is caught by the counts.  Full state
     against the oracle after every step."""
     rng = np.random.default_rng(77)
-    dbs, K, prefill, req = 700, 200, 5000, 3
+    dbs, K, req = 700, 200, 3
     st = orc.SieveState(1, req, dbs, K)
     for r in range(req):
         st.admit(r, prefill)
