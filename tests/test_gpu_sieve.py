@@ -715,6 +715,51 @@ def test_sieve_batch_consistency_flag(kvops, prefill):
     assert kvops.read_overflow() == 0
 
 
+@pytest.mark.parametrize("variant", [-1, 5])
+def test_stale_flag_after_table_rebuild(kvops, variant):
+    """A row re-seeded outside the admission path: new tokens with one token
+    in two slots, the table rebuilt by sieve_ht_init (which keeps the first
+    of the two), the hand record left as it was, its consistency flag still
+    set.  The live-token count exceeds the table's entries, so the kernels
+    (the LDS kernel at this shape, and the batch HBM kernel) check the row
+    and take the in-order path; the results match the oracle on the same
+    row."""
+    import torch
+    rng = np.random.default_rng(31)
+    dbs, K, prefill, req = 300, 128, 2000, 3
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(variant)
+    try:
+        for step in range(6):
+            if step == 3:
+                assert int(dev.hand[0, 1, 1]) == CANON_FLAG
+                tok = rng.choice(prefill, size=dbs, replace=False).astype(np.int32)
+                tok[7] = tok[3]
+                st.tokens[0, 1, :dbs] = tok
+                orc.sieve_ht_init(st.tokens, st.ht, 1, 1, 1, req, dbs, st.padded, st.ht_size)
+                dev.tokens[0, 1, :dbs] = torch.from_numpy(tok).cuda()
+                kvops.sieve_ht_init(dev.tokens.data_ptr(), dev.ht.data_ptr(), dev.prefill.data_ptr(), 1, 1, 1,
+                                    req, dbs, st.padded, st.ht_size, 0, 1)
+                torch.cuda.synchronize()
+                dev.assert_state_equal()
+                assert int(dev.hand[0, 1, 1]) == CANON_FLAG  # the rebuild cannot clear it
+            batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.3)
+            seq = np.full(req, prefill + 4)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            if variant >= 0:
+                assert kvops.last_sieve_variant() == variant
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_batch_scratch_across_shapes(kvops):
     """The batch HBM kernel's per-row scratch is laid out by table size and
     shared by every launch on the stream: launches on one shape, then on a
