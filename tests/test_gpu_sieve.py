@@ -760,6 +760,38 @@ def test_stale_flag_after_table_rebuild(kvops, variant):
     assert kvops.read_overflow() == 0
 
 
+def test_consistency_flag_shared_between_kernels(kvops):
+    """Every variant on the same rows in turn: the flag one kernel sets (the
+    LDS kernels and the batch HBM kernel) is what the next one trusts, and
+    the kernels that leave it alone keep the row consistent.  Full state
+    against the oracle after every step; the flag is set after the steps of
+    the kernels that set it."""
+    rng = np.random.default_rng(41)
+    dbs, K, prefill, req = 300, 128, 1500, 3
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    order = [2, 5, 3, 5, 4, 5, 0, 5, 1, 5, 2, 2, 5, 5]
+    try:
+        for step, variant in enumerate(order):
+            kvops.sieve_force_variant(variant)
+            batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.3)
+            seq = np.full(req, prefill + 4)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == variant
+            tag = "step {} variant {}".format(step, variant)
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=tag)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=tag)
+            dev.assert_state_equal()
+            if variant in (2, 4, 5):
+                assert list(dev.hand.cpu().numpy()[0, :, 1]) == [CANON_FLAG] * req, tag
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_batch_scratch_across_shapes(kvops):
     """The batch HBM kernel's per-row scratch is laid out by table size and
     shared by every launch on the stream: launches on one shape, then on a
