@@ -15,13 +15,18 @@
 //     row whose consistency flag (sieve_hand[row][1]) is set, which this
 //     kernel and the LDS kernel set when they leave the row consistent, only
 //     has its live tokens and entries counted;
-//  2. decide, on one lane, from LDS only: each position's first occurrence in
-//     the batch and the initial slot of its token are found in parallel
-//     first; a later occurrence hits the first one's slot (without a wrap
-//     nothing placed or hit in this step leaves it), a first occurrence hits
-//     its initial slot unless the hand evicted that slot earlier in the step,
-//     and a miss sweeps the visited bitmap from the hand;
-//  3. outputs, tokens, visited bits and hand, in parallel;
+//  2. decide: each position's first occurrence in the batch and the initial
+//     slot of its token are found in parallel first (a flagged row whose
+//     tokens lie below the table size marks the step's tokens in an LDS
+//     bitmap and finds their slots in one pass over the slots instead of a
+//     token map); up to the first miss every position is a hit, applied in
+//     parallel; from there one wave decides in order, from LDS only: a later
+//     occurrence hits the first one's slot (without a wrap nothing placed or
+//     hit in this step leaves it), a first occurrence hits its initial slot
+//     unless the hand evicted that slot earlier in the step, and a miss
+//     sweeps the visited bitmap from the hand;
+//  3. outputs, tokens, visited bits and hand, in parallel, and the cells of
+//     the evicted slots (a step without misses ends here);
 //  4. deletion of the evicted tokens' cells: Algorithm R leaves a table as if
 //     the deleted key had never been inserted, so all of the step's
 //     deletions give the same table in any order; one left-to-right pass per
@@ -54,8 +59,8 @@ constexpr uint32_t kExt = 0xFFFFFFFEu;       // position: at or past prefill
 constexpr uint32_t kNotRes = 0xFFFFFFFDu;    // position: first occurrence, token not resident
 constexpr uint32_t kDup = 0x80000000u;       // position: later occurrence of the position in the low bits
 constexpr uint32_t kMissBit = 0x80000000u;   // slotOut: the position was a miss
-constexpr int kCheckUnroll = 8;              // 64-cell loads in flight per lane in the check
-constexpr int kMapUnroll = 8;    // slots whose tokens a lane loads together in the check
+constexpr int kCheckUnroll = 8;              // loads of table cells in flight per lane in the scans
+constexpr int kMapUnroll = 8;                // token loads in flight per lane (slots or positions)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 bytes: eight table cells
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));   // 16 bytes: four slots' tokens
 
