@@ -792,6 +792,38 @@ def test_consistency_flag_shared_between_kernels(kvops):
     assert kvops.read_overflow() == 0
 
 
+@pytest.mark.parametrize("prefill", [262149, 400000])
+def test_sieve_batch_tokens_beyond_map(kvops, prefill):
+    """The batch HBM kernel with prefill lengths past its token map (2^18
+    tokens) and past the table size: steps whose tokens all fit take the
+    batch path, a row holding or asked for a larger token takes the
+    in-order path.  Full state against the oracle after every step."""
+    rng = np.random.default_rng(prefill)
+    dbs, K, req = 300, 128, 3
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(5)
+    try:
+        for step in range(8):
+            if step < 3:
+                # misses from below the map's reach first, then from the whole prefill
+                batch = _random_state_stream(rng, st, K, 200000, miss_frac=0.3)
+            else:
+                batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.3)
+            seq = np.full(req, prefill + 4)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == 5
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_batch_scratch_across_shapes(kvops):
     """The batch HBM kernel's per-row scratch is laid out by table size and
     shared by every launch on the stream: launches on one shape, then on a
