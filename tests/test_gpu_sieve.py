@@ -824,6 +824,40 @@ def test_sieve_batch_tokens_beyond_map(kvops, prefill):
     assert kvops.read_overflow() == 0
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_sieve_batch_fuzz_flagged(kvops, seed):
+    """The batch HBM kernel over random shapes whose tokens lie below the
+    table size (so flagged rows take the token bitmap), with the flag of a
+    random row cleared now and then, mixed hit/miss streams with duplicates
+    and invalid positions: full state against the oracle after every step."""
+    rng = np.random.default_rng(7000 + seed)
+    dbs = int(rng.integers(60, 1500))
+    K = int(rng.integers(50, 900))
+    req = int(rng.integers(1, 6))
+    st = orc.SieveState(1, req, dbs, K)
+    prefill = int(rng.integers(dbs + 10, st.ht_size + 1))
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(5)
+    try:
+        for step in range(8):
+            if step > 0 and rng.random() < 0.4:
+                dev.hand[0, int(rng.integers(0, req)), 1] = 0
+            batch = _random_state_stream(rng, st, K, prefill, miss_frac=float(rng.random() * 0.6))
+            seq = np.full(req, prefill + 4)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == 5
+            tag = "seed {} dbs {} K {} prefill {} step {}".format(seed, dbs, K, prefill, step)
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=tag)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=tag)
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_batch_scratch_across_shapes(kvops):
     """The batch HBM kernel's per-row scratch is laid out by table size and
     shared by every launch on the stream: launches on one shape, then on a
