@@ -762,7 +762,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         // wave 0 changes the state only after the staging barrier below
         if (sLeft <= 0 && sR < 0) break;
         // stage cells [chunk, chunk + kBatchStage) of the walk: entry | home << 16
-        const uint32_t chunk = sCur;
+        const uint32_t chunk = static_cast<uint32_t>(uniform32(static_cast<int32_t>(sCur)));
         const uint32_t chunkEnd = chunk + kBatchStage < static_cast<uint32_t>(H) ? chunk + kBatchStage
                                                                                 : static_cast<uint32_t>(H);
         for (uint32_t i = tid; i < kBatchStage; i += BT) {
@@ -783,9 +783,11 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         if (tid < 64) {
             const bool wr = lane == 0;
             bool bad = false;
-            int32_t R = sR;
-            uint32_t clusterLo = sClusterLo;
-            int32_t left = sLeft;
+            // the walk state in scalar registers (LDS values reach the wave in
+            // vector registers)
+            int32_t R = uniform32(sR);
+            uint32_t clusterLo = static_cast<uint32_t>(uniform32(static_cast<int32_t>(sClusterLo)));
+            int32_t left = uniform32(sLeft);
             uint32_t w0 = chunk;
             // wave 0's own state: uniform in the wave (the compiler cannot see
             // that past the branch on the thread index)
@@ -844,7 +846,6 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 uint64_t rem = active, E = 0ull, Mv = 0ull, taken = 0ull;
                 uint32_t tgt = 0u;
                 for (;;) {
-                    R = uniform32(R);
                     const uint64_t reach = R >= 0 ? __ballot(homeOff <= static_cast<uint32_t>(R)) & S : 0ull;
                     const uint64_t cand = uniform64((D | reach) & rem);
                     if (!cand) break;
