@@ -865,8 +865,9 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                                 qmask &= ~(1ull << t);
                             }
                         } else {
-                            const int64_t x = next_set(bits, h);
-                            if (x >= 0 && x < static_cast<int64_t>(offJ)) {
+                            // (a scalar like the lanes' hole, so both stay in scalar registers)
+                            const int32_t x = uniform32(static_cast<int32_t>(next_set(bits, h)));
+                            if (x >= 0 && static_cast<uint32_t>(x) < offJ) {
                                 hole = static_cast<uint32_t>(x);
                                 clr_bit3(bits, hole, wr);
                             }
