@@ -845,6 +845,39 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 const uint64_t below = (1ull << lane) - 1ull;
                 uint64_t rem = active, E = 0ull, Mv = 0ull, taken = 0ull;
                 uint32_t tgt = 0u;
+                if (!big && R >= 0 && D == 0ull) {
+                    // A window without deletions: the events are found in
+                    // parallel (each lane's previous event from the events so
+                    // far, grown to a fixpoint: an entry is an event iff its
+                    // home is at or before the previous event, so the set only
+                    // grows and each round adds the first one missing).  If no
+                    // mover's home reaches an older hole, each takes the hole
+                    // its previous event left (the rightmost one), all at once.
+                    const uint64_t older = qmask & ~(1ull << (qend - 1u));  // lane qend-1 holds R
+                    const int32_t R2 = older ? lane_value(static_cast<int32_t>(qv), 63 - __builtin_clzll(older)) : -1;
+                    uint64_t Ef = 0ull;
+                    uint32_t prev = static_cast<uint32_t>(R);
+                    for (int it = 0; it <= 64; ++it) {
+                        const uint64_t bl = Ef & below;
+                        prev = bl ? w0 + 63u - static_cast<uint32_t>(__builtin_clzll(bl)) : static_cast<uint32_t>(R);
+                        const uint64_t E2 = uniform64(Ef | (__ballot(homeOff <= prev) & S));
+                        if (E2 == Ef) break;
+                        Ef = E2;
+                    }
+                    const bool olderReached = __ballot(((Ef >> lane) & 1ull) && R2 >= 0 &&
+                                                       static_cast<int32_t>(homeOff) <= R2) != 0ull;
+                    if (!olderReached) {
+                        if (Ef) {
+                            const int last = 63 - __builtin_clzll(Ef);
+                            E = Mv = Ef;
+                            taken = Ef & ~(1ull << last);  // each event's cell is taken by the next one
+                            tgt = prev;
+                            R = static_cast<int32_t>(w0 + static_cast<uint32_t>(last));
+                            qv = static_cast<uint32_t>(lane_set(static_cast<int32_t>(qv), static_cast<int32_t>(qend - 1u), R));
+                        }
+                        rem = 0ull;  // nothing left for the one-at-a-time loop
+                    }
+                }
                 for (;;) {
                     const uint64_t reach = R >= 0 ? __ballot(homeOff <= static_cast<uint32_t>(R)) & S : 0ull;
                     const uint64_t cand = uniform64((D | reach) & rem);
