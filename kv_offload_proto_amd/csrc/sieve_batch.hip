@@ -877,6 +877,33 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                             qv = static_cast<uint32_t>(lane_set(static_cast<int32_t>(qv), static_cast<int32_t>(qend - 1u), R));
                         }
                         rem = 0ull;  // nothing left for the one-at-a-time loop
+                    } else if (qend + static_cast<uint32_t>(__builtin_popcountll(Ef)) <= 64u) {
+                        // the events are known; only the holes go in order: each
+                        // mover takes the leftmost hole at or after its home from
+                        // the lanes and its cell joins them
+                        for (uint64_t ev = Ef; ev; ev &= ev - 1ull) {
+                            const int j = __builtin_ctzll(ev);
+                            const uint32_t h = static_cast<uint32_t>(lane_value(static_cast<int32_t>(homeOff), j));
+                            const uint64_t m = uniform64(__ballot(qv >= h) & qmask);
+                            if (!m) {
+                                bad = true;  // the rightmost hole is at or after the home: only a broken invariant
+                                break;
+                            }
+                            const int t = __builtin_ctzll(m);
+                            const uint32_t hole = static_cast<uint32_t>(lane_value(static_cast<int32_t>(qv), t));
+                            qmask &= ~(1ull << t);
+                            tgt = static_cast<uint32_t>(lane_set(static_cast<int32_t>(tgt), j, static_cast<int32_t>(hole)));
+                            if (hole >= w0) taken |= 1ull << (hole - w0);
+                            const uint32_t offJ = w0 + static_cast<uint32_t>(j);
+                            qv = static_cast<uint32_t>(lane_set(static_cast<int32_t>(qv), static_cast<int32_t>(qend),
+                                                                static_cast<int32_t>(offJ)));
+                            qmask |= 1ull << qend;
+                            ++qend;
+                            Mv |= 1ull << j;
+                            E |= 1ull << j;
+                            R = static_cast<int32_t>(offJ);
+                        }
+                        rem = 0ull;
                     }
                 }
                 for (;;) {
