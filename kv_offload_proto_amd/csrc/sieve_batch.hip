@@ -38,8 +38,9 @@
 //     found one event at a time with one ballot each.  While the cluster
 //     holds at most 64 holes they sit in the wave's lanes (a mover's hole is
 //     one more ballot); beyond that, in a three-level hole bitmap for the
-//     rest of the cluster.  A window without deleted cells whose movers all
-//     take the hole their previous event left is decided in parallel.  A
+//     rest of the cluster.  A window without deleted cells finds its events
+//     in parallel; when its movers all take the hole their previous event
+//     left it is applied at once, otherwise only the holes go in order.  A
 //     window's moves are written after it, in parallel;
 //  5. the step's new tokens go in in position order, each into the first
 //     empty cell at or after its home (a three-level bitmap of empty cells):
