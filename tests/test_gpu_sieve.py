@@ -858,6 +858,52 @@ def test_sieve_batch_fuzz_flagged(kvops, seed):
     assert kvops.read_overflow() == 0
 
 
+@pytest.mark.parametrize("misses", [1, 3, 40, 400])
+def test_sieve_batch_cluster_walks(kvops, misses):
+    """The batch HBM kernel's deletion walk over one long cluster: every
+    token's home lies in the first eighth of the table, so the entries pile
+    up and each deletion's hole is carried through the cluster.  Steps with
+    1 to 400 misses per row exercise the windows decided in parallel (one
+    hole), the holes taken in order (several), the lanes packed and the
+    spill to the hole bitmap (more than 64).  Full state against the oracle
+    after every step."""
+    import torch
+    rng = np.random.default_rng(900 + misses)
+    dbs, K, req = 3000, 512, 2
+    st = orc.SieveState(1, req, dbs, K)
+    H = st.ht_size
+    prefill = 1 << 16
+    t = np.arange(prefill, dtype=np.int64)
+    home = (((t * 2654435761) & 0xFFFFFFFF) >> 16) & (H - 1)
+    pool = t[home < H // 8].astype(np.int32)
+    for r in range(req):
+        st.admit(r, prefill)
+        st.tokens[0, r, :dbs] = rng.choice(pool, size=dbs, replace=False)
+    orc.sieve_ht_init(st.tokens, st.ht, 0, req, 1, req, dbs, st.padded, H)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(5)
+    try:
+        for step in range(6):
+            batch = np.empty((req, K), dtype=np.int32)
+            for r in range(req):
+                live = st.tokens[0, r, :dbs]
+                hits = rng.choice(live, size=K - misses)
+                fresh = np.setdiff1d(pool, live)
+                batch[r] = rng.permutation(np.concatenate([hits, rng.choice(fresh, size=misses, replace=False)]))
+            seq = np.full(req, prefill)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == 5
+            tag = "misses {} step {}".format(misses, step)
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=tag)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=tag)
+            dev.assert_state_equal()
+            assert list(dev.hand.cpu().numpy()[0, :, 1]) == [CANON_FLAG] * req, tag
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_batch_scratch_across_shapes(kvops):
     """The batch HBM kernel's per-row scratch is laid out by table size and
     shared by every launch on the stream: launches on one shape, then on a
