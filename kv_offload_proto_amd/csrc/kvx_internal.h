@@ -209,8 +209,8 @@ __host__ __device__ __forceinline__ FastLayout fast_layout_for(uint32_t padded, 
 // The batch HBM SIEVE kernel (sieve_batch.hip): one workgroup of
 // kBatchThreads per batch row; LDS holds the row's visited and evicted
 // bitmaps, a bitmap over the table cells, per-position codes and slots, and
-// a stage of table cells; HBM scratch per row holds a token -> slot map and
-// first-occurrence table of kBatchMapCap tokens.
+// a stage of table cells; HBM scratch per row holds a token -> slot map,
+// first-occurrence table and token bitmap of kBatchMapCap tokens.
 // ---------------------------------------------------------------------------
 constexpr int kBatchThreads = 1024;
 constexpr int kBatchWaves = kBatchThreads / 64;
@@ -242,10 +242,11 @@ __host__ __device__ __forceinline__ BatchLayout batch_layout(uint32_t dbs, uint3
     return l;
 }
 
-// uint32 words of HBM scratch per row: map and first occurrences.
+// uint32 words of HBM scratch per row: map, first occurrences, a bitmap of
+// the step's tokens and two counters (entries, last empty cell + 1).
 __host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t)
 {
-    return 2ull * kBatchMapCap;
+    return 2ull * kBatchMapCap + kBatchMapCap / 32u + 4u;
 }
 
 // Launchers (implemented next to their kernels).

@@ -69,7 +69,7 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));   // 16 bytes: four s
 struct BatchParams {
     KvxLaunch<HispSieveUpdateArgs> L;
     int32_t *shadow;   // [maxNumReqs][H] table shadow for the in-order fallback
-    uint32_t *aux;     // [maxNumReqs][auxWords]: map [mapCap], first [mapCap]
+    uint32_t *aux;     // [maxNumReqs][auxWords]: map [mapCap], first [mapCap], bits [mapCap/32], counts [4]
     uint64_t auxWords;
     uint32_t mapCap;
     BatchLayout lay;
@@ -145,6 +145,86 @@ __device__ __forceinline__ void clr_bit3(const Bits3 &m, uint32_t i, bool writer
     if (writer) m.l2[v >> 6] = x2;
 }
 
+// The parts of a flagged row's check and decide that need no order, spread
+// over kPreSplit workgroups per row ahead of the row's own workgroup: the
+// positions' first occurrences (atomic max of K - k per token), the bitmap of
+// the step's tokens, and the table's entries and last empty cell.  A row the
+// batch kernel will not take in its bitmap form is left alone.
+constexpr int kPreSplit = 16;
+constexpr int kPreThreads = 256;
+
+__device__ __forceinline__ bool batch_bitmap_row(const HispSieveUpdateArgs &a, int32_t bid, int64_t &reqIdx,
+                                                 int32_t &prefill, int32_t &seqLen, uint32_t mapCap)
+{
+    const int32_t maxNumReqs = static_cast<int32_t>(a.maxNumReqs);
+    int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
+    if (numReal > maxNumReqs) numReal = maxNumReqs;
+    if (bid >= numReal) return false;
+    reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
+    if (reqIdx < 0 || reqIdx >= static_cast<int32_t>(a.poolSize)) return false;
+    const int32_t *hand = reinterpret_cast<const int32_t *>(a.sieveHand) + reqIdx * kHandStride;
+    if (hand[1] != kCanonFlag) return false;
+    prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
+    seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
+    const int32_t mapLim = prefill < static_cast<int32_t>(mapCap) ? prefill : static_cast<int32_t>(mapCap);
+    return mapLim <= static_cast<int32_t>(a.htSize);
+}
+
+__global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_pre(BatchParams P)
+{
+    const HispSieveUpdateArgs &a = P.L.a;
+    const int32_t bid = blockIdx.y, part = blockIdx.x, tid = threadIdx.x;
+    if (bid >= static_cast<int32_t>(a.maxNumReqs)) return;
+    int64_t reqIdx = 0;
+    int32_t prefill = 0, seqLen = 0;
+    if (!batch_bitmap_row(a, bid, reqIdx, prefill, seqLen, P.mapCap)) return;
+    const int32_t K = static_cast<int32_t>(a.topK);
+    const int32_t H = static_cast<int32_t>(a.htSize);
+    const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
+    KVX_GM uint32_t *first = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords + P.mapCap;
+    KVX_GM uint32_t *bits = first + P.mapCap;
+    KVX_GM uint32_t *counts = bits + P.mapCap / 32u;
+    const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    // this part's positions
+    const int32_t k0 = static_cast<int32_t>((static_cast<int64_t>(K) * part) / kPreSplit);
+    const int32_t k1 = static_cast<int32_t>((static_cast<int64_t>(K) * (part + 1)) / kPreSplit);
+    for (int32_t k = k0 + tid; k < k1; k += kPreThreads) {
+        const int32_t t = rt[k];
+        if (t >= 0 && t < seqLen && t < prefill && t < mapLim) {
+            __hip_atomic_fetch_max(first + t, static_cast<uint32_t>(K - k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_or(bits + (t >> 5), 1u << (t & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // this part's table cells, 8 a 16-byte load
+    const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(
+        reinterpret_cast<const KVX_GM uint16_t *>(a.deviceBufferHt) + reqIdx * H);
+    const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
+    const uint32_t c0 = static_cast<uint32_t>((static_cast<uint64_t>(nChunk) * part) / kPreSplit);
+    const uint32_t c1 = static_cast<uint32_t>((static_cast<uint64_t>(nChunk) * (part + 1)) / kPreSplit);
+    uint32_t occ = 0, lastPlus1 = 0;
+    for (uint32_t c = c0 + tid; c < c1; c += kPreThreads) {
+        const u32x4 v = t16[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const uint32_t lo = w[h] & 0xFFFFu, hi = w[h] >> 16;
+            occ += (lo != 0u) + (hi != 0u);
+            if (lo == 0u) lastPlus1 = c * 8u + 2u * h + 1u;
+            if (hi == 0u) lastPlus1 = c * 8u + 2u * h + 2u;
+        }
+    }
+    // a wave's sums, then one atomic per wave
+    for (int d = 32; d > 0; d >>= 1) {
+        occ += __shfl_xor(occ, d);
+        const uint32_t o = __shfl_xor(lastPlus1, d);
+        lastPlus1 = o > lastPlus1 ? o : lastPlus1;
+    }
+    if ((tid & 63) == 0) {
+        if (occ) __hip_atomic_fetch_add(counts, occ, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lastPlus1) __hip_atomic_fetch_max(counts + 1, lastPlus1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -193,6 +273,8 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     KVX_GM uint64_t *vis64 = (KVX_GM uint64_t *)r.vis32;
     KVX_GM uint32_t *map = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords;
     KVX_GM uint32_t *first = map + P.mapCap;
+    KVX_GM uint32_t *gBits = first + P.mapCap;     // the step's tokens, from kvx_sieve_batch_pre
+    KVX_GM uint32_t *gCounts = gBits + P.mapCap / 32u;
     const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
     // a row this kernel (or the LDS kernel) left consistent: the table scans
     // of the check are skipped, its live tokens and entries still counted
@@ -380,10 +462,15 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
     } else {
         // the entries counted and the last empty cell found, 8 cells a load
+        // (counted by the pre-pass for a row in the bitmap form)
         int32_t occ = 0, last = -1;
+        if (useBits && tid == 0) {
+            occ = static_cast<int32_t>(gCounts[0]);
+            last = static_cast<int32_t>(gCounts[1]) - 1;
+        }
         const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
         const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(r.ht);
-        for (uint32_t c0 = tid; c0 < nChunk; c0 += BT * kCheckUnroll) {
+        for (uint32_t c0 = tid; c0 < nChunk && !useBits; c0 += BT * kCheckUnroll) {
             u32x4 v[kCheckUnroll];
 #pragma unroll
             for (int q = 0; q < kCheckUnroll; ++q) {
@@ -434,16 +521,18 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                     c = kExt;
                     if (t < prefill) {
                         c = kNotRes;
-                        if (t < mapLim) {
+                        if (t < mapLim && !useBits) {  // (the pre-pass did these for the bitmap form)
                             __hip_atomic_fetch_max(first + t, static_cast<uint32_t>(K - k), __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
-                            if (useBits) atomicOr(tokBits + (t >> 5), 1u << (t & 31));
                         }
                     }
                 }
                 code[k] = c;
                 slotOut[k] = 0u;  // positions that change nothing read as hits of slot 0 without the miss bit
             }
+        }
+        if (useBits) {
+            for (int32_t w = tid; w < (mapLim + 31) / 32; w += BT) tokBits[w] = gBits[w];
         }
         __syncthreads();
         if (useBits) {
@@ -631,6 +720,13 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     for (int32_t k = tid; k < K; k += BT) {
         const int32_t t = rt[k];
         if (t >= 0 && t < seqLen && t < prefill && t < mapLim) first[t] = 0u;
+    }
+    if (useBits) {
+        for (int32_t w = tid; w < (mapLim + 31) / 32; w += BT) gBits[w] = 0u;
+        if (tid == 0) {
+            gCounts[0] = 0u;
+            gCounts[1] = 0u;
+        }
     }
     __syncthreads();  // the cleanup read the initial tokens; phase 3 replaces some
     if (!fast) {
@@ -1104,6 +1200,7 @@ hipError_t launch_sieve_update_batch(const HispSieveUpdateArgs &a, uint64_t over
     P.mapCap = kBatchMapCap;
     P.auxWords = batch_aux_words(a.htSize);
     P.lay = batch_layout(a.deviceBufferSize, a.htSize, a.topK);
+    hipLaunchKernelGGL(kvx_sieve_batch_pre, dim3(kPreSplit, a.maxNumReqs), dim3(kPreThreads), 0, stream, P);
     hipLaunchKernelGGL(kvx_sieve_update_batch, dim3(a.maxNumReqs), dim3(BT), P.lay.total, stream, P);
     return hipGetLastError();
 }
