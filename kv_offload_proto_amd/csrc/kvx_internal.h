@@ -210,7 +210,8 @@ __host__ __device__ __forceinline__ FastLayout fast_layout_for(uint32_t padded, 
 // kBatchThreads per batch row; LDS holds the row's visited and evicted
 // bitmaps, a bitmap over the table cells, per-position codes and slots, and
 // a stage of table cells; HBM scratch per row holds a token -> slot map,
-// first-occurrence table and token bitmap of kBatchMapCap tokens.
+// first-occurrence table and token bitmap of kBatchMapCap tokens and each
+// position's resident slot.
 // ---------------------------------------------------------------------------
 constexpr int kBatchThreads = 1024;
 constexpr int kBatchWaves = kBatchThreads / 64;
@@ -243,10 +244,12 @@ __host__ __device__ __forceinline__ BatchLayout batch_layout(uint32_t dbs, uint3
 }
 
 // uint32 words of HBM scratch per row: map, first occurrences, a bitmap of
-// the step's tokens and two counters (entries, last empty cell + 1).
-__host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t)
+// the step's tokens, four counters (entries, last empty cell + 1, live
+// tokens, a token past the map) and each position's resident slot + 1
+// (htSize/2 >= topK words).
+__host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t htSize)
 {
-    return 2ull * kBatchMapCap + kBatchMapCap / 32u + 4u;
+    return 2ull * kBatchMapCap + kBatchMapCap / 32u + 4u + htSize / 2u;
 }
 
 // Launchers (implemented next to their kernels).

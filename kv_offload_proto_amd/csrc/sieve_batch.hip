@@ -69,7 +69,8 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));   // 16 bytes: four s
 struct BatchParams {
     KvxLaunch<HispSieveUpdateArgs> L;
     int32_t *shadow;   // [maxNumReqs][H] table shadow for the in-order fallback
-    uint32_t *aux;     // [maxNumReqs][auxWords]: map [mapCap], first [mapCap], bits [mapCap/32], counts [4]
+    uint32_t *aux;     // [maxNumReqs][auxWords]: map [mapCap], first [mapCap], bits [mapCap/32], counts [4],
+                       // resident slot + 1 per position [topK]
     uint64_t auxWords;
     uint32_t mapCap;
     BatchLayout lay;
@@ -225,6 +226,55 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_pre(BatchParams P
     }
 }
 
+// The slots of such a row, after the pre-pass, spread the same way: live
+// tokens counted, a token past the map flagged, and each position that is the
+// first occurrence of a resident token given that token's slot (+ 1).
+__global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_slots(BatchParams P)
+{
+    const HispSieveUpdateArgs &a = P.L.a;
+    const int32_t bid = blockIdx.y, part = blockIdx.x, tid = threadIdx.x;
+    if (bid >= static_cast<int32_t>(a.maxNumReqs)) return;
+    int64_t reqIdx = 0;
+    int32_t prefill = 0, seqLen = 0;
+    if (!batch_bitmap_row(a, bid, reqIdx, prefill, seqLen, P.mapCap)) return;
+    const int32_t K = static_cast<int32_t>(a.topK);
+    const int32_t dbs = static_cast<int32_t>(a.deviceBufferSize);
+    const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
+    KVX_GM uint32_t *first = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords + P.mapCap;
+    const KVX_GM uint32_t *bits = first + P.mapCap;
+    KVX_GM uint32_t *counts = first + P.mapCap + P.mapCap / 32u;
+    KVX_GM uint32_t *resSlot = counts + 4;
+    const KVX_GM i32x4 *t4 = reinterpret_cast<const KVX_GM i32x4 *>(
+        reinterpret_cast<const KVX_GM int32_t *>(a.deviceBufferTokens) + reqIdx * static_cast<int32_t>(a.paddedBufferSize));
+    const int32_t nQuad = (dbs + 3) / 4;  // the row holds padded >= dbs slots, padded a multiple of 16
+    const int32_t q0 = static_cast<int32_t>((static_cast<int64_t>(nQuad) * part) / kPreSplit);
+    const int32_t q1 = static_cast<int32_t>((static_cast<int64_t>(nQuad) * (part + 1)) / kPreSplit);
+    uint32_t live = 0, bad = 0;
+    for (int32_t q = q0 + tid; q < q1; q += kPreThreads) {
+        const i32x4 v = t4[q];
+        const int32_t tv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int32_t sl = 4 * q + h, t = tv[h];
+            if (sl >= dbs || t < 0) continue;
+            ++live;
+            if (t >= mapLim) {
+                bad = 1;
+            } else if ((bits[t >> 5] >> (t & 31)) & 1u) {
+                resSlot[K - static_cast<int32_t>(first[t])] = static_cast<uint32_t>(sl + 1);
+            }
+        }
+    }
+    for (int d = 32; d > 0; d >>= 1) {
+        live += __shfl_xor(live, d);
+        bad |= __shfl_xor(bad, d);
+    }
+    if ((tid & 63) == 0) {
+        if (live) __hip_atomic_fetch_add(counts + 2, live, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (bad) __hip_atomic_fetch_or(counts + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -275,6 +325,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     KVX_GM uint32_t *first = map + P.mapCap;
     KVX_GM uint32_t *gBits = first + P.mapCap;     // the step's tokens, from kvx_sieve_batch_pre
     KVX_GM uint32_t *gCounts = gBits + P.mapCap / 32u;
+    KVX_GM uint32_t *gResSlot = gCounts + 4;        // from kvx_sieve_batch_slots
     const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
     // a row this kernel (or the LDS kernel) left consistent: the table scans
     // of the check are skipped, its live tokens and entries still counted
@@ -467,6 +518,9 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         if (useBits && tid == 0) {
             occ = static_cast<int32_t>(gCounts[0]);
             last = static_cast<int32_t>(gCounts[1]) - 1;
+            sLive = static_cast<int32_t>(gCounts[2]);
+            // a token past the map, or a live token without an entry (or the reverse)
+            if (gCounts[3] != 0u || gCounts[2] != gCounts[0]) sBad = 1;
         }
         const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
         const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(r.ht);
@@ -500,17 +554,19 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
     }
     __syncthreads();
-    // with the bitmap, the live tokens are counted in the decide phase (and
-    // compared with the entries there)
+    // (the bitmap form's counts were compared above)
     const bool canonical = sBad == 0 && (useBits || (sOcc == sLive && sNamed == sOcc));
-    uint32_t *tokBits = reinterpret_cast<uint32_t *>(delB);
 
     // ---- 2. decide -----------------------------------------------------
     if (canonical) {
         for (int32_t k0 = tid; k0 < K; k0 += BT * kMapUnroll) {
             int32_t tv[kMapUnroll];  // loads in flight together
+            uint32_t rv[kMapUnroll];
 #pragma unroll
-            for (int q = 0; q < kMapUnroll; ++q) tv[q] = k0 + q * BT < K ? rt[k0 + q * BT] : -1;
+            for (int q = 0; q < kMapUnroll; ++q) {
+                tv[q] = k0 + q * BT < K ? rt[k0 + q * BT] : -1;
+                rv[q] = (useBits && k0 + q * BT < K) ? gResSlot[k0 + q * BT] : 0u;
+            }
 #pragma unroll
             for (int q = 0; q < kMapUnroll; ++q) {
                 const int32_t k = k0 + q * BT;
@@ -521,7 +577,10 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                     c = kExt;
                     if (t < prefill) {
                         c = kNotRes;
-                        if (t < mapLim && !useBits) {  // (the pre-pass did these for the bitmap form)
+                        if (useBits) {
+                            // the pre-passes found the first occurrences and their slots
+                            if (rv[q] != 0u) c = rv[q] - 1u;
+                        } else if (t < mapLim) {
                             __hip_atomic_fetch_max(first + t, static_cast<uint32_t>(K - k), __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
                         }
@@ -531,57 +590,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                 slotOut[k] = 0u;  // positions that change nothing read as hits of slot 0 without the miss bit
             }
         }
-        if (useBits) {
-            for (int32_t w = tid; w < (mapLim + 31) / 32; w += BT) tokBits[w] = gBits[w];
-        }
         __syncthreads();
-        if (useBits) {
-            // the slots: live tokens counted; a slot holding a token of the
-            // step gives its first occurrence that slot
-            // (16 slots a lane per round: four 16-byte token loads, then the
-            // bit tests, then the first-occurrence loads of the hits, each
-            // group in flight together; the row holds padded >= dbs slots)
-            int32_t live = 0, bad = 0;
-            const KVX_GM i32x4 *t4 = reinterpret_cast<const KVX_GM i32x4 *>(r.tok);
-            const int32_t nQuad = (dbs + 3) / 4;
-            for (int32_t q0 = tid; q0 < nQuad; q0 += BT * 4) {
-                int32_t tv[16];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    i32x4 v = {-1, -1, -1, -1};
-                    if (q0 + q * BT < nQuad) v = t4[q0 + q * BT];
-                    tv[4 * q] = v.x;
-                    tv[4 * q + 1] = v.y;
-                    tv[4 * q + 2] = v.z;
-                    tv[4 * q + 3] = v.w;
-                }
-                bool hit[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int32_t sl = 4 * (q0 + (i >> 2) * BT) + (i & 3);
-                    const int32_t t = sl < dbs ? tv[i] : -1;
-                    hit[i] = false;
-                    if (t < 0) continue;
-                    ++live;
-                    if (t >= mapLim) {
-                        bad = 1;
-                    } else {
-                        hit[i] = (tokBits[t >> 5] >> (t & 31)) & 1u;
-                    }
-                }
-                uint32_t fv[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) fv[i] = hit[i] ? first[tv[i]] : 0u;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    if (hit[i]) code[K - static_cast<int32_t>(fv[i])] = static_cast<uint32_t>(4 * (q0 + (i >> 2) * BT) + (i & 3));
-                }
-            }
-            if (live) atomicAdd(&sLive, live);
-            if (bad) sBad = 1;
-            __syncthreads();
-            if (tid == 0 && sLive != sOcc) sBad = 1;  // a live token without an entry, or the reverse
-        }
         for (int32_t k = tid; k < K; k += BT) {
             if (code[k] != kNotRes) continue;
             const int32_t t = rt[k];
@@ -723,10 +732,8 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     }
     if (useBits) {
         for (int32_t w = tid; w < (mapLim + 31) / 32; w += BT) gBits[w] = 0u;
-        if (tid == 0) {
-            gCounts[0] = 0u;
-            gCounts[1] = 0u;
-        }
+        for (int32_t k = tid; k < K; k += BT) gResSlot[k] = 0u;
+        if (tid < 4) gCounts[tid] = 0u;
     }
     __syncthreads();  // the cleanup read the initial tokens; phase 3 replaces some
     if (!fast) {
@@ -1201,6 +1208,7 @@ hipError_t launch_sieve_update_batch(const HispSieveUpdateArgs &a, uint64_t over
     P.auxWords = batch_aux_words(a.htSize);
     P.lay = batch_layout(a.deviceBufferSize, a.htSize, a.topK);
     hipLaunchKernelGGL(kvx_sieve_batch_pre, dim3(kPreSplit, a.maxNumReqs), dim3(kPreThreads), 0, stream, P);
+    hipLaunchKernelGGL(kvx_sieve_batch_slots, dim3(kPreSplit, a.maxNumReqs), dim3(kPreThreads), 0, stream, P);
     hipLaunchKernelGGL(kvx_sieve_update_batch, dim3(a.maxNumReqs), dim3(BT), P.lay.total, stream, P);
     return hipGetLastError();
 }
