@@ -151,7 +151,7 @@ __device__ __forceinline__ void clr_bit3(const Bits3 &m, uint32_t i, bool writer
 // positions' first occurrences (atomic max of K - k per token), the bitmap of
 // the step's tokens, and the table's entries and last empty cell.  A row the
 // batch kernel will not take in its bitmap form is left alone.
-constexpr int kPreSplit = 16;
+constexpr int kPreSplit = 64;
 constexpr int kPreThreads = 256;
 
 __device__ __forceinline__ bool batch_bitmap_row(const HispSieveUpdateArgs &a, int32_t bid, int64_t &reqIdx,
