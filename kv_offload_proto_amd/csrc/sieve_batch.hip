@@ -1,7 +1,10 @@
 // SIEVE update for rows whose state does not fit LDS, decided in one pass
 // and applied to the hash table in batch (variant 5).
 //
-// One 1024-lane workgroup per batch row; the state stays in HBM.  The result
+// One 1024-lane workgroup per batch row, after two pre-passes of 64
+// workgroups per row that do a flagged row's order-free work (counts, first
+// occurrences, token bitmap, resident slots) in HBM scratch; the state
+// stays in HBM.  The result
 // equals the in-order recurrence of hisp_sieve_update.cpp:115-163 whenever
 // the row's table is canonical (every live token findable at its own slot)
 // and the step's hand does not pass a slot twice; otherwise the row runs that
@@ -16,10 +19,10 @@
 //     kernel and the LDS kernel set when they leave the row consistent, only
 //     has its live tokens and entries counted;
 //  2. decide: each position's first occurrence in the batch and the initial
-//     slot of its token are found in parallel first (a flagged row whose
-//     tokens lie below the table size marks the step's tokens in an LDS
-//     bitmap and finds their slots in one pass over the slots instead of a
-//     token map); up to the first miss every position is a hit, applied in
+//     slot of its token are found in parallel first (for a flagged row whose
+//     tokens lie below the table size the pre-passes mark the step's tokens
+//     in a bitmap and find their slots in one pass over the slots instead of
+//     a token map); up to the first miss every position is a hit, applied in
 //     parallel; from there one wave decides in order, from LDS only: a later
 //     occurrence hits the first one's slot (without a wrap nothing placed or
 //     hit in this step leaves it), a first occurrence hits its initial slot
