@@ -156,20 +156,39 @@ __device__ __forceinline__ void clr_bit3(const Bits3 &m, uint32_t i, bool writer
 // batch kernel will not take in its bitmap form is left alone.
 constexpr int kPreSplit = 64;
 constexpr int kPreThreads = 256;
+constexpr int kPreLoads = 2;  // a lane's first loads of tokens or cells, issued with the row header
 
-__device__ __forceinline__ bool batch_bitmap_row(const HispSieveUpdateArgs &a, int32_t bid, int64_t &reqIdx,
-                                                 int32_t &prefill, int32_t &seqLen, uint32_t mapCap)
+// Uniform values the pre-passes read and no kernel of the launch writes
+// before (num_real, the request index, lengths, the flag) load through the
+// constant address space, as scalar loads.
+#define KVX_CM __attribute__((address_space(4)))
+
+// The batch row's header, first level: num_real, the request index and the
+// length in one round trip (every bid < maxNumReqs has its entries, so they
+// are read before num_real is known).  False for a padding row or a request
+// index outside the pool.
+__device__ __forceinline__ bool batch_row_head(const HispSieveUpdateArgs &a, int32_t bid, int64_t &reqIdx,
+                                               int32_t &seqLen)
 {
+    int32_t numReal = *(KVX_CM const int32_t *)(a.numReal);
+    reqIdx = ((KVX_CM const int64_t *)(a.reqPoolIndices))[bid];
+    seqLen = ((KVX_CM const int32_t *)(a.seqLens))[bid];
+    asm volatile("" : : "s"(reqIdx), "s"(seqLen));
     const int32_t maxNumReqs = static_cast<int32_t>(a.maxNumReqs);
-    int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
     if (numReal > maxNumReqs) numReal = maxNumReqs;
     if (bid >= numReal) return false;
-    reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
-    if (reqIdx < 0 || reqIdx >= static_cast<int32_t>(a.poolSize)) return false;
-    const int32_t *hand = reinterpret_cast<const int32_t *>(a.sieveHand) + reqIdx * kHandStride;
-    if (hand[1] != kCanonFlag) return false;
-    prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
-    seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
+    return reqIdx >= 0 && reqIdx < static_cast<int32_t>(a.poolSize);
+}
+
+// Second level: the request's flag and prefill length.  True when the batch
+// kernel takes the row in its bitmap form (flagged, tokens below the table size).
+__device__ __forceinline__ bool batch_row_bitmap(const HispSieveUpdateArgs &a, int64_t reqIdx, int32_t &prefill,
+                                                 uint32_t mapCap)
+{
+    const int32_t flag = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride + 1];
+    prefill = ((KVX_CM const int32_t *)(a.prefillLens))[reqIdx];
+    asm volatile("" : : "s"(flag), "s"(prefill));
+    if (flag != kCanonFlag) return false;
     const int32_t mapLim = prefill < static_cast<int32_t>(mapCap) ? prefill : static_cast<int32_t>(mapCap);
     return mapLim <= static_cast<int32_t>(a.htSize);
 }
@@ -179,35 +198,54 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_pre(BatchParams P
     const HispSieveUpdateArgs &a = P.L.a;
     const int32_t bid = blockIdx.y, part = blockIdx.x, tid = threadIdx.x;
     if (bid >= static_cast<int32_t>(a.maxNumReqs)) return;
-    int64_t reqIdx = 0;
-    int32_t prefill = 0, seqLen = 0;
-    if (!batch_bitmap_row(a, bid, reqIdx, prefill, seqLen, P.mapCap)) return;
     const int32_t K = static_cast<int32_t>(a.topK);
     const int32_t H = static_cast<int32_t>(a.htSize);
+    // this part's positions and table cells (8 a 16-byte load)
+    const int32_t k0 = static_cast<int32_t>((static_cast<int64_t>(K) * part) / kPreSplit);
+    const int32_t k1 = static_cast<int32_t>((static_cast<int64_t>(K) * (part + 1)) / kPreSplit);
+    const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
+    const uint32_t c0 = static_cast<uint32_t>((static_cast<uint64_t>(nChunk) * part) / kPreSplit);
+    const uint32_t c1 = static_cast<uint32_t>((static_cast<uint64_t>(nChunk) * (part + 1)) / kPreSplit);
+    // the first tokens need only the batch row (topk_indices holds
+    // maxNumReqs rows): in flight with the header
+    const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
+    int32_t tk[kPreLoads];
+#pragma unroll
+    for (int q = 0; q < kPreLoads; ++q) {
+        const int32_t k = k0 + tid + q * kPreThreads;
+        tk[q] = k < k1 ? rt[k] : -1;
+    }
+    int64_t reqIdx = 0;
+    int32_t prefill = 0, seqLen = 0;
+    if (!batch_row_head(a, bid, reqIdx, seqLen)) return;
+    // the first cells need the request: in flight with the flag
+    const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(
+        reinterpret_cast<const KVX_GM uint16_t *>(a.deviceBufferHt) + reqIdx * H);
+    u32x4 cv[kPreLoads];
+#pragma unroll
+    for (int q = 0; q < kPreLoads; ++q) {
+        const uint32_t c = c0 + static_cast<uint32_t>(tid + q * kPreThreads);
+        if (c < c1) cv[q] = t16[c];
+    }
+    if (!batch_row_bitmap(a, reqIdx, prefill, P.mapCap)) return;
     const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
     KVX_GM uint32_t *first = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords + P.mapCap;
     KVX_GM uint32_t *bits = first + P.mapCap;
     KVX_GM uint32_t *counts = bits + P.mapCap / 32u;
-    const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
-    // this part's positions
-    const int32_t k0 = static_cast<int32_t>((static_cast<int64_t>(K) * part) / kPreSplit);
-    const int32_t k1 = static_cast<int32_t>((static_cast<int64_t>(K) * (part + 1)) / kPreSplit);
-    for (int32_t k = k0 + tid; k < k1; k += kPreThreads) {
-        const int32_t t = rt[k];
+    auto position = [&](int32_t k, int32_t t) {
         if (t >= 0 && t < seqLen && t < prefill && t < mapLim) {
             __hip_atomic_fetch_max(first + t, static_cast<uint32_t>(K - k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_fetch_or(bits + (t >> 5), 1u << (t & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+    };
+#pragma unroll
+    for (int q = 0; q < kPreLoads; ++q) {
+        const int32_t k = k0 + tid + q * kPreThreads;
+        if (k < k1) position(k, tk[q]);
     }
-    // this part's table cells, 8 a 16-byte load
-    const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(
-        reinterpret_cast<const KVX_GM uint16_t *>(a.deviceBufferHt) + reqIdx * H);
-    const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
-    const uint32_t c0 = static_cast<uint32_t>((static_cast<uint64_t>(nChunk) * part) / kPreSplit);
-    const uint32_t c1 = static_cast<uint32_t>((static_cast<uint64_t>(nChunk) * (part + 1)) / kPreSplit);
+    for (int32_t k = k0 + tid + kPreLoads * kPreThreads; k < k1; k += kPreThreads) position(k, rt[k]);
     uint32_t occ = 0, lastPlus1 = 0;
-    for (uint32_t c = c0 + tid; c < c1; c += kPreThreads) {
-        const u32x4 v = t16[c];
+    auto cells = [&](uint32_t c, u32x4 v) {
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
@@ -216,7 +254,13 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_pre(BatchParams P
             if (lo == 0u) lastPlus1 = c * 8u + 2u * h + 1u;
             if (hi == 0u) lastPlus1 = c * 8u + 2u * h + 2u;
         }
+    };
+#pragma unroll
+    for (int q = 0; q < kPreLoads; ++q) {
+        const uint32_t c = c0 + static_cast<uint32_t>(tid + q * kPreThreads);
+        if (c < c1) cells(c, cv[q]);
     }
+    for (uint32_t c = c0 + static_cast<uint32_t>(tid + kPreLoads * kPreThreads); c < c1; c += kPreThreads) cells(c, t16[c]);
     // a wave's sums, then one atomic per wave
     for (int d = 32; d > 0; d >>= 1) {
         occ += __shfl_xor(occ, d);
@@ -239,26 +283,33 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_slots(BatchParams
     if (bid >= static_cast<int32_t>(a.maxNumReqs)) return;
     int64_t reqIdx = 0;
     int32_t prefill = 0, seqLen = 0;
-    if (!batch_bitmap_row(a, bid, reqIdx, prefill, seqLen, P.mapCap)) return;
+    if (!batch_row_head(a, bid, reqIdx, seqLen)) return;
     const int32_t K = static_cast<int32_t>(a.topK);
     const int32_t dbs = static_cast<int32_t>(a.deviceBufferSize);
-    const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
-    KVX_GM uint32_t *first = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords + P.mapCap;
-    const KVX_GM uint32_t *bits = first + P.mapCap;
-    KVX_GM uint32_t *counts = first + P.mapCap + P.mapCap / 32u;
-    KVX_GM uint32_t *resSlot = counts + 4;
     const KVX_GM i32x4 *t4 = reinterpret_cast<const KVX_GM i32x4 *>(
         reinterpret_cast<const KVX_GM int32_t *>(a.deviceBufferTokens) + reqIdx * static_cast<int32_t>(a.paddedBufferSize));
     const int32_t nQuad = (dbs + 3) / 4;  // the row holds padded >= dbs slots, padded a multiple of 16
     const int32_t q0 = static_cast<int32_t>((static_cast<int64_t>(nQuad) * part) / kPreSplit);
     const int32_t q1 = static_cast<int32_t>((static_cast<int64_t>(nQuad) * (part + 1)) / kPreSplit);
+    // the first slots' tokens: in flight with the flag
+    i32x4 tv[kPreLoads];
+#pragma unroll
+    for (int j = 0; j < kPreLoads; ++j) {
+        const int32_t q = q0 + tid + j * kPreThreads;
+        if (q < q1) tv[j] = t4[q];
+    }
+    if (!batch_row_bitmap(a, reqIdx, prefill, P.mapCap)) return;
+    const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
+    KVX_GM uint32_t *first = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords + P.mapCap;
+    const KVX_GM uint32_t *bits = first + P.mapCap;
+    KVX_GM uint32_t *counts = first + P.mapCap + P.mapCap / 32u;
+    KVX_GM uint32_t *resSlot = counts + 4;
     uint32_t live = 0, bad = 0;
-    for (int32_t q = q0 + tid; q < q1; q += kPreThreads) {
-        const i32x4 v = t4[q];
-        const int32_t tv[4] = {v.x, v.y, v.z, v.w};
+    auto quad = [&](int32_t q, i32x4 v) {
+        const int32_t t4v[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-            const int32_t sl = 4 * q + h, t = tv[h];
+            const int32_t sl = 4 * q + h, t = t4v[h];
             if (sl >= dbs || t < 0) continue;
             ++live;
             if (t >= mapLim) {
@@ -267,7 +318,13 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_slots(BatchParams
                 resSlot[K - static_cast<int32_t>(first[t])] = static_cast<uint32_t>(sl + 1);
             }
         }
+    };
+#pragma unroll
+    for (int j = 0; j < kPreLoads; ++j) {
+        const int32_t q = q0 + tid + j * kPreThreads;
+        if (q < q1) quad(q, tv[j]);
     }
+    for (int32_t q = q0 + tid + kPreLoads * kPreThreads; q < q1; q += kPreThreads) quad(q, t4[q]);
     for (int d = 32; d > 0; d >>= 1) {
         live += __shfl_xor(live, d);
         bad |= __shfl_xor(bad, d);
@@ -292,26 +349,21 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     const int32_t maxNumReqs = static_cast<int32_t>(a.maxNumReqs);
     const int32_t H = static_cast<int32_t>(a.htSize);
     const uint32_t mask = static_cast<uint32_t>(H) - 1u;
-    const int32_t poolSize = static_cast<int32_t>(a.poolSize);
     const int32_t bid = blockIdx.x;
     const int tid = threadIdx.x;
     const uint32_t lane = lane_id();
     if (bid >= maxNumReqs) return;
 
-    int32_t numReal = *reinterpret_cast<const int32_t *>(a.numReal);
-    if (numReal > maxNumReqs) numReal = maxNumReqs;  // hisp_sieve_update.cpp:31-34
     KVX_GM int32_t *rs = reinterpret_cast<KVX_GM int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
     KVX_GM int8_t *rm = reinterpret_cast<KVX_GM int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
-    if (bid >= numReal) {
+    // a padding row (bid >= num_real, capped at maxNumReqs) or a request
+    // index outside the pool gets the dummy outputs (hisp_sieve_update.cpp:31-34,80-87)
+    int64_t reqIdx = 0;
+    int32_t seqLen = 0;
+    if (!batch_row_head(a, bid, reqIdx, seqLen)) {
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
-    const int64_t reqIdx = reinterpret_cast<const int64_t *>(a.reqPoolIndices)[bid];
-    if (reqIdx < 0 || reqIdx >= poolSize) {
-        write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
-        return;
-    }
-    const int32_t seqLen = reinterpret_cast<const int32_t *>(a.seqLens)[bid];
     const int32_t prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
     const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
     Row r;
