@@ -382,6 +382,23 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     KVX_GM uint32_t *gCounts = gBits + P.mapCap / 32u;
     KVX_GM uint32_t *gResSlot = gCounts + 4;        // from kvx_sieve_batch_slots
     const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
+    // loads that need only the batch row, issued before the flag is known:
+    // the pre-passes' counts (thread 0) and phase 2's first group of tokens
+    // and resident slots (the row's scratch always holds topK of them; used
+    // only in the bitmap form)
+    uint32_t pc[4] = {0u, 0u, 0u, 0u};
+    if (tid == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pc[q] = gCounts[q];
+    }
+    int32_t tv0[kMapUnroll];
+    uint32_t rv0[kMapUnroll];
+#pragma unroll
+    for (int q = 0; q < kMapUnroll; ++q) {
+        const int32_t k = tid + q * BT;
+        tv0[q] = k < K ? rt[k] : -1;
+        rv0[q] = k < K ? gResSlot[k] : 0u;
+    }
     // a row this kernel (or the LDS kernel) left consistent: the table scans
     // of the check are skipped, its live tokens and entries still counted
     const bool flagged = gHand[1] == kCanonFlag;
@@ -571,11 +588,11 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         // (counted by the pre-pass for a row in the bitmap form)
         int32_t occ = 0, last = -1;
         if (useBits && tid == 0) {
-            occ = static_cast<int32_t>(gCounts[0]);
-            last = static_cast<int32_t>(gCounts[1]) - 1;
-            sLive = static_cast<int32_t>(gCounts[2]);
+            occ = static_cast<int32_t>(pc[0]);
+            last = static_cast<int32_t>(pc[1]) - 1;
+            sLive = static_cast<int32_t>(pc[2]);
             // a token past the map, or a live token without an entry (or the reverse)
-            if (gCounts[3] != 0u || gCounts[2] != gCounts[0]) sBad = 1;
+            if (pc[3] != 0u || pc[2] != pc[0]) sBad = 1;
         }
         const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
         const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(r.ht);
@@ -617,10 +634,18 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         for (int32_t k0 = tid; k0 < K; k0 += BT * kMapUnroll) {
             int32_t tv[kMapUnroll];  // loads in flight together
             uint32_t rv[kMapUnroll];
+            if (k0 == tid) {  // the group loaded at the start
 #pragma unroll
-            for (int q = 0; q < kMapUnroll; ++q) {
-                tv[q] = k0 + q * BT < K ? rt[k0 + q * BT] : -1;
-                rv[q] = (useBits && k0 + q * BT < K) ? gResSlot[k0 + q * BT] : 0u;
+                for (int q = 0; q < kMapUnroll; ++q) {
+                    tv[q] = tv0[q];
+                    rv[q] = useBits ? rv0[q] : 0u;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kMapUnroll; ++q) {
+                    tv[q] = k0 + q * BT < K ? rt[k0 + q * BT] : -1;
+                    rv[q] = (useBits && k0 + q * BT < K) ? gResSlot[k0 + q * BT] : 0u;
+                }
             }
 #pragma unroll
             for (int q = 0; q < kMapUnroll; ++q) {
