@@ -806,7 +806,12 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
             if (tv[q] >= 0 && tv[q] < mapLim) map[tv[q]] = 0u;
         }
     }
-    for (int32_t k = tid; k < K; k += BT) {
+#pragma unroll
+    for (int q = 0; q < kMapUnroll; ++q) {  // the first group's tokens are still in registers
+        const int32_t t = tv0[q];
+        if (t >= 0 && t < seqLen && t < prefill && t < mapLim) first[t] = 0u;
+    }
+    for (int32_t k = tid + kMapUnroll * BT; k < K; k += BT) {
         const int32_t t = rt[k];
         if (t >= 0 && t < seqLen && t < prefill && t < mapLim) first[t] = 0u;
     }
