@@ -402,6 +402,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     // a row this kernel (or the LDS kernel) left consistent: the table scans
     // of the check are skipped, its live tokens and entries still counted
     const bool flagged = gHand[1] == kCanonFlag;
+    const int32_t hand0 = gHand[0];  // read with the flag: phase 2's wave starts from it
     // such a row, with its tokens below the table size, needs no map: the
     // step's tokens are marked in a bitmap over [0, mapLim) (the LDS of the
     // deleted-cell bits, unused until the outputs), and one pass over the
@@ -712,7 +713,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         // hand has not evicted, or a later occurrence) and is applied at
         // once; the miss then sweeps.  The wave's LDS operations complete in
         // order, so a sweep sees the visited bits set before it.
-        int32_t hand = gHand[0];
+        int32_t hand = hand0;
         if (hand < 0 || hand >= dbs) hand = 0;  // hisp_sieve_update.cpp:108-111
         int32_t passed = 0, nMiss = 0;
         bool wrapped = false;
