@@ -364,7 +364,11 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
-    const int32_t prefill = reinterpret_cast<const int32_t *>(a.prefillLens)[reqIdx];
+    // the prefill length, the flag and the hand as scalar loads, issued
+    // together (nothing in this launch writes them before they are read)
+    const int32_t prefill = ((KVX_CM const int32_t *)(a.prefillLens))[reqIdx];
+    const int32_t flagWord = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride + 1];
+    const int32_t hand0 = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride];  // phase 2's wave starts from it
     const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
     Row r;
     r.tok = reinterpret_cast<KVX_GM int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
@@ -401,8 +405,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     }
     // a row this kernel (or the LDS kernel) left consistent: the table scans
     // of the check are skipped, its live tokens and entries still counted
-    const bool flagged = gHand[1] == kCanonFlag;
-    const int32_t hand0 = gHand[0];  // read with the flag: phase 2's wave starts from it
+    const bool flagged = flagWord == kCanonFlag;
     // such a row, with its tokens below the table size, needs no map: the
     // step's tokens are marked in a bitmap over [0, mapLim) (the LDS of the
     // deleted-cell bits, unused until the outputs), and one pass over the
