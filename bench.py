@@ -242,12 +242,15 @@ def verify_against_oracle(runner, snap, plan, threads, log):
         by_layer.setdefault(ls.layer, []).append(ls)
     hot_bytes = runner.hot[0].numel()
     workers = max(1, min(threads, int((24 << 30) // (2 * hot_bytes))))
+    # threads left over when there are fewer layers than threads go to the
+    # requests of each layer-step (the slot-limit stress: 4 layers x 4 requests)
+    inner = max(1, min(cfg.req_num, threads // max(1, min(workers, len(by_layer)))))
 
     def one(layer):
         st = _layer_state(runner, snap, layer)
         hot = np.zeros(hot_bytes, dtype=np.uint8)
         for ls in by_layer[layer]:
-            slots, miss = st.update(0, ls.batch, b.req_pool, b.seq, b.R)
+            slots, miss = st.update(0, ls.batch, b.req_pool, b.seq, b.R, threads=inner)
             for s in range(cfg.node_num):
                 orc.gather_rows(b.segs, hot, layer * b.plsr, cfg.row_bytes, ls.batch, b.req_pool, b.host_base,
                                 slots, miss, b.R, cfg.top_k, b.R, cfg.stripe_rows, cfg.node_num, s,

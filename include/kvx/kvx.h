@@ -218,13 +218,17 @@ int kvx_stream_copy(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream)
  * 2 = parallel LDS-staged kernel, 4 = the same with the compact LDS layout
  * (16-bit token hashes in LDS, tokens in HBM) for rows whose full layout does
  * not fit, 0 = sequential LDS-staged kernel, 3 = sequential HBM-resident
- * kernel with wave-wide probes (rows too large for LDS), 1 = single-lane
+ * kernel with wave-wide probes, 5 = batch HBM-resident kernel (rows too large
+ * for LDS: decisions in one pass, the table's changes in batch, for a step
+ * with misses rebuilt in parallel by kernels of their own), 1 = single-lane
  * HBM-resident kernel (only when forced).  For tests and benchmarks. */
 int kvx_last_sieve_variant(void);
 
 /* Testing and benchmarking knob, no counterpart in the reference: force the
- * SIEVE variant of later kvx_sieve_update calls (-1 = automatic, 0..4 as
- * above; a variant whose LDS needs do not fit falls back to automatic). */
+ * SIEVE variant of later kvx_sieve_update calls (-1 = automatic, 0..5 as
+ * above; 6 = variant 5 with a step's table deletions and inserts applied by
+ * the batch kernel itself instead of the parallel rebuild; a variant whose
+ * LDS needs do not fit falls back to automatic). */
 int kvx_sieve_force_variant(int variant);
 
 #ifdef __cplusplus

@@ -21,7 +21,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "kvops_ext")
 INCLUDE = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["sieve.hip", "sieve_fast.hip", "sieve_wave.hip", "sieve_batch.hip", "rows.hip", "kvx_host.hip"]
+HIP_SOURCES = ["sieve.hip", "sieve_fast.hip", "sieve_wave.hip", "sieve_batch.hip", "sieve_table.hip", "rows.hip",
+               "kvx_host.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [
@@ -42,6 +43,10 @@ HIP_SOURCE_FLAGS = {
     # clauses gives it ~1% (same-box A/B against the default scheduler)
     "sieve_fast.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
 }
+
+
+# extra hipcc flags for every source (profiling builds, e.g. -DKVX_BATCH_STAMPS)
+EXTRA_FLAGS = os.environ.get("KVX_EXTRA_HIPFLAGS", "").split()
 
 
 def _run(cmd, verbose):
@@ -69,7 +74,7 @@ def build(verbose=False):
     with tempfile.TemporaryDirectory(prefix="kvx_build_") as bdir:
         def compile_one(src):
             obj = os.path.join(bdir, src + ".o")
-            cmd = [HIPCC] + HIP_FLAGS + HIP_SOURCE_FLAGS.get(src, [])
+            cmd = [HIPCC] + HIP_FLAGS + HIP_SOURCE_FLAGS.get(src, []) + EXTRA_FLAGS
             cmd += ["-c", "-I", INCLUDE, "-I", CSRC, "-o", obj, os.path.join(CSRC, src)]
             _run(cmd, verbose)
             return obj

@@ -46,6 +46,8 @@ struct StreamScratch {
     uint64_t shadowCells = 0;
     uint32_t *aux = nullptr;        // batch HBM SIEVE variant: per-row map, first occurrences, homes
     uint64_t auxWords = 0;
+    uint32_t *tbl = nullptr;        // its table rebuild: per-row cells, counts, new keys
+    uint64_t tblWords = 0;
 };
 
 // Scratch of kvx_import_all_noalloc: a fixed array in the library's code
@@ -72,6 +74,7 @@ struct State {
     std::vector<void *> retired;    // replaced scratch buffers, freed by kvx_close
     int lastSieveVariant = -1;
     int forcedSieveVariant = -1;
+    bool tableRebuild = false;      // the device's LDS holds the rebuild's chunk kernel
     void *noAllocScratch[64] = {};  // device address of `scratch`, per device (set at init)
 };
 
@@ -190,7 +193,7 @@ void CheckStatusBlock(uint64_t status, uint32_t firstNode, uint32_t nodes, uint3
 
 // Scratch needs of one launch (entries of each buffer; 0 = not used).
 struct ScratchNeed {
-    uint64_t win = 0, shadow = 0, aux = 0;
+    uint64_t win = 0, shadow = 0, aux = 0, tbl = 0;
 };
 
 bool Capturing(hipStream_t s)
@@ -224,7 +227,7 @@ StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *
     }
     const bool create = sc == nullptr;
     const bool grow = create || sc->rows.winEntries < need.win || sc->shadowCells < need.shadow ||
-                      sc->auxWords < need.aux;
+                      sc->auxWords < need.aux || sc->tblWords < need.tbl;
     if (!grow) return *sc;
     hipStream_t st = AsStream(stream);
     if (Capturing(st)) {
@@ -265,6 +268,12 @@ StreamScratch &ScratchFor(uint64_t stream, const ScratchNeed &need, const char *
         sc->aux = static_cast<uint32_t *>(p);
         sc->auxWords = need.aux;
     }
+    if (sc->tblWords < need.tbl) {
+        void *p = ScratchAlloc(need.tbl * sizeof(uint32_t), st, "sieve table rebuild scratch");
+        if (sc->tbl != nullptr) g.retired.push_back(sc->tbl);
+        sc->tbl = static_cast<uint32_t *>(p);
+        sc->tblWords = need.tbl;
+    }
     return *sc;
 }
 
@@ -277,6 +286,7 @@ struct SievePlan {
     int variant = 0;
     size_t ldsLaunch = 0;   // dynamic LDS of the launch
     uint32_t invCap = 0;    // entries of the parallel kernel's token -> slot map
+    bool rebuild = false;   // variant 5: a step's table changes by the rebuild kernels
 };
 
 SievePlan PlanSieve(uint32_t top_k, uint32_t dbs, uint32_t padded, uint32_t visStrideB, uint32_t poolSize,
@@ -300,8 +310,11 @@ SievePlan PlanSieve(uint32_t top_k, uint32_t dbs, uint32_t padded, uint32_t visS
     if (f == 2 && fastOk) v = 2;
     if (f == 3) v = 3;
     if (f == 4 && compactOk) v = 4;
-    if (f == 5 && batchOk) v = 5;
+    if ((f == 5 || f == 6) && batchOk) v = 5;
     p.variant = v;
+    // the batch kernel hands a step's table changes to the rebuild kernels
+    // where their windows fit (force 6: it applies them itself)
+    p.rebuild = v == 5 && f != 6 && g.tableRebuild && kvx::table_rebuild_ok(htSize, dbs, top_k);
     p.ldsLaunch = v == 2 ? ldsFast
                          : (v == 4 ? std::max(ldsCompact, lds) : (v == 0 ? lds : (v == 5 ? ldsBatch : 0)));
     // the parallel kernel's direct token -> slot map takes the LDS left over
@@ -318,6 +331,7 @@ ScratchNeed SieveScratchNeed(const SievePlan &p, uint32_t maxNumReqs, uint32_t h
     ScratchNeed n;
     if (p.variant == 3 || p.variant == 5) n.shadow = static_cast<uint64_t>(maxNumReqs) * htSize;
     if (p.variant == 5) n.aux = static_cast<uint64_t>(maxNumReqs) * kvx::batch_aux_words(htSize);
+    if (p.variant == 5 && p.rebuild) n.tbl = static_cast<uint64_t>(maxNumReqs) * kvx::table_layout(htSize).words;
     return n;
 }
 
@@ -504,6 +518,9 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
         hipCheck(kvx::sieve_fast_set_lds_limit(g.ldsLimit), "hipFuncSetAttribute(LDS fast)");
         g.ldsBatch = static_cast<size_t>(lds) - 6 * 1024;  // the batch kernel keeps ~4.7 KiB of static LDS
         hipCheck(kvx::sieve_batch_set_lds_limit(g.ldsBatch), "hipFuncSetAttribute(LDS batch)");
+        // the rebuild's chunk kernel keeps ~1.3 KiB of static LDS beside its dynamic part
+        g.tableRebuild = static_cast<size_t>(lds) >= kvx::kTblLdsBytes + 2 * 1024;
+        if (g.tableRebuild) hipCheck(kvx::sieve_table_set_lds_limit(kvx::kTblLdsBytes), "hipFuncSetAttribute(LDS table)");
         {
             // the null stream's scratch at a default size, so that callers on
             // the null stream start without an allocation on the launch path
@@ -546,6 +563,7 @@ int kvx_reserve_scratch(uint64_t stream, uint32_t max_num_reqs, uint32_t top_k, 
                 const ScratchNeed sn = SieveScratchNeed(p, max_num_reqs, static_cast<uint32_t>(ht));
                 need.shadow = sn.shadow;
                 need.aux = sn.aux;
+                need.tbl = sn.tbl;
             }
         }
         std::lock_guard<std::mutex> lk(g_scratchMu);
@@ -562,7 +580,7 @@ int kvx_scratch_bytes(uint64_t stream, uint64_t *out_bytes)
         for (const StreamScratch *s : g.scratch) {
             if (s->stream != stream) continue;
             b = kvx::kControlWords * sizeof(uint32_t) + s->rows.winEntries * sizeof(unsigned long long) +
-                s->shadowCells * sizeof(int32_t) + s->auxWords * sizeof(uint32_t);
+                s->shadowCells * sizeof(int32_t) + s->auxWords * sizeof(uint32_t) + s->tblWords * sizeof(uint32_t);
         }
         *out_bytes = b;
     });
@@ -902,7 +920,7 @@ int kvx_sieve_update(uint64_t topk_indices, uint64_t req_pool_indices, uint64_t 
             const StreamScratch &sc =
                 ScratchFor(stream, SieveScratchNeed(plan, max_num_reqs, static_cast<uint32_t>(htSize)), "sieve_update");
             hipCheck(kvx::launch_sieve_update_batch(a, reinterpret_cast<uint64_t>(g.overflow), sc.shadow, sc.aux,
-                                                    AsStream(stream)),
+                                                    plan.rebuild ? sc.tbl : nullptr, AsStream(stream)),
                      "hisp_sieve_update launch");
         } else {
             hipCheck(kvx::launch_sieve_update(a, reinterpret_cast<uint64_t>(g.overflow), plan.variant,
@@ -972,6 +990,7 @@ int kvx_close(void)
                 if (s->rows.counters != nullptr) (void)hipFree(s->rows.counters);
                 if (s->shadow != nullptr) (void)hipFree(s->shadow);
                 if (s->aux != nullptr) (void)hipFree(s->aux);
+                if (s->tbl != nullptr) (void)hipFree(s->tbl);
                 delete s;
             }
             g.scratch.clear();
@@ -1104,7 +1123,7 @@ int kvx_last_sieve_variant(void) { return g.lastSieveVariant; }
 int kvx_sieve_force_variant(int variant)
 {
     return Guarded([&] {
-        if (variant < -1 || variant > 5) throw Error("sieve_force_variant: variant must be -1 or 0..5");
+        if (variant < -1 || variant > 6) throw Error("sieve_force_variant: variant must be -1 or 0..6");
         g.forcedSieveVariant = variant;
     });
 }

@@ -243,14 +243,58 @@ __host__ __device__ __forceinline__ BatchLayout batch_layout(uint32_t dbs, uint3
     return l;
 }
 
+// The table rebuild of a step with misses (sieve_table.hip): per batch row,
+// HBM scratch of its own (table_layout(H).words uint32 words a row; nothing in
+// it needs to start zeroed, every launch writes what it reads):
+//   meta [16]          0: rebuild pending, 1: new keys, 2: linearization cell
+//   cellw [H]          per cell of the pre-step table: 0 empty, 0xFFFF0000 a
+//                      deleted key, else (home << 16) | entry of a survivor
+//   hist [min(H,2^16)] keys per home cell after the step (survivors + new keys)
+//   newk [H/2]         new keys in event order: (home << 16) | (slot + 1)
+//   evict [H/32]       the step's evicted slots (bitmap)
+//   chunkA [H/kTblChunkCells]  per cell chunk: start of its cluster, or -1
+constexpr uint32_t kTblChunkCells = 256;     // survivors' cells per chunk
+constexpr uint32_t kTblChunkKeys = 256;      // new keys per chunk
+constexpr uint32_t kTblWinBits = 3u << 16;   // free-cell window of a chunk (bits)
+constexpr uint32_t kTblMaxHt = 1u << 18;     // largest table the rebuild takes
+
+struct TableLayout {
+    uint64_t meta, cellw, hist, newk, evict, chunkA, words;
+};
+
+__host__ __device__ __forceinline__ uint64_t align16w(uint64_t w) { return (w + 15u) & ~15ull; }
+
+__host__ __device__ __forceinline__ TableLayout table_layout(uint32_t htSize)
+{
+    TableLayout t{};
+    const uint64_t H = htSize, HH = htSize < 65536u ? htSize : 65536u;
+    uint64_t o = 0;
+    t.meta = o;    o += 16;
+    t.cellw = o;   o += align16w(H);
+    t.hist = o;    o += align16w(HH);
+    t.newk = o;    o += align16w(H / 2);
+    t.evict = o;   o += align16w(H / 32 + 2);
+    t.chunkA = o;  o += align16w(H / kTblChunkCells + 1);
+    t.words = o;
+    return t;
+}
+
 // uint32 words of HBM scratch per row: map, first occurrences, a bitmap of
 // the step's tokens, four counters (entries, last empty cell + 1, live
 // tokens, a token past the map) and each position's resident slot + 1
-// (htSize/2 >= topK words).
+// (htSize/2 >= topK words).  Every launch leaves them zeroed, whatever the
+// shape of the next launch on the stream.
 __host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t htSize)
 {
     return 2ull * kBatchMapCap + kBatchMapCap / 32u + 4u + htSize / 2u;
 }
+
+// LDS bytes of the rebuild's chunk kernel: per-home counts (16 bits, 2^16
+// homes), the free-cell window's three bitmap levels and the scan partials.
+constexpr uint32_t kTblHistBytes = 65536u * 2u;
+constexpr uint32_t kTblWinWords = kTblWinBits / 64u;
+constexpr uint32_t kTblWinL1 = (kTblWinWords + 63u) / 64u;
+constexpr uint32_t kTblLdsBytes = kTblHistBytes + (kTblWinWords + kTblWinL1 + 1u) * 8u;
 
 // Launchers (implemented next to their kernels).
 hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int variant,
@@ -271,9 +315,23 @@ hipError_t launch_sieve_update_wave(const HispSieveUpdateArgs &a, uint64_t overf
                                     hipStream_t stream);
 hipError_t launch_sieve_update_fast(const HispSieveUpdateArgs &a, uint64_t overflowSlot, size_t ldsBytes,
                                     bool compact, hipStream_t stream);
+// tbl: the rebuild's scratch (rows of table_layout(htSize).words), or null
+// for the table changes applied inside the batch kernel.
 hipError_t launch_sieve_update_batch(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,
-                                     uint32_t *aux, hipStream_t stream);
+                                     uint32_t *aux, uint32_t *tbl, hipStream_t stream);
 hipError_t sieve_batch_set_lds_limit(size_t bytes);
+// The table rebuild after the batch kernel (rows it left pending), on the
+// same stream; table_rebuild_ok: the shape's windows fit (htSize <= kTblMaxHt).
+hipError_t launch_sieve_table_rebuild(const HispSieveUpdateArgs &a, uint64_t overflowSlot, uint32_t *tbl,
+                                      hipStream_t stream);
+hipError_t sieve_table_set_lds_limit(size_t bytes);
+__host__ __device__ __forceinline__ bool table_rebuild_ok(uint32_t htSize, uint32_t dbs, uint32_t topK)
+{
+    // windows: a survivor chunk spans its cluster (<= dbs cells) plus a chunk;
+    // a new-key chunk spans the 2^16 homes plus every key it can pass
+    return htSize >= 1024u && htSize <= kTblMaxHt && dbs <= 65535u && 65536ull + dbs + topK + 64u <= kTblWinBits &&
+           dbs + kTblChunkCells + 64u <= kTblWinBits;
+}
 
 struct GatherPlan {
     KvcGatherArgs a;               // args of the first (or only) segment

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void kvx_gather_prep(GatherParams P)
         if (threadIdx.x == 0) *x.chunkNext = 0u;
         for (uint32_t i = threadIdx.x; i < (n1 - n0) * 8u; i += blockDim.x) {
             x.counters[n0 * 8u + i] = 0u;
-            x.errs[n0 * 8u + i] = 0u;
+            x.errs[n0 * 8u + i] = 0xFFFFFFFFu;  // lowest failing position, min-reduced
         }
         if (a.status != 0) {
             for (uint32_t i = threadIdx.x; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void kvx_gather_span(GatherParams P)
                         }
                         const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
                         if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
-                            atomicCAS(&x.errs[key], 0u, row_error_code(static_cast<uint64_t>(p)));
+                            atomicMin(&x.errs[key], static_cast<uint32_t>(p));
                             winner = false;
                         }
                         copy = winner;
@@ -291,8 +291,8 @@ __global__ __launch_bounds__(256) void kvx_gather_span(GatherParams P)
         uint64_t word = 1ull << 32;  // kvc_gather_rows.cpp:29-33, :93
         if (static_cast<int64_t>(b * ppc) < total) {
             const uint32_t q = __hip_atomic_load(&x.counters[node * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint32_t err = __hip_atomic_load(&x.errs[node * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            word |= (static_cast<uint64_t>(q) << 40) | err;
+            const uint32_t e = __hip_atomic_load(&x.errs[node * 8u + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            word |= (static_cast<uint64_t>(q) << 40) | (e == 0xFFFFFFFFu ? 0u : row_error_code(e));
         }
         store_status(a.status + node * 64ull + b * 8ull, word);
     }
@@ -334,7 +334,10 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
             store_status(a.status + node * 64ull + b * 8ull, 0ull);
         }
     }
-    for (uint32_t i = tid; i < 64u * 8u; i += blockDim.x) sCnt[i] = sErr[i] = 0u;
+    for (uint32_t i = tid; i < 64u * 8u; i += blockDim.x) {
+        sCnt[i] = 0u;
+        sErr[i] = 0xFFFFFFFFu;  // lowest failing position, min-reduced
+    }
     if (tid == 0) {
         sN = 0u;
         sEpoch = *x.epoch;
@@ -366,7 +369,7 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
         atomicAdd(&sCnt[key], 1u);
         const uint64_t segRow = kvx_seg_row_of(row, a.stripeRows, a.nodeNum);
         if (segRow >= a.perLayerSegRows) {  // row outside the segment: report, do not read
-            atomicCAS(&sErr[key], 0u, row_error_code(static_cast<uint64_t>(p)));
+            atomicMin(&sErr[key], static_cast<uint32_t>(p));
             continue;
         }
         if (p < lo || p >= hi) continue;
@@ -409,7 +412,10 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
     for (uint32_t i = tid; i < (n1 - n0) * x.statusWords; i += blockDim.x) {
         const uint32_t node = n0 + i / x.statusWords, b = i % x.statusWords;
         uint64_t word = 1ull << 32;  // kvc_gather_rows.cpp:29-33, :93
-        if (static_cast<int64_t>(b * ppc) < total) word |= (static_cast<uint64_t>(sCnt[node * 8u + b]) << 40) | sErr[node * 8u + b];
+        if (static_cast<int64_t>(b * ppc) < total) {
+            const uint32_t e = sErr[node * 8u + b];
+            word |= (static_cast<uint64_t>(sCnt[node * 8u + b]) << 40) | (e == 0xFFFFFFFFu ? 0u : row_error_code(e));
+        }
         store_status(a.status + node * 64ull + b * 8ull, word);
     }
 }

@@ -77,6 +77,9 @@ struct BatchParams {
     uint64_t auxWords;
     uint32_t mapCap;
     BatchLayout lay;
+    uint32_t *tbl;      // the rebuild's scratch [maxNumReqs][t.words], or null: a step with
+                        // misses then applies its table changes here (phases 4, 5)
+    TableLayout t;
 };
 
 __device__ __forceinline__ int bit_get(const uint64_t *b, uint32_t i) { return (b[i >> 6] >> (i & 63)) & 1; }
@@ -356,6 +359,9 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 
     KVX_GM int32_t *rs = reinterpret_cast<KVX_GM int32_t *>(a.topKDeviceSlots) + static_cast<int64_t>(bid) * K;
     KVX_GM int8_t *rm = reinterpret_cast<KVX_GM int8_t *>(a.isMiss) + static_cast<int64_t>(bid) * K;
+    // no table rebuild pending for this row unless this launch hands it one
+    KVX_GM uint32_t *tbl = (KVX_GM uint32_t *)P.tbl + static_cast<uint64_t>(bid) * P.t.words;
+    if (P.tbl != nullptr && tid == 0) tbl[P.t.meta] = 0u;
     // a padding row (bid >= num_real, capped at maxNumReqs) or a request
     // index outside the pool gets the dummy outputs (hisp_sieve_update.cpp:31-34,80-87)
     int64_t reqIdx = 0;
@@ -428,6 +434,13 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     const uint32_t nL1 = (nCellW + 63u) / 64u;
     const uint32_t nL2 = (nL1 + 63u) / 64u;
 
+#ifdef KVX_BATCH_STAMPS
+    uint64_t stamp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    stamp[0] = __builtin_amdgcn_s_memtime();
+#define KVX_STAMP(i) stamp[i] = __builtin_amdgcn_s_memtime()
+#else
+#define KVX_STAMP(i) (void)0
+#endif
     // ---- 1. check ------------------------------------------------------
     if (tid == 0) {
         sBad = 0;
@@ -633,6 +646,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     // (the bitmap form's counts were compared above)
     const bool canonical = sBad == 0 && (useBits || (sOcc == sLive && sNamed == sOcc));
 
+    KVX_STAMP(1);
     // ---- 2. decide -----------------------------------------------------
     if (canonical) {
         for (int32_t k0 = tid; k0 < K; k0 += BT * kMapUnroll) {
@@ -794,6 +808,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
     }
     __syncthreads();
+    KVX_STAMP(2);
     const bool fast = canonical && sBad == 0 && sWrap == 0;
 
     // the map and first-occurrence scratch are left zeroed (tokens still the
@@ -825,6 +840,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         if (tid < 4) gCounts[tid] = 0u;
     }
     __syncthreads();  // the cleanup read the initial tokens; phase 3 replaces some
+    KVX_STAMP(3);
     if (!fast) {
         // the in-order recurrence on the untouched row, which the next launch
         // checks in full
@@ -855,6 +871,52 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     if (tid == 0) gHand[0] = sHand;
     for (uint32_t w = tid; w < nCellW; w += BT) delB[w] = 0ull;
     __syncthreads();  // code[] is dead from here on (its LDS becomes the bitmaps)
+    if (P.tbl != nullptr && sMisses > 0) {
+        // The table's deletions and inserts go to the rebuild kernels: the
+        // step's evicted slots, its new keys in event order with their homes
+        // (zeroed per-home counts for them to fill), then the new tokens.
+        const uint32_t HH = static_cast<uint32_t>(H) < 65536u ? static_cast<uint32_t>(H) : 65536u;
+        KVX_GM uint64_t *ev64 = (KVX_GM uint64_t *)(tbl + P.t.evict);
+        for (uint32_t w = tid; w < nVisW; w += BT) ev64[w] = evB[w];
+        for (uint32_t i = tid; i < HH; i += BT) tbl[P.t.hist + i] = 0u;
+        // the misses' ranks in position order: a contiguous run of positions per thread
+        const int32_t per = (K + BT - 1) / BT;
+        const int32_t k0 = tid * per, k1 = k0 + per < K ? k0 + per : K;
+        int32_t cnt = 0;
+        for (int32_t k = k0; k < k1; ++k) cnt += (slotOut[k] & kMissBit) ? 1 : 0;
+        int32_t inc = cnt;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int32_t o = __shfl_up(inc, d);
+            if (static_cast<int>(lane) >= d) inc += o;
+        }
+        if (lane == 63) sScan[tid >> 6] = inc;
+        __syncthreads();
+        if (tid == 0) {
+            int32_t run = 0;
+            for (int w = 0; w < kBatchWaves; ++w) {
+                const int32_t v = sScan[w];
+                sScan[w] = run;
+                run += v;
+            }
+        }
+        __syncthreads();
+        int32_t rank = sScan[tid >> 6] + inc - cnt;
+        KVX_GM uint32_t *newk = tbl + P.t.newk;
+        for (int32_t k = k0; k < k1; ++k) {
+            const uint32_t so = slotOut[k];
+            if (!(so & kMissBit)) continue;
+            const int32_t t = rt[k];
+            const uint32_t sl = so & 0xFFFFu;
+            newk[rank++] = ((ht_hash(t) & mask) << 16) | (sl + 1u);
+            r.tok[sl] = t;
+        }
+        if (tid == 0) {
+            tbl[P.t.meta + 1] = static_cast<uint32_t>(sMisses);
+            tbl[P.t.meta] = 1u;
+            gHand[1] = kCanonFlag;  // the rebuild leaves the table consistent
+        }
+        return;
+    }
     if (sMisses > 0) {
         // the cells whose entries name an evicted slot, 8 cells a load
         int32_t nd = 0;
@@ -897,6 +959,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     for (uint32_t w = tid; w < nL2; w += BT) bitL2[w] = 0ull;
     __syncthreads();
 
+    KVX_STAMP(4);
     // ---- 4. the deletions, one pass per cluster with a deleted cell ------
     // Offsets count cells from the empty cell sE0, so no cluster crosses 0.
     // The walk's state lives in LDS and only wave 0 changes it; every wave
@@ -1207,6 +1270,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     __threadfence_block();
     __syncthreads();
 
+    KVX_STAMP(5);
     // ---- 5. the new tokens, in position order ----------------------------
     if (sMisses == 0) {
         if (tid == 0) gHand[1] = sTableBad ? 0 : kCanonFlag;  // nothing to insert
@@ -1275,6 +1339,16 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
         // the row's table is consistent with its tokens unless a bound broke
         if (wr) gHand[1] = sTableBad ? 0 : kCanonFlag;
+#ifdef KVX_BATCH_STAMPS
+        KVX_STAMP(6);
+        if (tid == 0)
+            printf("stamps bid %d misses %d ndel %d: check %llu decide %llu cleanup %llu outputs %llu deletions %llu "
+                   "inserts %llu\n",
+                   bid, sMisses, sNdel, (unsigned long long)(stamp[1] - stamp[0]),
+                   (unsigned long long)(stamp[2] - stamp[1]), (unsigned long long)(stamp[3] - stamp[2]),
+                   (unsigned long long)(stamp[4] - stamp[3]), (unsigned long long)(stamp[5] - stamp[4]),
+                   (unsigned long long)(stamp[6] - stamp[5]));
+#endif
     }
 }
 
@@ -1287,7 +1361,7 @@ hipError_t sieve_batch_set_lds_limit(size_t bytes)
 }
 
 hipError_t launch_sieve_update_batch(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int32_t *shadow,
-                                     uint32_t *aux, hipStream_t stream)
+                                     uint32_t *aux, uint32_t *tbl, hipStream_t stream)
 {
     BatchParams P{};
     P.L = KvxLaunch<HispSieveUpdateArgs>{a, overflowSlot};
@@ -1296,9 +1370,16 @@ hipError_t launch_sieve_update_batch(const HispSieveUpdateArgs &a, uint64_t over
     P.mapCap = kBatchMapCap;
     P.auxWords = batch_aux_words(a.htSize);
     P.lay = batch_layout(a.deviceBufferSize, a.htSize, a.topK);
+    P.tbl = tbl;
+    P.t = table_layout(a.htSize);
     hipLaunchKernelGGL(kvx_sieve_batch_pre, dim3(kPreSplit, a.maxNumReqs), dim3(kPreThreads), 0, stream, P);
     hipLaunchKernelGGL(kvx_sieve_batch_slots, dim3(kPreSplit, a.maxNumReqs), dim3(kPreThreads), 0, stream, P);
     hipLaunchKernelGGL(kvx_sieve_update_batch, dim3(a.maxNumReqs), dim3(BT), P.lay.total, stream, P);
+    if (tbl != nullptr) {
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        return launch_sieve_table_rebuild(a, overflowSlot, tbl, stream);
+    }
     return hipGetLastError();
 }
 

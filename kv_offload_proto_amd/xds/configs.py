@@ -28,6 +28,11 @@ class Workload:
     stream: str = "state"          # "ref" (reference driver stream) or "state"
     zipf_s: Optional[float] = None
     adversarial: bool = False
+    # adversarial misses come from the positions whose 16-bit Knuth hash is
+    # below this bound (their homes share one window of the table); the pool
+    # must hold more than dbs + miss_ratio*topK positions, or it runs dry once
+    # the buffer is full of them
+    adversarial_hash_below: int = 40960
     export_reqs: Optional[int] = None   # prefill requests exported (default req_num)
     row_bytes: int = field(default_factory=row_bytes_of)
 
@@ -63,7 +68,10 @@ CONFIGS = {
     # large batch after a striped prefill export
     3: Workload("c3-large-batch-export", req_num=256, prefill=16384, top_k=2048, dbs=8192, miss_ratio=0.1,
                 layers=61, node_num=4, stripe_rows=64, steps=10, seed=11, export_reqs=16),
-    # SIEVE stress at the uint16 slot limit, adversarial hash collisions
+    # SIEVE stress at the uint16 slot limit, adversarial hash collisions: the
+    # misses come from the 81,922 positions below 131,072 whose hash is below
+    # 40,960 (more than dbs + 0.9*topK = 72,891), so every step has ~7,400
+    # misses per request inside one long probe run
     4: Workload("c4-slot-limit-stress", req_num=4, prefill=131072, top_k=8192, dbs=65518, miss_ratio=0.9, layers=4,
                 node_num=2, stripe_rows=1, steps=50, seed=3, adversarial=True),
 }

@@ -103,9 +103,10 @@ def state_batch(rng, tokens_rows, prefill, top_k, miss_ratio, zipf_s=None, miss_
     return out.astype(np.int32)
 
 
-def adversarial_pool(prefill, ht_bits_below=4096):
+def adversarial_pool(prefill, ht_bits_below):
     """Positions in [0, prefill) whose 16-bit Knuth hash is < ht_bits_below: their
-    home buckets pack into one window of the table (long probe runs)."""
+    home buckets pack into one window of the table (long probe runs).  About
+    prefill * ht_bits_below / 65536 positions."""
     t = np.arange(prefill, dtype=np.uint64)
     h = ((t * np.uint64(2654435761)) & np.uint64(0xFFFFFFFF)) >> np.uint64(16)
     return np.nonzero(h < ht_bits_below)[0].astype(np.int64)

@@ -134,7 +134,7 @@ class DecodeRunner:
         count; the state is restored afterwards so a replay reproduces it."""
         cfg = self.cfg
         rng = np.random.default_rng(cfg.seed if seed is None else seed)
-        pool = streams.adversarial_pool(cfg.prefill) if cfg.adversarial else None
+        pool = streams.adversarial_pool(cfg.prefill, cfg.adversarial_hash_below) if cfg.adversarial else None
         snap = self.snapshot()
         plan = []
         for step, layer in self.schedule(n_steps):

@@ -300,10 +300,21 @@ int orc_layout_validate(uint32_t nodeNum, uint32_t layerNum, uint32_t layerRows,
  * ceil(maxNumReqs*topK / blockDim) (kvops_ext.cpp:250-251).  An empty range
  * gives 1 << 32 (:29-33).
  *
+ * Rows outside the layer region (segRow >= perLayerSegRows): the reference
+ * reads segBase + (layerOffsetRows + segRow)*rowBytes regardless (:74-77), i.e.
+ * a row of the next layer's region, or past the segment's end for the last
+ * layer, where HCOMM's ReadNbi fails with the 0x200 + (pos & 0xFF) +
+ * (ret << 16) band (:78-81).  The rule here reads no such row: such a
+ * position is still counted in queued and still takes part in the winner
+ * rule (so a destination whose winner lies outside is left untouched), and
+ * the word of its block carries 0x200 + (p & 0xFF) + (1 << 16) for the
+ * lowest such position p owned by myNode.  perLayerSegRows = UINT32_MAX
+ * disables the check (the reference's read, in-segment cases only).
+ *
  * Returns the number of rows copied (winners owned by myNode).
  */
-int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffsetRows, uint32_t rowBytes,
-                        const int32_t *topk, const int64_t *reqPool, const int64_t *reqHostBase,
+int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffsetRows, uint32_t perLayerSegRows,
+                        uint32_t rowBytes, const int32_t *topk, const int64_t *reqPool, const int64_t *reqHostBase,
                         const int32_t *slots, const int8_t *isMiss, int32_t numRealIn, uint32_t topK,
                         uint32_t maxNumReqs, uint32_t S, uint32_t N, uint32_t myNode,
                         uint32_t hotReqStrideRows, uint32_t blockDim, uint64_t *statusWords)
@@ -315,6 +326,8 @@ int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffset
     if (blockDim == 0) blockDim = 1;
     const int64_t ppc = ((int64_t)maxNumReqs * topK + blockDim - 1) / blockDim;
     for (uint32_t b = 0; b < blockDim; ++b) statusWords[b] = 0;
+    int64_t firstErr[8];
+    for (uint32_t b = 0; b < 8; ++b) firstErr[b] = -1;
 
     int64_t copied = 0;
     /* Walk backwards: the first time a destination row is seen, that position
@@ -343,8 +356,13 @@ int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffset
             i = (i + 1) & (cap - 1);
         }
         if (winner) seen[i] = dst + 1;
-        if (!winner || node != myNode) continue;
+        if (node != myNode) continue;
         const uint64_t segRow = orc_seg_row_of(row, S, N);
+        if (segRow >= perLayerSegRows) {
+            if (blk < 8 && blk < (int64_t)blockDim) firstErr[blk] = p; /* walking backwards: the last write is the lowest */
+            continue;
+        }
+        if (!winner) continue;
         memcpy(hot + dst * rowBytes, segs[node] + ((uint64_t)layerOffsetRows + segRow) * rowBytes, rowBytes);
         ++copied;
     }
@@ -352,7 +370,9 @@ int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffset
     for (uint32_t b = 0; b < blockDim; ++b) {
         const int64_t lo = (int64_t)b * ppc;
         if (lo >= total) { statusWords[b] = 1ull << 32; continue; }
-        statusWords[b] = (statusWords[b] << 40) | (1ull << 32);
+        uint64_t err = 0;
+        if (b < 8 && firstErr[b] >= 0) err = 0x200u + ((uint64_t)firstErr[b] & 0xFFu) + (1u << 16);
+        statusWords[b] = (statusWords[b] << 40) | (1ull << 32) | err;
     }
     return copied;
 }

@@ -74,7 +74,8 @@ def lib():
         L.orc_layout_validate.restype = ctypes.c_int
         L.orc_layout_validate.argtypes = [ctypes.c_uint32] * 6
         L.orc_gather_rows.restype = ctypes.c_int64
-        L.orc_gather_rows.argtypes = [ctypes.POINTER(_u8p), _u8p, ctypes.c_uint32, ctypes.c_uint32, _i32p, _i64p,
+        L.orc_gather_rows.argtypes = [ctypes.POINTER(_u8p), _u8p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                      _i32p, _i64p,
                                       _i64p, _i32p, _i8p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32,
                                       ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                       ctypes.c_uint32, _u64p]
@@ -192,8 +193,12 @@ class SieveState:
         c.__dict__.update({k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in self.__dict__.items()})
         return c
 
-    def update(self, layer, topk, req_pool, seq_lens, num_real, max_num_reqs=None):
-        """One sieve_update of `layer`; returns (slots, is_miss) of shape [maxNumReqs, topK]."""
+    def update(self, layer, topk, req_pool, seq_lens, num_real, max_num_reqs=None, threads=1):
+        """One sieve_update of `layer`; returns (slots, is_miss) of shape [maxNumReqs, topK].
+
+        threads > 1 runs the batch rows on a thread pool, one oracle call per
+        row (the C call releases the GIL), when no two rows name the same pool
+        row; each row then sees exactly the state the in-order call gives it."""
         topk = np.ascontiguousarray(topk, dtype=np.int32)
         mnr = topk.shape[0] if max_num_reqs is None else max_num_reqs
         top_k = topk.shape[1]
@@ -202,8 +207,22 @@ class SieveState:
         slots = np.empty((mnr, top_k), dtype=np.int32)
         miss = np.empty((mnr, top_k), dtype=np.int8)
         tl, vl, hl, hdl = self.tokens[layer], self.vis[layer], self.ht[layer], self.hand[layer]
-        sieve_update(topk, np.ascontiguousarray(req_pool, dtype=np.int64),
-                     np.ascontiguousarray(seq_lens, dtype=np.int32), self.prefill_lens, tl, vl, hl, hdl, slots, miss,
+        req_pool = np.ascontiguousarray(req_pool, dtype=np.int64)
+        seq_lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+        nr = max(0, min(int(num_real), mnr))
+        live = [int(r) for r in req_pool[:nr] if 0 <= int(r) < self.pool_size]
+        if threads > 1 and nr > 1 and len(set(live)) == len(live):
+            from concurrent.futures import ThreadPoolExecutor
+
+            def one(b):
+                sieve_update(topk[b:b + 1], req_pool[b:b + 1], seq_lens[b:b + 1], self.prefill_lens, tl, vl, hl,
+                             hdl, slots[b:b + 1], miss[b:b + 1], 1 if b < nr else 0, top_k, self.dbs, self.padded,
+                             self.vis_stride, 1, self.ht_size, self.pool_size)
+
+            with ThreadPoolExecutor(max_workers=threads) as ex:
+                list(ex.map(one, range(mnr)))
+            return slots, miss
+        sieve_update(topk, req_pool, seq_lens, self.prefill_lens, tl, vl, hl, hdl, slots, miss,
                      num_real, top_k, self.dbs, self.padded, self.vis_stride, mnr, self.ht_size, self.pool_size)
         return slots, miss
 
@@ -224,12 +243,17 @@ def sieve_ht_init(tokens, ht, req_start, num_reqs, layer_num, pool_size, dbs, pa
 
 # ---------------------------------------------------------------- row movers
 def gather_rows(segs, hot, layer_offset_rows, row_bytes, topk, req_pool, req_host_base, slots, is_miss, num_real,
-                top_k, max_num_reqs, stripe_rows, node_num, my_node, hot_req_stride_rows=0, block_dim=1):
+                top_k, max_num_reqs, stripe_rows, node_num, my_node, hot_req_stride_rows=0, block_dim=1,
+                per_layer_seg_rows=None):
     """Oracle import for segment my_node.  segs: list of N uint8 arrays (whole
-    segments); hot: uint8 hot buffer.  Returns (rows copied, status words)."""
+    segments); hot: uint8 hot buffer.  per_layer_seg_rows: rows of one layer's
+    region in a segment; a host row whose segment row lies past it is not read
+    and its status word carries the 0x200 error band (None: every segment row
+    is read, as the reference does).  Returns (rows copied, status words)."""
     arr = (_u8p * len(segs))(*[_p(s, _u8p) for s in segs])
     words = np.zeros(max(block_dim, 1), dtype=np.uint64)
-    n = lib().orc_gather_rows(arr, _p(hot, _u8p), layer_offset_rows, row_bytes,
+    plsr = 0xFFFFFFFF if per_layer_seg_rows is None else int(per_layer_seg_rows)
+    n = lib().orc_gather_rows(arr, _p(hot, _u8p), layer_offset_rows, plsr, row_bytes,
                               _p(np.ascontiguousarray(topk, dtype=np.int32), _i32p),
                               _p(np.ascontiguousarray(req_pool, dtype=np.int64), _i64p),
                               _p(np.ascontiguousarray(req_host_base, dtype=np.int64), _i64p),

@@ -30,8 +30,8 @@ uint32_t orc_seg_row_of(uint32_t row, uint32_t S, uint32_t N);
 uint64_t orc_seg_offset(uint32_t layer, uint32_t row, uint32_t S, uint32_t N, uint32_t plsr, uint32_t rowBytes);
 int orc_layout_validate(uint32_t nodeNum, uint32_t layerNum, uint32_t layerRows, uint32_t plsr, uint32_t rowBytes,
                         uint32_t S);
-int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffsetRows, uint32_t rowBytes,
-                        const int32_t *topk, const int64_t *reqPool, const int64_t *reqHostBase, const int32_t *slots,
+int64_t orc_gather_rows(uint8_t *const *segs, uint8_t *hot, uint32_t layerOffsetRows, uint32_t perLayerSegRows,
+                        uint32_t rowBytes, const int32_t *topk, const int64_t *reqPool, const int64_t *reqHostBase, const int32_t *slots,
                         const int8_t *isMiss, int32_t numRealIn, uint32_t topK, uint32_t maxNumReqs, uint32_t S,
                         uint32_t N, uint32_t myNode, uint32_t hotReqStrideRows, uint32_t blockDim,
                         uint64_t *statusWords);
@@ -119,7 +119,7 @@ static void sieve_and_rows(int trial)
         uint8_t *hot = xmalloc(hotRows * ROWB);
         uint64_t status[8];
         for (uint32_t n = 0; n < N; ++n)
-            orc_gather_rows(segs, hot, layerOff, ROWB, topk, reqPool, hostBase, slots, miss, numReal, (uint32_t)topK,
+            orc_gather_rows(segs, hot, layerOff, (rnd() & 1) ? 0xFFFFFFFFu : maxRow / S / N / 2u, ROWB, topk, reqPool, hostBase, slots, miss, numReal, (uint32_t)topK,
                             (uint32_t)maxReqs, S, N, n, stride, (uint32_t)rint_in(1, 8), status);
         const size_t total = (size_t)maxReqs * topK;
         uint8_t *staging = xmalloc(total * ROWB);

@@ -173,6 +173,64 @@ def test_gather_large_batch_parity(kvops, req, top_k, num_real, S, N, stride_mod
         pool.destroy(close_ext=False)
 
 
+@pytest.mark.parametrize("top_k", [1000, 3000])   # 3 x 1000 positions: one-launch form; 3 x 3000: two launches
+@pytest.mark.parametrize("fused", [False, True])    # import_seg per segment, or import_all
+def test_gather_rows_past_layer_region(kvops, top_k, fused):
+    """Host rows whose segment row lies past the layer region (host base +
+    token >= N * per_layer_seg_rows): the reference would read the next
+    layer's region, or past the segment's end for the last layer
+    (kvc_gather_rows.cpp:69-81).  Here such a row is not read, it still counts
+    as queued and still competes for its destination, and its block's status
+    word carries 0x200 + (p & 0xFF) + (1 << 16) for the lowest such position
+    p; the oracle applies the same rule.  Every hot byte and status word."""
+    print("past-region case", top_k, fused, flush=True)
+    req, L, prefill, dbs, N, block_dim = 3, 2, 4096, 2048, 2, 3
+    padded = dbs
+    layer_rows = req * prefill
+    pool = HostSegPool(0, L, layer_rows, ROW, stripe_rows=1, node_num=N)
+    pool.create_pool()
+    try:
+        plsr = pool.per_layer_seg_rows
+        assert plsr * N == layer_rows
+        rng = np.random.default_rng(top_k + fused)
+        views = pool.segment_views()
+        for v in views:
+            v[...] = rng.integers(0, 256, size=v.shape, dtype=np.uint8)
+        segs = [v.reshape(-1) for v in views]
+        # request 2's run starts 1000 rows before the end of the layer, so its
+        # tokens >= 1000 name rows past the region of either layer
+        host_base = np.array([0, prefill, layer_rows - 1000], dtype=np.int64)
+        topk = rng.integers(0, prefill, size=(req, top_k)).astype(np.int32)
+        slots = rng.integers(0, dbs, size=(req, top_k)).astype(np.int32)
+        miss = (rng.random((req, top_k)) < 0.6).astype(np.int8)
+        pool_idx = np.arange(req, dtype=np.int64)
+        outside = (miss[2] != 0) & (host_base[2] + topk[2] >= layer_rows)
+        assert outside.sum() > 100
+        for layer in (0, L - 1):
+            hot_np = rng.integers(0, 256, size=(req * padded, ROW), dtype=np.uint8)
+            hot = torch.from_numpy(hot_np.copy()).cuda()
+            args = (layer, to_dev(topk), to_dev(pool_idx), to_dev(host_base), to_dev(slots), to_dev(miss),
+                    to_dev(np.array([req], dtype=np.int32)), hot, req, top_k)
+            read = pool.batch_read_fused if fused else pool.batch_read
+            status = read(*args, block_dim=block_dim, hot_req_stride_rows=padded)
+            # the blocks that report the rows past the region fail the wait
+            with pytest.raises(RuntimeError, match="kv op failed on node"):
+                pool.wait(status, block_dim=block_dim)
+            torch.cuda.synchronize()
+            errs = 0
+            for s in range(N):
+                _, words = orc.gather_rows(segs, hot_np.reshape(-1), layer * plsr, ROW, topk, pool_idx, host_base,
+                                           slots, miss, req, top_k, req, 1, N, s, hot_req_stride_rows=padded,
+                                           block_dim=block_dim, per_layer_seg_rows=plsr)
+                got = _read_words(status + s * 64, block_dim)
+                assert got == [int(w) for w in words], (layer, s, [hex(w) for w in got], [hex(w) for w in words])
+                errs += sum(1 for w in words if int(w) & 0xFFFFFFFF)
+            assert errs >= 1, "no block reported the rows past the region"
+            np.testing.assert_array_equal(hot.cpu().numpy(), hot_np, err_msg="layer {}".format(layer))
+    finally:
+        pool.destroy(close_ext=False)
+
+
 def test_status_poll_and_timeout(kvops):
     st = kvops.alloc_status(4)
     # nothing launched: the slot stays pending and the poll times out

@@ -468,22 +468,24 @@ def test_sieve_config3_parity(kvops):
 
 def test_sieve_config4_parity(kvops):
     """The slot-limit stress shapes (4 requests, 65518 slots, topK 8192, a
-    262144-entry table kept in HBM) with adversarial keys whose Knuth hashes
-    share 4096 home buckets: the first step (thousands of evictions inside
-    one long probe run) and the next ones, full state after each."""
+    262144-entry table kept in HBM) with 90% misses drawn from the keys whose
+    Knuth hashes share the table's first 40,960 homes: over 7,000 evictions per
+    request on every step inside one long probe run, full state after each."""
     cfg = CONFIGS[4]
     st = orc.SieveState(1, cfg.req_num, cfg.dbs, cfg.top_k)
     for r in range(cfg.req_num):
         st.admit(r, cfg.prefill)
     dev = DevSieve(st)
     rng = np.random.default_rng(cfg.seed)
-    pool = streams.adversarial_pool(cfg.prefill, 4096)
+    pool = streams.adversarial_pool(cfg.prefill, cfg.adversarial_hash_below)
     req_pool = np.arange(cfg.req_num)
     seq = np.full(cfg.req_num, cfg.prefill)
     for step in range(4):
         batch = streams.state_batch(rng, st.tokens[0, :, :cfg.dbs], cfg.prefill, cfg.top_k, cfg.miss_ratio,
                                     miss_pool=pool)
-        e_slots, e_miss = st.update(0, batch, req_pool, seq, cfg.req_num)
+        e_slots, e_miss = st.update(0, batch, req_pool, seq, cfg.req_num, threads=4)
+        print("c4 step", step, "misses per request", e_miss.sum(axis=1), flush=True)
+        assert e_miss.sum(axis=1).min() >= 7000
         g_slots, g_miss, _ = dev.update(kvops, 0, batch, req_pool, seq, cfg.req_num, cfg.req_num, cfg.top_k)
         assert kvops.last_sieve_variant() == 5
         np.testing.assert_array_equal(g_miss, e_miss)
@@ -618,7 +620,8 @@ def test_sieve_hbm_noncanonical_table(kvops, variant):
 
 
 @pytest.mark.parametrize("seed", range(4))
-def test_sieve_batch_kernel_wraps_and_dups(kvops, seed):
+@pytest.mark.parametrize("form", [5, 6])  # table changes: parallel rebuild, or in the batch kernel
+def test_sieve_batch_kernel_wraps_and_dups(kvops, form, seed):
     """The batch HBM kernel on rows whose steps sometimes wrap the hand
     (more misses than slots: the in-order path) and sometimes do not,
     with duplicate positions, invalid and decode-extension positions."""
@@ -631,7 +634,7 @@ def test_sieve_batch_kernel_wraps_and_dups(kvops, seed):
     for r in range(req):
         st.admit(r, prefill)
     dev = DevSieve(st)
-    kvops.sieve_force_variant(5)
+    kvops.sieve_force_variant(form)
     try:
         for step in range(6):
             seq = np.full(req, prefill + 5)
@@ -825,7 +828,8 @@ def test_sieve_batch_tokens_beyond_map(kvops, prefill):
 
 
 @pytest.mark.parametrize("seed", range(6))
-def test_sieve_batch_fuzz_flagged(kvops, seed):
+@pytest.mark.parametrize("form", [5, 6])  # table changes: parallel rebuild, or in the batch kernel
+def test_sieve_batch_fuzz_flagged(kvops, form, seed):
     """The batch HBM kernel over random shapes whose tokens lie below the
     table size (so flagged rows take the token bitmap), with the flag of a
     random row cleared now and then, mixed hit/miss streams with duplicates
@@ -839,7 +843,7 @@ def test_sieve_batch_fuzz_flagged(kvops, seed):
     for r in range(req):
         st.admit(r, prefill)
     dev = DevSieve(st)
-    kvops.sieve_force_variant(5)
+    kvops.sieve_force_variant(form)
     try:
         for step in range(8):
             if step > 0 and rng.random() < 0.4:
@@ -859,7 +863,8 @@ def test_sieve_batch_fuzz_flagged(kvops, seed):
 
 
 @pytest.mark.parametrize("misses", [1, 3, 40, 400])
-def test_sieve_batch_cluster_walks(kvops, misses):
+@pytest.mark.parametrize("form", [5, 6])  # table changes: parallel rebuild, or in the batch kernel
+def test_sieve_batch_cluster_walks(kvops, form, misses):
     """The batch HBM kernel's deletion walk over one long cluster: every
     token's home lies in the first eighth of the table, so the entries pile
     up and each deletion's hole is carried through the cluster.  Steps with
@@ -881,7 +886,7 @@ def test_sieve_batch_cluster_walks(kvops, misses):
         st.tokens[0, r, :dbs] = rng.choice(pool, size=dbs, replace=False)
     orc.sieve_ht_init(st.tokens, st.ht, 0, req, 1, req, dbs, st.padded, H)
     dev = DevSieve(st)
-    kvops.sieve_force_variant(5)
+    kvops.sieve_force_variant(form)
     try:
         for step in range(6):
             batch = np.empty((req, K), dtype=np.int32)
@@ -904,14 +909,15 @@ def test_sieve_batch_cluster_walks(kvops, misses):
     assert kvops.read_overflow() == 0
 
 
-def test_sieve_batch_scratch_across_shapes(kvops):
+@pytest.mark.parametrize("form", [5, 6])  # table changes: parallel rebuild, or in the batch kernel
+def test_sieve_batch_scratch_across_shapes(kvops, form):
     """The batch HBM kernel's per-row scratch is laid out by table size and
     shared by every launch on the stream: launches on one shape, then on a
     larger one with more rows, then the first again, all match the oracle
     (each launch leaves the scratch zeroed)."""
     shapes = [(7, 40, 64, 300), (4, 3000, 1000, 20000), (7, 40, 64, 300)]
     rng = np.random.default_rng(4)
-    kvops.sieve_force_variant(5)
+    kvops.sieve_force_variant(form)
     try:
         for i, (req, dbs, K, prefill) in enumerate(shapes):
             st = orc.SieveState(1, req, dbs, K)
@@ -927,6 +933,53 @@ def test_sieve_batch_scratch_across_shapes(kvops):
                 np.testing.assert_array_equal(g_miss, e_miss, err_msg="shape {} step {}".format(i, step))
                 np.testing.assert_array_equal(g_slots, e_slots, err_msg="shape {} step {}".format(i, step))
                 dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
+@pytest.mark.parametrize("case", ["wrap", "past-2^16"])
+def test_sieve_table_rebuild_cluster_edges(kvops, case):
+    """The parallel table rebuild where the cell order matters most: "wrap"
+    puts every token's home in the last eighth of an 8192-cell table, so the
+    clusters run past the table's end into cell 0; "past-2^16" (a 131072-cell
+    table) homes the tokens in the 16384 cells below 65536, so the clusters run
+    past cell 65535 and the order must start after it.  Steps with 1 to 300
+    misses per row, full state against the oracle after every step."""
+    rng = np.random.default_rng(31 if case == "wrap" else 32)
+    dbs, K, req = (3000, 512, 2) if case == "wrap" else (40000, 4096, 1)
+    st = orc.SieveState(1, req, dbs, K)
+    H = st.ht_size
+    assert H == (8192 if case == "wrap" else 131072)
+    prefill = 1 << 18
+    t = np.arange(prefill, dtype=np.int64)
+    home = (((t * 2654435761) & 0xFFFFFFFF) >> 16) & (H - 1)
+    lo = H - H // 8 if case == "wrap" else 65536 - 16384
+    pool = t[(home >= lo) & (home < lo + (H // 8 if case == "wrap" else 16384))].astype(np.int32)
+    assert len(pool) > dbs + 4 * 300
+    for r in range(req):
+        st.admit(r, prefill)
+        st.tokens[0, r, :dbs] = rng.choice(pool, size=dbs, replace=False)
+    orc.sieve_ht_init(st.tokens, st.ht, 0, req, 1, req, dbs, st.padded, H)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(5)
+    try:
+        for step, misses in enumerate([1, 40, 300, 7]):
+            batch = np.empty((req, K), dtype=np.int32)
+            for r in range(req):
+                live = st.tokens[0, r, :dbs]
+                hits = rng.choice(live, size=K - misses)
+                fresh = np.setdiff1d(pool, live)
+                batch[r] = rng.permutation(np.concatenate([hits, rng.choice(fresh, size=misses, replace=False)]))
+            seq = np.full(req, prefill)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == 5
+            tag = "{} step {}".format(case, step)
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=tag)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=tag)
+            dev.assert_state_equal()
+            assert list(dev.hand.cpu().numpy()[0, :, 1]) == [CANON_FLAG] * req, tag
     finally:
         kvops.sieve_force_variant(-1)
     assert kvops.read_overflow() == 0

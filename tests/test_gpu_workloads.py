@@ -55,9 +55,11 @@ def _check_export(pool, src, row_lo, row_cnt, layers, seg_rows=None):
                                           err_msg="layer {} segment {}".format(l, s))
 
 
-def _decode_parity(kvops, cfg, layers, steps, fused, seed_src, block_dim=2, miss_pool=None):
+def _decode_parity(kvops, cfg, layers, steps, fused, seed_src, block_dim=2, miss_pool=None, min_misses=0,
+                   oracle_threads=1):
     """Run `steps` decode steps over `layers` layers of workload `cfg` on the
-    GPU and the oracle side by side; returns (rows imported, layer-steps)."""
+    GPU and the oracle side by side; every request of every layer-step must
+    see at least `min_misses` misses.  Returns (rows imported, layer-steps)."""
     rb = cfg.row_bytes
     L = layers
     rows = cfg.layer_rows
@@ -101,7 +103,10 @@ def _decode_parity(kvops, cfg, layers, steps, fused, seed_src, block_dim=2, miss
             for layer in range(L):
                 batch = streams.state_batch(rng, st.tokens[layer, :, :cfg.dbs], cfg.prefill, cfg.top_k,
                                             cfg.miss_ratio, zipf_s=cfg.zipf_s, miss_pool=miss_pool)
-                e_slots, e_miss = st.update(layer, batch, req_pool, seq, R)
+                e_slots, e_miss = st.update(layer, batch, req_pool, seq, R, threads=oracle_threads)
+                per_req = e_miss.sum(axis=1)
+                print("  step", step, "layer", layer, "misses per request min", int(per_req.min()), flush=True)
+                assert per_req.min() >= min_misses, (step, layer, per_req)
                 topk_d = torch.from_numpy(batch).cuda()
                 coord.sieve_update(layer, topk_d)
                 hot_l = hot_dev[layer]
@@ -154,11 +159,16 @@ def test_large_batch_striped_gather_parity(kvops):
 
 
 def test_slot_limit_gather_parity(kvops):
-    """65518-slot rows with colliding hashes (HBM-resident table), 8192 positions."""
+    """65518-slot rows with colliding hashes (HBM-resident table), 8192
+    positions, 90% misses drawn from the 81,922 positions whose hashes share
+    the table's first 40,960 homes: over 7,000 misses per request on every
+    step (each one an eviction, a backward-shift deletion and an insert inside
+    one long probe run)."""
     cfg = CONFIGS[4]
-    moved, done = _decode_parity(kvops, cfg, layers=2, steps=2, fused=True, seed_src=73,
-                                 miss_pool=streams.adversarial_pool(cfg.prefill))
-    assert done == 4 and moved > 4 * 7000
+    moved, done = _decode_parity(kvops, cfg, layers=1, steps=3, fused=True, seed_src=73,
+                                 miss_pool=streams.adversarial_pool(cfg.prefill, cfg.adversarial_hash_below),
+                                 min_misses=7000, oracle_threads=4)
+    assert done == 3 and moved > 3 * 4 * 7000
 
 
 def test_large_batch_full_export(kvops):

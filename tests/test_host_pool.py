@@ -111,10 +111,37 @@ def test_state_batch_miss_fraction():
 
 
 def test_adversarial_pool_collides():
-    pool = streams.adversarial_pool(CONFIGS[4].prefill, 4096)
-    assert len(pool) > 0
+    cfg = CONFIGS[4]
+    pool = streams.adversarial_pool(cfg.prefill, cfg.adversarial_hash_below)
     h = (pool.astype(np.uint64) * np.uint64(2654435761) % np.uint64(1 << 32)) >> np.uint64(16)
-    assert (h < 4096).all()
+    assert (h < cfg.adversarial_hash_below).all()
+    # every position with a hash below the bound is in the pool
+    t = np.arange(cfg.prefill, dtype=np.uint64)
+    all_h = (t * np.uint64(2654435761) % np.uint64(1 << 32)) >> np.uint64(16)
+    assert len(pool) == int((all_h < cfg.adversarial_hash_below).sum()) == 81922
+    # more candidates than a full buffer plus one step's misses: the pool
+    # never runs dry, whatever the buffer holds
+    assert len(pool) > cfg.dbs + cfg.miss_ratio * cfg.top_k
+
+
+def test_adversarial_stream_misses_every_step():
+    """The slot-limit stress stream keeps its 90% misses step after step (the
+    oracle's state drives the draw): over 7,000 misses per request on each of
+    the first three steps."""
+    from oracle import oracle as orc
+
+    cfg = CONFIGS[4]
+    pool = streams.adversarial_pool(cfg.prefill, cfg.adversarial_hash_below)
+    st = orc.SieveState(1, cfg.req_num, cfg.dbs, cfg.top_k)
+    for r in range(cfg.req_num):
+        st.admit(r, cfg.prefill)
+    rng = np.random.default_rng(cfg.seed)
+    for _ in range(3):
+        batch = streams.state_batch(rng, st.tokens[0, :, :cfg.dbs], cfg.prefill, cfg.top_k, cfg.miss_ratio,
+                                    miss_pool=pool)
+        _, miss = st.update(0, batch, np.arange(cfg.req_num), np.full(cfg.req_num, cfg.prefill), cfg.req_num,
+                            threads=4)
+        assert miss.sum(axis=1).min() >= 7000
 
 
 @pytest.mark.parametrize("bad", ["gpu", -1, 1024, 1.0, True, None])

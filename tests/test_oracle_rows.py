@@ -61,9 +61,14 @@ def _gather_case(rng, S, N, stride, block_dim):
                 stride=stride, block_dim=block_dim, hot_rows=hot_rows)
 
 
-def _model_gather(c, my_node):
-    """Forward walk: later positions overwrite earlier ones."""
+def _model_gather(c, my_node, plsr=None):
+    """Forward walk: later positions overwrite earlier ones.  With plsr, a
+    row whose segment row is >= plsr is not read: it still claims its
+    destination (so the destination keeps its old bytes if it is the last
+    claim) and still counts as queued, and the first such position of a
+    block sets that block's error field."""
     hot = {}
+    first_err = {}
     counts = np.zeros(c["block_dim"], dtype=np.int64)
     numr = max(0, min(c["num_real"], c["max_num_reqs"]))
     total = numr * c["top_k"]
@@ -75,17 +80,22 @@ def _model_gather(c, my_node):
             continue
         row = int(c["host_base"][b]) + t
         node = (row // c["S"]) % c["N"] if c["S"] else 0
+        seg_row = (row // c["S"]) // c["N"] if c["S"] else row
+        inside = plsr is None or seg_row < plsr
         dst = slot + b * c["stride"]
-        hot[dst] = (node, row)
+        hot[dst] = (node, row, inside)
         if node == my_node:
             counts[p // ppc] += 1
+            if not inside:
+                first_err.setdefault(p // ppc, p)
     words = []
     for b in range(c["block_dim"]):
         if b * ppc >= total:
             words.append(1 << 32)
         else:
-            words.append((int(counts[b]) << 40) | (1 << 32))
-    return {d: r for d, (n, r) in hot.items() if n == my_node}, words
+            err = (0x200 + (first_err[b] & 0xFF) + (1 << 16)) if b in first_err else 0
+            words.append((int(counts[b]) << 40) | (1 << 32) | err)
+    return {d: r for d, (n, r, ok) in hot.items() if n == my_node and ok}, words
 
 
 @pytest.mark.parametrize("seed", range(6))
@@ -130,6 +140,42 @@ def _model_gather_all(c):
     for my in range(c["N"]):
         dests |= set(_model_gather(c, my)[0])
     return dests
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("S,N,stride,block_dim", [(1, 2, 0, 1), (1, 4, 12, 3), (64, 2, 12, 8), (3, 3, 12, 2)])
+def test_gather_rows_past_layer_region(seed, S, N, stride, block_dim):
+    """Host rows past the layer region (segment row >= plsr, reachable when a
+    request's host base sits near the end of the layer's rows): not read,
+    counted as queued, still the winner of their destination, and the lowest
+    such position of each block reported in the 0x200 band."""
+    rng = np.random.default_rng(500 + 100 * seed + 7 * N + S)
+    c = _gather_case(rng, S, N, stride, block_dim)
+    edge = N * c["plsr"] * max(S, 1)  # the first global row past the region
+    c["host_base"] = c["host_base"] + (edge - 60)
+    c["num_real"] = c["max_num_reqs"]
+    errs = 0
+    for my in range(N):
+        hot = np.full(c["hot_rows"] * ROW_BYTES, 0xA5, dtype=np.uint8)
+        n, words = orc.gather_rows(c["segs"], hot, c["layer"] * c["plsr"], ROW_BYTES, c["topk"], c["req_pool"],
+                                   c["host_base"], c["slots"], c["is_miss"], c["num_real"], c["top_k"],
+                                   c["max_num_reqs"], S, N, my, hot_req_stride_rows=c["stride"],
+                                   block_dim=block_dim, per_layer_seg_rows=c["plsr"])
+        want, want_words = _model_gather(c, my, plsr=c["plsr"])
+        assert list(words) == want_words
+        assert n == len(want)
+        errs += sum(1 for w in want_words if w & 0xFFFFFFFF)
+        for dst in range(c["hot_rows"]):
+            got = hot[dst * ROW_BYTES:(dst + 1) * ROW_BYTES]
+            if dst in want:
+                row = want[dst]
+                node = (row // S) % N if S else 0
+                seg_row = (row // S) // N if S else row
+                off = (c["layer"] * c["plsr"] + seg_row) * ROW_BYTES
+                np.testing.assert_array_equal(got, c["segs"][node][off:off + ROW_BYTES])
+            else:
+                assert (got == 0xA5).all()
+    assert errs > 0
 
 
 def test_gather_empty_slice_words():
