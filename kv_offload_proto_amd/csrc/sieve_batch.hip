@@ -338,6 +338,389 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_slots(BatchParams
     }
 }
 
+// ---------------------------------------------------------------------------
+// The step's decisions in parallel (rows whose hand does not wrap).
+//
+// Within a step the hand passes each slot at most once, so a slot's fate
+// depends on its class (the decision of the in-order recurrence,
+// hisp_sieve_update.cpp:115-163): visited before the step (passed: cleared,
+// set again by a later hit); unvisited and not hit (evicted by whichever miss
+// the hand serves when it arrives); unvisited with its first hit at position k
+// (evicted iff the hand arrives while serving a miss before k; the hit at k is
+// then itself a miss, a conversion).  Walking the ring from the hand, slot i
+// of the last class is evicted iff a_i = cc_i - n_i - 1 >= D_i, with cc_i the
+// misses of non-resident tokens before k_i, n_i the unvisited unhit slots
+// before i and D_i the evicted slots of the same class before i with a later
+// first hit.  a_i < 0: passed; a_i >= U_i (the same count over every earlier
+// slot with a_j >= 0, a bound on D_i): evicted; the rest in ring order.  The
+// misses, in position order, take the evicted slots in ring order.  The hand
+// stops at the last one; a slot passed while serving miss r is visited at the
+// end iff a hit on it comes after that miss.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPdMaxSM = 512;  // slots of the last class within reach (more: the in-order loop)
+
+struct PdLds {
+    uint32_t *code, *slotOut;
+    uint64_t *visB, *evB;     // visited bits; evB: the step's hit slots, then its evicted slots
+    unsigned char *regA;      // scratch (the deleted-cell bitmap's LDS, unused while deciding)
+    uint32_t regABytes;
+    unsigned char *regB;      // scratch (the walk's stage)
+    uint32_t regBBytes;
+};
+
+__device__ __forceinline__ uint64_t low_bits(uint32_t n) { return n >= 64u ? ~0ull : ((1ull << n) - 1ull); }
+
+// n <= 64 bits of an absolute slot bitmap from slot `start` (start + n <= dbs)
+__device__ __forceinline__ uint64_t bits_at(const uint64_t *bm, uint32_t start, uint32_t n)
+{
+    if (n == 0u) return 0ull;
+    const uint32_t w = start >> 6, o = start & 63u;
+    uint64_t v = bm[w] >> o;
+    if (o != 0u && o + n > 64u) v |= bm[w + 1u] << (64u - o);
+    return v & low_bits(n);
+}
+
+// Ring word j: the 64 ring offsets [64j, 64j + 64) from the hand (slot
+// (hand + offset) mod dbs), as bits of an absolute slot bitmap.
+__device__ __forceinline__ uint64_t ring_word(const uint64_t *bm, uint32_t j, uint32_t hand, uint32_t dbs)
+{
+    const uint32_t r0 = j << 6;
+    const uint32_t len = dbs - r0 < 64u ? dbs - r0 : 64u;
+    const uint32_t s0 = hand + r0 < dbs ? hand + r0 : hand + r0 - dbs;
+    const uint32_t n1 = dbs - s0 < len ? dbs - s0 : len;
+    uint64_t v = bits_at(bm, s0, n1);
+    if (len > n1) v |= bits_at(bm, 0u, len - n1) << n1;
+    return v;
+}
+
+// Exclusive prefix sum of one value per thread of the block; total in *tot.
+__device__ __forceinline__ uint32_t block_exscan(uint32_t v, uint32_t *tot, uint32_t *sPart)
+{
+    const uint32_t lane = static_cast<uint32_t>(__lane_id()), wave = threadIdx.x >> 6;
+    uint32_t inc = v;
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(inc), d));
+        if (lane >= static_cast<uint32_t>(d)) inc += o;
+    }
+    if (lane == 63u) sPart[wave] = inc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int w = 0; w < kBatchWaves; ++w) {
+            const uint32_t x = sPart[w];
+            sPart[w] = run;
+            run += x;
+        }
+        sPart[kBatchWaves] = run;
+    }
+    __syncthreads();
+    const uint32_t r = sPart[wave] + inc - v;
+    *tot = sPart[kBatchWaves];
+    __syncthreads();
+    return r;
+}
+
+// Offset of the r-th set bit (r < popcount) of x.
+__device__ __forceinline__ uint32_t select_bit(uint64_t x, uint32_t r)
+{
+    uint32_t base = 0;
+    for (uint32_t w = 32; w >= 1; w >>= 1) {
+        const uint64_t lo = x & low_bits(w);
+        const uint32_t c = static_cast<uint32_t>(__builtin_popcountll(lo));
+        if (r >= c) {
+            r -= c;
+            x >>= w;
+            base += w;
+        } else {
+            x = lo;
+        }
+    }
+    return base;
+}
+
+// All threads call it; true: the step is decided (slotOut from firstMiss on,
+// visB, evB = evicted slots, *hand, *misses); false: nothing was changed and
+// the in-order loop decides.
+__device__ bool decide_parallel(const PdLds &L, int32_t K, int32_t dbs, int32_t hand0, int32_t firstMiss,
+                                int32_t *outHand, int32_t *outMisses)
+{
+    __shared__ uint32_t sPart[kBatchWaves + 1];
+    __shared__ uint32_t sRel, sNev, sEnd;
+    const uint32_t tid = threadIdx.x, lane = static_cast<uint32_t>(__lane_id());
+    const uint32_t D = static_cast<uint32_t>(dbs);
+    const uint32_t hand = (hand0 < 0 || hand0 >= dbs) ? 0u : static_cast<uint32_t>(hand0);
+    const uint32_t nR = (D + 63u) / 64u, nW = nR;  // ring words; absolute words of the slot bitmaps
+    const uint32_t nP = (static_cast<uint32_t>(K) + 63u) / 64u;  // position words
+    // scratch: ring masks and their prefix counts (A); the candidate list and
+    // the position bitmaps (B)
+    const uint32_t needA = nR * 8u * 2u + (nR + 1u) * 4u * 2u;
+    const uint32_t needB = kPdMaxSM * 8u * 2u + nP * 8u * 2u + (nP + 1u) * 4u * 2u;
+    if (needA > L.regABytes || needB > L.regBBytes || nP > static_cast<uint32_t>(BT)) return false;
+    uint64_t *snR = reinterpret_cast<uint64_t *>(L.regA);       // ring: unvisited, unhit (then: evicted)
+    uint64_t *relR = snR + nR;                                   // ring: candidate slots of the last class
+    uint32_t *snPre = reinterpret_cast<uint32_t *>(relR + nR);
+    uint32_t *relPre = snPre + nR + 1u;
+    uint64_t *list0 = reinterpret_cast<uint64_t *>(L.regB);     // candidates, unordered: ring << 40 | k << 20 | a
+    uint64_t *list = list0 + kPdMaxSM;                           // the same in ring order
+    uint64_t *cB = list + kPdMaxSM;                               // positions: non-resident first occurrences
+    uint64_t *eB = cB + nP;                                       // positions: every miss
+    uint32_t *cPre = reinterpret_cast<uint32_t *>(eB + nP);
+    uint32_t *ePre = cPre + nP + 1u;
+    auto ringOf = [&](uint32_t s) { return s >= hand ? s - hand : s + D - hand; };
+    auto slotOf = [&](uint32_t r) { return hand + r < D ? hand + r : hand + r - D; };
+    auto below = [](uint32_t b) { return low_bits(b); };
+    const uint32_t k0 = static_cast<uint32_t>(firstMiss);
+
+    // 1. positions from the first miss: non-resident first occurrences; the
+    // slots hit by resident first occurrences (evB, zero until now)
+    for (uint32_t w = tid; w < nP; w += BT) {
+        cB[w] = 0ull;
+        eB[w] = 0ull;
+    }
+    if (tid == 0) {
+        sRel = 0u;
+        sNev = 0u;
+    }
+    __syncthreads();
+    for (uint32_t k = k0 + tid; k < static_cast<uint32_t>(K); k += BT) {
+        const uint32_t c = L.code[k];
+        if (c == kNotRes) {
+            atomicOr(reinterpret_cast<unsigned long long *>(cB + (k >> 6)), 1ull << (k & 63u));
+        } else if (c != kInvalid && c != kExt && !(c & kDup)) {
+            atomicOr(reinterpret_cast<unsigned long long *>(L.evB + (c >> 6)), 1ull << (c & 63u));
+        }
+    }
+    __syncthreads();
+    // 2. ring words: unvisited unhit slots, counted in ring order
+    uint32_t mySn = 0;
+    if (tid < nR) {
+        const uint32_t len = D - (tid << 6) < 64u ? D - (tid << 6) : 64u;
+        const uint64_t v = ring_word(L.visB, tid, hand, D), h = ring_word(L.evB, tid, hand, D);
+        const uint64_t sn = ~v & ~h & low_bits(len);
+        snR[tid] = sn;
+        relR[tid] = 0ull;
+        mySn = static_cast<uint32_t>(__builtin_popcountll(sn));
+    }
+    uint32_t totSN = 0;
+    const uint32_t snEx = block_exscan(mySn, &totSN, sPart);
+    if (tid < nR) snPre[tid] = snEx;
+    uint32_t myC = tid < nP ? static_cast<uint32_t>(__builtin_popcountll(cB[tid])) : 0u;
+    uint32_t M = 0;
+    const uint32_t cEx = block_exscan(myC, &M, sPart);
+    if (tid < nP) cPre[tid] = cEx;
+    __syncthreads();
+    // from here on a refusal clears the hit bits (evB starts the in-order loop empty)
+    auto refuse = [&]() {
+        for (uint32_t w = tid; w < nW; w += BT) L.evB[w] = 0ull;
+        __syncthreads();
+        return false;
+    };
+    // every non-resident first occurrence needs an unvisited unhit slot
+    // within one turn of the ring (more: the hand wraps)
+    if (totSN < M) return refuse();
+    // 3. candidates of the last class within reach (a >= 0)
+    for (uint32_t k = k0 + tid; k < static_cast<uint32_t>(K); k += BT) {
+        const uint32_t c = L.code[k];
+        if (c == kInvalid || c == kExt || c == kNotRes || (c & kDup)) continue;
+        if ((L.visB[c >> 6] >> (c & 63u)) & 1ull) continue;  // visited: passed
+        const uint32_t r = ringOf(c), j = r >> 6;
+        const uint32_t n = snPre[j] + static_cast<uint32_t>(__builtin_popcountll(snR[j] & below(r & 63u)));
+        const uint32_t cc = cPre[k >> 6] + static_cast<uint32_t>(__builtin_popcountll(cB[k >> 6] & below(k & 63u)));
+        if (cc < n + 1u) continue;  // a < 0: the hand reaches it while serving a miss after k (or never)
+        const uint32_t a = cc - n - 1u;
+        const uint32_t at = atomicAdd(&sRel, 1u);
+        if (at < kPdMaxSM) {
+            list0[at] = (static_cast<uint64_t>(r) << 40) | (static_cast<uint64_t>(k) << 20) | a;
+            atomicOr(reinterpret_cast<unsigned long long *>(relR + j), 1ull << (r & 63u));
+        }
+    }
+    __syncthreads();
+    const uint32_t nRel = sRel;
+    if (nRel > kPdMaxSM) return refuse();
+    uint32_t myRel = tid < nR ? static_cast<uint32_t>(__builtin_popcountll(relR[tid])) : 0u;
+    uint32_t relTot = 0;
+    const uint32_t relEx = block_exscan(myRel, &relTot, sPart);
+    if (tid < nR) relPre[tid] = relEx;
+    __syncthreads();
+    if (tid < nRel) {
+        const uint64_t e = list0[tid];
+        const uint32_t r = static_cast<uint32_t>(e >> 40), j = r >> 6;
+        list[relPre[j] + static_cast<uint32_t>(__builtin_popcountll(relR[j] & below(r & 63u)))] = e;
+    }
+    __syncthreads();
+    // 4. decide them: evicted for sure, passed, or in ring order
+    // state: 1 = evicted, 2 = undecided
+    uint32_t st = 0, myK = 0, myA = 0;
+    if (tid < nRel) {
+        const uint64_t e = list[tid];
+        myK = static_cast<uint32_t>(e >> 20) & 0xFFFFFu;
+        myA = static_cast<uint32_t>(e) & 0xFFFFFu;
+        uint32_t U = 0;
+        for (uint32_t i = 0; i < tid; ++i) U += ((static_cast<uint32_t>(list[i] >> 20) & 0xFFFFFu) > myK) ? 1u : 0u;
+        st = myA >= U ? 1u : 2u;
+    }
+    // the undecided ones in ring order by one wave; its lanes hold the list,
+    // entry i in lane i % 64 of register i / 64
+    {
+        uint32_t *sState = reinterpret_cast<uint32_t *>(list0);  // (the unordered list is dead)
+        if (tid < nRel) sState[tid] = st;
+        __syncthreads();
+        if (tid < 64) {
+            constexpr int R = kPdMaxSM / 64;
+            uint32_t ks[R], sts[R];
+#pragma unroll
+            for (int q = 0; q < R; ++q) {
+                const uint32_t i = static_cast<uint32_t>(q) * 64u + lane;
+                ks[q] = i < nRel ? (static_cast<uint32_t>(list[i] >> 20) & 0xFFFFFu) : 0u;
+                sts[q] = i < nRel ? sState[i] : 0u;
+            }
+#pragma unroll
+            for (int q = 0; q < R; ++q) {
+                uint64_t und = __ballot(sts[q] == 2u);
+                while (und) {
+                    const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(und));
+                    und &= und - 1ull;
+                    const uint32_t i = static_cast<uint32_t>(q) * 64u + l;
+                    const uint32_t ki = static_cast<uint32_t>(__shfl(static_cast<int>(ks[q]), static_cast<int>(l)));
+                    const uint32_t ai = static_cast<uint32_t>(list[i]) & 0xFFFFFu;
+                    uint32_t Dn = 0;
+#pragma unroll
+                    for (int q2 = 0; q2 < R; ++q2) {
+                        const uint32_t i2 = static_cast<uint32_t>(q2) * 64u + lane;
+                        Dn += static_cast<uint32_t>(__builtin_popcountll(__ballot(i2 < i && sts[q2] == 1u && ks[q2] > ki)));
+                    }
+                    const uint32_t dec = ai >= Dn ? 1u : 0u;
+                    if (lane == l) sts[q] = dec;
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < R; ++q) {
+                const uint32_t i = static_cast<uint32_t>(q) * 64u + lane;
+                if (i < nRel) sState[i] = sts[q];
+            }
+        }
+        __syncthreads();
+        st = tid < nRel ? sState[tid] : 0u;
+    }
+    // 5. evictions in ring order: the unvisited unhit slots and the evicted
+    // slots of the last class; the misses are the non-resident first
+    // occurrences and the conversions, the hand stops at the last one
+    if (st == 1u) {
+        const uint32_t r = static_cast<uint32_t>(list[tid] >> 40);
+        atomicOr(reinterpret_cast<unsigned long long *>(snR + (r >> 6)), 1ull << (r & 63u));
+        atomicOr(reinterpret_cast<unsigned long long *>(eB + (myK >> 6)), 1ull << (myK & 63u));
+        atomicAdd(&sNev, 1u);
+    }
+    __syncthreads();
+    const uint32_t E = M + sNev;
+    uint32_t myEv = tid < nR ? static_cast<uint32_t>(__builtin_popcountll(snR[tid])) : 0u;
+    uint32_t evTot = 0;
+    const uint32_t evEx = block_exscan(myEv, &evTot, sPart);
+    if (tid < nR) {
+        snPre[tid] = evEx;
+        if (E > 0u && evEx <= E - 1u && E - 1u < evEx + myEv) sEnd = (tid << 6) + select_bit(snR[tid], E - 1u - evEx);
+    }
+    if (tid < nP) eB[tid] |= cB[tid];
+    __syncthreads();
+    if (evTot < E) return refuse();  // not reachable (the count of unhit slots was checked)
+    const uint32_t endRing = sEnd;
+    uint32_t myE = tid < nP ? static_cast<uint32_t>(__builtin_popcountll(eB[tid])) : 0u;
+    uint32_t eTot = 0;
+    const uint32_t eEx = block_exscan(myE, &eTot, sPart);
+    if (tid < nP) ePre[tid] = eEx;
+    __syncthreads();
+    // 6. outputs: misses take the evicted slot of their rank; hits keep theirs
+    auto evictedSlot = [&](uint32_t r) {  // the r-th eviction in ring order
+        uint32_t lo = 0, hi = nR;  // the last word whose prefix is <= r
+        while (hi - lo > 1u) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (snPre[mid] <= r) lo = mid; else hi = mid;
+        }
+        return slotOf((lo << 6) + select_bit(snR[lo], r - snPre[lo]));
+    };
+    // (kNotRes carries the kDup bit: later occurrences are c & kDup other than it)
+    auto isDup = [](uint32_t c) { return c != kInvalid && c != kExt && c != kNotRes && (c & kDup); };
+    for (uint32_t k = k0 + tid; k < static_cast<uint32_t>(K); k += BT) {
+        const uint32_t c = L.code[k];
+        if (c == kInvalid || c == kExt || isDup(c)) continue;
+        if ((eB[k >> 6] >> (k & 63u)) & 1ull) {
+            const uint32_t r = ePre[k >> 6] + static_cast<uint32_t>(__builtin_popcountll(eB[k >> 6] & below(k & 63u)));
+            L.slotOut[k] = evictedSlot(r) | kMissBit;
+        } else {
+            L.slotOut[k] = c;
+        }
+    }
+    __syncthreads();
+    for (uint32_t k = k0 + tid; k < static_cast<uint32_t>(K); k += BT) {
+        const uint32_t c = L.code[k];
+        if (isDup(c)) L.slotOut[k] = L.slotOut[c & ~kDup] & 0xFFFFu;
+    }
+    // 7. visited bits: swept slots (ring offsets up to endRing) end cleared,
+    // or set when evicted; the rest keep theirs; then the hits
+    const uint32_t endSlot = slotOf(endRing);
+    auto sweptMask = [&](uint32_t w) {  // slots of word w with ring offset <= endRing
+        const uint32_t a0 = w << 6, a1 = a0 + 64u < D ? a0 + 64u : D;
+        uint64_t m = 0;
+        // the swept slots: [hand, hand + endRing] mod dbs, one or two runs
+        const uint32_t e1 = hand + endRing;  // inclusive end, may pass dbs
+        const uint32_t r1lo = hand, r1hi = e1 < D ? e1 + 1u : D;
+        if (r1hi > a0 && r1lo < a1) {
+            const uint32_t lo = r1lo > a0 ? r1lo : a0, hi = r1hi < a1 ? r1hi : a1;
+            m |= low_bits(hi - lo) << (lo - a0);
+        }
+        if (e1 >= D) {
+            const uint32_t r2hi = e1 - D + 1u;
+            if (r2hi > a0) {
+                const uint32_t hi = r2hi < a1 ? r2hi : a1;
+                m |= low_bits(hi - a0);
+            }
+        }
+        return m;
+    };
+    uint64_t nv = 0, ne = 0;
+    if (tid < nW) {
+        const uint32_t a0 = tid << 6, len = D - a0 < 64u ? D - a0 : 64u;
+        const uint64_t v = L.visB[tid], h = L.evB[tid], sw = sweptMask(tid);
+        const uint64_t sn = ~v & ~h & low_bits(len);
+        nv = (v & ~sw) | (sn & sw);
+        ne = sn & sw;
+    }
+    __syncthreads();
+    if (tid < nW) {
+        L.visB[tid] = nv;
+        L.evB[tid] = ne;
+    }
+    __syncthreads();
+    if (st == 1u) {
+        const uint32_t s = slotOf(static_cast<uint32_t>(list[tid] >> 40));
+        atomicOr(reinterpret_cast<unsigned long long *>(L.visB + (s >> 6)), 1ull << (s & 63u));
+        atomicOr(reinterpret_cast<unsigned long long *>(L.evB + (s >> 6)), 1ull << (s & 63u));
+    }
+    __syncthreads();
+    for (uint32_t k = k0 + tid; k < static_cast<uint32_t>(K); k += BT) {
+        const uint32_t c = L.code[k];
+        if (c == kInvalid || c == kExt || c == kNotRes) continue;
+        const uint32_t so = L.slotOut[k];
+        if (so & kMissBit) continue;
+        const uint32_t s = so & 0xFFFFu;
+        const uint32_t r = ringOf(s);
+        bool set = true;
+        if (r <= endRing) {
+            if ((L.evB[s >> 6] >> (s & 63u)) & 1ull) continue;  // evicted: visited already
+            // passed while serving the miss of rank rs: visited again iff this hit comes after it
+            const uint32_t j = r >> 6;
+            const uint32_t rs = snPre[j] + static_cast<uint32_t>(__builtin_popcountll(snR[j] & below(r & 63u)));
+            const uint32_t before = ePre[k >> 6] + static_cast<uint32_t>(__builtin_popcountll(eB[k >> 6] & below(k & 63u)));
+            set = before > rs;
+        }
+        if (set) atomicOr(reinterpret_cast<unsigned long long *>(L.visB + (s >> 6)), 1ull << (s & 63u));
+    }
+    __syncthreads();
+    *outHand = static_cast<int32_t>(endSlot + 1u == D ? 0u : endSlot + 1u);
+    *outMisses = static_cast<int32_t>(E);
+    return true;
+}
+
 __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -724,66 +1107,106 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
         __syncthreads();
     }
-    if (canonical && sBad == 0 && tid < 64) {
-        // One wave, 64 positions per round: up to the round's first miss
-        // every position is a hit (a resident first occurrence whose slot the
-        // hand has not evicted, or a later occurrence) and is applied at
-        // once; the miss then sweeps.  The wave's LDS operations complete in
-        // order, so a sweep sees the visited bits set before it.
+    bool decided = false;
+    if (canonical && sBad == 0 && sFirstMiss < K) {
+        const PdLds pl{code, slotOut, visB, evB, reinterpret_cast<unsigned char *>(delB), nCellW * 8u,
+                       reinterpret_cast<unsigned char *>(stage), kBatchStage * 4u};
+        int32_t ph = 0, pm = 0;
+        decided = decide_parallel(pl, K, dbs, hand0, sFirstMiss, &ph, &pm);
+        if (decided && tid == 0) {
+            sHand = ph;
+            sWrap = 0;
+            sMisses = pm;
+        }
+    }
+    if (canonical && sBad == 0 && !decided && tid < 64) {
+        // One wave, 64 positions per round, in position order.  What each
+        // position needs from LDS is read for the whole round at once (its
+        // code; for a resident first occurrence whether an earlier round
+        // evicted its slot; for a later occurrence of an earlier round's
+        // token that token's slot).  The positions are then decided one at a
+        // time in scalar registers: the hand, the visited word it sweeps, the
+        // round's evictions (in lanes) and results (in lanes).  A hit's
+        // visited bit goes to that word, or to LDS with an atomic OR when it
+        // lies elsewhere; the wave's LDS operations complete in order, so a
+        // word the sweep loads later holds it.
         int32_t hand = hand0;
         if (hand < 0 || hand >= dbs) hand = 0;  // hisp_sieve_update.cpp:108-111
         int32_t passed = 0, nMiss = 0;
         bool wrapped = false;
         const uint32_t lastW = nVisW - 1u;
         const uint64_t lastMask = (dbs & 63) ? ((1ull << (dbs & 63)) - 1ull) : ~0ull;
-        // from the round of the first miss (the positions before it applied
-        // again change nothing)
+        uint32_t cwIdx = static_cast<uint32_t>(hand) >> 6;  // the visited word held in registers
+        uint64_t cwVal = uniform64(visB[cwIdx]);
+        // lane classes of a round: a hit candidate on slot v, a later
+        // occurrence of lane v's token, a hit on slot v, a miss
+        constexpr uint32_t kRes = 1u << 24, kDupLane = 2u << 24, kHit = 3u << 24, kMiss = 4u << 24;
+        // from the round of the first miss (the positions before it, applied
+        // again, change nothing)
         for (int32_t k0 = sFirstMiss & ~63; k0 < K && !wrapped; k0 += 64) {
             const int32_t k = k0 + static_cast<int32_t>(lane);
             const uint32_t c = k < K ? code[k] : kInvalid;
-            const bool rel = c != kInvalid && c != kExt;
-            const bool res = rel && c != kNotRes && !(c & kDup);  // resident first occurrence: c is its slot
-            const bool dup = rel && c != kNotRes && (c & kDup);
-            const uint32_t cs = res ? c : 0u;  // an in-range slot for every lane
-            uint64_t pend = __ballot(rel);
+            uint32_t info = 0u;
+            if (c == kNotRes) {
+                info = kMiss;
+            } else if (c != kInvalid && c != kExt) {
+                if (c & kDup) {
+                    const int32_t f = static_cast<int32_t>(c & ~kDup);
+                    info = f >= k0 ? (kDupLane | static_cast<uint32_t>(f - k0)) : (kHit | (slotOut[f] & 0xFFFFu));
+                } else {
+                    info = bit_get(evB, c) ? kMiss : (kRes | c);
+                }
+            }
+            uint64_t pend = __ballot(info != 0u);
+            uint32_t result = 0u;             // lane j: position k0 + j's slot (| kMissBit)
+            uint32_t evRound = 0xFFFFFFFFu;   // lane i: the round's i-th eviction
+            int32_t nEv = 0;
             while (pend) {
-                const bool mine = (pend >> lane) & 1ull;
-                const bool missNow = mine && (c == kNotRes || (res && bit_get(evB, cs)));
-                const uint64_t mm = __ballot(missNow);
-                const int j = mm ? __builtin_ctzll(mm) : 64;
-                const uint64_t seg = pend & (j < 64 ? ((1ull << j) - 1ull) : ~0ull);
-                if (((seg >> lane) & 1ull) && res) {
-                    slotOut[k] = c;
-                    atomicOr(reinterpret_cast<unsigned long long *>(visB + (c >> 6)), 1ull << (c & 63));
+                const int j = __builtin_ctzll(pend);
+                pend &= pend - 1ull;
+                const uint32_t inf = static_cast<uint32_t>(lane_value(static_cast<int32_t>(info), j));
+                const uint32_t kd = inf & 0xFF000000u, val = inf & 0xFFFFFFu;
+                bool miss = kd == kMiss;
+                uint32_t sl = val;
+                if (kd == kRes) {
+                    // evicted earlier in this round: the hit becomes a miss
+                    const uint64_t inRound = nEv == 0 ? 0ull : (nEv >= 64 ? ~0ull : ((1ull << nEv) - 1ull));
+                    miss = (__ballot(evRound == val) & inRound) != 0ull;
+                } else if (kd == kDupLane) {
+                    sl = static_cast<uint32_t>(lane_value(static_cast<int32_t>(result), static_cast<int32_t>(val))) & 0xFFFFu;
                 }
-                if (((seg >> lane) & 1ull) && dup) {
-                    // the first occurrence came earlier (an earlier round or
-                    // the slots just written): a hit on its slot, visited again
-                    const uint32_t sd = slotOut[c & ~kDup] & 0xFFFFu;
-                    slotOut[k] = sd;
-                    atomicOr(reinterpret_cast<unsigned long long *>(visB + (sd >> 6)), 1ull << (sd & 63));
+                if (!miss) {
+                    if ((sl >> 6) == cwIdx) {
+                        cwVal |= 1ull << (sl & 63u);
+                    } else if (lane == 0) {
+                        atomicOr(reinterpret_cast<unsigned long long *>(visB + (sl >> 6)), 1ull << (sl & 63u));
+                    }
+                    result = static_cast<uint32_t>(lane_set(static_cast<int32_t>(result), j, static_cast<int32_t>(sl)));
+                    continue;
                 }
-                pend &= ~seg;
-                if (j == 64) break;
                 // the miss: the hand passes visited slots, clearing them, and
                 // stops at the first unvisited one
                 int32_t h = -1;
                 while (h < 0) {
                     const uint32_t wi = static_cast<uint32_t>(hand) >> 6;
+                    if (wi != cwIdx) {
+                        if (lane == 0) visB[cwIdx] = cwVal;
+                        cwIdx = wi;
+                        cwVal = uniform64(visB[wi]);
+                    }
                     const uint32_t b = static_cast<uint32_t>(hand) & 63u;
                     const uint64_t inRing = wi == lastW ? lastMask : ~0ull;
-                    const uint64_t word = visB[wi];
-                    const uint64_t unv = ~word & inRing & (~0ull << b);
+                    const uint64_t unv = ~cwVal & inRing & (~0ull << b);
                     if (unv) {
                         const uint32_t f = static_cast<uint32_t>(__builtin_ctzll(unv));
                         const uint64_t cleared = ((1ull << f) - 1ull) & (~0ull << b);  // visited bits passed
                         passed += static_cast<int32_t>(f - b) + 1;
                         h = static_cast<int32_t>((wi << 6) + f);
-                        if (lane == 0) visB[wi] = (word & ~cleared) | (1ull << f);
+                        cwVal = (cwVal & ~cleared) | (1ull << f);
                     } else {
                         const uint64_t cleared = inRing & (~0ull << b);
                         passed += static_cast<int32_t>(__builtin_popcountll(cleared));
-                        if (lane == 0) visB[wi] = word & ~cleared;
+                        cwVal &= ~cleared;
                         hand = wi == lastW ? 0 : static_cast<int32_t>((wi + 1u) << 6);
                     }
                     if (passed > dbs) {
@@ -792,16 +1215,20 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                     }
                 }
                 if (wrapped) break;
-                if (lane == 0) {
-                    evB[h >> 6] |= 1ull << (h & 63);
-                    slotOut[k0 + j] = static_cast<uint32_t>(h) | kMissBit;
-                }
+                evRound = static_cast<uint32_t>(lane_set(static_cast<int32_t>(evRound), nEv, h));
+                ++nEv;
+                result = static_cast<uint32_t>(lane_set(static_cast<int32_t>(result), j, h | static_cast<int32_t>(kMissBit)));
                 ++nMiss;
                 hand = h + 1 == dbs ? 0 : h + 1;
-                pend &= ~(1ull << j);
+            }
+            if (wrapped) break;
+            if (info != 0u) slotOut[k] = result;
+            if (static_cast<int32_t>(lane) < nEv) {
+                atomicOr(reinterpret_cast<unsigned long long *>(evB + (evRound >> 6)), 1ull << (evRound & 63u));
             }
         }
         if (lane == 0) {
+            visB[cwIdx] = cwVal;
             sHand = hand;
             sWrap = wrapped ? 1 : 0;
             sMisses = nMiss;
@@ -915,6 +1342,13 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
             tbl[P.t.meta] = 1u;
             gHand[1] = kCanonFlag;  // the rebuild leaves the table consistent
         }
+#ifdef KVX_BATCH_STAMPS
+        KVX_STAMP(4);
+        if (tid == 0)
+            printf("stamps bid %d misses %d: check %llu decide %llu cleanup %llu handoff %llu\n", bid, sMisses,
+                   (unsigned long long)(stamp[1] - stamp[0]), (unsigned long long)(stamp[2] - stamp[1]),
+                   (unsigned long long)(stamp[3] - stamp[2]), (unsigned long long)(stamp[4] - stamp[3]));
+#endif
         return;
     }
     if (sMisses > 0) {
