@@ -290,11 +290,10 @@ __host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t htSize)
 }
 
 // LDS bytes of the rebuild's chunk kernel: per-home counts (16 bits, 2^16
-// homes), the free-cell window's three bitmap levels and the scan partials.
-constexpr uint32_t kTblHistBytes = 65536u * 2u;
+// homes and a 64-cell margin, read 8 at a time) and the free-cell window.
+constexpr uint32_t kTblHistBytes = 65536u * 2u + 256u;
 constexpr uint32_t kTblWinWords = kTblWinBits / 64u;
-constexpr uint32_t kTblWinL1 = (kTblWinWords + 63u) / 64u;
-constexpr uint32_t kTblLdsBytes = kTblHistBytes + (kTblWinWords + kTblWinL1 + 1u) * 8u;
+constexpr uint32_t kTblLdsBytes = kTblHistBytes + kTblWinWords * 8u;
 
 // Launchers (implemented next to their kernels).
 hipError_t launch_sieve_update(const HispSieveUpdateArgs &a, uint64_t overflowSlot, int variant,
