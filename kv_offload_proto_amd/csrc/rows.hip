@@ -16,6 +16,8 @@
 // status words with a system-scope release, after every workgroup fenced its
 // own row stores.  The reference's per-block Commit/Drain + MTE3 flush has the
 // same meaning: all rows of the launch have landed.
+#include <cstddef>
+
 #include "kvx_internal.h"
 
 namespace kvx {
@@ -487,6 +489,18 @@ struct ExportRowsParams {
     uint32_t *epoch;
 };
 
+// Segment base of `node` from the kernel's argument block, read in place
+// (the kernels' only argument starts at offset 0 of the argument segment):
+// indexing the by-value argument at run time would copy the whole block to
+// private memory.
+__device__ __forceinline__ uint64_t export_seg_base(uint32_t node)
+{
+    typedef __attribute__((address_space(4))) const uint64_t KU64;
+    typedef __attribute__((address_space(4))) const char KChar;
+    const KChar *k = (KChar *)__builtin_amdgcn_kernarg_segment_ptr();
+    return reinterpret_cast<KU64 *>(k + offsetof(ExportRowsParams, segBases))[node];
+}
+
 __device__ __forceinline__ bool export_row_target(const ExportRowsArgs &a, int64_t row, uint32_t &node,
                                                   uint32_t &segRow)
 {
@@ -559,7 +573,7 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
                 const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
                 copy = w >= P.winEntries || win_load(P.win + w) == (tagHi | static_cast<unsigned long long>(i));
                 src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
-                dst = (a.fused ? P.segBases[node] : a.segBase) +
+                dst = (a.fused ? export_seg_base(node) : a.segBase) +
                       (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;
             }
         }
@@ -668,7 +682,7 @@ __global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
                    win_load(P.win + w) ==
                        (tagHi | static_cast<unsigned long long>(i));
             src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
-            dst = (a.fused ? P.segBases[node] : a.segBase) +
+            dst = (a.fused ? export_seg_base(node) : a.segBase) +
                   (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;
         }
         const uint64_t cm = __ballot(copy);

@@ -441,7 +441,7 @@ __device__ __forceinline__ uint32_t select_bit(uint64_t x, uint32_t r)
 // All threads call it; true: the step is decided (slotOut from firstMiss on,
 // visB, evB = evicted slots, *hand, *misses); false: nothing was changed and
 // the in-order loop decides.
-__device__ bool decide_parallel(const PdLds &L, int32_t K, int32_t dbs, int32_t hand0, int32_t firstMiss,
+__device__ __forceinline__ bool decide_parallel(const PdLds L, int32_t K, int32_t dbs, int32_t hand0, int32_t firstMiss,
                                 int32_t *outHand, int32_t *outMisses)
 {
     __shared__ uint32_t sPart[kBatchWaves + 1];
@@ -754,10 +754,14 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         return;
     }
     // the prefill length, the flag and the hand as scalar loads, issued
-    // together (nothing in this launch writes them before they are read)
+    // together.  This kernel writes the flag and the hand later (the
+    // outputs, the end of the table update), and a load from the constant
+    // address space may be issued again at any later use: the two words pass
+    // through an opaque asm, so every use reads the registers loaded here.
     const int32_t prefill = ((KVX_CM const int32_t *)(a.prefillLens))[reqIdx];
-    const int32_t flagWord = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride + 1];
-    const int32_t hand0 = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride];  // phase 2's wave starts from it
+    int32_t flagWord = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride + 1];
+    int32_t hand0 = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride];  // phase 2 starts from it
+    asm volatile("" : "+s"(flagWord), "+s"(hand0));
     const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
     Row r;
     r.tok = reinterpret_cast<KVX_GM int32_t *>(a.deviceBufferTokens) + reqIdx * padded;

@@ -169,7 +169,7 @@ __device__ __forceinline__ void build_shadow(const Row &r)
 // The recurrence over every position of the row, run by one wave after the
 // shadow is built: outputs rs/rm, state updated in place, the hand stored in
 // gHand[0] and a bound violation reported to the tail slot.
-static __device__ void recurrence(const Row &r, const KVX_GM int32_t *rt, KVX_GM int32_t *rs, KVX_GM int8_t *rm,
+static __device__ __forceinline__ void recurrence(const Row r, const KVX_GM int32_t *rt, KVX_GM int32_t *rs, KVX_GM int8_t *rm,
                                   int32_t K, int32_t seqLen, int32_t prefill, KVX_GM int32_t *gHand,
                                   uint64_t overflowSlot)
 {

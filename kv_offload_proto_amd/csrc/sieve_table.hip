@@ -397,6 +397,7 @@ __device__ __forceinline__ void chunk_free_cells(uint32_t x0, uint32_t x1, uint3
     const uint32_t s0 = x0 + tid * seg;
     const uint32_t s1 = s0 + seg < x1 ? s0 + seg : x1;
     MP m{kNegInf, 0};
+#pragma unroll 2
     for (uint32_t x = s0; x < s1; x += 8u) {
         int32_t c[8];
         count8(x, c);
@@ -408,6 +409,7 @@ __device__ __forceinline__ void chunk_free_cells(uint32_t x0, uint32_t x1, uint3
     int32_t b = mp_apply(ex, 0);
     for (uint32_t xw = s0; xw < s1; xw += 64u) {
         uint64_t free = 0;
+#pragma unroll 2
         for (uint32_t x = xw; x < xw + 64u; x += 8u) {
             int32_t c[8];
             count8(x, c);
