@@ -542,6 +542,86 @@ def sieve_pipelined(runner, snap, warm, timed, log):
             "per_launch_median_us": per}
 
 
+def sieve_standard_events(runner, snap, warm, timed, fused, log):
+    """The decode loop again from the same starting state, each SIEVE launch
+    bracketed by torch events, whose record releases to system scope (a
+    write-back of the GPU caches): per-launch times that include that
+    write-back, beside the fence-free figures of the main loop."""
+    import torch
+
+    runner.restore(snap)
+    for ls in warm:
+        runner.sieve(ls.layer, ls.topk)
+        runner.gather(ls.layer, ls.topk, fused=fused)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in timed]
+    for (a, b), ls in zip(evs, timed):
+        a.record()
+        runner.sieve(ls.layer, ls.topk)
+        b.record()
+        runner.gather(ls.layer, ls.topk, fused=fused)
+    torch.cuda.synchronize()
+    us = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    log("[bench] SIEVE per launch with standard (system-release) events: median {:.2f} us, p99 {:.2f}".format(
+        pct(us, 50), pct(us, 99)))
+    return {"median": pct(us, 50), "p99": pct(us, 99), "mean": sum(us) / len(us),
+            "timing": "per launch inside the decode loop, torch events (system-scope release: includes the cache "
+                      "write-back each event record costs)"}
+
+
+def import_curve(runner, log, reps=20, warm=3):
+    """Import latency against batch size (the reference design's import
+    batch-size curve): one request of n positions, every one a miss with its
+    own token and slot, fused over the workload's segments, n = 16 .. 4096 rows
+    (the one-launch form) and 8192, 16384 (two launches)."""
+    import numpy as np
+    import torch
+    from kv_offload_proto_amd.kvops_ext import _kvops
+
+    cfg = runner.cfg
+    dev = runner.dev
+    rb, plsr = cfg.row_bytes, runner.pool.per_layer_seg_rows
+    fev = FenceFreeEvents()
+    stream = torch.cuda.current_stream()
+    status = runner.pool.next_status()
+    out = []
+    n_max = min(16384, cfg.layer_rows, runner.hot[0].shape[0])
+    n = 16
+    while n <= n_max:
+        rng = np.random.default_rng(n)
+        topk = torch.from_numpy(rng.permutation(min(cfg.layer_rows, 1 << 22))[:n].astype(np.int32)).to(dev).view(1, n)
+        slots = torch.arange(n, dtype=torch.int32, device=dev).view(1, n)
+        miss = torch.ones((1, n), dtype=torch.int8, device=dev)
+        pool_idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        base = torch.zeros(1, dtype=torch.int64, device=dev)
+        nr = torch.ones(1, dtype=torch.int32, device=dev)
+        hot = runner.hot[0]
+
+        def once():
+            _kvops.import_all(runner.seg_bases, 0, plsr, rb, topk.data_ptr(), pool_idx.data_ptr(), base.data_ptr(),
+                              slots.data_ptr(), miss.data_ptr(), nr.data_ptr(), hot.data_ptr(), n, 1,
+                              cfg.stripe_rows, status, stream.cuda_stream, 1, 0)
+
+        for _ in range(warm):
+            once()
+        torch.cuda.synchronize()
+        evs = [(fev.event(), fev.event()) for _ in range(reps)]
+        for a, b in evs:
+            fev.record(a, stream)
+            once()
+            fev.record(b, stream)
+        torch.cuda.synchronize()
+        us = [fev.elapsed_ms(a, b) * 1e3 for a, b in evs]
+        med = pct(us, 50)
+        out.append({"rows": n, "us_median": med, "GBps": n * rb / (med * 1e-6) / 1e9})
+        n *= 2
+    fev.close()
+    log("[bench] import latency by rows per layer: " + ", ".join(
+        "{}: {:.1f} us".format(e["rows"], e["us_median"]) for e in out))
+    return {"points": out, "what": "one request of n miss positions (own tokens and slots), fused import over the "
+                                   "segments, median of {} launches between fence-free events".format(reps)}
+
+
 def export_rows_pass(runner, log, reps=3):
     """Decode-incremental export: one row per request per layer (the row a
     decode step would append; here the last prefill row, rewritten with the
@@ -690,6 +770,9 @@ def main():
                    "bytes_per_launch": moved * cfg.row_bytes / len(timed),
                    "bytes_rule": "rows moved (distinct destinations after the winner rule) x row_bytes, read over "
                                  "the host link",
+                   "traffic_basis": "FETCH_SIZE + WRITE_SIZE of the listed kernels per layer-step: the host rows "
+                                    "read, the hot rows written and the index scan",
+                   "algorithmic_traffic": sum(hbm_bytes) / len(timed),
                    "avg_launch_us": sum(gather_us) / len(timed),
                    "hbm": {"achieved": hbm_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": hbm_gbps / HBM_PEAK_GBPS,
                            "bytes_rule": "rows moved x row_bytes read + written, + 9 B per position of index scan"}}
@@ -699,7 +782,13 @@ def main():
     sieve_roof = {"kernel": sieve_kernel, "bound": "hbm", "achieved": sieve_gbps_alg, "peak": HBM_PEAK_GBPS,
                   "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS,
                   "traffic": traffic_of(sieve_kernel), "traffic_source": traffic_src, "bytes_per_launch": sb,
+                  "traffic_basis": "FETCH_SIZE + WRITE_SIZE of the kernel per launch, against bytes_per_launch (the "
+                                   "row state read and written back, the batch row read, the outputs written)",
+                  "algorithmic_traffic": sb,
                   "avg_launch_us": sum(sieve_us) / len(timed)}
+    for roof in (gather_roof, sieve_roof):
+        t_, a_ = roof.get("traffic"), roof.get("algorithmic_traffic")
+        roof["traffic_over_algorithmic"] = (t_ / a_) if (t_ and a_) else None
     dominant, other = (gather_roof, sieve_roof) if sum(gather_us) >= sum(sieve_us) else (sieve_roof, gather_roof)
 
     value = rows / (total_ms * 1e-3)
@@ -737,9 +826,11 @@ def main():
         "verify": None if verify is None else verify["ok"],
         "verify_detail": verify,
     }
+    out["sieve_us_per_layer"]["standard_events"] = sieve_standard_events(runner, snap, warm, timed, fused, log)
     out["sieve_back_to_back"] = sieve_pipelined(runner, snap, warm, timed, log)
     out["graph"] = None if args.no_graph else graph_pass(runner, snap, warm, timed, fused, total_ms, log)
     out["export_rows"] = export_rows_pass(runner, log)
+    out["import_curve"] = import_curve(runner, log)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(runner, snap, plan, len(warm), args.cpu_sample_s, threads, log)
     else:

@@ -91,8 +91,10 @@ int kvx_import_all(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32
  * status words as kvx_import_all; it allocates nothing and creates no
  * per-stream scratch: its scratch is one fixed array per GPU (17.8 MB, held
  * from library load to process exit) shared by every call of this entry
- * point on that GPU, so calls that overlap on one GPU race (run them on one
- * stream, or order them).  Limit:
+ * point on that GPU, so calls must not overlap on one GPU: a call on another
+ * stream than the last one, while that one may still run, fails with an
+ * error (calls captured in a graph are not checked; their replays must not
+ * overlap other calls of this entry point).  Limit:
  * (max_num_reqs - 1) * min(hot_req_stride_rows, 65536) + 65536 <= 2228224;
  * a larger call fails with an error before anything is queued. */
 int kvx_import_all_noalloc(const uint64_t *seg_bases, uint32_t layer_offset_rows, uint32_t per_layer_seg_rows,

@@ -76,6 +76,11 @@ struct State {
     int forcedSieveVariant = -1;
     bool tableRebuild = false;      // the device's LDS holds the rebuild's chunk kernel
     void *noAllocScratch[64] = {};  // device address of `scratch`, per device (set at init)
+    // the last eager call of the no-allocation import per device: its stream
+    // and an event recorded after its launches (created at init)
+    hipEvent_t noAllocDone[64] = {};
+    uint64_t noAllocStream[64] = {};
+    bool noAllocPending[64] = {};
 };
 
 State g;
@@ -538,6 +543,10 @@ int kvx_init(int device_id, const char *code_object_path, const char *rt_lib)
             if (p == nullptr) throw Error("hipGetSymbolAddress(scratch) returned null");
             g.noAllocScratch[device_id] = p;
         }
+        if (g.noAllocDone[device_id] == nullptr) {
+            hipCheck(hipEventCreateWithFlags(&g.noAllocDone[device_id], hipEventDisableTiming),
+                     "hipEventCreateWithFlags(no-allocation import)");
+        }
         hipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
         g.inited = true;
     });
@@ -742,6 +751,20 @@ int kvx_import_all_noalloc(const uint64_t *seg_bases, uint32_t layer_offset_rows
         fixed.epoch = fixed.tickets + 9;
         fixed.win = reinterpret_cast<unsigned long long *>(b + kNoAllocControlBytes);
         fixed.winEntries = kNoAllocMaxWinEntries;
+        // every call on this GPU shares the fixed scratch: a call on another
+        // stream while the last one may still run is refused (the event query
+        // and record allocate nothing; under capture neither is issued, and a
+        // captured call must not overlap other calls of this entry point)
+        const int dev = g.device;
+        const bool capturing = Capturing(AsStream(stream));
+        if (!capturing && g.noAllocPending[dev] && g.noAllocStream[dev] != stream) {
+            const hipError_t q = hipEventQuery(g.noAllocDone[dev]);
+            if (q == hipErrorNotReady) {
+                throw Error("import_all_noalloc: a call on another stream may still be running on this GPU; its fixed "
+                            "scratch is shared by every call, so order the calls (synchronize that stream first)");
+            }
+            if (q != hipSuccess) hipCheck(q, "hipEventQuery(no-allocation import)");
+        }
         GatherCall c{};
         c.fused = true;
         c.nSeg = node_num;
@@ -766,6 +789,11 @@ int kvx_import_all_noalloc(const uint64_t *seg_bases, uint32_t layer_offset_rows
         c.blockDim = block_dim;
         c.stride = hot_req_stride_rows;
         DoGather(c, &fixed);
+        if (!capturing) {
+            hipCheck(hipEventRecord(g.noAllocDone[dev], AsStream(stream)), "hipEventRecord(no-allocation import)");
+            g.noAllocStream[dev] = stream;
+            g.noAllocPending[dev] = true;
+        }
     });
 }
 
@@ -1001,6 +1029,11 @@ int kvx_close(void)
             std::lock_guard<std::mutex> lk(g_statusMu);
             for (const Alloc &a : g.status) (void)hipHostFree(reinterpret_cast<void *>(a.addr));
             g.status.clear();
+        }
+        for (int d = 0; d < 64; ++d) {
+            if (g.noAllocDone[d] != nullptr) (void)hipEventDestroy(g.noAllocDone[d]);
+            g.noAllocDone[d] = nullptr;
+            g.noAllocPending[d] = false;
         }
         g.inited = false;
     });

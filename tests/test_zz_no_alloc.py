@@ -107,3 +107,95 @@ def test_import_all_noalloc_matches_import_all(kvops):
         assert torch.equal(before, hot_b)
     finally:
         pool.destroy(close_ext=False)
+
+
+def test_import_all_noalloc_fresh_stream_graph_and_overlap(kvops):
+    """The property the entry point exists for: calls on a stream the library
+    has never seen leave that stream without scratch (scratch_bytes 0), and a
+    call captured in a HIP graph (where any allocation is refused) replays
+    with the results of import_all.  Calls on two streams that may overlap
+    are refused: the fixed scratch is shared by every call on the GPU."""
+    L, R, prefill, dbs, top_k, N = 1, 8, 4096, 2048, 1024, 2
+    print("no-alloc fresh stream / graph / overlap", R, top_k, N, flush=True)
+    lib = _lib()
+    rows = R * prefill
+    pool = HostSegPool(0, L, rows, ROW, stripe_rows=1, node_num=N)
+    pool.create_pool()
+    try:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(43)
+        src = torch.randint(0, 256, (L, rows, ROW), dtype=torch.uint8, device="cuda", generator=g)
+        pool.wait(pool.batch_write_alllayers(0, rows, src, rows * ROW))
+        coord = XdsOffloadCoordinator("cuda", L, R, dbs, top_k, R, prefill)
+        st = orc.SieveState(L, R, dbs, top_k)
+        for r in range(R):
+            coord.admit_request(r, r, prefill, r * prefill)
+            st.admit(r, prefill)
+        coord.set_batch(torch.arange(R, dtype=torch.int64, device="cuda"),
+                        torch.full((R,), prefill, dtype=torch.int32, device="cuda"))
+        padded = coord.padded_buffer_size
+        batch = streams.state_batch(np.random.default_rng(14), st.tokens[0, :, :dbs], prefill, top_k, 0.3)
+        topk_d = torch.from_numpy(batch).cuda()
+        nr = torch.tensor([R], dtype=torch.int32, device="cuda")
+        coord.sieve_update(0, topk_d)
+        torch.cuda.synchronize()
+        hot_a = torch.zeros((R * padded, ROW), dtype=torch.uint8, device="cuda")
+        sa = kvops.alloc_status(N)
+        assert _call(lib, "kvx_import_all", pool, 0, topk_d, coord, nr, hot_a, top_k, R, sa, padded) == 0
+        pool.wait(sa, block_dim=2)
+        torch.cuda.synchronize()
+        want_words = [read_words(sa + s * 64, 2) for s in range(N)]
+
+        # a stream the library has never used: no scratch before or after
+        fresh = torch.cuda.Stream()
+        assert kvops.scratch_bytes(fresh.cuda_stream) == 0
+        hot_b = torch.zeros_like(hot_a)
+        sb = kvops.alloc_status(N)
+        with torch.cuda.stream(fresh):
+            assert _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_b, top_k, R, sb,
+                         padded) == 0, lib.kvx_last_error()
+        fresh.synchronize()
+        assert kvops.scratch_bytes(fresh.cuda_stream) == 0
+        assert torch.equal(hot_a, hot_b)
+        assert [read_words(sb + s * 64, 2) for s in range(N)] == want_words
+
+        # captured in a graph on another fresh stream, replayed three times
+        cap = torch.cuda.Stream()
+        hot_c = torch.zeros_like(hot_a)
+        sc = kvops.alloc_status(N)
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cap):
+            assert _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_c, top_k, R, sc,
+                         padded) == 0, lib.kvx_last_error()
+        assert kvops.scratch_bytes(cap.cuda_stream) == 0
+        for rep in range(3):
+            hot_c.zero_()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(hot_a, hot_c), rep
+            assert [read_words(sc + s * 64, 2) for s in range(N)] == want_words, rep
+        del graph
+
+        # overlap: a call queued behind a long kernel on one stream, then a
+        # call on another stream while the first may still run
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        hot_d = torch.zeros_like(hot_a)
+        sd = kvops.alloc_status(N)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s1):
+            torch.cuda._sleep(200_000_000)  # a bounded spin on the GPU (~0.1 s)
+            assert _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_d, top_k, R, sd,
+                         padded) == 0, lib.kvx_last_error()
+        with torch.cuda.stream(s2):
+            rc = _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_b, top_k, R, sb, padded)
+        assert rc != 0 and b"another stream" in lib.kvx_last_error()
+        s1.synchronize()
+        with torch.cuda.stream(s2):
+            assert _call(lib, "kvx_import_all_noalloc", pool, 0, topk_d, coord, nr, hot_b, top_k, R, sb,
+                         padded) == 0, lib.kvx_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(hot_a, hot_d) and torch.equal(hot_a, hot_b)
+    finally:
+        pool.destroy(close_ext=False)
