@@ -1124,68 +1124,75 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
     }
     if (canonical && sBad == 0 && !decided && tid < 64) {
-        // One wave, 64 positions per round, in position order.  What each
-        // position needs from LDS is read for the whole round at once (its
-        // code; for a resident first occurrence whether an earlier round
-        // evicted its slot; for a later occurrence of an earlier round's
-        // token that token's slot).  The positions are then decided one at a
-        // time in scalar registers: the hand, the visited word it sweeps, the
-        // round's evictions (in lanes) and results (in lanes).  A hit's
-        // visited bit goes to that word, or to LDS with an atomic OR when it
-        // lies elsewhere; the wave's LDS operations complete in order, so a
-        // word the sweep loads later holds it.
+        // One wave, 64 positions per round, in position order, from LDS only.
+        // The hand may pass a slot twice in a step (a full turn clearing
+        // visited bits, then evictions from where it started), so a token hit
+        // earlier in the step can be evicted: a token's state is the slot it
+        // was last found in or placed into, and whether the step had evicted
+        // that slot then; it is resident while that has not changed.  No slot
+        // is evicted twice when topK < dbs: between two evictions of a slot
+        // the hand passes every slot twice, the second time clearing only
+        // bits set after the first (by a placement, or a hit), so the
+        // positions in between number at least dbs.  code[f] of a first
+        // occurrence f holds its token's state (slot | evicted << 16) from the
+        // round that last changed it (a resident token's initial slot to begin
+        // with).  Per round, what each position needs from LDS is read at
+        // once: its first occurrence and that token's state, resident or not
+        // at the round's start.  The positions are then decided one at a time
+        // in scalar registers: the hand, the visited word it sweeps, the
+        // round's evictions (in lanes; a token found at the round's start
+        // stays while the round has not evicted its slot) and results (in
+        // lanes).  A hit's visited bit goes to that word, or to LDS with an
+        // atomic OR when it lies elsewhere; the wave's LDS operations
+        // complete in order, so a word the sweep loads later holds it.
         int32_t hand = hand0;
         if (hand < 0 || hand >= dbs) hand = 0;  // hisp_sieve_update.cpp:108-111
         int32_t passed = 0, nMiss = 0;
-        bool wrapped = false;
+        bool bail = K >= dbs;  // a slot could be evicted twice: decided in order instead
+        const int32_t passLimit = dbs + 2 * K;
         const uint32_t lastW = nVisW - 1u;
         const uint64_t lastMask = (dbs & 63) ? ((1ull << (dbs & 63)) - 1ull) : ~0ull;
         uint32_t cwIdx = static_cast<uint32_t>(hand) >> 6;  // the visited word held in registers
         uint64_t cwVal = uniform64(visB[cwIdx]);
-        // lane classes of a round: a hit candidate on slot v, a later
-        // occurrence of lane v's token, a hit on slot v, a miss
-        constexpr uint32_t kRes = 1u << 24, kDupLane = 2u << 24, kHit = 3u << 24, kMiss = 4u << 24;
+        constexpr uint32_t kGone = 0xFFu;  // a lane's token not resident
         // from the round of the first miss (the positions before it, applied
         // again, change nothing)
-        for (int32_t k0 = sFirstMiss & ~63; k0 < K && !wrapped; k0 += 64) {
+        for (int32_t k0 = sFirstMiss & ~63; k0 < K && !bail; k0 += 64) {
             const int32_t k = k0 + static_cast<int32_t>(lane);
             const uint32_t c = k < K ? code[k] : kInvalid;
-            uint32_t info = 0u;
-            if (c == kNotRes) {
-                info = kMiss;
-            } else if (c != kInvalid && c != kExt) {
-                if (c & kDup) {
-                    const int32_t f = static_cast<int32_t>(c & ~kDup);
-                    info = f >= k0 ? (kDupLane | static_cast<uint32_t>(f - k0)) : (kHit | (slotOut[f] & 0xFFFFu));
-                } else {
-                    info = bit_get(evB, c) ? kMiss : (kRes | c);
+            const bool work = c != kInvalid && c != kExt;
+            // the lane's first occurrence, its token's slot, and the number of
+            // the round's evictions of that slot at which the token is there
+            uint32_t myF = 0xFFFFFFFFu, mySlot = 0u, myNeed = kGone;
+            bool myRel = false;  // placed in this round
+            if (work) {
+                uint32_t st = c;
+                myF = static_cast<uint32_t>(k);
+                if (c != kNotRes && (c & kDup)) {
+                    myF = c & ~kDup;
+                    st = code[myF];
+                }
+                if (st != kNotRes) {
+                    mySlot = st & 0xFFFFu;
+                    myNeed = static_cast<uint32_t>(bit_get(evB, mySlot)) == (st >> 16) ? 0u : kGone;
                 }
             }
-            uint64_t pend = __ballot(info != 0u);
+            uint64_t pend = __ballot(work);
             uint32_t result = 0u;             // lane j: position k0 + j's slot (| kMissBit)
             uint32_t evRound = 0xFFFFFFFFu;   // lane i: the round's i-th eviction
             int32_t nEv = 0;
             while (pend) {
                 const int j = __builtin_ctzll(pend);
                 pend &= pend - 1ull;
-                const uint32_t inf = static_cast<uint32_t>(lane_value(static_cast<int32_t>(info), j));
-                const uint32_t kd = inf & 0xFF000000u, val = inf & 0xFFFFFFu;
-                bool miss = kd == kMiss;
-                uint32_t sl = val;
-                if (kd == kRes) {
-                    // evicted earlier in this round: the hit becomes a miss
-                    const uint64_t inRound = nEv == 0 ? 0ull : (nEv >= 64 ? ~0ull : ((1ull << nEv) - 1ull));
-                    miss = (__ballot(evRound == val) & inRound) != 0ull;
-                } else if (kd == kDupLane) {
-                    sl = static_cast<uint32_t>(lane_value(static_cast<int32_t>(result), static_cast<int32_t>(val))) & 0xFFFFu;
-                }
-                if (!miss) {
-                    if ((sl >> 6) == cwIdx) {
-                        cwVal |= 1ull << (sl & 63u);
+                const uint32_t sj = static_cast<uint32_t>(lane_value(static_cast<int32_t>(mySlot), j));
+                const uint32_t nd = static_cast<uint32_t>(lane_value(static_cast<int32_t>(myNeed), j));
+                if (nd != kGone && static_cast<uint32_t>(__builtin_popcountll(__ballot(evRound == sj))) == nd) {
+                    if ((sj >> 6) == cwIdx) {
+                        cwVal |= 1ull << (sj & 63u);
                     } else if (lane == 0) {
-                        atomicOr(reinterpret_cast<unsigned long long *>(visB + (sl >> 6)), 1ull << (sl & 63u));
+                        atomicOr(reinterpret_cast<unsigned long long *>(visB + (sj >> 6)), 1ull << (sj & 63u));
                     }
-                    result = static_cast<uint32_t>(lane_set(static_cast<int32_t>(result), j, static_cast<int32_t>(sl)));
+                    result = static_cast<uint32_t>(lane_set(static_cast<int32_t>(result), j, static_cast<int32_t>(sj)));
                     continue;
                 }
                 // the miss: the hand passes visited slots, clearing them, and
@@ -1213,28 +1220,44 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
                         cwVal &= ~cleared;
                         hand = wi == lastW ? 0 : static_cast<int32_t>((wi + 1u) << 6);
                     }
-                    if (passed > dbs) {
-                        wrapped = true;
+                    if (passed > passLimit) {  // past the travel bound (dbs + 2 topK): not reachable
+                        bail = true;
                         break;
                     }
                 }
-                if (wrapped) break;
+                if (bail) break;
                 evRound = static_cast<uint32_t>(lane_set(static_cast<int32_t>(evRound), nEv, h));
                 ++nEv;
                 result = static_cast<uint32_t>(lane_set(static_cast<int32_t>(result), j, h | static_cast<int32_t>(kMissBit)));
+                // every occurrence of the token now finds it in h, which the
+                // round has evicted once
+                const uint32_t fj = static_cast<uint32_t>(lane_value(static_cast<int32_t>(myF), j));
+                if (myF == fj) {
+                    mySlot = static_cast<uint32_t>(h);
+                    myNeed = 1u;
+                    myRel = true;
+                }
                 ++nMiss;
                 hand = h + 1 == dbs ? 0 : h + 1;
             }
-            if (wrapped) break;
-            if (info != 0u) slotOut[k] = result;
-            if (static_cast<int32_t>(lane) < nEv) {
-                atomicOr(reinterpret_cast<unsigned long long *>(evB + (evRound >> 6)), 1ull << (evRound & 63u));
+            if (bail) break;
+            if (work) {
+                slotOut[k] = result;
+                if (myRel) code[myF] = mySlot | (1u << 16);
             }
+            // the round's evictions; a slot evicted before (not reachable)
+            // sends the row to the in-order recurrence
+            bool again = false;
+            if (static_cast<int32_t>(lane) < nEv) {
+                const unsigned long long bit = 1ull << (evRound & 63u);
+                again = (atomicOr(reinterpret_cast<unsigned long long *>(evB + (evRound >> 6)), bit) & bit) != 0ull;
+            }
+            bail = bail || __ballot(again) != 0ull;
         }
         if (lane == 0) {
             visB[cwIdx] = cwVal;
             sHand = hand;
-            sWrap = wrapped ? 1 : 0;
+            sWrap = bail ? 1 : 0;
             sMisses = nMiss;
         }
     }

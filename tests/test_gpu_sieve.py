@@ -654,6 +654,53 @@ def test_sieve_batch_kernel_wraps_and_dups(kvops, form, seed):
 CANON_FLAG = 0x4B565843  # sieve_hand[row][1] of a row a SIEVE kernel left consistent
 
 
+@pytest.mark.parametrize("prefill", [40000, 12000])  # tokens past the table size (a token map), or below it
+@pytest.mark.parametrize("form", [5, 6])  # table changes: parallel rebuild, or in the batch kernel
+def test_sieve_batch_second_pass(kvops, form, prefill):
+    """Steps whose hand turns the whole ring (every slot visited) and then
+    evicts slots it passed earlier in the step: tokens hit before the turn are
+    evicted after it, so their next occurrences miss and the ones after those
+    hit the new slots.  With topK < dbs the batch kernel decides such a step
+    in its one pass (the row's consistency flag is set after every step; the
+    in-order recurrence clears it), equal to the oracle."""
+    dbs, K, req = 3000, 2048, 3
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+        st.hand[0, r, 0] = dbs - 100 + 10 * r  # the turn also crosses the ring's end
+    bits = np.zeros(st.vis_stride * 8, dtype=bool)
+    bits[:dbs] = True
+    all_visited = np.packbits(bits, bitorder="little")
+    rng = np.random.default_rng(77)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(form)
+    try:
+        for step in range(4):
+            st.vis[0, :, :] = all_visited
+            dev.vis.copy_(to_dev(st.vis))
+            batch = np.empty((req, K), dtype=np.int32)
+            for r in range(req):
+                h0 = int(st.hand[0, r, 0])
+                early = st.tokens[0, r, (h0 + np.arange(64)) % dbs].copy()
+                fresh = rng.choice(np.setdiff1d(np.arange(prefill), st.tokens[0, r, :dbs]), size=1200, replace=False)
+                rest = rng.integers(-2, prefill + 9, size=K - 64 - 1200 - 128)
+                batch[r] = np.concatenate([early, fresh, early, early[::-1], rest])
+            seq = np.full(req, prefill + 5)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == 5
+            msg = "form {} prefill {} step {}".format(form, prefill, step)
+            # the scenario: hits, then the same tokens evicted (misses), then hits again
+            assert not e_miss[:, :64].any() and e_miss[:, 1264:1328].all() and not e_miss[:, 1328:1392].any(), msg
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=msg)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=msg)
+            dev.assert_state_equal()
+            assert (dev.hand.cpu().numpy()[0, :, 1] == CANON_FLAG).all(), msg
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 @pytest.mark.parametrize("prefill", [5000, 1500])
 def test_sieve_batch_consistency_flag(kvops, prefill):
     """The batch HBM kernel sets a row's consistency flag when it leaves the

@@ -384,3 +384,169 @@ def test_batched_sweep_build_equals_sequential_inserts(mode):
         for batch, cap in ((64, 4), (8, 1), (4, 4)):
             np.testing.assert_array_equal(_batch_sweep_build(tok, dbs, H, batch, cap), want[0, 0],
                                           err_msg="{} {} {} {}".format(mode, trial, batch, cap))
+
+
+# ---- the batch SIEVE kernel's in-order decision when the hand wraps -------
+def _round_decide(ring, vis, hand0, batch, seq_len, prefill):
+    """The one-wave decision loop of kvx_sieve_update_batch (csrc/sieve_batch.hip),
+    64 positions a round.  A token's state is (slot, whether the step had
+    evicted that slot when the token was found or placed there); it is
+    resident while that has not changed.  Within a round the evictions are a
+    list: a token found at the round's start stays while the round has not
+    evicted its slot; one placed in the round stays while the round has
+    evicted its slot once.  Returns (outputs [(slot, miss)], visited, hand,
+    evicted, misses [(position, slot)], again): `again` is a slot evicted a
+    second time, which the kernel does not decide (it runs the in-order
+    recurrence instead) and which cannot happen while topK < dbs."""
+    dbs, K = len(ring), len(batch)
+    where = {t: s for s, t in enumerate(ring) if t is not None}
+    code, first = [None] * K, {}
+    for k, t in enumerate(batch):
+        if t < 0 or t >= seq_len:
+            code[k] = ("inv",)
+        elif t >= prefill:
+            code[k] = ("ext",)
+        elif t in first:
+            code[k] = ("dup", first[t])
+        else:
+            first[t] = k
+            code[k] = ("st", where[t], 0) if t in where else ("not",)
+    first_miss = min([k for k in range(K) if code[k][0] == "not"], default=K)
+    vis = list(vis)
+    out = [(0, 0)] * K
+    for k in range(first_miss):  # all hits, applied in parallel
+        c = code[k]
+        if c[0] in ("inv", "ext"):
+            continue
+        s = c[1] if c[0] == "st" else code[c[1]][1]
+        out[k] = (s, 0)
+        vis[s] = True
+    evicted = [0] * dbs
+    hand = hand0 if 0 <= hand0 < dbs else 0
+    misses, again = [], False
+    k0 = first_miss & ~63
+    while k0 < K:
+        lanes = range(k0, min(k0 + 64, K))
+        st = {}
+        for k in lanes:
+            c = code[k]
+            if c[0] in ("inv", "ext"):
+                continue
+            f, s = (c[1], code[c[1]]) if c[0] == "dup" else (k, c)
+            st[k] = [f, 0, None, False] if s[0] == "not" else [f, s[1], 0 if evicted[s[1]] == s[2] else None, False]
+        ev = []
+        for j in lanes:
+            if j not in st:
+                continue
+            f, s, need, _ = st[j]
+            if need is not None and ev.count(s) == need:
+                vis[s] = True
+                out[j] = (s, 0)
+                continue
+            while vis[hand]:
+                vis[hand] = False
+                hand = (hand + 1) % dbs
+            h = hand
+            vis[h] = True
+            ev.append(h)
+            out[j] = (h, 1)
+            misses.append((j, h))
+            for q in st.values():
+                if q[0] == f:
+                    q[1:] = [h, 1, True]
+            hand = (h + 1) % dbs
+        for f, s, need, rel in st.values():
+            if rel:
+                code[f] = ("st", s, 1)
+        for h in ev:
+            again |= evicted[h] != 0
+            evicted[h] = 1
+        k0 += 64
+    return out, vis, hand, evicted, misses, again
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_wrapping_step_decisions_and_table(seed):
+    """The decision loop against the ring-clock model (sieve_model.py, written
+    from the policy) on steps whose hand passes slots twice (a full turn of
+    clearing, then evictions of slots hit earlier in the step), and the table
+    the rebuild is handed (deleted: the initial tokens of the evicted slots;
+    new keys: the misses in position order) against the step's inserts and
+    Algorithm R deletions replayed in order."""
+    from tests.sieve_model import RingClock
+
+    rng = random.Random(seed)
+    seen = {"passed_twice": 0, "hit_then_evicted": 0, "evicted_then_again": 0}
+    for trial in range(400):
+        storm = trial % 3 == 0  # misses on a nearly all-visited ring, repeats of the step's hits
+        dbs = rng.choice([20, 33, 64, 65, 70, 130])
+        K = dbs - 1 if storm else rng.randint(1, dbs - 1)  # topK < dbs
+        prefill = 3 * dbs if storm else rng.choice([dbs // 2, dbs, 3 * dbs])
+        seq_len = prefill + rng.randint(0, 5)
+        toks = rng.sample(range(prefill), min(prefill, dbs - rng.randint(0, 3)))
+        ring = toks + [None] * (dbs - len(toks))
+        rng.shuffle(ring)
+        p_vis = 0.97 if storm else rng.choice([0.5, 0.95, 1.0])
+        vis = [t is not None and rng.random() < p_vis for t in ring]
+        hand0 = rng.choice([rng.randrange(dbs), dbs - 1, -1])
+        pool = [t for t in ring if t is not None]
+        batch = []
+        for _ in range(K):
+            u = rng.random()
+            if u < (0.3 if storm else 0.15) and batch:
+                batch.append(rng.choice(batch))              # a repeat within the step
+            elif u < 0.35 and pool:
+                batch.append(rng.choice(pool))               # a resident token
+            elif u < 0.4 and not storm:
+                batch.append(rng.choice([-1, seq_len, prefill]))  # invalid or decode-extension
+            else:
+                batch.append(rng.randrange(prefill))
+        out, vis_g, hand_g, evicted, misses, again = _round_decide(ring, vis, hand0, batch, seq_len, prefill)
+        assert not again, (seed, trial)
+        rc = RingClock(dbs, dbs, [t if t is not None else -1 for t in ring], vis, hand0)
+        want = [rc.access(t, seq_len, prefill) for t in batch]
+        got = [(-1, 0) if batch[k] < 0 or batch[k] >= seq_len else
+               ((dbs + batch[k] - prefill, 0) if batch[k] >= prefill else out[k]) for k in range(K)]
+        assert got == want, (seed, trial)
+        assert vis_g == rc.ref and hand_g == rc.hand, (seed, trial)
+        final = list(ring)
+        for k, s in misses:
+            final[s] = batch[k]
+        assert final == rc.ring, (seed, trial)
+        # the table: the step replayed, against the initial survivors (slot
+        # order) then the new keys (position order)
+        H = 1 << max(4, (2 * dbs).bit_length())
+
+        def hf(k, H=H):
+            return _knuth_home(k, H)
+
+        seq = [None] * H
+        for t in ring:
+            if t is not None:
+                _insert(seq, t, hf)
+        cur = list(ring)
+        for k, s in misses:
+            if cur[s] is not None:
+                _erase(seq, cur[s], hf)
+            cur[s] = batch[k]
+            _insert(seq, batch[k], hf)
+        fcfs = [None] * H
+        for s, t in enumerate(ring):
+            if t is not None and not evicted[s]:
+                _insert(fcfs, t, hf)
+        for k, _ in misses:
+            _insert(fcfs, batch[k], hf)
+        assert fcfs == seq, (seed, trial)
+        # coverage: a slot hit in the step and evicted later; then the token again
+        hits = {}
+        for k, (s, m) in enumerate(out):
+            if not m and 0 <= batch[k] < prefill and k < K:
+                hits.setdefault(batch[k], k)
+        evk = {s: k for k, s in misses}
+        seen["passed_twice"] += any(hits.get(ring[s], K) < k for k, s in misses if ring[s] is not None)
+        tw = [t for t, k1 in hits.items() if any(batch[k2] == t for k2, _ in misses if k2 > k1)]
+        seen["hit_then_evicted"] += bool(tw)
+        seen["evicted_then_again"] += any(sum(1 for k in range(K) if batch[k] == t and out[k][1] == 0 and
+                                              k > max(k2 for k2, _ in misses if batch[k2] == t)) > 0 for t in tw)
+        del evk
+    assert all(v > 0 for v in seen.values()), seen
