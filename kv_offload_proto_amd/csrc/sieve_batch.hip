@@ -7,8 +7,8 @@
 // stays in HBM.  The result
 // equals the in-order recurrence of hisp_sieve_update.cpp:115-163 whenever
 // the row's table is canonical (every live token findable at its own slot)
-// and the step's hand does not pass a slot twice; otherwise the row runs that
-// recurrence (sieve_hbm.h) instead.  Phases:
+// and topK < dbs (then no slot is evicted twice in a step); otherwise the row
+// runs that recurrence (sieve_hbm.h) instead.  Phases:
 //
 //  1. check: a token -> slot map of the row (HBM scratch: every launch leaves
 //     the map and first-occurrence table zeroed) finds duplicate tokens; a
@@ -23,11 +23,12 @@
 //     tokens lie below the table size the pre-passes mark the step's tokens
 //     in a bitmap and find their slots in one pass over the slots instead of
 //     a token map); up to the first miss every position is a hit, applied in
-//     parallel; from there one wave decides in order, from LDS only: a later
-//     occurrence hits the first one's slot (without a wrap nothing placed or
-//     hit in this step leaves it), a first occurrence hits its initial slot
-//     unless the hand evicted that slot earlier in the step, and a miss
-//     sweeps the visited bitmap from the hand;
+//     parallel; a step whose hand does not come back to where it started is
+//     then decided in parallel (decide_parallel); otherwise one wave decides
+//     in order, from LDS only: a token is resident at the slot it was last
+//     found in or placed into unless the hand evicted that slot since (a
+//     hand that turns the whole ring comes back to slots hit earlier in the
+//     step), and a miss sweeps the visited bitmap from the hand;
 //  3. outputs, tokens, visited bits and hand, in parallel, and the cells of
 //     the evicted slots (a step without misses ends here);
 //  4. deletion of the evicted tokens' cells: Algorithm R leaves a table as if
