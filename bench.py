@@ -172,8 +172,11 @@ def sieve_bytes(cfg, padded, vis_stride, ht_size, dirty_reqs):
 TRAFFIC_PROFILES = {"c2-dsa-decode": "profiles/pmc_traffic_dsa_decode.md",
                     "c4-slot-limit-stress": "profiles/pmc_traffic_slot_limit_stress.md"}
 # SIEVE kernel of each variant (kvx_last_sieve_variant), as named in the profiles
-SIEVE_KERNELS = {0: "kvx_sieve_update", 1: "kvx_sieve_update", 2: "kvx_sieve_update_fast",
-                 3: "kvx_sieve_update_wave", 4: "kvx_sieve_update_fast", 5: "kvx_sieve_update_batch"}
+SIEVE_KERNELS = {0: ("kvx_sieve_update",), 1: ("kvx_sieve_update",), 2: ("kvx_sieve_update_fast",),
+                 3: ("kvx_sieve_update_wave",), 4: ("kvx_sieve_update_fast",),
+                 5: ("kvx_sieve_batch_pre", "kvx_sieve_batch_slots", "kvx_sieve_update_batch")}
+# variant 5's table rebuild, when the step's launches include it
+SIEVE_TABLE_KERNELS = ("kvx_sieve_table_cells", "kvx_sieve_table_final", "kvx_sieve_table_chunks")
 
 
 def load_traffic(workload):
@@ -778,10 +781,12 @@ def main():
                            "bytes_rule": "rows moved x row_bytes read + written, + 9 B per position of index scan"}}
     from kv_offload_proto_amd.kvops_ext import _kvops
 
-    sieve_kernel = SIEVE_KERNELS.get(_kvops.last_sieve_variant(), "kvx_sieve_update")
-    sieve_roof = {"kernel": sieve_kernel, "bound": "hbm", "achieved": sieve_gbps_alg, "peak": HBM_PEAK_GBPS,
-                  "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS,
-                  "traffic": traffic_of(sieve_kernel), "traffic_source": traffic_src, "bytes_per_launch": sb,
+    sieve_kernels = SIEVE_KERNELS.get(_kvops.last_sieve_variant(), ("kvx_sieve_update",))
+    if sieve_kernels[-1] == "kvx_sieve_update_batch" and traffic_of(*SIEVE_TABLE_KERNELS) is not None:
+        sieve_kernels = sieve_kernels + SIEVE_TABLE_KERNELS
+    sieve_roof = {"kernel": "+".join(sieve_kernels), "bound": "hbm", "achieved": sieve_gbps_alg,
+                  "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": sieve_gbps_alg / HBM_PEAK_GBPS,
+                  "traffic": traffic_of(*sieve_kernels), "traffic_source": traffic_src, "bytes_per_launch": sb,
                   "traffic_basis": "FETCH_SIZE + WRITE_SIZE of the kernel per launch, against bytes_per_launch (the "
                                    "row state read and written back, the batch row read, the outputs written)",
                   "algorithmic_traffic": sb,
