@@ -39,6 +39,19 @@ constexpr int32_t kHandStride = 16;
 // consistent with its tokens (every live token findable at its own slot, one
 // entry per live slot); any other writer of the row clears it.
 constexpr int32_t kCanonFlag = 0x4B565843;
+// sieve_hand[row][3]: written with the flag, the sum over slots [0, dbs) of
+// slot_token_mix(slot, token) (mod 2^32) of the tokens the kernel left.  A
+// flagged row is trusted only while its tokens still sum to it, so a token
+// edited in place without clearing the flag sends the row to the full check.
+constexpr int32_t kFingerprintWord = 3;
+__host__ __device__ __forceinline__ uint32_t slot_token_mix(uint32_t slot, int32_t token)
+{
+    uint32_t x = static_cast<uint32_t>(token) * 0x9E3779B1u + slot * 0x85EBCA77u;
+    x ^= x >> 16;
+    x *= 0x7FEB352Du;
+    x ^= x >> 15;
+    return x;
+}
 
 // ---------------------------------------------------------------------------
 // Scratch of the row movers.  The library keeps one set per stream (launches
@@ -280,13 +293,14 @@ __host__ __device__ __forceinline__ TableLayout table_layout(uint32_t htSize)
 }
 
 // uint32 words of HBM scratch per row: map, first occurrences, a bitmap of
-// the step's tokens, four counters (entries, last empty cell + 1, live
-// tokens, a token past the map) and each position's resident slot + 1
-// (htSize/2 >= topK words).  Every launch leaves them zeroed, whatever the
-// shape of the next launch on the stream.
+// the step's tokens, kBatchCounts counters (entries, last empty cell + 1,
+// live tokens, a token past the map, the tokens' fingerprint) and each
+// position's resident slot + 1 (htSize/2 >= topK words).  Every launch leaves
+// them zeroed, whatever the shape of the next launch on the stream.
+constexpr uint32_t kBatchCounts = 8;
 __host__ __device__ __forceinline__ uint64_t batch_aux_words(uint32_t htSize)
 {
-    return 2ull * kBatchMapCap + kBatchMapCap / 32u + 4u + htSize / 2u;
+    return 2ull * kBatchMapCap + kBatchMapCap / 32u + kBatchCounts + htSize / 2u;
 }
 
 // LDS bytes of the rebuild's chunk kernel: per-home counts (16 bits, 2^16

@@ -17,7 +17,8 @@
 //     an entry's home and its cell (so a probe from the home reaches it).  A
 //     row whose consistency flag (sieve_hand[row][1]) is set, which this
 //     kernel and the LDS kernel set when they leave the row consistent, only
-//     has its live tokens and entries counted;
+//     has its live tokens and entries counted, and its tokens' fingerprint
+//     compared with the one written with the flag (sieve_hand[row][3]);
 //  2. decide: each position's first occurrence in the batch and the initial
 //     slot of its token are found in parallel first (for a flagged row whose
 //     tokens lie below the table size the pre-passes mark the step's tokens
@@ -307,14 +308,16 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_slots(BatchParams
     KVX_GM uint32_t *first = (KVX_GM uint32_t *)P.aux + static_cast<uint64_t>(bid) * P.auxWords + P.mapCap;
     const KVX_GM uint32_t *bits = first + P.mapCap;
     KVX_GM uint32_t *counts = first + P.mapCap + P.mapCap / 32u;
-    KVX_GM uint32_t *resSlot = counts + 4;
-    uint32_t live = 0, bad = 0;
+    KVX_GM uint32_t *resSlot = counts + kBatchCounts;
+    uint32_t live = 0, bad = 0, fp = 0;
     auto quad = [&](int32_t q, i32x4 v) {
         const int32_t t4v[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
             const int32_t sl = 4 * q + h, t = t4v[h];
-            if (sl >= dbs || t < 0) continue;
+            if (sl >= dbs) continue;
+            fp += slot_token_mix(static_cast<uint32_t>(sl), t);
+            if (t < 0) continue;
             ++live;
             if (t >= mapLim) {
                 bad = 1;
@@ -332,10 +335,12 @@ __global__ __launch_bounds__(kPreThreads) void kvx_sieve_batch_slots(BatchParams
     for (int d = 32; d > 0; d >>= 1) {
         live += __shfl_xor(live, d);
         bad |= __shfl_xor(bad, d);
+        fp += __shfl_xor(fp, d);
     }
     if ((tid & 63) == 0) {
         if (live) __hip_atomic_fetch_add(counts + 2, live, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (bad) __hip_atomic_fetch_or(counts + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (fp) __hip_atomic_fetch_add(counts + 4, fp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -727,6 +732,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ int32_t sScan[BT];
     __shared__ int32_t sBad, sWrap, sLive, sOcc, sNamed, sNdel, sHand, sE0, sTableBad, sFirstMiss, sMisses;
+    __shared__ uint32_t sFp, sFpD;  // the pre-step tokens' fingerprint; its change by the step's new tokens
 
     const HispSieveUpdateArgs &a = P.L.a;
     const int32_t K = static_cast<int32_t>(a.topK);
@@ -762,7 +768,9 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     const int32_t prefill = ((KVX_CM const int32_t *)(a.prefillLens))[reqIdx];
     int32_t flagWord = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride + 1];
     int32_t hand0 = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride];  // phase 2 starts from it
-    asm volatile("" : "+s"(flagWord), "+s"(hand0));
+    // the fingerprint of the tokens the flag was written with
+    int32_t fpWord = ((KVX_CM const int32_t *)(a.sieveHand))[reqIdx * kHandStride + kFingerprintWord];
+    asm volatile("" : "+s"(flagWord), "+s"(hand0), "+s"(fpWord));
     const KVX_GM int32_t *rt = reinterpret_cast<const KVX_GM int32_t *>(a.topkIndices) + static_cast<int64_t>(bid) * K;
     Row r;
     r.tok = reinterpret_cast<KVX_GM int32_t *>(a.deviceBufferTokens) + reqIdx * padded;
@@ -778,16 +786,16 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     KVX_GM uint32_t *first = map + P.mapCap;
     KVX_GM uint32_t *gBits = first + P.mapCap;     // the step's tokens, from kvx_sieve_batch_pre
     KVX_GM uint32_t *gCounts = gBits + P.mapCap / 32u;
-    KVX_GM uint32_t *gResSlot = gCounts + 4;        // from kvx_sieve_batch_slots
+    KVX_GM uint32_t *gResSlot = gCounts + kBatchCounts;  // from kvx_sieve_batch_slots
     const int32_t mapLim = prefill < static_cast<int32_t>(P.mapCap) ? prefill : static_cast<int32_t>(P.mapCap);
     // loads that need only the batch row, issued before the flag is known:
     // the pre-passes' counts (thread 0) and phase 2's first group of tokens
     // and resident slots (the row's scratch always holds topK of them; used
     // only in the bitmap form)
-    uint32_t pc[4] = {0u, 0u, 0u, 0u};
+    uint32_t pc[5] = {0u, 0u, 0u, 0u, 0u};
     if (tid == 0) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) pc[q] = gCounts[q];
+        for (int q = 0; q < 5; ++q) pc[q] = gCounts[q];
     }
     int32_t tv0[kMapUnroll];
     uint32_t rv0[kMapUnroll];
@@ -841,6 +849,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         sTableBad = 0;
         sFirstMiss = K;
         sMisses = 0;
+        sFp = sFpD = 0u;
     }
     for (uint32_t w = tid; w < nVisW; w += BT) {
         visB[w] = vis64[w];
@@ -854,6 +863,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         // kMapUnroll slots' tokens are loaded before any is used (one memory
         // round trip per group, not per slot).
         int32_t live = 0, bad = 0;
+        uint32_t fp = 0;
         for (int32_t s0 = tid; s0 < dbs; s0 += BT * kMapUnroll) {
             int32_t tv[kMapUnroll];
 #pragma unroll
@@ -864,6 +874,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
 #pragma unroll
             for (int q = 0; q < kMapUnroll; ++q) {
                 const int32_t t = tv[q];
+                if (s0 + q * BT < dbs) fp += slot_token_mix(static_cast<uint32_t>(s0 + q * BT), t);
                 if (t < 0) continue;
                 ++live;
                 if (t >= mapLim) {
@@ -875,8 +886,18 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
         if (live) atomicAdd(&sLive, live);
         if (bad) sBad = 1;
+        for (int d = 32; d > 0; d >>= 1) fp += __shfl_xor(fp, d);
+        if (lane == 0 && fp) atomicAdd(&sFp, fp);
     }
-    if (!flagged) {
+    // a flagged row whose tokens changed since the flag was written (an edit
+    // in place) is checked in full like an unflagged one (in the bitmap form,
+    // without a map, it takes the in-order recurrence instead, below)
+    bool full = !flagged;
+    if (flagged && !useBits) {
+        __syncthreads();
+        full = sFp != static_cast<uint32_t>(fpWord);
+    }
+    if (full) {
         __syncthreads();
         {
             int32_t bad = 0;
@@ -996,8 +1017,11 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
             occ = static_cast<int32_t>(pc[0]);
             last = static_cast<int32_t>(pc[1]) - 1;
             sLive = static_cast<int32_t>(pc[2]);
-            // a token past the map, or a live token without an entry (or the reverse)
-            if (pc[3] != 0u || pc[2] != pc[0]) sBad = 1;
+            sFp = pc[4];
+            // a token past the map, or a live token without an entry (or the
+            // reverse), or tokens changed since the flag was written: the
+            // in-order recurrence instead
+            if (pc[3] != 0u || pc[2] != pc[0] || pc[4] != static_cast<uint32_t>(fpWord)) sBad = 1;
         }
         const uint32_t nChunk = static_cast<uint32_t>(H) / 8u;
         const KVX_GM u32x4 *t16 = reinterpret_cast<const KVX_GM u32x4 *>(r.ht);
@@ -1292,7 +1316,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     if (useBits) {
         for (int32_t w = tid; w < (mapLim + 31) / 32; w += BT) gBits[w] = 0u;
         for (int32_t k = tid; k < K; k += BT) gResSlot[k] = 0u;
-        if (tid < 4) gCounts[tid] = 0u;
+        if (tid < static_cast<int>(kBatchCounts)) gCounts[tid] = 0u;
     }
     __syncthreads();  // the cleanup read the initial tokens; phase 3 replaces some
     KVX_STAMP(3);
@@ -1357,18 +1381,36 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         __syncthreads();
         int32_t rank = sScan[tid >> 6] + inc - cnt;
         KVX_GM uint32_t *newk = tbl + P.t.newk;
-        for (int32_t k = k0; k < k1; ++k) {
-            const uint32_t so = slotOut[k];
-            if (!(so & kMissBit)) continue;
-            const int32_t t = rt[k];
-            const uint32_t sl = so & 0xFFFFu;
-            newk[rank++] = ((ht_hash(t) & mask) << 16) | (sl + 1u);
-            r.tok[sl] = t;
+        // 8 positions at a time: their tokens and their slots' old tokens
+        // are loaded before any store (each evicted slot is named once)
+        uint32_t fpd = 0;
+        for (int32_t kb = k0; kb < k1; kb += 8) {
+            uint32_t so[8];
+            int32_t tk[8], old[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int32_t k = kb + q;
+                so[q] = k < k1 ? slotOut[k] : 0u;
+                tk[q] = (so[q] & kMissBit) ? rt[k] : 0;
+                old[q] = (so[q] & kMissBit) ? r.tok[so[q] & 0xFFFFu] : 0;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (!(so[q] & kMissBit)) continue;
+                const uint32_t sl = so[q] & 0xFFFFu;
+                newk[rank++] = ((ht_hash(tk[q]) & mask) << 16) | (sl + 1u);
+                r.tok[sl] = tk[q];
+                fpd += slot_token_mix(sl, tk[q]) - slot_token_mix(sl, old[q]);
+            }
         }
+        for (int d = 32; d > 0; d >>= 1) fpd += __shfl_xor(fpd, d);
+        if (lane == 0 && fpd) atomicAdd(&sFpD, fpd);
+        __syncthreads();
         if (tid == 0) {
             tbl[P.t.meta + 1] = static_cast<uint32_t>(sMisses);
             tbl[P.t.meta] = 1u;
             gHand[1] = kCanonFlag;  // the rebuild leaves the table consistent
+            gHand[kFingerprintWord] = static_cast<int32_t>(sFp + sFpD);
         }
 #ifdef KVX_BATCH_STAMPS
         KVX_STAMP(4);
@@ -1411,10 +1453,30 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         }
         if (nd) atomicAdd(&sNdel, nd);
     }
-    // the new tokens (each evicted slot gets one: no wrap)
-    for (int32_t k = tid; k < K; k += BT) {
-        const uint32_t s = slotOut[k];
-        if (s & kMissBit) r.tok[s & 0xFFFFu] = rt[k];
+    // the new tokens (each evicted slot gets one), 8 positions a thread at a
+    // time: their tokens and their slots' old tokens loaded before any store
+    {
+        uint32_t fpd = 0;
+        for (int32_t kb = tid; kb < K; kb += BT * 8) {
+            uint32_t so[8];
+            int32_t tk[8], old[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int32_t k = kb + q * BT;
+                so[q] = k < K ? slotOut[k] : 0u;
+                tk[q] = (so[q] & kMissBit) ? rt[k] : 0;
+                old[q] = (so[q] & kMissBit) ? r.tok[so[q] & 0xFFFFu] : 0;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (!(so[q] & kMissBit)) continue;
+                const uint32_t sl = so[q] & 0xFFFFu;
+                r.tok[sl] = tk[q];
+                fpd += slot_token_mix(sl, tk[q]) - slot_token_mix(sl, old[q]);
+            }
+        }
+        for (int d = 32; d > 0; d >>= 1) fpd += __shfl_xor(fpd, d);
+        if (lane == 0 && fpd) atomicAdd(&sFpD, fpd);
     }
     for (uint32_t w = tid; w < nCellW; w += BT) bitL0[w] = 0ull;  // holes, in offsets from sE0
     for (uint32_t w = tid; w < nL1; w += BT) bitL1[w] = 0ull;
@@ -1735,7 +1797,10 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
     KVX_STAMP(5);
     // ---- 5. the new tokens, in position order ----------------------------
     if (sMisses == 0) {
-        if (tid == 0) gHand[1] = sTableBad ? 0 : kCanonFlag;  // nothing to insert
+        if (tid == 0) {  // nothing to insert
+            gHand[1] = sTableBad ? 0 : kCanonFlag;
+            gHand[kFingerprintWord] = static_cast<int32_t>(sFp);
+        }
         return;
     }
     for (uint32_t w = tid; w < nCellW; w += BT) {
@@ -1800,7 +1865,10 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
             }
         }
         // the row's table is consistent with its tokens unless a bound broke
-        if (wr) gHand[1] = sTableBad ? 0 : kCanonFlag;
+        if (wr) {
+            gHand[1] = sTableBad ? 0 : kCanonFlag;
+            gHand[kFingerprintWord] = static_cast<int32_t>(sFp + sFpD);
+        }
 #ifdef KVX_BATCH_STAMPS
         KVX_STAMP(6);
         if (tid == 0)

@@ -123,6 +123,7 @@ struct Misc {
     int32_t nEv, handOut;
     int32_t bad, ovf, late, nSM, nUnd, uEnd, nTakes, nLead, nDone, snNext;
     int32_t diff;  // live tokens minus table entries
+    uint32_t fp0, fpd;  // the staged tokens' fingerprint; its change by the step's new tokens
     uint32_t M;    // candidates (first occurrences of missing tokens)
     uint32_t uL[64];  // undecided SM slots in ring order: evictions settled before them with a larger k
     uint16_t ui[64];  // ... and their SM indices
@@ -402,6 +403,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         ms.bad = ms.ovf = ms.late = 0;
         ms.nSM = ms.nUnd = ms.uEnd = ms.nTakes = ms.nLead = ms.nDone = ms.snNext = 0;
         ms.diff = 0;
+        ms.fp0 = ms.fpd = 0u;
         ms.M = 0;
         ms.evMask = 0ull;
     }
@@ -499,14 +501,18 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     int32_t flagw = ((KVX_C const int32_t *)gHand)[1];
     // sieve_hand[row][2]: steps in a row this kernel could not take in parallel
     int32_t hintw = ((KVX_C const int32_t *)gHand)[2];
+    // sieve_hand[row][3]: the fingerprint of the tokens a flagged row was left with
+    int32_t fpw = ((KVX_C const int32_t *)gHand)[kFingerprintWord];
 
     // The in-order recurrence (hisp_sieve_update.cpp:115-163) on a staged copy
     // of the row, then its write back: registers for consistent rows of up to
     // 64 slots, else one lane for small tables, else 64 cells/slots per step.
     // canon: the row was consistent before the step.
     __shared__ int32_t s_dirty;
+    __shared__ uint32_t s_fp;
     auto run_inorder = [&](int32_t *tokF, uint16_t *htF, uint8_t *visF, bool canon) {
         STAMP(12);
+        if (tid == 0) s_fp = 0u;
         if (wave == 0) {
             int32_t hand = hand0;
             Guard g;
@@ -529,6 +535,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         STAMP(13);
         __syncthreads();
         wg_copy16((KVX_G v4u *)gVis, reinterpret_cast<const v4u *>(visF), static_cast<uint32_t>(visStrideB));
+        // the fingerprint of the tokens left (read only with the flag)
+        uint32_t f = 0;
+        for (int32_t s = tid; s < dbs; s += NT) f += slot_token_mix(static_cast<uint32_t>(s), tokF[s]);
+        f = wave_sum(f);
+        if (lane == 0 && f != 0u) atomicAdd(&s_fp, f);
+        __syncthreads();
+        if (tid == 0) gHand[kFingerprintWord] = static_cast<int32_t>(s_fp);
         STAMP(14);
         if (s_dirty) {
             wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tokF), static_cast<uint32_t>(padded) * 4u);
@@ -561,11 +574,15 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const int32_t Pn = (Nev + NT - 1) / NT;
         Guard g;
         uint32_t ecR = 0;  // ecell of the lane's first event, carried across the phases
+        int32_t oldR = 0;  // compact form: the token that event's slot loses (read early, used at placement)
         for (int32_t q = 0; q < Pn; ++q) {
             const int32_t r = tid + q * NT;
             if (r >= Nev) break;
             const uint32_t ec = ecell[r];
-            if (q == 0) ecR = ec;
+            if (q == 0) {
+                ecR = ec;
+                if constexpr (kC) oldR = gTok[ec >> 16];
+            }
             const uint32_t s = ec >> 16;
             if (setVset) atomicOr(vset + (s >> 5), 1u << (s & 31u));
             const uint32_t c = ec & 0xFFFFu;
@@ -614,18 +631,24 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         __syncthreads();
         STAMP(7);
         // ---- new tokens; tentative placement (the final occupied cells do
-        // not depend on order), entries padded+1+r name the event
+        // not depend on order), entries padded+1+r name the event; the
+        // fingerprint's change (each event's slot loses one token, gains one)
+        uint32_t fpd = 0;
         for (int32_t q = 0; q < Pn; ++q) {
             const int32_t r = tid + q * NT;
             if (r >= Nev) break;
             const uint32_t s = ((q == 0) ? ecR : ecell[r]) >> 16;
             const int32_t t = ntokv[r];
+            int32_t old;
             if constexpr (kC) {
+                old = (q == 0) ? oldR : gTok[s];
                 hv[s] = static_cast<uint16_t>(ht_hash(t) & static_cast<uint32_t>(mask));
                 gTok[s] = t;
             } else {
+                old = tok[s];
                 tok[s] = t;
             }
+            fpd += slot_token_mix(s, t) - slot_token_mix(s, old);
             const int32_t c = lds_claim_bit(fin, static_cast<int32_t>(ht_hash(t)) & mask, mask);
             if (c < 0) {
                 g.code = kOverflowProbe;
@@ -635,6 +658,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             atomicOr(nkb + (c >> 5), 1u << (c & 31));
             ecell[r] = static_cast<uint32_t>(c) | (s << 16);
             if (q == 0) ecR = static_cast<uint32_t>(c) | (s << 16);
+        }
+        {
+            const uint32_t fw = wave_sum(fpd);
+            if (lane == 0 && fw != 0u) atomicAdd(&ms.fpd, fw);
         }
         __syncthreads();
         STAMP(8);
@@ -812,7 +839,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         KVX_G const v4u *sT = (KVX_G const v4u *)gTok;
         KVX_G const v4u *sH = (KVX_G const v4u *)gHt;
         KVX_G const v4u *sV = (KVX_G const v4u *)gVis;
-        uint32_t nTok = 0, nEnt = 0;
+        uint32_t nTok = 0, nEnt = 0, fpS = 0;
         // Each region loads into registers of its own, all before the first
         // use: loads that share a destination register across divergent
         // branches would each wait for the previous one to land.
@@ -842,8 +869,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             // (the scalar values pass through the statement, so that nothing
             // computed from them is scheduled, and waited for, before the loads)
             if (p == 0) {
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : "+s"(prefill), "+s"(hand0), "+s"(flagw), "+s"(hintw)
-                             : : "memory");
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : "+s"(prefill), "+s"(hand0), "+s"(flagw), "+s"(hintw),
+                             "+s"(fpw) : : "memory");
                 lim = min(prefill, seqLen);
                 direct = !kC && lim > 0 && lim <= invCap;
             }
@@ -873,6 +900,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     for (int i = 0; i < 4; ++i) {
                         const bool live = i < room && tt[i] >= 0;
                         nTok += live ? 1u : 0u;
+                        fpS += i < room ? slot_token_mix(static_cast<uint32_t>(s0 + i), tt[i]) : 0u;
                         if (direct && i < room && static_cast<uint32_t>(tt[i]) < static_cast<uint32_t>(lim))
                             inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
                     }
@@ -920,10 +948,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         for (int32_t i = tid; i < 2 * P * NWAVES; i += NT) emask[i] = 0ull;  // emask, smask (adjacent)
         const int32_t dw = static_cast<int32_t>(wave_sum(nTok)) - static_cast<int32_t>(wave_sum(nEnt));
         if (lane == 0 && dw != 0) atomicAdd(&ms.diff, dw);
+        const uint32_t fw = wave_sum(fpS);
+        if (lane == 0) atomicAdd(&ms.fp0, fw);
     }
     __syncthreads();
     STAMP(1);
-    const bool flagged = flagw == kCanonFlag;
+    // the flag counts only while the tokens are the ones it was written with
+    const bool flagged = flagw == kCanonFlag && ms.fp0 == static_cast<uint32_t>(fpw);
     if (badReq) {  // hisp_sieve_update.cpp:80-87: the row gets the dummy outputs, the state is untouched
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
@@ -990,6 +1021,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 gHand[0] = ms.handOut;
                 gHand[1] = kCanonFlag;
                 gHand[2] = min(hintw, (1 << 30)) + 1;
+                gHand[kFingerprintWord] = static_cast<int32_t>(ms.fp0 + ms.fpd);
             }
             return;
         }
@@ -1001,7 +1033,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
     // ---- consistency: the table indexes exactly the non-negative tokens of
     // [0, dbs), each at its own slot.  A row this kernel wrote last carries
-    // the flag, and then only the counts are checked.
+    // the flag (and the fingerprint of the tokens it left), and then only the
+    // counts are checked.
     if (!flagged) {
         bool bad = false;
         for (int32_t s = tid; s < dbs; s += NT) {
@@ -1661,6 +1694,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
                 gHand[0] = hd;
                 gHand[1] = kCanonFlag;
+                gHand[kFingerprintWord] = static_cast<int32_t>(ms.fp0 + ms.fpd);
                 if (hintw != 0) gHand[2] = 0;
             }
             STAMP(11);

@@ -654,6 +654,58 @@ def test_sieve_batch_kernel_wraps_and_dups(kvops, form, seed):
 CANON_FLAG = 0x4B565843  # sieve_hand[row][1] of a row a SIEVE kernel left consistent
 
 
+@pytest.mark.parametrize("variant,prefill", [(2, 1500), (4, 1500), (5, 1500), (5, 5000), (6, 1500)])
+def test_sieve_flag_with_token_edited_in_place(kvops, variant, prefill):
+    """sieve_hand[row][3] carries a fingerprint of the tokens a kernel left
+    with the consistency flag.  A caller that changes a token value in place
+    and leaves element 1 set (the reference's results depend only on tokens,
+    visited bits, table and hand: hisp_sieve_update.cpp:103-111) gets the
+    reference's results: the fingerprint no longer matches, so the row is
+    checked in full (or runs the in-order recurrence) instead of being trusted.
+    Variants: 2 the parallel LDS kernel (direct token map), 4 its compact
+    form, 5 the batch HBM kernel (token bitmap below the table size, 2048
+    cells, or a token map above it), 6 the batch kernel without the rebuild."""
+    rng = np.random.default_rng(31 + variant)
+    dbs, K, req = 700, 200, 3
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(variant)
+    try:
+        for step in range(5):
+            batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.3)
+            if step == 2:
+                # row 1: a resident token becomes one the row does not hold
+                assert int(dev.hand[0, 1, 1]) == CANON_FLAG
+                toks = st.tokens[0, 1, :dbs]
+                s = int(np.nonzero(toks >= 0)[0][5])
+                t_old = int(toks[s])
+                absent = np.setdiff1d(np.arange(prefill), toks)
+                t_new = int(absent[rng.integers(len(absent))])
+                st.tokens[0, 1, s] = t_new
+                dev.tokens[0, 1, s] = t_new
+                batch[1, [0, 9, 77]] = t_new
+                batch[1, [3, 40]] = t_old
+            seq = np.full(req, prefill + 4)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == (5 if variant == 6 else variant)
+            msg = "variant {} prefill {} step {}".format(variant, prefill, step)
+            if step == 2:
+                # the table has no entry for the new value: the reference misses it
+                assert e_miss[1, 0] == 1, msg
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=msg)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=msg)
+            dev.assert_state_equal()
+            flags = dev.hand.cpu().numpy()[0, :, 1]
+            if step == 1:
+                assert list(flags) == [CANON_FLAG] * req, msg
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 @pytest.mark.parametrize("prefill", [40000, 12000])  # tokens past the table size (a token map), or below it
 @pytest.mark.parametrize("form", [5, 6])  # table changes: parallel rebuild, or in the batch kernel
 def test_sieve_batch_second_pass(kvops, form, prefill):
