@@ -1158,7 +1158,10 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         // is evicted twice when topK < dbs: between two evictions of a slot
         // the hand passes every slot twice, the second time clearing only
         // bits set after the first (by a placement, or a hit), so the
-        // positions in between number at least dbs.  code[f] of a first
+        // positions in between number at least dbs.  (With topK >= dbs a
+        // second eviction is possible: the round that makes one finds the
+        // slot's eviction bit already set, and the row takes the in-order
+        // recurrence instead.)  code[f] of a first
         // occurrence f holds its token's state (slot | evicted << 16) from the
         // round that last changed it (a resident token's initial slot to begin
         // with).  Per round, what each position needs from LDS is read at
@@ -1173,7 +1176,7 @@ __global__ __launch_bounds__(BT) void kvx_sieve_update_batch(BatchParams P)
         int32_t hand = hand0;
         if (hand < 0 || hand >= dbs) hand = 0;  // hisp_sieve_update.cpp:108-111
         int32_t passed = 0, nMiss = 0;
-        bool bail = K >= dbs;  // a slot could be evicted twice: decided in order instead
+        bool bail = false;  // a slot evicted twice: decided in order instead
         const int32_t passLimit = dbs + 2 * K;
         const uint32_t lastW = nVisW - 1u;
         const uint64_t lastMask = (dbs & 63) ? ((1ull << (dbs & 63)) - 1ull) : ~0ull;

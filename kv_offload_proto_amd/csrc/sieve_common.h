@@ -16,6 +16,7 @@ namespace sieve {
 
 struct Guard {
     uint64_t code = 0;
+    uint32_t fpd = 0;  // change of the row's token fingerprint (slot_token_mix sum) by the replaced tokens
 };
 
 // Tables up to this many cells run the in-order recurrence on one lane (short
@@ -170,6 +171,7 @@ __device__ bool sieve_row_sequential(const int32_t *rt, int32_t *rs, int8_t *rm,
         const int32_t old = tok[h];
         if (old >= 0) ht_erase(ht, tok, padded, old, mask, g);
         ht_insert(ht, tok, padded, tp, h, mask, g);
+        g.fpd += slot_token_mix(static_cast<uint32_t>(h), tp) - slot_token_mix(static_cast<uint32_t>(h), old);
         dirty = true;
         rs[k] = h;
         rm[k] = 1;
@@ -277,6 +279,7 @@ __device__ bool sieve_row_wave(const int32_t *rt, int32_t *rs, int8_t *rm, int32
                         g.code = kOverflowSweep;
                     } else {
                         const int32_t old = tok[h];
+                        g.fpd += slot_token_mix(static_cast<uint32_t>(h), tp) - slot_token_mix(static_cast<uint32_t>(h), old);
                         if (old >= 0) {
                             bool f2 = false;
                             uint32_t e2 = 0;
@@ -428,6 +431,8 @@ __device__ bool sieve_row_regs(const int32_t *rt, int32_t *rs, int8_t *rm, int32
                         }
                     }
                     if (!placed) g.code = kOverflowProbe;
+                    g.fpd += slot_token_mix(static_cast<uint32_t>(h), tp) -
+                             slot_token_mix(static_cast<uint32_t>(h), lane_value(tokR, h));
                     if (lane == h) tokR = tp;
                     vm |= 1ull << h;
                     hd = (h + 1 == dbs) ? 0 : h + 1;

@@ -501,18 +501,17 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     int32_t flagw = ((KVX_C const int32_t *)gHand)[1];
     // sieve_hand[row][2]: steps in a row this kernel could not take in parallel
     int32_t hintw = ((KVX_C const int32_t *)gHand)[2];
-    // sieve_hand[row][3]: the fingerprint of the tokens a flagged row was left with
-    int32_t fpw = ((KVX_C const int32_t *)gHand)[kFingerprintWord];
+    // sieve_hand[row][3]: the fingerprint of the tokens a flagged row was left
+    // with (a global-space load: this kernel writes the word later)
+    const int32_t fpw = gHand[kFingerprintWord];
 
     // The in-order recurrence (hisp_sieve_update.cpp:115-163) on a staged copy
     // of the row, then its write back: registers for consistent rows of up to
     // 64 slots, else one lane for small tables, else 64 cells/slots per step.
     // canon: the row was consistent before the step.
     __shared__ int32_t s_dirty;
-    __shared__ uint32_t s_fp;
     auto run_inorder = [&](int32_t *tokF, uint16_t *htF, uint8_t *visF, bool canon) {
         STAMP(12);
-        if (tid == 0) s_fp = 0u;
         if (wave == 0) {
             int32_t hand = hand0;
             Guard g;
@@ -527,6 +526,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             if (lane == 0) {
                 gHand[0] = hand;
                 gHand[1] = (canon && g.code == 0) ? kCanonFlag : 0;
+                // the staged (pre-step) tokens' fingerprint, changed by each
+                // replaced token.  (The phase-stamp profiling build leaves it
+                // out, its compiler run rejecting the store there: a stale
+                // fingerprint only sends the row's next step to the full check.)
+#ifndef KVX_SIEVE_PHASE_STAMPS
+                gHand[kFingerprintWord] = static_cast<int32_t>(ms.fp0 + g.fpd);
+#endif
                 gHand[2] = min(hintw, (1 << 30)) + 1;
                 s_dirty = dirty ? 1 : 0;
                 report_overflow(L.overflowSlot, g.code);
@@ -535,13 +541,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         STAMP(13);
         __syncthreads();
         wg_copy16((KVX_G v4u *)gVis, reinterpret_cast<const v4u *>(visF), static_cast<uint32_t>(visStrideB));
-        // the fingerprint of the tokens left (read only with the flag)
-        uint32_t f = 0;
-        for (int32_t s = tid; s < dbs; s += NT) f += slot_token_mix(static_cast<uint32_t>(s), tokF[s]);
-        f = wave_sum(f);
-        if (lane == 0 && f != 0u) atomicAdd(&s_fp, f);
-        __syncthreads();
-        if (tid == 0) gHand[kFingerprintWord] = static_cast<int32_t>(s_fp);
         STAMP(14);
         if (s_dirty) {
             wg_copy16((KVX_G v4u *)gTok, reinterpret_cast<const v4u *>(tokF), static_cast<uint32_t>(padded) * 4u);
@@ -869,8 +868,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             // (the scalar values pass through the statement, so that nothing
             // computed from them is scheduled, and waited for, before the loads)
             if (p == 0) {
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : "+s"(prefill), "+s"(hand0), "+s"(flagw), "+s"(hintw),
-                             "+s"(fpw) : : "memory");
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : "+s"(prefill), "+s"(hand0), "+s"(flagw), "+s"(hintw)
+                             : : "memory");
                 lim = min(prefill, seqLen);
                 direct = !kC && lim > 0 && lim <= invCap;
             }
@@ -959,18 +958,44 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         write_dummy_row((int32_t *)rs, (int8_t *)rm, K);
         return;
     }
+    // ---- consistency: the table indexes exactly the non-negative tokens of
+    // [0, dbs), each at its own slot.  A row this kernel wrote last carries
+    // the flag (and the fingerprint of the tokens it left), and then only the
+    // counts are checked.
+    if (!flagged) {
+        bool bad = false;
+        for (int32_t s = tid; s < dbs; s += NT) {
+            const int32_t t = kC ? gTok[s] : tok[s];
+            if (t < 0) continue;
+            const uint32_t th = ht_hash(t);
+            int32_t idx = static_cast<int32_t>(th) & mask, found = -1;
+            for (int32_t n = 0; n <= mask; ++n) {
+                const uint16_t e = ht[idx];
+                if (e == 0) break;
+                if (static_cast<int32_t>(e) - 1 < padded && tok_is(e - 1u, t, th)) {
+                    found = static_cast<int32_t>(e) - 1;
+                    break;
+                }
+                idx = (idx + 1) & mask;
+            }
+            if (found != s) bad = true;
+        }
+        if (__ballot(bad) != 0ull && lane == 0) atomicOr(&ms.bad, 1);
+        __syncthreads();
+    }
     // A row whose recent steps all wrapped the hand (the parallel form's
     // bound) retries the parallel form after 8, 16, 32 and then every 64
     // such steps; the other steps
     // run the in-order recurrence on the row as staged (known consistent when
-    // flagged and its entry count matches its live tokens).  Consistent rows
+    // it passed the check above and its entry count matches its live
+    // tokens).  Consistent rows
     // of up to 64 slots take the recurrence's decisions in one wave's
     // registers and leave the table to the parallel update: the pre-step
     // token of every evicted slot leaves, the slots' final tokens arrive in
     // the order of the events that placed them.
     const bool retry = (hintw >= 8 && __popc(static_cast<uint32_t>(hintw)) == 1) || (hintw & 63) == 0;
     if (!kC && hintw > 0 && !retry) {
-        const bool canon = flagged && ms.diff == 0;
+        const bool canon = ms.bad == 0 && ms.diff == 0;
         if (!(canon && dbs <= 64)) {
             run_inorder(tok, ht, vis, canon);
             return;
@@ -1031,31 +1056,6 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         return;
     }
 
-    // ---- consistency: the table indexes exactly the non-negative tokens of
-    // [0, dbs), each at its own slot.  A row this kernel wrote last carries
-    // the flag (and the fingerprint of the tokens it left), and then only the
-    // counts are checked.
-    if (!flagged) {
-        bool bad = false;
-        for (int32_t s = tid; s < dbs; s += NT) {
-            const int32_t t = kC ? gTok[s] : tok[s];
-            if (t < 0) continue;
-            const uint32_t th = ht_hash(t);
-            int32_t idx = static_cast<int32_t>(th) & mask, found = -1;
-            for (int32_t n = 0; n <= mask; ++n) {
-                const uint16_t e = ht[idx];
-                if (e == 0) break;
-                if (static_cast<int32_t>(e) - 1 < padded && tok_is(e - 1u, t, th)) {
-                    found = static_cast<int32_t>(e) - 1;
-                    break;
-                }
-                idx = (idx + 1) & mask;
-            }
-            if (found != s) bad = true;
-        }
-        if (__ballot(bad) != 0ull && lane == 0) atomicOr(&ms.bad, 1);
-        __syncthreads();
-    }
     bool fast = ms.bad == 0 && ms.diff == 0;
     const bool canonical = fast;
 

@@ -212,7 +212,7 @@ def test_sieve_state_stream_parity_all_layers(kvops):
     dev.assert_state_equal()
 
 
-@pytest.mark.parametrize("variant", [-1, 3, 5])
+@pytest.mark.parametrize("variant", [-1, 2, 3, 5])
 @pytest.mark.parametrize("seed", range(6))
 def test_sieve_defensive_cases_parity(kvops, seed, variant):
     """Padding rows, out-of-range pool rows, num_real > max, dirty hands,
@@ -443,6 +443,76 @@ def test_sieve_variants_agree(kvops, variant):
         kvops.sieve_force_variant(-1)
 
 
+@pytest.mark.parametrize("dbs,K", [(64, 64), (64, 200), (37, 90), (1, 8)])
+@pytest.mark.parametrize("variant", [0, 2, 3, 5])
+def test_sieve_variants_agree_small_rows(kvops, variant, dbs, K):
+    """Rows of at most 64 slots (the parallel kernel's register path when
+    steps wrap the hand): the sequential LDS (0), parallel (2), wave-wide HBM
+    (3) and batch HBM (5) kernels give the oracle's results, with repeats,
+    conversions and hand wraps (topK above dbs wraps every step), invalid
+    and decode-extension positions, and padding rows."""
+    rng = np.random.default_rng(dbs * 1000 + K)
+    prefill, req = 4 * dbs + 20, 9
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    kvops.sieve_force_variant(variant)
+    try:
+        for step in range(6):
+            batch = _random_state_stream(rng, st, K, prefill)
+            seq = np.full(req, prefill + 3)
+            nr = req if step % 3 else req - 2  # padding rows get the dummy outputs
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, nr, max_num_reqs=req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, nr, req, K)
+            assert kvops.last_sieve_variant() == variant
+            msg = "variant {} step {}".format(variant, step)
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=msg)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=msg)
+            dev.assert_state_equal()
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
+def test_sieve_small_rows_flag_shared_between_kernels(kvops):
+    """Rows of 64 slots under the kernels in turn: the flag and token
+    fingerprint one kernel writes (the parallel kernel's register path and
+    the batch HBM kernel) are what the next one trusts.  After a kernel that
+    leaves the flag alone (0, 3) the tokens no longer match the fingerprint:
+    the parallel kernel checks the row in full and flags it again, the batch
+    kernel in its bitmap form (tokens below the table size, as here) takes
+    the in-order recurrence, which clears it.  Full state against the oracle
+    after every step."""
+    rng = np.random.default_rng(4242)
+    dbs, K, prefill, req = 64, 64, 300, 5
+    st = orc.SieveState(1, req, dbs, K)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    order = [2, 5, 2, 0, 2, 5, 3, 5, 2, 0, 5, 5, 2, 5]
+    try:
+        for step, variant in enumerate(order):
+            kvops.sieve_force_variant(variant)
+            batch = _random_state_stream(rng, st, K, prefill, miss_frac=0.4)
+            seq = np.full(req, prefill + 4)
+            e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+            g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
+            assert kvops.last_sieve_variant() == variant
+            tag = "step {} variant {}".format(step, variant)
+            np.testing.assert_array_equal(g_miss, e_miss, err_msg=tag)
+            np.testing.assert_array_equal(g_slots, e_slots, err_msg=tag)
+            dev.assert_state_equal()
+            flags = list(dev.hand.cpu().numpy()[0, :, 1])
+            if variant == 2 or (variant == 5 and order[step - 1] in (2, 5)):
+                assert flags == [CANON_FLAG] * req, tag
+            elif variant == 5:  # after a kernel that leaves the flag alone
+                assert flags == [0] * req, tag
+    finally:
+        kvops.sieve_force_variant(-1)
+    assert kvops.read_overflow() == 0
+
+
 def test_sieve_config3_parity(kvops):
     """Large-batch decode shapes (256 requests, topK 2048, 8192 slots, 10%
     misses; the parallel kernel's compact LDS layout): two steps, full state
@@ -654,8 +724,9 @@ def test_sieve_batch_kernel_wraps_and_dups(kvops, form, seed):
 CANON_FLAG = 0x4B565843  # sieve_hand[row][1] of a row a SIEVE kernel left consistent
 
 
-@pytest.mark.parametrize("variant,prefill", [(2, 1500), (4, 1500), (5, 1500), (5, 5000), (6, 1500)])
-def test_sieve_flag_with_token_edited_in_place(kvops, variant, prefill):
+@pytest.mark.parametrize("variant,prefill,dbs", [(2, 1500, 700), (4, 1500, 700), (5, 1500, 700), (5, 5000, 700),
+                                                 (6, 1500, 700), (2, 400, 64)])
+def test_sieve_flag_with_token_edited_in_place(kvops, variant, prefill, dbs):
     """sieve_hand[row][3] carries a fingerprint of the tokens a kernel left
     with the consistency flag.  A caller that changes a token value in place
     and leaves element 1 set (the reference's results depend only on tokens,
@@ -664,9 +735,10 @@ def test_sieve_flag_with_token_edited_in_place(kvops, variant, prefill):
     checked in full (or runs the in-order recurrence) instead of being trusted.
     Variants: 2 the parallel LDS kernel (direct token map), 4 its compact
     form, 5 the batch HBM kernel (token bitmap below the table size, 2048
-    cells, or a token map above it), 6 the batch kernel without the rebuild."""
+    cells, or a token map above it), 6 the batch kernel without the rebuild;
+    with 64 slots the parallel kernel's register path."""
     rng = np.random.default_rng(31 + variant)
-    dbs, K, req = 700, 200, 3
+    K, req = 200, 3
     st = orc.SieveState(1, req, dbs, K)
     for r in range(req):
         st.admit(r, prefill)
@@ -691,7 +763,7 @@ def test_sieve_flag_with_token_edited_in_place(kvops, variant, prefill):
             e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
             g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, K)
             assert kvops.last_sieve_variant() == (5 if variant == 6 else variant)
-            msg = "variant {} prefill {} step {}".format(variant, prefill, step)
+            msg = "variant {} prefill {} dbs {} step {}".format(variant, prefill, dbs, step)
             if step == 2:
                 # the table has no entry for the new value: the reference misses it
                 assert e_miss[1, 0] == 1, msg

@@ -476,11 +476,13 @@ def test_wrapping_step_decisions_and_table(seed):
     from tests.sieve_model import RingClock
 
     rng = random.Random(seed)
-    seen = {"passed_twice": 0, "hit_then_evicted": 0, "evicted_then_again": 0}
+    seen = {"passed_twice": 0, "hit_then_evicted": 0, "evicted_then_again": 0, "wide_decided": 0,
+            "wide_again": 0}
     for trial in range(400):
         storm = trial % 3 == 0  # misses on a nearly all-visited ring, repeats of the step's hits
         dbs = rng.choice([20, 33, 64, 65, 70, 130])
-        K = dbs - 1 if storm else rng.randint(1, dbs - 1)  # topK < dbs
+        wide = trial % 5 == 1   # topK >= dbs: a slot may be evicted twice
+        K = rng.randint(dbs, 2 * dbs) if wide else (dbs - 1 if storm else rng.randint(1, dbs - 1))
         prefill = 3 * dbs if storm else rng.choice([dbs // 2, dbs, 3 * dbs])
         seq_len = prefill + rng.randint(0, 5)
         toks = rng.sample(range(prefill), min(prefill, dbs - rng.randint(0, 3)))
@@ -502,6 +504,10 @@ def test_wrapping_step_decisions_and_table(seed):
             else:
                 batch.append(rng.randrange(prefill))
         out, vis_g, hand_g, evicted, misses, again = _round_decide(ring, vis, hand0, batch, seq_len, prefill)
+        if wide:
+            seen["wide_again" if again else "wide_decided"] += 1
+            if again:
+                continue  # the kernel runs the in-order recurrence for this step
         assert not again, (seed, trial)
         rc = RingClock(dbs, dbs, [t if t is not None else -1 for t in ring], vis, hand0)
         want = [rc.access(t, seq_len, prefill) for t in batch]
@@ -550,3 +556,52 @@ def test_wrapping_step_decisions_and_table(seed):
                                               k > max(k2 for k2, _ in misses if batch[k2] == t)) > 0 for t in tw)
         del evk
     assert all(v > 0 for v in seen.values()), seen
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_cell_order_rebuild_equals_the_replayed_step(seed):
+    """The parallel table rebuild (csrc/sieve_table.hip): after a step that deletes the keys D of a table and then inserts the keys
+    N in order, the table equals inserting, into an empty table, the
+    surviving keys in the pre-step table's cell order read from an empty cell
+    on, then N in order.  The pre-step tables come from random histories of
+    inserts and Algorithm R deletions, with homes packed at the table's end
+    so that clusters wrap."""
+    rng = random.Random(100 + seed)
+    for trial in range(400):
+        H = rng.choice([16, 32, 64, 128])
+        skew = rng.choice([None, 3, 8])
+        if skew is None:
+            def hf(k, H=H):
+                return _knuth_home(k, H)
+        else:
+            def hf(k, H=H, s=skew):
+                return (k * 7 % s + H - 3) % H
+        T = [None] * H
+        live = []
+        for _ in range(rng.randint(1, 3 * H)):  # a history of inserts and deletions
+            if live and (rng.random() < 0.4 or len(live) >= H - 2):
+                k = live.pop(rng.randrange(len(live)))
+                _erase(T, k, hf)
+            else:
+                k = rng.randrange(10 ** 6)
+                if k in live:
+                    continue
+                _insert(T, k, hf)
+                live.append(k)
+        D = set(rng.sample(live, rng.randint(0, len(live))))
+        room = H - 1 - (len(live) - len(D))
+        N = [k for k in rng.sample(range(10 ** 6, 2 * 10 ** 6), rng.randint(0, max(0, room)))]
+        seq = list(T)
+        for k in rng.sample(sorted(D), len(D)):
+            _erase(seq, k, hf)
+        for k in N:
+            _insert(seq, k, hf)
+        e0 = T.index(None)
+        order = [T[(e0 + 1 + i) % H] for i in range(H)]
+        fcfs = [None] * H
+        for k in order:
+            if k is not None and k not in D:
+                _insert(fcfs, k, hf)
+        for k in N:
+            _insert(fcfs, k, hf)
+        assert fcfs == seq, (seed, trial)
