@@ -44,7 +44,9 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true",
                    help="skip the replay of the timed steps as captured HIP graphs")
     p.add_argument("--sieve-variant", type=int, default=-1,
-                   help="force a SIEVE kernel variant (0-4, see include/kvx/kvx.h); -1 = chosen per shape")
+                   help="force a SIEVE kernel variant (0-6, see include/kvx/kvx.h); -1 = chosen per shape")
+    p.add_argument("--loop-only", action="store_true",
+                   help="only the decode loop (no extra passes, no CPU baseline): for counter profiles")
     return p.parse_args()
 
 
@@ -170,6 +172,7 @@ def sieve_bytes(cfg, padded, vis_stride, ht_size, dirty_reqs):
 # Counter profiles committed per workload: HBM bytes per dispatch, from
 # FETCH_SIZE and WRITE_SIZE runs scaled by a known-size copy.
 TRAFFIC_PROFILES = {"c2-dsa-decode": "profiles/pmc_traffic_dsa_decode.md",
+                    "c3-large-batch-export": "profiles/pmc_traffic_large_batch_export.md",
                     "c4-slot-limit-stress": "profiles/pmc_traffic_slot_limit_stress.md"}
 # SIEVE kernel of each variant (kvx_last_sieve_variant), as named in the profiles
 SIEVE_KERNELS = {0: ("kvx_sieve_update",), 1: ("kvx_sieve_update",), 2: ("kvx_sieve_update_fast",),
@@ -831,12 +834,16 @@ def main():
         "verify": None if verify is None else verify["ok"],
         "verify_detail": verify,
     }
-    out["sieve_us_per_layer"]["standard_events"] = sieve_standard_events(runner, snap, warm, timed, fused, log)
-    out["sieve_back_to_back"] = sieve_pipelined(runner, snap, warm, timed, log)
-    out["graph"] = None if args.no_graph else graph_pass(runner, snap, warm, timed, fused, total_ms, log)
-    out["export_rows"] = export_rows_pass(runner, log)
-    out["import_curve"] = import_curve(runner, log)
-    if not args.no_cpu:
+    if args.loop_only:  # counter profiles: only the decode loop's dispatches
+        out["sieve_us_per_layer"]["standard_events"] = None
+        out["sieve_back_to_back"] = out["graph"] = out["export_rows"] = out["import_curve"] = None
+    else:
+        out["sieve_us_per_layer"]["standard_events"] = sieve_standard_events(runner, snap, warm, timed, fused, log)
+        out["sieve_back_to_back"] = sieve_pipelined(runner, snap, warm, timed, log)
+        out["graph"] = None if args.no_graph else graph_pass(runner, snap, warm, timed, fused, total_ms, log)
+        out["export_rows"] = export_rows_pass(runner, log)
+        out["import_curve"] = import_curve(runner, log)
+    if not args.no_cpu and not args.loop_only:
         out["cpu_baseline"] = cpu_baseline(runner, snap, plan, len(warm), args.cpu_sample_s, threads, log)
     else:
         out["cpu_baseline"] = None
