@@ -44,11 +44,17 @@ constexpr int32_t kCanonFlag = 0x4B565843;
 // flagged row is trusted only while its tokens still sum to it, so a token
 // edited in place without clearing the flag sends the row to the full check.
 constexpr int32_t kFingerprintWord = 3;
+// For a fixed slot the mix is a bijection of the token (every step is), so
+// one edited token always changes the sum.  It uses only full-rate 24-bit
+// multiplies (slot < 2^16): 32-bit ones issue at a quarter of the rate, and
+// the parallel kernel mixes every slot of the row each step.  Step 3 is a
+// bijection: its low 24 bits are x_lo * odd mod 2^24, which fixes x_lo, and
+// then its top byte fixes x_hi.
 __host__ __device__ __forceinline__ uint32_t slot_token_mix(uint32_t slot, int32_t token)
 {
-    uint32_t x = static_cast<uint32_t>(token) * 0x9E3779B1u + slot * 0x85EBCA77u;
+    uint32_t x = static_cast<uint32_t>(token) + (slot & 0xFFFFFFu) * 0x9E3779u;
     x ^= x >> 16;
-    x *= 0x7FEB352Du;
+    x = (x & 0xFFFFFFu) * 0x7FEB35u + (x & 0xFF000000u);
     x ^= x >> 15;
     return x;
 }

@@ -899,7 +899,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     for (int i = 0; i < 4; ++i) {
                         const bool live = i < room && tt[i] >= 0;
                         nTok += live ? 1u : 0u;
-                        fpS += i < room ? slot_token_mix(static_cast<uint32_t>(s0 + i), tt[i]) : 0u;
+                        // masked, not branched on: the mix is a few full-rate instructions
+                        fpS += slot_token_mix(static_cast<uint32_t>(s0 + i), tt[i]) & (i < room ? 0xFFFFFFFFu : 0u);
                         if (direct && i < room && static_cast<uint32_t>(tt[i]) < static_cast<uint32_t>(lim))
                             inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
                     }
