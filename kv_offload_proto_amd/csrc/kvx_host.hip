@@ -322,11 +322,11 @@ SievePlan PlanSieve(uint32_t top_k, uint32_t dbs, uint32_t padded, uint32_t visS
     p.rebuild = v == 5 && f != 6 && g.tableRebuild && kvx::table_rebuild_ok(htSize, dbs, top_k);
     p.ldsLaunch = v == 2 ? ldsFast
                          : (v == 4 ? std::max(ldsCompact, lds) : (v == 0 ? lds : (v == 5 ? ldsBatch : 0)));
-    // the parallel kernel's direct token -> slot map takes the LDS left over
-    // (rows whose prefill exceeds it probe the table instead)
+    // the parallel kernel's direct token -> slot map (32-bit entries) takes the
+    // LDS left over (rows whose prefill exceeds it probe the table instead)
     if (v == 2 && g.ldsLimit > ldsFast) {
-        p.invCap = static_cast<uint32_t>(std::min<size_t>((g.ldsLimit - ldsFast) / 2, 65536)) & ~15u;
-        p.ldsLaunch = ldsFast + static_cast<size_t>(p.invCap) * 2;
+        p.invCap = static_cast<uint32_t>(std::min<size_t>((g.ldsLimit - ldsFast) / 4, 65536)) & ~15u;
+        p.ldsLaunch = ldsFast + static_cast<size_t>(p.invCap) * 4;
     }
     return p;
 }

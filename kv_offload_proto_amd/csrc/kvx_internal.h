@@ -116,7 +116,8 @@ __host__ __device__ __forceinline__ uint32_t align16(uint32_t x) { return (x + 1
 // list with the conversions' old slots, the event sequence with the list of
 // undecided SM slots, and the SM list with the per-event cells and tokens.
 // In the compact form (rows whose full layout does not fit) the tokens row is
-// replaced by the Knuth hash of each slot's token (full tokens stay in HBM).
+// replaced by the Knuth hash of each slot's token (full tokens stay in HBM),
+// and the per-slot first-hit codes (vt) take 16 bits instead of 32.
 // cmask/emask/smask/rsn/rsm hold one 64-bit ballot per (wave, block of one
 // entry per lane).  ber, occ, fin and nkb are one bit per table cell: cells
 // of evicted tokens, the pre-step occupancy, the occupancy as the erase and
@@ -134,7 +135,7 @@ __host__ __device__ __forceinline__ FastLayout fast_layout(uint32_t padded, uint
     l.vis = o;     o += align16(visStrideB);
     l.ptok = o;    o += align16(topK * 4u);
     l.pinf = o;    o += align16(topK * 4u);
-    l.vt = o;      o += align16(padded * 2u);
+    l.vt = o;      o += align16(padded * (compact ? 2u : 4u));
     l.evslot = o;  o += align16(topK * 2u);
     l.smKp = o;    o += align16(topK * 2u + 16u);
     l.eseq = o;    o += align16(topK * 2u);
@@ -181,7 +182,7 @@ __host__ __device__ __forceinline__ FastLayout fast_layout_fixed(uint32_t padded
     uint32_t o = 0;
     l.ptok = o;    o += Kx * 4u;
     l.pinf = o;    o += Kx * 4u;
-    l.vt = o;      o += Dx * 2u;
+    l.vt = o;      o += Dx * (compact ? 2u : 4u);
     l.evslot = o;  o += Kx * 2u;
     l.smKp = o;    o += align16(Kx * 2u + 16u);
     l.eseq = o;    o += Kx * 2u;

@@ -383,9 +383,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     const int64_t reqIdx = badReq ? 0 : reqRaw;
     // direct token -> slot map over the tokens that can be looked up (below
     // both prefill and seqLen) when they fit the LDS left over after the
-    // layout: 0, slot+1 of the slot holding the token, or padded+1+k for a
-    // missing token first seen at position k (smallest k wins).  Cleared over
-    // min(seqLen, capacity) entries before the state row lands.
+    // layout, 32-bit entries: all ones, slot+1 of the slot holding the token,
+    // or padded+1+k for a missing token first seen at position k (the smallest
+    // k, by an LDS min).  Cleared over min(seqLen, capacity) entries before the
+    // state row lands.
     constexpr bool kFixed = PM > 0 && QM > 0;
     // fixed-count instantiations: compile-time offsets for the regions sized by topK and dbs
     const FastLayout lay = kFixed ? fast_layout_fixed<(kFixed ? PM : 1), (kFixed ? QM : 1)>(padded, H, visStrideB, kC)
@@ -393,11 +394,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // words of the visited bits set this step (bits of slots below dbs)
     const int32_t vsetWords = kFixed ? QM * NT / 32 : (visStrideB >> 2);
     const int32_t invCap = static_cast<int32_t>(a.reserved >> 8);
-    uint16_t *inv = reinterpret_cast<uint16_t *>(smem + lay.total);
-    uint32_t *inv32 = reinterpret_cast<uint32_t *>(smem + lay.total);
+    uint32_t *inv = reinterpret_cast<uint32_t *>(smem + lay.total);
     if (!kC && invCap > 0 && seqLen > 0) {
-        const int32_t n16 = (min(seqLen, invCap) + 7) >> 3;
-        for (int32_t i = tid; i < n16; i += NT) reinterpret_cast<v4u *>(inv)[i] = v4u{0u, 0u, 0u, 0u};
+        const int32_t n4 = (min(seqLen, invCap) + 3) >> 2;
+        for (int32_t i = tid; i < n4; i += NT) reinterpret_cast<v4u *>(inv)[i] = v4u{~0u, ~0u, ~0u, ~0u};
     }
     if (tid == 0) {  // ordered before every update by the barrier in the staging pass
         ms.bad = ms.ovf = ms.late = 0;
@@ -421,8 +421,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     uint32_t *vis32 = reinterpret_cast<uint32_t *>(smem + lay.vis);
     int32_t *ptok = reinterpret_cast<int32_t *>(smem + lay.ptok);
     uint32_t *pinf = reinterpret_cast<uint32_t *>(smem + lay.pinf);
-    uint16_t *vt = reinterpret_cast<uint16_t *>(smem + lay.vt);
-    uint32_t *vt32 = reinterpret_cast<uint32_t *>(smem + lay.vt);
+    // first-hit code per slot: 32 bits in the full form (an LDS min updates
+    // it), 16 in the compact form (a CAS on the containing word)
+    using VT = typename std::conditional<kC, uint16_t, uint32_t>::type;
+    VT *vt = reinterpret_cast<VT *>(smem + lay.vt);
     uint16_t *evslot = reinterpret_cast<uint16_t *>(smem + lay.evslot);
     uint16_t *smKp = reinterpret_cast<uint16_t *>(smem + lay.smKp);  // k of SM slots that can be evicted, else 0
     uint16_t *eseq = reinterpret_cast<uint16_t *>(smem + lay.eseq);
@@ -516,8 +518,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             int32_t hand = hand0;
             Guard g;
             bool dirty = false;
-            if (canon && dbs <= 64 && invCap >= H + 64) {  // scratch: the direct map's region
-                dirty = sieve_row_regs((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, inv, hand, g);
+            if (canon && dbs <= 64 && 2 * invCap >= H + 64) {  // scratch: the direct map's region
+                dirty = sieve_row_regs((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF,
+                                       reinterpret_cast<uint16_t *>(inv), hand, g);
             } else if (H <= kSmallTable) {
                 if (lane == 0) dirty = sieve_row_sequential((const int32_t *)rt, (int32_t *)rs, (int8_t *)rm, K, seqLen, prefill, dbs, padded, mask, tokF, visF, htF, hand, g);
             } else {
@@ -890,9 +893,14 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                     if (4 * c < dbs) {  // first-hit codes of the ring's slots: 0 visited, 0xFFFF not
                         const uint32_t nv4 = ~(vB[j] >> ((c & 1) * 4));  // bit i: slot 4c+i not visited
-                        const uint2 code = make_uint2(((nv4 & 1u) | ((nv4 & 2u) << 15)) * 0xFFFFu,
-                                                      (((nv4 >> 2) & 1u) | ((nv4 & 8u) << 13)) * 0xFFFFu);
-                        reinterpret_cast<uint2 *>(vt32)[c] = code;
+                        if constexpr (kC) {
+                            const uint2 code = make_uint2(((nv4 & 1u) | ((nv4 & 2u) << 15)) * 0xFFFFu,
+                                                          (((nv4 >> 2) & 1u) | ((nv4 & 8u) << 13)) * 0xFFFFu);
+                            reinterpret_cast<uint2 *>(vt)[c] = code;
+                        } else {
+                            reinterpret_cast<v4u *>(vt)[c] = v4u{(nv4 & 1u) * 0xFFFFu, ((nv4 >> 1) & 1u) * 0xFFFFu,
+                                                                 ((nv4 >> 2) & 1u) * 0xFFFFu, ((nv4 >> 3) & 1u) * 0xFFFFu};
+                        }
                     }
                     const int32_t s0 = c * 4, room = dbs - s0;  // slots of the chunk below dbs: i < room
 #pragma unroll
@@ -902,7 +910,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         // masked, not branched on: the mix is a few full-rate instructions
                         fpS += slot_token_mix(static_cast<uint32_t>(s0 + i), tt[i]) & (i < room ? 0xFFFFFFFFu : 0u);
                         if (direct && i < room && static_cast<uint32_t>(tt[i]) < static_cast<uint32_t>(lim))
-                            inv[tt[i]] = static_cast<uint16_t>(s0 + i + 1);
+                            inv[tt[i]] = static_cast<uint32_t>(s0 + i + 1);
                     }
                 }
             }
@@ -1062,12 +1070,12 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 
     // ---- classify every position; dedup the candidates (smallest position
     // of each missing token).  With the direct map a hit is an entry naming a
-    // slot, and a missing token keeps the smallest padded+1+k; the steps of a
-    // lane's positions interleave (map words, then first-hit words, then the
-    // updates).  Otherwise one probe of the table does both: a hit stops at
-    // its entry (provisional entries only fill empty cells, never the probe
-    // path of a resident token), a miss stops at its token's provisional
-    // entry padded+1+k or claims the first empty cell
+    // slot and lowers the slot's first-hit code, and a missing token lowers
+    // its entry to padded+1+k: both LDS mins, returning nothing, so a
+    // position is one map read and one update.  Otherwise one probe of the
+    // table does both: a hit stops at its entry (provisional entries only fill
+    // empty cells, never the probe path of a resident token), a miss stops at
+    // its token's provisional entry padded+1+k or claims the first empty cell
     if (fast && direct) {
         constexpr int PB = kFixed ? PM : 1;  // positions handled together
         for (int32_t q0 = 0; q0 < P; q0 += PB) {
@@ -1079,47 +1087,23 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 const int32_t t = k < K ? (kFixed ? tR[kFixed ? b : 0] : ptok[k]) : -1;
                 tq[b] = t;
                 inf[b] = (t < 0 || t >= seqLen) ? (CLS_INV << 30) : (t >= prefill) ? (CLS_EXT << 30) : 0xFFFFFFFFu;
-                wq[b] = inf[b] == 0xFFFFFFFFu ? inv32[t >> 1] : 0u;
-            }
-#pragma unroll
-            for (int b = 0; b < PB; ++b) {
-                if (inf[b] != 0xFFFFFFFFu) continue;
-                const int32_t k = tid + (q0 + b) * NT, t = tq[b];
-                const uint32_t sh = (static_cast<uint32_t>(t) & 1u) * 16u;
-                uint32_t old = wq[b];
-                const uint32_t cur0 = (old >> sh) & 0xFFFFu;
-                if (cur0 - 1u < static_cast<uint32_t>(dbs)) {
-                    inf[b] = (CLS_HIT << 30) | (cur0 - 1u);
-                    wq[b] = vt32[(cur0 - 1u) >> 1];
-                    continue;
-                }
-                inf[b] = CLS_CAND << 30;
-                const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
-                uint32_t *w = inv32 + (t >> 1);
-                for (;;) {  // the entry stays 0 or provisional: resident entries are written in staging only
-                    const uint32_t cur = (old >> sh) & 0xFFFFu;
-                    if (cur != 0u && cur <= v) break;  // an earlier position of the token holds it
-                    const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
-                    if (prev == old) break;
-                    old = prev;
-                }
+                wq[b] = inf[b] == 0xFFFFFFFFu ? inv[t] : 0u;
             }
 #pragma unroll
             for (int b = 0; b < PB; ++b) {
                 const int32_t k = tid + (q0 + b) * NT;
-                if (k >= K) continue;
-                if ((inf[b] >> 30) == CLS_HIT) {  // first hit of the slot: 16-bit min by CAS on its word
-                    const uint32_t s0 = inf[b] & 0xFFFFu;
-                    uint32_t *w = vt32 + (s0 >> 1);
-                    const uint32_t sh = (s0 & 1u) * 16u, v = static_cast<uint32_t>(k + 1);
-                    uint32_t old = wq[b];
-                    for (;;) {
-                        if (((old >> sh) & 0xFFFFu) <= v) break;
-                        const uint32_t prev = atomicCAS(w, old, (old & ~(0xFFFFu << sh)) | (v << sh));
-                        if (prev == old) break;
-                        old = prev;
+                if (inf[b] == 0xFFFFFFFFu) {
+                    const uint32_t cur0 = wq[b];
+                    if (cur0 - 1u < static_cast<uint32_t>(dbs)) {  // first hit of the slot: the smallest k + 1
+                        inf[b] = (CLS_HIT << 30) | (cur0 - 1u);
+                        if constexpr (!kC) atomicMin(vt + (cur0 - 1u), static_cast<uint32_t>(k + 1));
+                    } else {  // the entry stays all ones or provisional: resident entries are written in staging only
+                        inf[b] = CLS_CAND << 30;
+                        const uint32_t v = static_cast<uint32_t>(padded + 1 + k);
+                        if (v < cur0) atomicMin(inv + tq[b], v);
                     }
                 }
+                if (k >= K) continue;
                 if constexpr (kFixed) iR[b] = inf[b];
                 else pinf[k] = inf[b];
             }
@@ -1160,7 +1144,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         } else if (cur <= static_cast<uint32_t>(padded)) {
                             if (tok_is(cur - 1u, t, th)) {
                                 inf = (CLS_HIT << 30) | (cur - 1u);
-                                lds_min16(vt32, cur - 1u, static_cast<uint16_t>(k + 1));
+                                if constexpr (kC) lds_min16(reinterpret_cast<uint32_t *>(vt), cur - 1u, static_cast<uint16_t>(k + 1));
+                                else atomicMin(vt + (cur - 1u), static_cast<uint32_t>(k + 1));
                             } else {
                                 next = true;
                             }
@@ -1227,7 +1212,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     uint32_t k1;
                     if (direct) {
                         const int32_t t = kFixed ? tR[kFixed ? q : 0] : ptok[k];
-                        k1 = static_cast<uint32_t>(inv[t]) - static_cast<uint32_t>(padded) - 1u;
+                        k1 = inv[t] - static_cast<uint32_t>(padded) - 1u;
                         if constexpr (kFixed) iR[q] = (CLS_CAND << 30) | k1;
                         else pinf[k] = (CLS_CAND << 30) | k1;
                     } else {
