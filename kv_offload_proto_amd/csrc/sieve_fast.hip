@@ -95,10 +95,12 @@ constexpr uint32_t NOCELL = 0xFFFFu;   // evicted slot without a table entry
 __device__ unsigned long long kvx_dbg_stamps[1024][16];
 __device__ unsigned long long kvx_dbg_sub[1024][16];
 // the arrays' addresses are taken once, at entry: a stamp is then a clock
-// read and a store, with no address load queued ahead of the clock read
-#define DBG_SETUP()                                           \
-    unsigned long long *dbgSt = &kvx_dbg_stamps[0][0];        \
-    unsigned long long *dbgSub = &kvx_dbg_sub[0][0];          \
+// read and a store, with no address load queued ahead of the clock read.  The
+// pointers carry the global address space: a flat store would also count
+// against the LDS wait counter and hold up the phase after each stamp.
+#define DBG_SETUP()                                                                         \
+    KVX_G unsigned long long *dbgSt = (KVX_G unsigned long long *)&kvx_dbg_stamps[0][0];    \
+    KVX_G unsigned long long *dbgSub = (KVX_G unsigned long long *)&kvx_dbg_sub[0][0];      \
     asm volatile("" : "+s"(dbgSt), "+s"(dbgSub))
 #define STAMP(i)                                                        \
     do {                                                                \
@@ -1202,6 +1204,21 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     MaskPrefix snP, smP;                // SN / SM slots before a ring offset
     if (fast) {
         uint32_t cw = 0;
+        // the fixed-count kernels issue this half's LDS reads (map entries,
+        // first-hit codes) together, unconditionally at clamped indices: a
+        // read under a branch is waited for before the next one issues
+        uint32_t mq[PR], vq[QR];
+        if constexpr (kFixed) {
+            if (direct) {
+#pragma unroll
+                for (int q = 0; q < PR; ++q) {
+                    const bool cand = tid + q * NT < K && (iR[q] >> 30) == CLS_CAND;
+                    mq[q] = inv[cand ? tR[q] : 0];  // a candidate's token lies below lim <= invCap
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < QR; ++j) vq[j] = vt[ring_slot(hand0, min(tid + j * NT, dbs - 1), dbs)];
+        }
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
@@ -1212,7 +1229,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     uint32_t k1;
                     if (direct) {
                         const int32_t t = kFixed ? tR[kFixed ? q : 0] : ptok[k];
-                        k1 = inv[t] - static_cast<uint32_t>(padded) - 1u;
+                        k1 = (kFixed ? mq[kFixed ? q : 0] : inv[t]) - static_cast<uint32_t>(padded) - 1u;
                         if constexpr (kFixed) iR[q] = (CLS_CAND << 30) | k1;
                         else pinf[k] = (CLS_CAND << 30) | k1;
                     } else {
@@ -1231,7 +1248,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 #pragma unroll
         for (int32_t j = 0; j < Q; ++j) {
             const int32_t u = tid + j * NT;
-            const uint32_t v = (u < dbs) ? vt[ring_slot(hand0, u, dbs)] : 0u;
+            const uint32_t v = (u < dbs) ? (kFixed ? vq[kFixed ? j : 0] : vt[ring_slot(hand0, u, dbs)]) : 0u;
             if constexpr (kFixed) vR[j] = v;
             const bool sn = u < dbs && v == VT_NONE, sm = u < dbs && v != 0u && v != VT_NONE;
             snM |= (sn ? 1u : 0u) << j;
@@ -1259,7 +1276,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 if (snP.base(e) >= M) continue;  // the whole block lies past the M-th SN slot
                 const bool isSM = (smM >> j) & 1u, isSN = (snM >> j) & 1u;
                 const int32_t u = tid + j * NT;
-                const uint32_t nsn = snP.own(e), nsm = smP.own(e);
+                // this wave's own ballots of block j, rebuilt from the lane's class
+                // bits (no LDS read)
+                const uint32_t nsn = snP.base(e) + lanes_below(__ballot(isSN)),
+                               nsm = smP.base(e) + lanes_below(__ballot(isSM));
                 uint32_t k = 0;
                 if (isSM) k = (kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)])) - 1u;
                 const uint32_t cc = cp.before(static_cast<int32_t>(k >> 6), k & 63u);
@@ -1580,10 +1600,11 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             const int32_t e = j * NWAVES + wave;
             // with N SN slots before the block, every offset in it has r >= N
             if (snP.base(e) >= static_cast<uint32_t>(N)) continue;
-            const uint32_t nsn2 = snP.own(e), nsm2 = min(smP.own(e), nSMu);
+            const bool isSN = (snM >> j) & 1u, isSM = (smM >> j) & 1u;
+            const uint32_t nsn2 = snP.base(e) + lanes_below(__ballot(isSN)),
+                           nsm2 = min(smP.base(e) + lanes_below(__ballot(isSM)), nSMu);
             if (u >= dbs) continue;
             const int32_t s = ring_slot(hand0, u, dbs);
-            const bool isSN = (snM >> j) & 1u, isSM = (smM >> j) & 1u;
             const uint32_t tbv = tb[nsm2];
             const int32_t r = static_cast<int32_t>(nsn2 + (tbv & 0x7FFFu));
             if (r < N) {
