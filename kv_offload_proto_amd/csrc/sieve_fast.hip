@@ -1315,10 +1315,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const uint4 *kp4 = reinterpret_cast<const uint4 *>(smKp);
         for (int32_t i = tid / G; i < nSM; i += NT / G) {
             const uint32_t eb = smB[i];
+            const uint32_t ki = smA[i] >> 16;  // read with eb: a read under the branch would wait on its own
             const int32_t ai = static_cast<int32_t>(eb >> 16) - static_cast<int32_t>(eb & 0xFFFFu) - 1;
             uint16_t dec = 0;  // 0 passed, 1 evicted, 2 undecided
             if (ai >= 0) {
-                const uint32_t ki = smA[i] >> 16;
                 uint32_t U = 0;
                 const int32_t nb = i >> 3;  // blocks of 8 entirely before i
                 // two entries per 32-bit word: saturating k_j - k_i, capped at
@@ -1382,17 +1382,23 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
             if (lane_value(old, 0) == NWAVES - 1) {
                 __threadfence_block();
-                uint32_t kq[4], bq[4];
+                uint32_t kq[4], bq[4], tq[4];
                 uint64_t evq[4], undq[4];
+                // all twelve reads issued together (clamped, unconditional)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const int32_t j = c * 64 + static_cast<int32_t>(lane);
-                    const bool ok = j < nSM;
-                    const uint32_t t = ok ? tb[j] : 0u;
-                    kq[c] = ok ? (smA[j] >> 16) : 0u;
-                    bq[c] = ok ? smB[j] : 0u;
-                    evq[c] = __ballot(t == 1u);
-                    undq[c] = __ballot(t == 2u);
+                    const int32_t j = min(c * 64 + static_cast<int32_t>(lane), max(nSM - 1, 0));
+                    tq[c] = tb[j];
+                    kq[c] = smA[j];
+                    bq[c] = smB[j];
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const bool ok = c * 64 + static_cast<int32_t>(lane) < nSM;
+                    kq[c] = ok ? (kq[c] >> 16) : 0u;
+                    bq[c] = ok ? bq[c] : 0u;
+                    evq[c] = __ballot(ok && tq[c] == 1u);
+                    undq[c] = __ballot(ok && tq[c] == 2u);
                 }
                 if ((undq[0] | undq[1] | undq[2] | undq[3]) != 0ull) {
 #pragma unroll
@@ -1605,6 +1611,10 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                            nsm2 = min(smP.base(e) + lanes_below(__ballot(isSM)), nSMu);
             if (u >= dbs) continue;
             const int32_t s = ring_slot(hand0, u, dbs);
+            // the evicted token's table cell, looked up (and marked in ber)
+            // while deciding (SN: vt) or in the events phase (SM: smCell);
+            // read with tb so the three reads wait together
+            const uint32_t cellSN = vt[s], cellSM = smCell[nsm2];
             const uint32_t tbv = tb[nsm2];
             const int32_t r = static_cast<int32_t>(nsn2 + (tbv & 0x7FFFu));
             if (r < N) {
@@ -1617,9 +1627,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                         const uint32_t v0 = kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[s]);
                         vt[s] = static_cast<uint16_t>(VT_EVICTED | (v0 - 1u));
                     }
-                    // looked up (and marked in ber) while deciding (SN) or in
-                    // the events phase (SM)
-                    const uint32_t cell = isSN ? static_cast<uint32_t>(vt[s]) : static_cast<uint32_t>(smCell[nsm2]);
+                    const uint32_t cell = isSN ? (cellSN & 0xFFFFu) : cellSM;
                     ecell[r] = cell | (static_cast<uint32_t>(s) << 16);
                 } else {
                     vt[s] = static_cast<uint16_t>(VT_PASSED | p);
