@@ -455,6 +455,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     int32_t *ntokv = reinterpret_cast<int32_t *>(smB);       // per event: the token inserted
     uint16_t *snList = evslot;                               // scan -> decide: the evicted SN slots in ring order
     uint16_t *smCell = smKp;                                 // events -> marks: table cell of each evicted SM slot
+    // decide -> events: every SM slot's cell (fixed-count kernels, whose
+    // topK tokens stay in registers: the row's region is dead after classify)
+    uint16_t *smCellX = reinterpret_cast<uint16_t *>(ptok);
 
     // token of slot s equals t (th = its hash); the compact form checks the
     // hash in LDS and confirms with the HBM row
@@ -470,22 +473,28 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if constexpr (kC) return static_cast<int32_t>(hv[s]) & mask;
         else return static_cast<int32_t>(ht_hash(tok[s])) & mask;
     };
+    // table cell of live slot s's entry, NOCELL when the probe does not find it
+    auto cell_find = [&](int32_t s) -> uint32_t {
+        int32_t idx = slot_home(s);
+        for (int32_t n = 0; n <= mask; ++n) {
+            const uint32_t ev = ht[idx];
+            if (ev == static_cast<uint32_t>(s + 1)) return static_cast<uint32_t>(idx);
+            if (ev == 0u) break;
+            idx = (idx + 1) & mask;
+        }
+        return NOCELL;
+    };
+    // mark the cell of a live slot's entry in ber (a missing entry is a bound violation)
+    auto cell_mark = [&](uint32_t cell) {
+        if (cell == NOCELL) atomicOr(&ms.ovf, 1);
+        else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+    };
     // table cell of slot s's entry (NOCELL for an empty slot), marked in ber
     auto cell_of = [&](int32_t s) -> uint32_t {
         uint32_t cell = NOCELL;
         if (slot_live(s)) {
-            int32_t idx = slot_home(s);
-            for (int32_t n = 0; n <= mask; ++n) {
-                const uint32_t ev = ht[idx];
-                if (ev == static_cast<uint32_t>(s + 1)) {
-                    cell = static_cast<uint32_t>(idx);
-                    break;
-                }
-                if (ev == 0u) break;
-                idx = (idx + 1) & mask;
-            }
-            if (cell == NOCELL) atomicOr(&ms.ovf, 1);
-            else atomicOr(ber + (cell >> 5), 1u << (cell & 31u));
+            cell = cell_find(s);
+            cell_mark(cell);
         }
         return cell;
     };
@@ -1428,15 +1437,23 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                     }
                 }
             }
+            // lookups 64 at a time from a shared counter: the evicted SN slots'
+            // cells, then (fixed-count kernels) every SM slot's cell, kept
+            // unmarked in smCellX for the events phase, which marks the ones
+            // the settled decisions evict; the waves not settling do them
+            const int32_t nLook = nSNev + (kFixed ? nSM : 0);
             for (;;) {
                 int32_t x0 = 0;
                 if (lane == 0) x0 = atomicAdd(&ms.snNext, 64);
                 x0 = lane_value(x0, 0);
-                if (x0 >= nSNev) break;
+                if (x0 >= nLook) break;
                 const int32_t x = x0 + static_cast<int32_t>(lane);
                 if (x < nSNev) {
                     const int32_t sl = snList[x];
                     vt[sl] = static_cast<uint16_t>(cell_of(sl));
+                } else if (x < nLook) {  // an SM slot holds the token its first hit found: live
+                    const int32_t i = x - nSNev;
+                    smCellX[i] = static_cast<uint16_t>(cell_find(ring_slot(hand0, static_cast<int32_t>(smA[i] & 0xFFFFu), dbs)));
                 }
             }
             __syncthreads();
@@ -1582,11 +1599,20 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
             }
         }
         if (ep.total != static_cast<uint32_t>(N)) fast = false;  // same value in every wave
-        // table cells of the evicted SM slots' tokens
+        // table cells of the evicted SM slots' tokens (looked up while
+        // deciding when the short list's lookups ran there)
+        const bool smPre = kFixed && nSM <= 4 * 64;
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
             if (i < nSM && ((smask[i >> 6] >> (i & 63)) & 1ull)) {
-                smCell[i] = static_cast<uint16_t>(cell_of(ring_slot(hand0, static_cast<int32_t>(smA[i] & 0xFFFFu), dbs)));
+                uint32_t cell;
+                if (smPre) {
+                    cell = smCellX[i];
+                    cell_mark(cell);
+                } else {
+                    cell = cell_of(ring_slot(hand0, static_cast<int32_t>(smA[i] & 0xFFFFu), dbs));
+                }
+                smCell[i] = static_cast<uint16_t>(cell);
             }
         }
         __syncthreads();
