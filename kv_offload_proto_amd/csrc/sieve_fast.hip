@@ -1672,7 +1672,19 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         const int32_t uEnd = ms.uEnd;
         // ---- outputs and visited bits set this step (vset); erase the
         // evicted tokens: the rightmost marked cell of each pre-step cluster
-        // (from the occupancy snapshot) leads it and deletes right to left
+        // (from the occupancy snapshot) leads it and deletes right to left.
+        // The fixed-count kernels read every position's code (hit) and
+        // event slot (candidate) together, at clamped indices.
+        uint32_t vq[PR], eq[PR];
+        if constexpr (kFixed) {
+#pragma unroll
+            for (int q = 0; q < PR; ++q) {
+                const bool ok = tid + q * NT < K;
+                const uint32_t cls = iR[q] >> 30, x = iR[q] & 0xFFFFu;
+                vq[q] = vt[(ok && cls == CLS_HIT) ? x : 0u];
+                eq[q] = evslot[(ok && cls == CLS_CAND) ? x : 0u];
+            }
+        }
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
@@ -1685,7 +1697,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 slot = padded + ((kFixed ? tR[kFixed ? q : 0] : ptok[k]) - prefill);
             } else if (cls == CLS_HIT) {
                 const uint32_t s0 = inf & 0xFFFFu;
-                const uint16_t v = vt[s0];
+                const uint16_t v = kFixed ? vq[kFixed ? q : 0] : vt[s0];
                 if (v & VT_EVICTED) {  // evicted before its first hit: converted at time c
                     const uint32_t c = v & VT_NOCONV;
                     slot = evslot[c];
@@ -1698,7 +1710,7 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                 }
             } else if (cls == CLS_CAND) {
                 const uint32_t k1 = inf & 0xFFFFu;
-                slot = evslot[k1];
+                slot = kFixed ? eq[kFixed ? q : 0] : evslot[k1];
                 miss = (k1 == static_cast<uint32_t>(k)) ? 1 : 0;
             }
             rs[k] = slot;
