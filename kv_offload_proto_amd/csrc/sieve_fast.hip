@@ -271,15 +271,18 @@ template <bool kC>
 __device__ void rdel_at(uint16_t *ht, uint32_t *fin, const void *tokv, int32_t ntok, int32_t c, int32_t mask,
                         Guard &g)
 {
-    int32_t j = c, i = c;
+    // the next cell is read with the current entry's token: a move writes
+    // only cells left of the current one, never the next
+    int32_t j = c, i = (c + 1) & mask;
+    uint16_t e = ht[i];
     for (int32_t n = 0;; ++n) {
         if (n > mask) {
             g.code = kOverflowProbe;
             return;
         }
-        i = (i + 1) & mask;
-        const uint16_t e = ht[i];
         if (e == 0) break;
+        const int32_t inext = (i + 1) & mask;
+        const uint16_t enext = ht[inext];
         int32_t home;
         if constexpr (kC) {
             const uint16_t *hv = static_cast<const uint16_t *>(tokv);
@@ -292,6 +295,8 @@ __device__ void rdel_at(uint16_t *ht, uint32_t *fin, const void *tokv, int32_t n
             ht[j] = e;
             j = i;
         }
+        i = inext;
+        e = enext;
     }
     ht[j] = 0;
     atomicAnd(fin + (j >> 5), ~(1u << (j & 31)));
