@@ -324,6 +324,38 @@ def test_sieve_fast_kernel_parity_mid(kvops, seed):
     assert kvops.read_overflow() == 0
 
 
+@pytest.mark.parametrize("dbs,top_k,prefill", [(4096, 2048, 6000), (4096, 1500, 9000), (4096, 2048, 60000),
+                                               (3500, 1100, 7000), (8192, 2048, 12000), (8192, 1300, 50000)])
+def test_sieve_fixed_kernels_mixed_streams(kvops, dbs, top_k, prefill):
+    """The fixed-count kernels (two positions per lane, four or eight ring
+    offsets) on streams with duplicate positions, invalid and decode-extension
+    positions and a random miss share per step; topK below 2048 leaves the
+    upper lanes' second position past topK; a prefill above the direct map's
+    capacity takes the probing classify; 8192 slots take the compact form."""
+    req = 6
+    st = orc.SieveState(1, req, dbs, top_k)
+    for r in range(req):
+        st.admit(r, prefill)
+    dev = DevSieve(st)
+    rng = np.random.default_rng(dbs + top_k + prefill)
+    parallel = 0
+    for step in range(5):
+        # miss shares the hand can serve without coming round (else the row
+        # takes the in-order recurrence for the next steps)
+        batch = _random_state_stream(rng, st, top_k, prefill, miss_frac=float(rng.uniform(0.05, 0.3)))
+        seq = np.full(req, prefill + 2)
+        e_slots, e_miss = st.update(0, batch, np.arange(req), seq, req)
+        g_slots, g_miss, _ = dev.update(kvops, 0, batch, np.arange(req), seq, req, req, top_k)
+        assert kvops.last_sieve_variant() == (4 if dbs > 4096 else 2)
+        np.testing.assert_array_equal(g_miss, e_miss, err_msg="step {}".format(step))
+        np.testing.assert_array_equal(g_slots, e_slots, err_msg="step {}".format(step))
+        dev.assert_state_equal()
+        # sieve_hand[row][2] counts the steps in a row taken in order: 0 after a parallel one
+        parallel += int((dev.hand[0, :, 2].cpu().numpy() == 0).sum())
+    assert parallel >= 5 * req // 2
+    assert kvops.read_overflow() == 0
+
+
 @pytest.mark.parametrize("dbs", [4096, 8192])
 def test_sieve_fast_kernel_shuffled_batch(kvops, dbs):
     """The fixed-count kernels (topK 2048; rings of 4096 slots in the full LDS
