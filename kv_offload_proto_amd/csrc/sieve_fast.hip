@@ -1578,15 +1578,30 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     int32_t N = 0;
     if (fast) {
         const int32_t Ps = (nSM + NT - 1) / NT;
+        // the fixed-count kernels read this wave's own mask entries (evicted SM
+        // slots; event positions) and, for the short list, its SM slots'
+        // looked-up cells once, together with the prefix inputs
+        constexpr int PS2 = kFixed ? 2 : 1;  // nSM <= topK <= 2 NT
+        uint64_t entS[PS2], entE[PR];
+        uint32_t cellX = 0;
+        const bool smPre = kFixed && nSM <= 4 * 64;
+        if constexpr (kFixed) {
+#pragma unroll
+            for (int q = 0; q < PS2; ++q) entS[q] = smask[q * NWAVES + wave];
+#pragma unroll
+            for (int q = 0; q < PR; ++q) entE[q] = cmask[q * NWAVES + wave] | emask[q * NWAVES + wave];
+            if (smPre) cellX = smCellX[min(tid, 4 * 64 - 1)];
+        }
         MaskPrefix sp, ep;
         // events: candidates' first occurrences (cmask) and conversions (emask)
         MaskPrefix::init_pair(sp, smask, Ps * NWAVES, ep, cmask, P * NWAVES, lane, emask);
         const uint32_t T = sp.total;
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
-            const uint32_t pre = sp.own(q * NWAVES + wave);
+            const uint64_t es = kFixed ? entS[kFixed ? q : 0] : sp.ent(q * NWAVES + wave);
+            const uint32_t pre = sp.base(q * NWAVES + wave) + lanes_below(es);
             if (i < nSM) {
-                const uint32_t tk = static_cast<uint32_t>((smask[i >> 6] >> (i & 63)) & 1ull);  // evicted
+                const uint32_t tk = static_cast<uint32_t>((es >> lane) & 1ull);  // evicted
                 tb[i] = static_cast<uint16_t>(pre | (tk << 15));
             }
         }
@@ -1595,8 +1610,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
 #pragma unroll
         for (int32_t q = 0; q < P; ++q) {
             const int32_t k = tid + q * NT;
-            const uint32_t pre = ep.own(q * NWAVES + wave);
-            if (k < K && ((ep.ent(k >> 6) >> (k & 63)) & 1ull)) {
+            const uint64_t ee = kFixed ? entE[kFixed ? q : 0] : ep.ent(q * NWAVES + wave);
+            const uint32_t pre = ep.base(q * NWAVES + wave) + lanes_below(ee);
+            if (k < K && ((ee >> lane) & 1ull)) {
                 // the event inserts the position's own token: a candidate's,
                 // or for a conversion the token of the slot its hit lost
                 eseq[pre] = static_cast<uint16_t>(k);
@@ -1606,13 +1622,13 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
         if (ep.total != static_cast<uint32_t>(N)) fast = false;  // same value in every wave
         // table cells of the evicted SM slots' tokens (looked up while
         // deciding when the short list's lookups ran there)
-        const bool smPre = kFixed && nSM <= 4 * 64;
         for (int32_t q = 0; q < Ps; ++q) {
             const int32_t i = tid + q * NT;
-            if (i < nSM && ((smask[i >> 6] >> (i & 63)) & 1ull)) {
+            const uint64_t es = kFixed ? entS[kFixed ? q : 0] : smask[i >> 6];
+            if (i < nSM && ((es >> (i & 63)) & 1ull)) {
                 uint32_t cell;
                 if (smPre) {
-                    cell = smCellX[i];
+                    cell = cellX;  // smPre: nSM <= 256, so q == 0 and i == tid
                     cell_mark(cell);
                 } else {
                     cell = cell_of(ring_slot(hand0, static_cast<int32_t>(smA[i] & 0xFFFFu), dbs));
