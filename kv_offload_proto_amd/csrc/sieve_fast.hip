@@ -1296,7 +1296,16 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
                                nsm = smP.base(e) + lanes_below(__ballot(isSM));
                 uint32_t k = 0;
                 if (isSM) k = (kFixed ? vR[kFixed ? j : 0] : static_cast<uint32_t>(vt[ring_slot(hand0, u, dbs)])) - 1u;
-                const uint32_t cc = cp.before(static_cast<int32_t>(k >> 6), k & 63u);
+                uint32_t cc;
+                if constexpr (kFixed) {
+                    // one mask entry per lane (P * NWAVES <= 64): the prefix of entry
+                    // k/64 and its bits below k, the two LDS reads issued together
+                    const int32_t e2 = static_cast<int32_t>(k >> 6);
+                    const uint32_t pre = static_cast<uint32_t>(__shfl(static_cast<int>(cp.ex), e2));
+                    cc = pre + static_cast<uint32_t>(__popcll(cmask[e2] & ((1ull << (k & 63u)) - 1ull)));
+                } else {
+                    cc = cp.before(static_cast<int32_t>(k >> 6), k & 63u);
+                }
                 if (isSM && nsn < M) {
                     smA[nsm] = static_cast<uint32_t>(u) | (k << 16);
                     smB[nsm] = nsn | (cc << 16);
