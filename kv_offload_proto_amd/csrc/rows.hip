@@ -301,10 +301,17 @@ __global__ __launch_bounds__(256) void kvx_gather_span(GatherParams P)
 }
 
 // Small batches (max_num_reqs * top_k <= kSmallMaxPositions): the three
-// passes in one launch.  Every workgroup tags the winners of all positions
-// (the same atomicMax values, so the repeats are harmless) and counts the
-// queued rows and errors of all positions in its own LDS, then moves the
-// winners among its own kSmallSpan positions: the rows spread over
+// passes in one launch.  A winner is the last miss on its destination row;
+// the rows of request b start at b * spanRows, so a row that a later request
+// can also reach is one whose slot is at or past spanRows.  Each workgroup
+// loads the slots of the requests its own kSmallSpan positions belong to
+// into LDS; when none of its own positions has such a slot (the usual case),
+// eight lanes per own position look for a later position of the same
+// request with the same slot, and no global tags are needed.  Otherwise the
+// workgroup tags every position of the call (relaxed device-scope max, as
+// the two-launch path does) and reads its own positions' tags.  Each
+// workgroup counts the queued rows and errors of all positions in its own
+// LDS, then moves the winners among its own positions: the rows spread over
 // ceil(positions / kSmallSpan) CUs (one CU reads only a few GB/s from host
 // memory), with no counters shared between workgroups.  The last workgroup
 // (ticket) advances the epoch and stores the status words.
@@ -315,7 +322,8 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
 {
     __shared__ uint32_t sCnt[64 * 8], sErr[64 * 8];
     __shared__ uint64_t sSrc[kSmallSpan], sDst[kSmallSpan];
-    __shared__ uint32_t sN, sEpoch;
+    __shared__ int32_t sKey[kSmallMaxPositions];  // slot of each position of the requests met, or -1
+    __shared__ uint32_t sN, sEpoch, sLose;         // sLose bit i: own position lo + i is not a winner
     __shared__ int sLast;
     const KvcGatherArgs &a = P.l.a;
     const GatherExtra &x = P.x;
@@ -346,24 +354,59 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
     }
     __syncthreads();
     const unsigned long long tagHi = static_cast<unsigned long long>(sEpoch) << 32;
-    for (int64_t p = tid; p < total; p += blockDim.x) {
-        if (miss[p] == 0) continue;
-        const int32_t t = topk[p], s = slots[p];
-        if (t < 0 || s < 0 || s >= 65536) continue;
-        const int64_t bid = p / a.topK;
-        if (pool[bid] < 0) continue;
-        const uint64_t d = win_index(bid, s, x.spanRows);
-        if (d < x.winEntries) win_max(x.win + d, tagHi | static_cast<unsigned long long>(p));
-    }
-    __threadfence();
-    __syncthreads();
     const int64_t lo = static_cast<int64_t>(blockIdx.x) * kSmallSpan, hi = lo + kSmallSpan;
-    for (int64_t p = tid; p < total; p += blockDim.x) {
-        if (miss[p] == 0) continue;
-        const int32_t t = topk[p], s = slots[p];
+    // the slot of position p when p takes part in the winner rule, else -1
+    // (the four reads issued together)
+    auto tagged_slot = [&](int64_t p) -> int32_t {
         const int64_t bid = p / a.topK;
-        if (t < 0 || s < 0 || pool[bid] < 0) continue;
-        const uint32_t row = static_cast<uint32_t>(hostBase[bid] + t);  // kvc_gather_rows.cpp:69-73
+        const int8_t m = miss[p];
+        const int32_t t = topk[p], s = slots[p];
+        const int64_t pl = pool[bid];
+        if (m == 0 || t < 0 || s < 0 || s >= 65536 || pl < 0) return -1;
+        return win_index(bid, s, x.spanRows) < x.winEntries ? s : -1;
+    };
+    // the positions of the requests that [lo, hi) meets (at most the call's)
+    const int64_t tagLo = lo < total ? (lo / a.topK) * a.topK : total;
+    const int64_t tagHiPos = hi < total ? ((hi - 1) / a.topK + 1) * a.topK : total;
+    int shared = 0;
+    for (int64_t p = tagLo + tid; p < tagHiPos; p += blockDim.x) {
+        const int32_t s = tagged_slot(p);
+        sKey[p - tagLo] = s;
+        shared |= (p >= lo && p < hi && s >= 0 && static_cast<uint32_t>(s) >= x.spanRows) ? 1 : 0;
+    }
+    if (tid == 0) sLose = 0u;
+    const bool global = __syncthreads_or(shared) != 0;
+    if (global) {
+        for (int64_t p = tid; p < total; p += blockDim.x) {
+            const int32_t s = tagged_slot(p);
+            if (s >= 0) win_max(x.win + win_index(p / a.topK, s, x.spanRows), tagHi | static_cast<unsigned long long>(p));
+        }
+        __threadfence();
+    } else {
+        // lanes 8i .. 8i+7: own position lo + i against the later positions of its request
+        const int64_t p = lo + static_cast<int64_t>(tid >> 3);
+        int32_t s = -1;
+        int64_t end = 0;
+        if (p < hi && p < total) {
+            s = sKey[p - tagLo];
+            end = (p / a.topK + 1) * a.topK;
+        }
+        bool later = false;
+        if (s >= 0) {
+            for (int64_t q = p + 1 + static_cast<int64_t>(tid & 7u); q < end; q += 8) later |= sKey[q - tagLo] == s;
+        }
+        const uint64_t m = __ballot(later);
+        const uint32_t lane = static_cast<uint32_t>(lane_id());
+        if ((tid & 7u) == 0u && ((m >> lane) & 0xFFull) != 0ull) atomicOr(&sLose, 1u << (tid >> 3));
+    }
+    __syncthreads();
+    for (int64_t p = tid; p < total; p += blockDim.x) {
+        const int64_t bid = p / a.topK;
+        const int8_t m = miss[p];  // the five reads issued together
+        const int32_t t = topk[p], s = slots[p];
+        const int64_t pl = pool[bid], hb = hostBase[bid];
+        if (m == 0 || t < 0 || s < 0 || pl < 0) continue;
+        const uint32_t row = static_cast<uint32_t>(hb + t);  // kvc_gather_rows.cpp:69-73
         const uint32_t node = kvx_node_of(row, a.stripeRows, a.nodeNum);
         const bool owned = x.fused ? (node < a.nodeNum) : (node == a.myNode);
         if (!owned) continue;
@@ -377,9 +420,8 @@ __global__ __launch_bounds__(256) void kvx_gather_small(GatherParams P)
         if (p < lo || p >= hi) continue;
         if (s < 65536) {
             const uint64_t d = win_index(bid, s, x.spanRows);
-            if (d < x.winEntries &&
-                win_load(x.win + d) !=
-                    (tagHi | static_cast<unsigned long long>(p))) {
+            if (d < x.winEntries && (global ? win_load(x.win + d) != (tagHi | static_cast<unsigned long long>(p))
+                                            : ((sLose >> (p - lo)) & 1u) != 0u)) {
                 continue;
             }
         }

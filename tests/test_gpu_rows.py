@@ -61,12 +61,14 @@ def _read_words(addr, n):
     return [int(x) for x in buf]
 
 
-@pytest.mark.parametrize("stride_mode", ["reference", "per_request"])
+@pytest.mark.parametrize("stride_mode", ["reference", "per_request", "overlap"])
 @pytest.mark.parametrize("fused", [False, True])
 def test_gather_parity_after_sieve(kvops, stride_mode, fused):
     """config-1 shapes: SIEVE on the GPU, then import; the hot buffer must equal
     the oracle's byte for byte after every step (last-position-wins rule when
-    destinations collide, which stride 0 makes common)."""
+    destinations collide: within a request when a step's sweep reuses a slot,
+    across requests with stride 0 (every request on the same rows) and with a
+    stride of 24 rows (request b's slots 24.. are request b+1's rows))."""
     req, prefill, top_k, dbs, L, N = 8, 256, 64, 64, 2, 2
     row_bytes = 1152
     layer_rows = req * prefill
@@ -81,8 +83,8 @@ def test_gather_parity_after_sieve(kvops, stride_mode, fused):
             st.admit(r, prefill)
         dev = DevSieve(st)
         padded = st.padded
-        stride = 0 if stride_mode == "reference" else padded
-        hot_rows = padded if stride == 0 else req * padded
+        stride = {"reference": 0, "per_request": padded, "overlap": 24}[stride_mode]
+        hot_rows = (req - 1) * stride + padded
         hot = torch.zeros((L, hot_rows, row_bytes), dtype=torch.uint8, device="cuda")
         hot_np = np.zeros((L, hot_rows, row_bytes), dtype=np.uint8)
         host_base = np.arange(req, dtype=np.int64) * prefill
