@@ -660,21 +660,27 @@ __global__ __launch_bounds__(256) void kvx_export_rows_copy(ExportRowsParams P)
 }
 
 // Short exports (max_rows <= kExportSmallMax, the rows a decode step
-// appends): both passes in one launch.  Every workgroup tags the winners of
-// all entries (the same atomicMax values, so the repeats are harmless) and
-// counts the owned entries and the lowest out-of-region entry per status word
-// in its own LDS, then copies the winners among its own entries (8 per
-// wave); the last workgroup (ticket) advances the epoch and stores the
-// status words from its counts.
+// appends): both passes in one launch.  A winner is the last entry on its
+// destination row.  Up to kExportSmallLds entries, every workgroup loads the
+// destinations of all entries into LDS and eight lanes per own entry look for
+// a later entry with the same destination (no device-scope atomics, no
+// fence); above that, every workgroup tags the winners of all entries (the
+// same atomicMax values, so the repeats are harmless) and reads its own
+// entries' tags.  Each workgroup counts the owned entries and the lowest
+// out-of-region entry per status word in its own LDS, then copies the
+// winners among its own 32 entries (8 per wave); the last workgroup (ticket)
+// advances the epoch and stores the status words from its counts.
 constexpr uint32_t kExportSmallMax = 4096;
+constexpr uint32_t kExportSmallLds = 1024;
 
 __global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
 {
     __shared__ uint64_t sSrc[kWaves][64];
     __shared__ uint64_t sDst[kWaves][64];
     __shared__ uint32_t sCnt[64 * 8], sErr[64 * 8];
+    __shared__ uint64_t sDest[kExportSmallLds];  // destination of each entry (~0: none), for n <= kExportSmallLds
     __shared__ int sLast;
-    __shared__ uint32_t sEpoch;
+    __shared__ uint32_t sEpoch, sLose;  // sLose bit e: own entry e is not a winner
     const ExportRowsArgs &a = P.a;
     const int wave = threadIdx.x / 64;
     const uint32_t lane = static_cast<uint32_t>(lane_id());
@@ -696,13 +702,37 @@ __global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
     if (threadIdx.x == 0) sEpoch = *P.epoch;
     __syncthreads();
     const unsigned long long tagHi = static_cast<unsigned long long>(sEpoch) << 32;
-    for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
+    // the destination of entry i when the winner rule applies to it, else ~0
+    auto entry_dest = [&](int32_t i) -> uint64_t {
         uint32_t node, segRow;
-        if (!export_row_target(a, idx[i], node, segRow) || segRow >= a.perLayerSegRows) continue;
+        if (!export_row_target(a, idx[i], node, segRow) || segRow >= a.perLayerSegRows) return ~0ull;
         const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
-        if (w < P.winEntries) win_max(P.win + w, tagHi | static_cast<unsigned long long>(i));
+        return w < P.winEntries ? w : ~0ull;
+    };
+    const int32_t first = static_cast<int32_t>(blockIdx.x) * kWaves * kExportRowsPerWave;  // own entries: 32 from here
+    const bool inLds = n <= static_cast<int32_t>(kExportSmallLds);
+    if (inLds) {
+        for (int32_t i = threadIdx.x; i < n; i += blockDim.x) sDest[i] = entry_dest(i);
+        if (threadIdx.x == 0) sLose = 0u;
+        __syncthreads();
+        // lanes 8e .. 8e+7: own entry first + e against the later entries
+        const int32_t e = static_cast<int32_t>(threadIdx.x >> 3), i = first + e;
+        bool later = false;
+        if (i < n) {
+            const uint64_t w = sDest[i];
+            if (w != ~0ull) {
+                for (int32_t j = i + 1 + static_cast<int32_t>(threadIdx.x & 7u); j < n; j += 8) later |= sDest[j] == w;
+            }
+        }
+        const uint64_t m = __ballot(later);
+        if ((threadIdx.x & 7u) == 0u && ((m >> lane) & 0xFFull) != 0ull) atomicOr(&sLose, 1u << e);
+    } else {
+        for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const uint64_t w = entry_dest(i);
+            if (w != ~0ull) win_max(P.win + w, tagHi | static_cast<unsigned long long>(i));
+        }
+        __threadfence();
     }
-    __threadfence();
     __syncthreads();
     for (int32_t i = threadIdx.x; i < n; i += blockDim.x) {
         uint32_t node, segRow;
@@ -720,9 +750,8 @@ __global__ __launch_bounds__(256) void kvx_export_rows_small(ExportRowsParams P)
         if (static_cast<int32_t>(lane) < R && i < n && export_row_target(a, idx[i], node, segRow) &&
             segRow < a.perLayerSegRows) {
             const uint64_t w = (a.fused ? static_cast<uint64_t>(node) * a.perLayerSegRows : 0ull) + segRow;
-            copy = w >= P.winEntries ||
-                   win_load(P.win + w) ==
-                       (tagHi | static_cast<unsigned long long>(i));
+            copy = w >= P.winEntries || (inLds ? ((sLose >> (i - first)) & 1u) == 0u
+                                               : win_load(P.win + w) == (tagHi | static_cast<unsigned long long>(i)));
             src = a.srcLayerBase + static_cast<uint64_t>(i) * a.rowBytes;
             dst = (a.fused ? export_seg_base(node) : a.segBase) +
                   (static_cast<uint64_t>(a.layerId) * a.perLayerSegRows + segRow) * a.rowBytes;

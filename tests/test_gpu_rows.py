@@ -259,13 +259,15 @@ def test_status_poll_device_memory(kvops):
 @pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("S,N,block_dim,max_rows,num_real", [(1, 2, 1, 64, 64), (1, 3, 3, 500, 377), (64, 4, 2, 256, 256),
                                                              (4, 2, 8, 1000, 999), (1, 1, 1, 40, 0),
-                                                             (1, 2, 4, 5000, 4999)])
+                                                             (1, 2, 2, 3000, 2900), (1, 2, 4, 5000, 4999)])
 def test_export_rows_parity(kvops, S, N, block_dim, max_rows, num_real, fused):
     """Decode-incremental export of one layer into every segment against the
     oracle: host rows with duplicates (last entry wins), negative rows and rows
     outside the layer region (reported, not written), num_real below the
     capacity; all segment bytes and every node's status words.  Up to 4096
-    entries the export is one launch, above it two (the 5000-entry case)."""
+    entries the export is one launch, above it two (the 5000-entry case); the
+    one launch decides winners in LDS up to 1024 entries and by device-scope
+    tags above (the 2900-entry case)."""
     print("export_rows case", S, N, block_dim, max_rows, num_real, fused, flush=True)
     L, layer_rows = 3, 4096
     pool = HostSegPool(0, L, layer_rows, ROW, stripe_rows=S, node_num=N)
