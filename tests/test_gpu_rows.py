@@ -175,6 +175,63 @@ def test_gather_large_batch_parity(kvops, req, top_k, num_real, S, N, stride_mod
         pool.destroy(close_ext=False)
 
 
+@pytest.mark.parametrize("req,top_k,dbs,stride_mode,fused,block_dim", [
+    (12, 20, 16, "padded", True, 2),     # a workgroup's 32 positions straddle two requests
+    (40, 7, 8, "padded", False, 3),      # ... and five
+    (10, 48, 32, "half", True, 1),       # stride 16 < slots in use: neighbouring requests share rows
+    (6, 100, 64, "zero", False, 2),      # stride 0: every request on the same rows
+    (1, 4096, 4096, "padded", True, 8),  # the largest one-launch call: one request of 4096 positions
+])
+def test_gather_small_batch_winners(kvops, req, top_k, dbs, stride_mode, fused, block_dim):
+    """The one-launch import (max_num_reqs * top_k <= 4096) against the oracle
+    on constructed inputs with many misses on one destination row: within a
+    request (the winner decided in LDS from the workgroup's own requests,
+    whose positions may straddle workgroups) and across requests (a stride
+    below the slots in use: device-scope tags of every position); invalid
+    tokens and slots, a request without a pool row; every hot byte and every
+    node's status words."""
+    print("small import case", req, top_k, dbs, stride_mode, fused, block_dim, flush=True)
+    L, layer, prefill, S, N = 2, 1, 512, 1, 2
+    padded = (dbs + 15) // 16 * 16
+    layer_rows = req * prefill
+    pool = HostSegPool(0, L, layer_rows, ROW, stripe_rows=S, node_num=N)
+    pool.create_pool()
+    try:
+        rng = np.random.default_rng(req * 1000 + top_k + dbs)
+        views = pool.segment_views()
+        for v in views:
+            v[...] = rng.integers(0, 256, size=v.shape, dtype=np.uint8)
+        segs = [v.reshape(-1) for v in views]
+        topk = rng.integers(0, prefill, size=(req, top_k)).astype(np.int32)
+        topk[rng.random((req, top_k)) < 0.03] = -1
+        slots = rng.integers(0, dbs, size=(req, top_k)).astype(np.int32)
+        slots[rng.random((req, top_k)) < 0.02] = -1
+        miss = (rng.random((req, top_k)) < 0.6).astype(np.int8)
+        pool_idx = np.arange(req, dtype=np.int64)
+        if req >= 3:
+            pool_idx[2] = -1
+        host_base = np.arange(req, dtype=np.int64) * prefill
+        stride = {"padded": padded, "zero": 0, "half": padded // 2}[stride_mode]
+        hot_rows = (req - 1) * stride + padded
+        hot_np = rng.integers(0, 256, size=(hot_rows, ROW), dtype=np.uint8)
+        hot = torch.from_numpy(hot_np.copy()).cuda()
+        args = (layer, to_dev(topk), to_dev(pool_idx), to_dev(host_base), to_dev(slots), to_dev(miss),
+                to_dev(np.array([req], dtype=np.int32)), hot, req, top_k)
+        read = pool.batch_read_fused if fused else pool.batch_read
+        status = read(*args, block_dim=block_dim, hot_req_stride_rows=stride)
+        pool.wait(status, block_dim=block_dim)
+        torch.cuda.synchronize()
+        plsr = pool.per_layer_seg_rows
+        for s in range(N):
+            _, words = orc.gather_rows(segs, hot_np.reshape(-1), layer * plsr, ROW, topk, pool_idx, host_base, slots,
+                                       miss, req, top_k, req, S, N, s, hot_req_stride_rows=stride,
+                                       block_dim=block_dim)
+            assert _read_words(status + s * 64, block_dim) == [int(w) for w in words], s
+        np.testing.assert_array_equal(hot.cpu().numpy(), hot_np)
+    finally:
+        pool.destroy(close_ext=False)
+
+
 @pytest.mark.parametrize("top_k", [1000, 3000])   # 3 x 1000 positions: one-launch form; 3 x 3000: two launches
 @pytest.mark.parametrize("fused", [False, True])    # import_seg per segment, or import_all
 def test_gather_rows_past_layer_region(kvops, top_k, fused):
