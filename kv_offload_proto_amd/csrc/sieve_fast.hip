@@ -1010,7 +1010,9 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     }
     // A row whose recent steps all wrapped the hand (the parallel form's
     // bound) retries the parallel form after 8, 16, 32 and then every 64
-    // such steps; the other steps
+    // such steps, a row of up to 64 slots (whose decisions in registers cost
+    // about what the parallel form does, while a retry that fails restages
+    // the row) after 8, 16 and then every 256; the other steps
     // run the in-order recurrence on the row as staged (known consistent when
     // it passed the check above and its entry count matches its live
     // tokens).  Consistent rows
@@ -1018,7 +1020,8 @@ __global__ __launch_bounds__(NT) void kvx_sieve_update_fast(KvxLaunch<HispSieveU
     // registers and leave the table to the parallel update: the pre-step
     // token of every evicted slot leaves, the slots' final tokens arrive in
     // the order of the events that placed them.
-    const bool retry = (hintw >= 8 && __popc(static_cast<uint32_t>(hintw)) == 1) || (hintw & 63) == 0;
+    const bool retry = dbs <= 64 ? (hintw == 8 || hintw == 16 || (hintw & 255) == 0)
+                                 : ((hintw >= 8 && __popc(static_cast<uint32_t>(hintw)) == 1) || (hintw & 63) == 0);
     if (!kC && hintw > 0 && !retry) {
         const bool canon = ms.bad == 0 && ms.diff == 0;
         if (!(canon && dbs <= 64)) {
